@@ -1,0 +1,269 @@
+"""Benchmark of the MI355X MoE layer.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-prefill] [--no-cpu]
+
+Workload ("C2"): single-token decode through 48
+distinct MoE layers back to back (T=1, H=2048, E=128, top-8 softmax, SwiGLU
+I=768, GPTQ int4 g128 fp16 scales, random weights generated on the GPU).
+One step = one token through all 48 layers (router GEMV, top-k, gate_up,
+down), so the 48 x 20.5 MB of touched weights (985 MB) exceed the 256 MB
+MALL.  `value` is HBM GB/s over the algorithmic bytes of the step: the
+distinct experts each layer touches (payload + scales), the fp32 router,
+x and y.  Inputs are resident in HBM before timing starts.
+
+The JSON line also carries:
+  roofline      gate_up decode kernel (the dominant one), timed with HIP
+                events on its stream, against 8 TB/s;
+  cpu_baseline  the reference's own CPU oracle (src/moe_ref.cpp, built into
+                oracle/_ref) on a bounded sample of the same layers;
+  prefill       C4 (T=4096, E=512, top-10, int8, shared expert): layer time
+                and grouped-GEMM TFLOPS against the bf16 MFMA peak.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from grimoire_amd import _abi, configs, ops  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+LAYERS = 48
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Timer:
+    """HIP events recorded on the given stream."""
+
+    def __init__(self, stream):
+        self.s = stream
+        self.a = torch.cuda.Event(enable_timing=True)
+        self.b = torch.cuda.Event(enable_timing=True)
+
+    def __enter__(self):
+        self.a.record(self.s)
+        return self
+
+    def __exit__(self, *exc):
+        self.b.record(self.s)
+
+    def ms(self):
+        self.b.synchronize()
+        return self.a.elapsed_time(self.b)
+
+
+def decode_bench(steps, warmup, dev, stream):
+    cfg = configs.CONFIGS["c2"]
+    layers = [configs.make_layer(cfg, dev, seed=100 + i) for i in range(LAYERS)]
+    x = configs.make_x(cfg, dev, seed=7)
+    fwds = [ops.MoeForward(L, 1, configs.route_params(cfg, None), regime=1) for L in layers]
+    ys = [torch.empty(1, cfg.H, device=dev) for _ in layers]
+    oes = [torch.empty(1, cfg.K, dtype=torch.int32, device=dev) for _ in layers]
+    ows = [torch.empty(1, cfg.K, dtype=torch.float32, device=dev) for _ in layers]
+
+    def step():
+        for f, y, oe, ow in zip(fwds, ys, oes, ows):
+            f(x, y, oe, ow, stream=stream)
+
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        # algorithmic bytes from the actual routing
+        ebytes = layers[0].expert_bytes()
+        step_bytes = 0.0
+        for oe in oes:
+            distinct = len(set(oe.flatten().tolist()))
+            step_bytes += distinct * ebytes + cfg.E * cfg.H * 4 + 2 * cfg.H * 4
+        torch.cuda.synchronize()
+        with Timer(stream) as tm:
+            for _ in range(steps):
+                step()
+        ms = tm.ms() / steps
+        torch.cuda.synchronize()
+
+        # dominant kernel: gate_up, launched alone per layer on this stream
+        h = torch.empty(1, cfg.K, cfg.I, device=dev)
+        gu_bytes = cfg.K * layers[0].gate_up.row_bytes_total() * 2 * cfg.I + cfg.H * 4
+        reps = max(steps, 10)
+        for L, oe in zip(layers, oes):
+            ops.launch_moe_gate_up_batched(L, oe, x, h, 1, stream=stream)
+        torch.cuda.synchronize()
+        with Timer(stream) as tg:
+            for _ in range(reps):
+                for L, oe in zip(layers, oes):
+                    ops.launch_moe_gate_up_batched(L, oe, x, h, 1, stream=stream)
+        gu_us = tg.ms() * 1e3 / (reps * LAYERS)
+
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    return dict(cfg=cfg, ms=ms, step_bytes=step_bytes, gbs=gbs, gu_us=gu_us, gu_bytes=gu_bytes,
+                layers=layers, x=x, oes=oes, ows=ows)
+
+
+def prefill_bench(dev, stream, reps=5):
+    cfg = configs.CONFIGS["c4"]
+    wl = configs.make_workload(cfg, dev, seed=11)
+    L = wl.layer
+    fwd = ops.MoeForward(L, cfg.T, configs.route_params(cfg, wl.route_bias), regime=2)
+    y = torch.empty(cfg.T, cfg.H, device=dev)
+    oe = torch.empty(cfg.T, cfg.K, dtype=torch.int32, device=dev)
+    ow = torch.empty(cfg.T, cfg.K, dtype=torch.float32, device=dev)
+    with torch.cuda.stream(stream):
+        fwd(wl.x, y, oe, ow, stream=stream)
+        torch.cuda.synchronize()
+        with Timer(stream) as tm:
+            for _ in range(reps):
+                fwd(wl.x, y, oe, ow, stream=stream)
+        layer_ms = tm.ms() / reps
+        # the routed grouped GEMMs alone, on the same routing
+        R = cfg.T * cfg.K
+        tmax = cfg.E + (R + 127) // 128
+        counts = torch.empty(cfg.E, dtype=torch.int32, device=dev)
+        offsets = torch.empty(cfg.E, dtype=torch.int32, device=dev)
+        inverse = torch.empty(R, dtype=torch.int32, device=dev)
+        te = torch.empty(tmax, dtype=torch.int32, device=dev)
+        tmb = torch.empty(tmax, dtype=torch.int32, device=dev)
+        xperm = torch.empty(R, cfg.H, dtype=torch.int16, device=dev)
+        ops.launch_moe_route_grouped(wl.x, oe, xperm, None, counts, offsets, inverse, te, tmb, tmax,
+                                     cfg.T, cfg.H, cfg.E, 128, cfg.K, stream=stream)
+        hp = torch.empty(R, 2, cfg.I, dtype=torch.int16, device=dev)
+        yp = torch.empty(R, cfg.H, device=dev)
+        ops.grouped_gemm(L.gate_up, 2 * cfg.I, True, xperm, hp, offsets, counts, cfg.E, R, stream=stream)
+        ops.grouped_gemm(L.down, cfg.H, False, hp, yp, offsets, counts, cfg.E, R, a_pair=True,
+                         stream=stream)
+        torch.cuda.synchronize()
+        with Timer(stream) as tg:
+            for _ in range(reps):
+                ops.grouped_gemm(L.gate_up, 2 * cfg.I, True, xperm, hp, offsets, counts, cfg.E, R,
+                                 stream=stream)
+        gu_ms = tg.ms() / reps
+        with Timer(stream) as td:
+            for _ in range(reps):
+                ops.grouped_gemm(L.down, cfg.H, False, hp, yp, offsets, counts, cfg.E, R,
+                                 a_pair=True, stream=stream)
+        dn_ms = td.ms() / reps
+        cnt = counts.cpu()
+    touched = int((cnt > 0).sum())
+    routed_flops = 6.0 * R * cfg.H * cfg.I
+    shared_flops = 6.0 * cfg.T * cfg.H * cfg.I
+    gu_flops, dn_flops = 4.0 * R * cfg.H * cfg.I, 2.0 * R * cfg.H * cfg.I
+    ebytes = L.expert_bytes()
+    layer_bytes = touched * ebytes + L.shared_bytes() + cfg.E * cfg.H * 4 + 2 * cfg.T * cfg.H * 4
+    return {
+        "workload": "c4: T=4096 H=2048 E=512 top-10 softmax (Zipf 1.2) I=512 int8 + shared I=512",
+        "layer_us": round(layer_ms * 1e3, 1),
+        "layer_tflops": round((routed_flops + shared_flops) / (layer_ms * 1e-3) / 1e12, 2),
+        "experts_touched": touched,
+        "layer_hbm_gbs": round(layer_bytes / (layer_ms * 1e-3) / 1e9, 1),
+        "gate_up_gemm_us": round(gu_ms * 1e3, 1),
+        "gate_up_gemm_tflops": round(gu_flops / (gu_ms * 1e-3) / 1e12, 2),
+        "down_gemm_us": round(dn_ms * 1e3, 1),
+        "down_gemm_tflops": round(dn_flops / (dn_ms * 1e-3) / 1e12, 2),
+        "down_gemm_mfma_passes": 2,
+        "mfma_peak_tflops": BF16_MFMA_PEAK_TFLOPS,
+        "gate_up_mfma_frac": round(gu_flops / (gu_ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4),
+    }
+
+
+def cpu_baseline(d, budget_s=15.0):
+    """The reference's src/moe_ref.cpp (oracle/_ref) on the same layers."""
+    try:
+        from oracle import oracle as O
+    except Exception as e:  # pragma: no cover
+        return {"error": f"oracle unavailable: {e}"}
+    r = O.ref()
+    kind = "reference"
+    if r is None:
+        kind = "port"
+    cfg = d["cfg"]
+    x = d["x"].cpu()
+    done, nbytes, t0 = 0, 0.0, time.perf_counter()
+    for L, oe, ow in zip(d["layers"], d["oes"], d["ows"]):
+        Lc = L.to("cpu")
+        s = Lc.struct()
+        y = torch.empty(1, cfg.H)
+        e, w = oe.cpu().contiguous(), ow.cpu().contiguous()
+        if r is not None:
+            r.ref_moe_forward(O.byref(s), O._p(e), O._p(w), O._p(x), O._p(y), 1)
+        else:
+            O.orc().orc_moe_forward(O.byref(s), O._p(e), O._p(w), None, O._p(x), O._p(y), 1)
+        done += 1
+        nbytes += len(set(e.flatten().tolist())) * L.expert_bytes() + cfg.E * cfg.H * 4 + 2 * cfg.H * 4
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"{done} of the {LAYERS} C2 layers, one token, single thread "
+                      f"({dt:.1f} s; includes copying each layer to host memory)",
+            "us_per_layer": round(dt / done * 1e6, 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(expert parallelism is a design note, not code).", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    _abi.lib()
+    stream = torch.cuda.Stream()
+    log("decode bench (C2, 48 layers)...")
+    d = decode_bench(a.steps, a.warmup, dev, stream)
+    out = {
+        "metric": "MoE decode layer HBM GB/s (T=1, C2, 48 layers back to back)",
+        "value": round(d["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(d["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 weights (fp16 group scales), fp32 accumulate",
+        "data": "synthetic (seeded random weights and activations of the C2 shapes)",
+        "config": {"workload": "c2: T=1 H=2048 E=128 top-8 softmax I=768 GPTQ int4 g128, "
+                               "48 distinct layers", "layers": LAYERS},
+        "us_per_layer": round(d["ms"] * 1e3 / LAYERS, 2),
+        "hbm_frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "moe_gate_up_slots<INT4_F16> (decode gate_up + SwiGLU)",
+            "achieved": round(d["gu_bytes"] / (d["gu_us"] * 1e-6) / 1e9, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(d["gu_bytes"] / (d["gu_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "launch_us": round(d["gu_us"], 3),
+            "bytes_per_launch": int(d["gu_bytes"]),
+        },
+    }
+    if not a.no_prefill:
+        log("prefill bench (C4)...")
+        out["prefill"] = prefill_bench(dev, stream)
+    if not a.no_cpu:
+        log("cpu baseline...")
+        out["cpu_baseline"] = cpu_baseline(d)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,144 @@
+"""ctypes view of include/grimoire_moe.h and the loader of libgrimoire_moe.so.
+
+The library is loaded from this package directory only.  There is no CPU
+fallback: if the library is missing, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libgrimoire_moe.so"
+
+# enum grim_fmt (include/grimoire_moe.h); codes 0..6 follow the reference's
+# Fmt numbering (include/b70/formats.hpp:237-239).
+FMT_BF16 = 0
+FMT_INT8 = 3
+FMT_INT4 = 4
+FMT_MXFP4 = 6
+FMT_INT4_F16 = 64
+
+ROUTE_SOFTMAX = 0
+ROUTE_SIGMOID = 1
+ROUTE_GROUP = 2
+
+ERR_FORMAT, ERR_SHAPE, ERR_ARG, ERR_WORKSPACE = -1, -2, -3, -4
+
+
+class QuantWeight(C.Structure):
+    """b70::QuantWeight (include/b70/weights.hpp:46-126)."""
+    _fields_ = [
+        ("fmt", C.c_int32),
+        ("N", C.c_int32),
+        ("K", C.c_int32),
+        ("row_scales", C.c_int32),
+        ("row_bytes", C.c_int64),
+        ("payload", C.c_void_p),
+        ("scales", C.c_void_p),
+        ("zeros", C.c_void_p),
+    ]
+
+
+class MoeConfig(C.Structure):
+    """b70::MoeConfig (include/b70/moe.hpp:70-77)."""
+    _fields_ = [
+        ("hidden", C.c_int32),
+        ("inter", C.c_int32),
+        ("num_experts", C.c_int32),
+        ("top_k", C.c_int32),
+        ("shared_inter", C.c_int32),
+        ("norm_topk", C.c_int32),
+    ]
+
+
+class MoeLayer(C.Structure):
+    """b70::MoeLayer (include/b70/moe.hpp:85-117)."""
+    _fields_ = [
+        ("cfg", MoeConfig),
+        ("gate_up", QuantWeight),
+        ("down", QuantWeight),
+        ("has_shared", C.c_int32),
+        ("_pad", C.c_int32),
+        ("shared_gate_up", QuantWeight),
+        ("shared_down", QuantWeight),
+        ("router", C.c_void_p),
+    ]
+
+
+class RouteParams(C.Structure):
+    _fields_ = [
+        ("mode", C.c_int32),
+        ("n_group", C.c_int32),
+        ("topk_group", C.c_int32),
+        ("scaling", C.c_float),
+        ("bias", C.c_void_p),
+    ]
+
+
+P = C.c_void_p
+I32 = C.c_int
+F32 = C.c_float
+SZ = C.c_size_t
+QWP = C.POINTER(QuantWeight)
+LP = C.POINTER(MoeLayer)
+RPP = C.POINTER(RouteParams)
+
+# name -> (restype, argtypes); must match include/grimoire_moe.h
+SIGNATURES = {
+    "grimoire_moe_last_error": (C.c_char_p, []),
+    "grimoire_moe_version": (C.c_char_p, []),
+    "grimoire_moe_router_logits": (I32, [P, P, P, P, I32, I32, I32]),
+    "grimoire_moe_router_topk": (I32, [P, P, I32, I32, P, P, I32]),
+    "grimoire_moe_router_topk_batched": (I32, [P, P, I32, I32, I32, P, P, I32]),
+    "grimoire_moe_router_topk_sigmoid": (I32, [P, P, P, I32, I32, I32, P, P, I32, F32]),
+    "grimoire_moe_router_topk_group": (I32, [P, P, P, I32, I32, I32, I32, I32, P, P, I32, F32]),
+    "grimoire_moe_gate_up": (I32, [P, LP, P, P, P]),
+    "grimoire_moe_down": (I32, [P, LP, P, P, P, P]),
+    "grimoire_moe_gate_up_shared": (I32, [P, LP, QWP, P, P, P, P, P]),
+    "grimoire_moe_down_shared": (I32, [P, LP, QWP, P, P, P, P, P]),
+    "grimoire_moe_gate_up_batched": (I32, [P, LP, P, P, P, I32]),
+    "grimoire_moe_down_batched": (I32, [P, LP, P, P, P, P, I32]),
+    "grimoire_moe_shared_rows": (I32, [P, LP, QWP, QWP, P, P, P, P, P, P, P, I32]),
+    "grimoire_moe_route_workspace_bytes": (SZ, [I32, I32, I32]),
+    "grimoire_moe_route_grouped": (I32, [P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32,
+                                         I32, P, P, SZ]),
+    "grimoire_moe_remap_bf16": (I32, [P, P, P, P, P, P, P, I32, I32, I32, I32, P, SZ]),
+    "grimoire_moe_unpermute": (I32, [P, P, P, P, P, I32, I32, I32]),
+    "grimoire_moe_unpermute_bf16": (I32, [P, P, P, P, P, I32, I32, I32]),
+    "grimoire_moe_combine": (I32, [P, P, P, P, P, P, P, I32, I32, I32]),
+    "grimoire_moe_grouped_gemm": (I32, [P, QWP, I32, I32, P, I32, P, I32, P, P, I32, I32]),
+    "grimoire_xe2_grouped_mxfp4_bf16": (None, [P, P, P, P, P, I32, I32, P, P, I32, P]),
+    "grimoire_xe2_grouped_w4a16": (None, [P, P, P, P, P, I32, I32, P, P, I32, I32, P]),
+    "grimoire_xe2_fused_moe_gate_up_mxfp4_silu_bf16": (None, [P, P, P, P, P, I32, I32, P, I32, P]),
+    "grimoire_moe_forward_workspace_bytes": (SZ, [LP, I32]),
+    "grimoire_moe_forward": (I32, [P, LP, RPP, P, P, P, I32, P, P, I32, P, SZ]),
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """The loaded library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m grimoire_amd.build` "
+                "(there is no CPU fallback)")
+        l = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(l, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = l
+    return _lib
+
+
+class GrimoireError(RuntimeError):
+    pass
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = lib().grimoire_moe_last_error().decode()
+        raise GrimoireError(f"{what} failed with status {status}: {msg}")

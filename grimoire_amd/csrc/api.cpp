@@ -1,0 +1,511 @@
+// api.cpp -- the extern "C" entry points of libgrimoire_moe.so.
+//
+// Argument checks happen here, on the host, before any launch: a shape the
+// kernels do not support is rejected with a negative status and a message
+// (grimoire_moe_last_error), never launched.  Each entry point cites the
+// reference launcher it replaces in include/grimoire_moe.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "../../include/grimoire_moe.h"
+#include "common.hpp"
+#include "dispatch.hpp"
+#include "gemm.hpp"
+#include "gemv.hpp"
+#include "router.hpp"
+
+using namespace grim;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int status(hipError_t e) {
+    if (e == hipSuccess) return GRIM_OK;
+    std::snprintf(g_err, sizeof g_err, "HIP error: %s", hipGetErrorString(e));
+    return int(e);
+}
+
+hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
+
+bool fmt_known(int f) {
+    return f == GRIM_FMT_BF16 || f == GRIM_FMT_INT8 || f == GRIM_FMT_INT4 ||
+           f == GRIM_FMT_INT4_F16 || f == GRIM_FMT_MXFP4;
+}
+
+// Check a weight view against the rows/cols the kernels will touch.
+int check_weight(const grim_quant_weight* w, const char* name, int64_t rows, int K) {
+    if (!w) return fail(GRIM_ERR_ARG, "%s: null weight", name);
+    if (!fmt_known(w->fmt)) return fail(GRIM_ERR_FORMAT, "%s: format %d not supported", name, w->fmt);
+    if (!w->payload) return fail(GRIM_ERR_ARG, "%s: null payload", name);
+    if (w->K != K) return fail(GRIM_ERR_SHAPE, "%s: K=%d, expected %d", name, w->K, K);
+    if (int64_t(w->N) < rows) return fail(GRIM_ERR_SHAPE, "%s: N=%d < %lld rows", name, w->N, (long long)rows);
+    const int CH = chunk_elems(w->fmt);
+    if (K % CH) return fail(GRIM_ERR_SHAPE, "%s: K=%d not a multiple of %d", name, K, CH);
+    int64_t need = 0;
+    switch (w->fmt) {
+    case GRIM_FMT_BF16: need = int64_t(K) * 2; break;
+    case GRIM_FMT_INT8: need = K; break;
+    default: need = K / 2; break;
+    }
+    if (w->row_bytes < need || (w->row_bytes % 16))
+        return fail(GRIM_ERR_SHAPE, "%s: row_bytes=%lld (need >= %lld, multiple of 16)", name,
+                    (long long)w->row_bytes, (long long)need);
+    if (reinterpret_cast<uintptr_t>(w->payload) % 16)
+        return fail(GRIM_ERR_ARG, "%s: payload not 16-byte aligned", name);
+    if (w->fmt != GRIM_FMT_BF16 && !w->scales) return fail(GRIM_ERR_ARG, "%s: null scales", name);
+    if (w->fmt == GRIM_FMT_MXFP4 && w->row_scales < K / 32)
+        return fail(GRIM_ERR_SHAPE, "%s: row_scales=%d < K/32", name, w->row_scales);
+    if (w->fmt == GRIM_FMT_INT4 || w->fmt == GRIM_FMT_INT4_F16) {
+        const int gs = 1 << int4_gshift(w->row_scales, K);
+        if (K % gs || w->row_scales * gs != K)
+            return fail(GRIM_ERR_SHAPE, "%s: INT4 group layout (row_scales=%d, K=%d)", name,
+                        w->row_scales, K);
+        if (gs < 32) return fail(GRIM_ERR_SHAPE, "%s: INT4 group < 32", name);
+    }
+    return GRIM_OK;
+}
+
+WView view(const grim_quant_weight& w) { return make_view(w); }
+
+int check_layer(const grim_moe_layer* L) {
+    if (!L) return fail(GRIM_ERR_ARG, "null layer");
+    const auto& c = L->cfg;
+    if (c.hidden <= 0 || c.inter <= 0 || c.num_experts <= 0 || c.top_k <= 0)
+        return fail(GRIM_ERR_SHAPE, "bad config");
+    if (c.top_k > 16 || c.top_k > c.num_experts) return fail(GRIM_ERR_SHAPE, "top_k=%d", c.top_k);
+    if (c.num_experts > 512) return fail(GRIM_ERR_SHAPE, "num_experts=%d > 512", c.num_experts);
+    int r = check_weight(&L->gate_up, "gate_up", int64_t(c.num_experts) * 2 * c.inter, c.hidden);
+    if (r) return r;
+    return check_weight(&L->down, "down", int64_t(c.num_experts) * c.hidden, c.inter);
+}
+
+// LDS ceiling of one work-group on gfx950 (160 KiB).
+constexpr size_t kMaxLds = 160 * 1024;
+
+int gemv_common(void* stream, const grim_moe_layer* L, const grim_quant_weight* wsh,
+                const uint16_t* gate_w, const int32_t* rex, const float* x, float* h,
+                float* gate_out, int M) {
+    int r = check_layer(L);
+    if (r) return r;
+    if (M <= 0) return GRIM_OK;
+    if (!rex || !x || !h) return fail(GRIM_ERR_ARG, "null routing/x/h");
+    const auto& c = L->cfg;
+    if (wsh) {
+        r = check_weight(wsh, "shared gate_up", 2 * int64_t(c.inter), c.hidden);
+        if (r) return r;
+        if (wsh->fmt != L->gate_up.fmt)
+            return fail(GRIM_ERR_FORMAT, "shared expert format must match routed experts");
+    }
+    if (gate_w && !gate_out) return fail(GRIM_ERR_ARG, "gate_w without gate_out");
+    if (gemv_lds_bytes(L->gate_up.fmt, c.hidden, c.inter, 0, false) > kMaxLds)
+        return fail(GRIM_ERR_SHAPE, "hidden=%d too large for the decode kernel", c.hidden);
+    GemvArgs a{};
+    a.w = view(L->gate_up);
+    a.ws = wsh ? view(*wsh) : a.w;
+    a.shared = wsh != nullptr;
+    a.rex = rex;
+    a.x = x;
+    a.h = h;
+    a.gate_w = gate_w;
+    a.gate_out = gate_out;
+    a.H = c.hidden;
+    a.I = c.inter;
+    a.K = c.top_k;
+    a.M = M;
+    a.E = c.num_experts;
+    return status(gemv_launch(S(stream), L->gate_up.fmt, a, false));
+}
+
+int down_common(void* stream, const grim_moe_layer* L, const grim_quant_weight* wd,
+                const int32_t* rex, const float* rwt, const float* gate_in, const float* h,
+                float* y, int M) {
+    int r = check_layer(L);
+    if (r) return r;
+    if (M <= 0) return GRIM_OK;
+    if (!rex || !rwt || !h || !y) return fail(GRIM_ERR_ARG, "null routing/h/y");
+    const auto& c = L->cfg;
+    if (wd) {
+        r = check_weight(wd, "shared down", c.hidden, c.inter);
+        if (r) return r;
+        if (wd->fmt != L->down.fmt)
+            return fail(GRIM_ERR_FORMAT, "shared expert format must match routed experts");
+    }
+    const int KS = c.top_k + (wd ? 1 : 0);
+    if (gemv_lds_bytes(L->down.fmt, c.hidden, c.inter, KS, true) > kMaxLds)
+        return fail(GRIM_ERR_SHAPE, "(top_k+shared)*inter too large for the decode kernel");
+    GemvArgs a{};
+    a.w = view(L->down);
+    a.ws = wd ? view(*wd) : a.w;
+    a.shared = wd != nullptr;
+    a.rex = rex;
+    a.rwt = rwt;
+    a.gate_in = gate_in;
+    a.h = const_cast<float*>(h);
+    a.y = y;
+    a.H = c.hidden;
+    a.I = c.inter;
+    a.K = c.top_k;
+    a.M = M;
+    a.E = c.num_experts;
+    return status(gemv_launch(S(stream), L->down.fmt, a, true));
+}
+
+// Library-held scratch for the bridges, whose signatures carry none.
+struct BridgeScratch {
+    int device = -1;
+    void* p = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_scratch_mu;
+std::vector<BridgeScratch> g_scratch;
+
+void* bridge_scratch(size_t bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    for (auto& s : g_scratch)
+        if (s.device == dev) {
+            if (s.bytes >= bytes) return s.p;
+            if (hipFree(s.p) != hipSuccess) return nullptr;
+            s.p = nullptr;
+            if (hipMalloc(&s.p, bytes) != hipSuccess) { s.bytes = 0; return nullptr; }
+            s.bytes = bytes;
+            return s.p;
+        }
+    BridgeScratch s;
+    s.device = dev;
+    if (hipMalloc(&s.p, bytes) != hipSuccess) return nullptr;
+    s.bytes = bytes;
+    g_scratch.push_back(s);
+    return s.p;
+}
+
+__global__ void tiles_from_counts(const int* __restrict__ rows, int ne, int mc,
+                                  int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                                  int32_t* __restrict__ tile_e, int32_t* __restrict__ tile_mb,
+                                  int tmax, int32_t* __restrict__ n_tiles) {
+    // single thread: ne is at most a few hundred
+    if (threadIdx.x != 0) return;
+    int off = 0, nt = 0;
+    for (int e = 0; e < ne; ++e) {
+        const int c = rows[e] > 0 ? rows[e] : 0;
+        counts[e] = c;
+        offsets[e] = off;
+        off += c;
+        for (int mb = 0; mb * mc < c; ++mb) {
+            if (nt < tmax) { tile_e[nt] = e; tile_mb[nt] = mb; }
+            ++nt;
+        }
+    }
+    *n_tiles = nt < tmax ? nt : tmax;
+}
+
+constexpr int kBridgeTileCap = 1 << 16;
+
+// Shared body of the three bridges: counts -> tile table, then one grouped
+// GEMM over [ne][n (x2 for swiglu)][k] packed experts.
+int bridge_common(void* stream, const grim_quant_weight& w, int N, int I, int swiglu,
+                  const void* a, void* d, const int* rows, int ne) {
+    const size_t need = size_t(4 * ne + 2 * kBridgeTileCap + 4) * sizeof(int32_t);
+    int32_t* sc = static_cast<int32_t*>(bridge_scratch(need));
+    if (!sc) return fail(GRIM_ERR_WORKSPACE, "bridge scratch allocation failed");
+    int32_t* counts = sc;
+    int32_t* offsets = sc + ne;
+    int32_t* tile_e = sc + 2 * ne;
+    int32_t* tile_mb = tile_e + kBridgeTileCap;
+    int32_t* n_tiles = tile_mb + kBridgeTileCap;
+    hipLaunchKernelGGL(tiles_from_counts, dim3(1), dim3(64), 0, S(stream), rows, ne, kGemmBM,
+                       counts, offsets, tile_e, tile_mb, kBridgeTileCap, n_tiles);
+    GemmArgs g{};
+    g.w = view(w);
+    g.N = N;
+    g.K = w.K;
+    g.I = I;
+    g.swiglu = swiglu;
+    g.a_pair = 0;
+    g.out_bf16 = 1;
+    g.A = static_cast<const uint16_t*>(a);
+    g.out = d;
+    g.offsets = offsets;
+    g.counts = counts;
+    g.tile_e = tile_e;
+    g.tile_mb = tile_mb;
+    g.tmax = kBridgeTileCap;
+    g.n_tiles_dev = n_tiles;
+    g.T_sh = 0;
+    return status(gemm_launch(S(stream), w.fmt, g));
+}
+
+}  // namespace
+
+extern "C" {
+
+__attribute__((visibility("hidden"))) void grimoire_moe_set_error_(const char* msg) {
+    std::snprintf(g_err, sizeof g_err, "%s", msg);
+}
+
+const char* grimoire_moe_last_error(void) { return g_err; }
+const char* grimoire_moe_version(void) { return "grimoire_amd 0.1 (gfx950)"; }
+
+int grimoire_moe_router_logits(void* stream, const float* router, const float* x, float* logits,
+                               int tokens, int n_experts, int hidden) {
+    if (tokens <= 0) return GRIM_OK;
+    if (!router || !x || !logits) return fail(GRIM_ERR_ARG, "null pointer");
+    if (n_experts <= 0 || hidden <= 0 || hidden % 4) return fail(GRIM_ERR_SHAPE, "hidden %% 4");
+    return status(router_logits_launch(S(stream), router, x, nullptr, logits, tokens, n_experts, hidden));
+}
+
+static int topk_common(void* stream, const TopkArgs& a) {
+    if (a.T <= 0) return GRIM_OK;
+    if (!a.logits || !a.out_e || !a.out_w) return fail(GRIM_ERR_ARG, "null pointer");
+    if (a.E <= 0 || a.E > 512) return fail(GRIM_ERR_SHAPE, "n_experts=%d (1..512)", a.E);
+    if (a.K <= 0 || a.K > 16 || a.K > a.E) return fail(GRIM_ERR_SHAPE, "top_k=%d (1..16)", a.K);
+    return status(topk_launch(S(stream), a));
+}
+
+int grimoire_moe_router_topk(void* stream, const float* logits, int n_experts, int top_k,
+                             int32_t* out_expert, float* out_weight, int normalize) {
+    TopkArgs a{logits, 1, n_experts, top_k, 0, normalize, 1.0f, nullptr, nullptr, 0, 0,
+               out_expert, out_weight};
+    return topk_common(stream, a);
+}
+
+int grimoire_moe_router_topk_batched(void* stream, const float* logits, int tokens, int n_experts,
+                                     int top_k, int32_t* out_expert, float* out_weight,
+                                     int normalize) {
+    TopkArgs a{logits, tokens, n_experts, top_k, 1, normalize, 1.0f, nullptr, nullptr, 0, 0,
+               out_expert, out_weight};
+    return topk_common(stream, a);
+}
+
+int grimoire_moe_router_topk_sigmoid(void* stream, const float* logits, const uint16_t* bias_bf16,
+                                     int tokens, int n_experts, int top_k, int32_t* out_expert,
+                                     float* out_weight, int normalize, float scaling) {
+    TopkArgs a{logits, tokens, n_experts, top_k, 2, normalize, scaling, bias_bf16, nullptr, 0, 0,
+               out_expert, out_weight};
+    return topk_common(stream, a);
+}
+
+int grimoire_moe_router_topk_group(void* stream, const float* logits, const float* bias,
+                                   int tokens, int n_experts, int top_k, int n_group,
+                                   int topk_group, int32_t* out_expert, float* out_weight,
+                                   int normalize, float scaling) {
+    if (n_group <= 0 || n_group > 64 || n_experts % n_group)
+        return fail(GRIM_ERR_SHAPE, "n_group=%d must divide n_experts=%d (<= 64 groups)", n_group,
+                    n_experts);
+    if (topk_group <= 0 || topk_group > n_group) return fail(GRIM_ERR_SHAPE, "topk_group=%d", topk_group);
+    if (top_k > topk_group * (n_experts / n_group))
+        return fail(GRIM_ERR_SHAPE, "top_k exceeds the experts of the kept groups");
+    TopkArgs a{logits, tokens, n_experts, top_k, 3, normalize, scaling, nullptr, bias, n_group,
+               topk_group, out_expert, out_weight};
+    return topk_common(stream, a);
+}
+
+int grimoire_moe_gate_up(void* stream, const grim_moe_layer* L, const int32_t* d_expert,
+                         const float* x, float* h) {
+    return gemv_common(stream, L, nullptr, nullptr, d_expert, x, h, nullptr, 1);
+}
+
+int grimoire_moe_down(void* stream, const grim_moe_layer* L, const int32_t* d_expert,
+                      const float* d_weight, const float* h, float* y) {
+    return down_common(stream, L, nullptr, d_expert, d_weight, nullptr, h, y, 1);
+}
+
+int grimoire_moe_gate_up_shared(void* stream, const grim_moe_layer* L, const grim_quant_weight* ws,
+                                const uint16_t* gate_w, const int32_t* d_expert, const float* x,
+                                float* h, float* gate_out) {
+    if (!ws) return fail(GRIM_ERR_ARG, "null shared weight");
+    return gemv_common(stream, L, ws, gate_w, d_expert, x, h, gate_out, 1);
+}
+
+int grimoire_moe_down_shared(void* stream, const grim_moe_layer* L, const grim_quant_weight* wd,
+                             const int32_t* d_expert, const float* d_weight, const float* gate_in,
+                             const float* h, float* y) {
+    if (!wd) return fail(GRIM_ERR_ARG, "null shared weight");
+    return down_common(stream, L, wd, d_expert, d_weight, gate_in, h, y, 1);
+}
+
+int grimoire_moe_gate_up_batched(void* stream, const grim_moe_layer* L, const int32_t* d_expert,
+                                 const float* x, float* h, int tokens) {
+    return gemv_common(stream, L, nullptr, nullptr, d_expert, x, h, nullptr, tokens);
+}
+
+int grimoire_moe_down_batched(void* stream, const grim_moe_layer* L, const int32_t* d_expert,
+                              const float* d_weight, const float* h, float* y, int tokens) {
+    return down_common(stream, L, nullptr, d_expert, d_weight, nullptr, h, y, tokens);
+}
+
+int grimoire_moe_shared_rows(void* stream, const grim_moe_layer* L, const grim_quant_weight* ws,
+                             const grim_quant_weight* wd, const uint16_t* gate_w,
+                             const int32_t* rex, const float* rwt, const float* x, float* h,
+                             float* gate_out, float* y, int M) {
+    if (!ws || !wd) return fail(GRIM_ERR_ARG, "null shared weight");
+    int r = gemv_common(stream, L, ws, gate_w, rex, x, h, gate_out, M);
+    if (r) return r;
+    return down_common(stream, L, wd, rex, rwt, gate_w ? gate_out : nullptr, h, y, M);
+}
+
+size_t grimoire_moe_route_workspace_bytes(int tokens, int top_k, int num_experts) {
+    return dispatch_workspace_bytes(tokens, top_k, num_experts);
+}
+
+static int dispatch_common(void* stream, const DispatchArgs& a, size_t ws_bytes) {
+    if (a.T <= 0) return GRIM_OK;
+    if (!a.ids || !a.counts || !a.offsets || !a.inverse) return fail(GRIM_ERR_ARG, "null pointer");
+    if (a.E <= 0 || a.K <= 0 || a.K > 16) return fail(GRIM_ERR_SHAPE, "E/top_k");
+    if (a.xperm && (a.H % 4 || !a.hidden)) return fail(GRIM_ERR_SHAPE, "hidden_size %% 4 / null hidden");
+    if (!a.workspace || ws_bytes < dispatch_workspace_bytes(a.T, a.K, a.E))
+        return fail(GRIM_ERR_WORKSPACE, "dispatch workspace too small (need %zu)",
+                    dispatch_workspace_bytes(a.T, a.K, a.E));
+    return status(dispatch_launch(S(stream), a));
+}
+
+int grimoire_moe_route_grouped(void* stream, const float* hidden, const int32_t* topk_ids,
+                               uint16_t* xperm, uint16_t* xrow, int32_t* counts, int32_t* offsets,
+                               int32_t* inverse, int32_t* tile_e, int32_t* tile_mb, int tmax,
+                               int tokens, int hidden_size, int num_experts, int mc, int top_k,
+                               int32_t* perm_token, void* workspace, size_t workspace_bytes) {
+    if ((tile_e == nullptr) != (tile_mb == nullptr)) return fail(GRIM_ERR_ARG, "tile_e/tile_mb");
+    if (tile_e && mc <= 0) return fail(GRIM_ERR_ARG, "mc must be > 0");
+    DispatchArgs a{};
+    a.ids = topk_ids; a.T = tokens; a.K = top_k; a.E = num_experts; a.H = hidden_size;
+    a.hidden = hidden; a.hidden_bf16 = 0; a.xperm = xperm; a.xrow = xrow;
+    a.counts = counts; a.offsets = offsets; a.inverse = inverse; a.perm_token = perm_token;
+    a.tile_e = tile_e; a.tile_mb = tile_mb; a.tmax = tile_e ? tmax : 0; a.mc = mc;
+    a.workspace = workspace;
+    return dispatch_common(stream, a, workspace_bytes);
+}
+
+int grimoire_moe_remap_bf16(void* stream, const uint16_t* hidden, const int32_t* topk_ids,
+                            uint16_t* remapped, int32_t* rows_per_expert, int32_t* expert_offsets,
+                            int32_t* inverse, int tokens, int hidden_size, int num_experts,
+                            int top_k, void* workspace, size_t workspace_bytes) {
+    DispatchArgs a{};
+    a.ids = topk_ids; a.T = tokens; a.K = top_k; a.E = num_experts; a.H = hidden_size;
+    a.hidden = hidden; a.hidden_bf16 = 1; a.xperm = remapped; a.xrow = nullptr;
+    a.counts = rows_per_expert; a.offsets = expert_offsets; a.inverse = inverse;
+    a.perm_token = nullptr; a.tile_e = nullptr; a.tile_mb = nullptr; a.tmax = 0; a.mc = 0;
+    a.workspace = workspace;
+    return dispatch_common(stream, a, workspace_bytes);
+}
+
+static int combine_common(void* stream, const CombineArgs& a) {
+    if (a.T <= 0) return GRIM_OK;
+    if (!a.src || !a.inverse || !a.rw || !a.dst) return fail(GRIM_ERR_ARG, "null pointer");
+    if (a.K <= 0 || a.K > 16) return fail(GRIM_ERR_SHAPE, "top_k=%d", a.K);
+    if (a.H % 4) return fail(GRIM_ERR_SHAPE, "hidden %% 4");
+    return status(combine_launch(S(stream), a));
+}
+
+int grimoire_moe_unpermute(void* stream, const float* src, const int32_t* inverse,
+                           const float* route_weight, float* dst, int tokens, int top_k,
+                           int hidden) {
+    CombineArgs a{src, 0, inverse, route_weight, nullptr, 0, nullptr, dst, tokens, top_k, hidden};
+    return combine_common(stream, a);
+}
+
+int grimoire_moe_unpermute_bf16(void* stream, const uint16_t* src, const int32_t* inverse,
+                                const float* route_weight, float* dst, int tokens, int top_k,
+                                int hidden) {
+    CombineArgs a{src, 1, inverse, route_weight, nullptr, 0, nullptr, dst, tokens, top_k, hidden};
+    return combine_common(stream, a);
+}
+
+int grimoire_moe_combine(void* stream, const uint16_t* src, const int32_t* inverse,
+                         const float* route_weight, const uint16_t* shared_src, const float* gate,
+                         float* dst, int tokens, int top_k, int hidden) {
+    CombineArgs a{src, 1, inverse, route_weight, shared_src, 1, gate, dst, tokens, top_k, hidden};
+    return combine_common(stream, a);
+}
+
+int grimoire_moe_grouped_gemm(void* stream, const grim_quant_weight* w, int N, int swiglu,
+                              const uint16_t* A, int a_pair, void* out, int out_bf16,
+                              const int32_t* offsets, const int32_t* counts, int num_experts,
+                              int total_rows) {
+    if (!w || !A || !out || !offsets || !counts) return fail(GRIM_ERR_ARG, "null pointer");
+    if (!gemm_format_ok(w->fmt))
+        return fail(GRIM_ERR_FORMAT, "grouped GEMM supports int8, mxfp4 and bf16 weights");
+    int r = check_weight(w, "grouped weight", int64_t(num_experts) * N, w->K);
+    if (r) return r;
+    if (w->K % 64) return fail(GRIM_ERR_SHAPE, "K=%d not a multiple of 64", w->K);
+    if (swiglu && (N % 2 || a_pair)) return fail(GRIM_ERR_SHAPE, "swiglu needs even N, bf16 A");
+    if (total_rows <= 0) return GRIM_OK;
+    // counts/offsets live on the device: build the tile table there
+    const int tmax = num_experts + (total_rows + kGemmBM - 1) / kGemmBM;
+    const size_t need = size_t(2 * tmax + 4) * sizeof(int32_t);
+    int32_t* sc = static_cast<int32_t*>(bridge_scratch(need + size_t(2 * num_experts) * 4));
+    if (!sc) return fail(GRIM_ERR_WORKSPACE, "scratch allocation failed");
+    int32_t* tile_e = sc;
+    int32_t* tile_mb = sc + tmax;
+    int32_t* n_tiles = sc + 2 * tmax;
+    int32_t* cnt2 = n_tiles + 4;
+    int32_t* off2 = cnt2 + num_experts;
+    hipLaunchKernelGGL(tiles_from_counts, dim3(1), dim3(64), 0, S(stream), counts, num_experts,
+                       kGemmBM, cnt2, off2, tile_e, tile_mb, tmax, n_tiles);
+    GemmArgs g{};
+    g.w = view(*w);
+    g.N = N;
+    g.K = w->K;
+    g.I = swiglu ? N / 2 : 0;
+    g.swiglu = swiglu;
+    g.a_pair = a_pair;
+    g.out_bf16 = swiglu ? 1 : out_bf16;
+    g.A = A;
+    g.out = out;
+    g.offsets = offsets;
+    g.counts = counts;
+    g.tile_e = tile_e;
+    g.tile_mb = tile_mb;
+    g.tmax = tmax;
+    g.n_tiles_dev = n_tiles;
+    return status(gemm_launch(S(stream), w->fmt, g));
+}
+
+void grimoire_xe2_grouped_mxfp4_bf16(void* stream, const void* a, const unsigned char* b,
+                                     const unsigned char* scales, void* d, int n, int k,
+                                     const int* rows_per_expert, const int* expert_ids,
+                                     int num_experts, int* atomic_buffer) {
+    (void)expert_ids;
+    (void)atomic_buffer;
+    grim_quant_weight w{GRIM_FMT_MXFP4, num_experts * n, k, k / 32, k / 2, b, scales, nullptr};
+    if (check_weight(&w, "xe2 mxfp4", int64_t(num_experts) * n, k) || k % 64) return;
+    bridge_common(stream, w, n, 0, 0, a, d, rows_per_expert, num_experts);
+}
+
+void grimoire_xe2_grouped_w4a16(void* stream, const void* activations_bf16,
+                                const unsigned char* weights_int4, const void* scales_bf16,
+                                void* outputs_bf16, int n, int k, const int* rows_per_expert,
+                                const int* expert_ids, int num_experts, int group_size,
+                                int* atomic_buffer) {
+    (void)stream; (void)activations_bf16; (void)weights_int4; (void)scales_bf16;
+    (void)outputs_bf16; (void)n; (void)k; (void)rows_per_expert; (void)expert_ids;
+    (void)num_experts; (void)group_size; (void)atomic_buffer;
+    fail(GRIM_ERR_FORMAT, "grimoire_xe2_grouped_w4a16: int4 grouped GEMM not built yet");
+}
+
+void grimoire_xe2_fused_moe_gate_up_mxfp4_silu_bf16(void* stream, const void* activations,
+                                                    const unsigned char* weights,
+                                                    const unsigned char* scales, void* outputs,
+                                                    int n, int k, const int* rows_per_expert,
+                                                    int num_experts, int32_t* atomic_buffer) {
+    (void)atomic_buffer;
+    (void)stream; (void)activations; (void)weights; (void)scales; (void)outputs; (void)n; (void)k;
+    (void)rows_per_expert; (void)num_experts;
+    fail(GRIM_ERR_FORMAT, "fused gate_up bridge: bf16-out SwiGLU epilogue not built yet");
+}
+
+}  // extern "C"

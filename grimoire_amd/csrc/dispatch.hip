@@ -1,0 +1,261 @@
+// dispatch.hip -- expert histogram, scan, stable permutation, and combine.
+//
+// The permutation is deterministic: expert-major, ascending route index,
+// i.e. the order of the reference's host counting sort
+// (src/grimoire.cpp:23162-23170), produced on the device without global
+// atomics:
+//   1. count   each block counts its chunk of routes per expert in LDS and
+//              writes the row bcount[b][E];
+//   2. scan    one block turns bcount into per-(block, expert) bases,
+//              per-expert counts and exclusive offsets, and the m-tile
+//              table (src/prefill.cpp:2770-2782);
+//   3. rank    each block ranks its routes inside their expert by counting
+//              earlier routes of the same expert in the block (stable);
+//   4. permute one block per token writes bf16(x[t]) to its K rows
+//              (src/prefill.cpp:2784-2806).
+#include "common.hpp"
+#include "dispatch.hpp"
+
+namespace grim {
+
+constexpr int kDispThreads = 256;
+constexpr int kRoutesPerBlock = 1024;
+
+__global__ __launch_bounds__(kDispThreads) void disp_count(const int32_t* __restrict__ ids, int R,
+                                                           int E, int32_t* __restrict__ bcount) {
+    extern __shared__ int32_t hist[];
+    for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
+    __syncthreads();
+    const int r0 = blockIdx.x * kRoutesPerBlock;
+    for (int i = threadIdx.x; i < kRoutesPerBlock; i += blockDim.x) {
+        const int r = r0 + i;
+        if (r < R) {
+            const int e = ids[r];
+            if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
+        }
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) bcount[int64_t(blockIdx.x) * E + e] = hist[e];
+}
+
+// One block of 1024 threads; expert e is handled by thread e (and e+1024...).
+__global__ __launch_bounds__(1024) void disp_scan(int32_t* __restrict__ bcount, int nb, int E,
+                                                  int32_t* __restrict__ counts,
+                                                  int32_t* __restrict__ offsets,
+                                                  int32_t* __restrict__ tile_e,
+                                                  int32_t* __restrict__ tile_mb, int tmax, int mc,
+                                                  int32_t* __restrict__ n_tiles_out) {
+    __shared__ int32_t part[1024];
+    __shared__ int32_t tpart[1024];
+    __shared__ int32_t carry[2];
+    if (threadIdx.x == 0) { carry[0] = 0; carry[1] = 0; }
+    __syncthreads();
+    for (int e0 = 0; e0 < E; e0 += 1024) {
+        const int e = e0 + threadIdx.x;
+        int c = 0;
+        if (e < E) {
+            // per-block bases inside the expert (block order = route order)
+            for (int b = 0; b < nb; ++b) {
+                const int v = bcount[int64_t(b) * E + e];
+                bcount[int64_t(b) * E + e] = c;
+                c += v;
+            }
+        }
+        const int nt = (mc > 0 && e < E) ? (c + mc - 1) / mc : 0;
+        part[threadIdx.x] = c;
+        tpart[threadIdx.x] = nt;
+        __syncthreads();
+        // inclusive Hillis-Steele scans of counts and tiles
+        for (int off = 1; off < 1024; off <<= 1) {
+            const int a = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
+            const int b = threadIdx.x >= off ? tpart[threadIdx.x - off] : 0;
+            __syncthreads();
+            part[threadIdx.x] += a;
+            tpart[threadIdx.x] += b;
+            __syncthreads();
+        }
+        const int rbase = carry[0] + part[threadIdx.x] - c;
+        const int tbase = carry[1] + tpart[threadIdx.x] - nt;
+        if (e < E) {
+            counts[e] = c;
+            offsets[e] = rbase;
+            for (int b = 0; b < nb; ++b) bcount[int64_t(b) * E + e] += rbase;
+            if (tile_e)
+                for (int i = 0; i < nt; ++i)
+                    if (tbase + i < tmax) { tile_e[tbase + i] = e; tile_mb[tbase + i] = i; }
+        }
+        __syncthreads();
+        if (threadIdx.x == 1023) { carry[0] += part[1023]; carry[1] += tpart[1023]; }
+        __syncthreads();
+    }
+    if (tile_e)
+        for (int t = carry[1] + threadIdx.x; t < tmax; t += 1024) { tile_e[t] = -1; tile_mb[t] = 0; }
+    if (threadIdx.x == 0 && n_tiles_out) *n_tiles_out = carry[1];
+}
+
+__global__ __launch_bounds__(kDispThreads) void disp_rank(const int32_t* __restrict__ ids, int R,
+                                                          int E, int K,
+                                                          const int32_t* __restrict__ bbase,
+                                                          int32_t* __restrict__ inverse,
+                                                          int32_t* __restrict__ perm_token) {
+    __shared__ int32_t le[kRoutesPerBlock];
+    const int r0 = blockIdx.x * kRoutesPerBlock;
+    const int n = R - r0 < kRoutesPerBlock ? R - r0 : kRoutesPerBlock;
+    for (int i = threadIdx.x; i < kRoutesPerBlock; i += blockDim.x) le[i] = i < n ? ids[r0 + i] : -1;
+    __syncthreads();
+    constexpr int PER = kRoutesPerBlock / kDispThreads;
+    int my_e[PER], rank[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) { my_e[j] = le[threadIdx.x + j * kDispThreads]; rank[j] = 0; }
+    // count earlier routes of the same expert (uniform loop: LDS broadcast)
+    for (int i = 0; i < n; ++i) {
+        const int ei = le[i];
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+            rank[j] += (i < threadIdx.x + j * kDispThreads && ei == my_e[j]) ? 1 : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int i = threadIdx.x + j * kDispThreads;
+        if (i >= n) continue;
+        const int e = my_e[j];
+        const int r = r0 + i;
+        if (e < 0 || e >= E) { inverse[r] = -1; continue; }
+        const int p = bbase[int64_t(blockIdx.x) * E + e] + rank[j];
+        inverse[r] = p;
+        if (perm_token) perm_token[p] = r / K;
+    }
+}
+
+// One block per token: bf16 row written to each of its K permuted rows.
+template <bool SRC_BF16>
+__global__ __launch_bounds__(kDispThreads) void disp_permute(const void* __restrict__ hidden,
+                                                             const int32_t* __restrict__ inverse,
+                                                             uint16_t* __restrict__ xperm,
+                                                             uint16_t* __restrict__ xrow, int H,
+                                                             int K) {
+    const int t = blockIdx.x;
+    int dst[16];
+    for (int s = 0; s < K; ++s) dst[s] = inverse[int64_t(t) * K + s];
+    for (int d = threadIdx.x * 4; d < H; d += blockDim.x * 4) {
+        uint32_t lo, hi;
+        if constexpr (SRC_BF16) {
+            const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(hidden) +
+                                                            int64_t(t) * H + d);
+            lo = v.x; hi = v.y;
+        } else {
+            const float4 f = *reinterpret_cast<const float4*>(static_cast<const float*>(hidden) +
+                                                              int64_t(t) * H + d);
+            lo = uint32_t(f32_to_bf16(f.x)) | (uint32_t(f32_to_bf16(f.y)) << 16);
+            hi = uint32_t(f32_to_bf16(f.z)) | (uint32_t(f32_to_bf16(f.w)) << 16);
+        }
+        const uint2 v = make_uint2(lo, hi);
+        for (int s = 0; s < K; ++s)
+            if (dst[s] >= 0) *reinterpret_cast<uint2*>(xperm + int64_t(dst[s]) * H + d) = v;
+        if (xrow) *reinterpret_cast<uint2*>(xrow + int64_t(t) * H + d) = v;
+    }
+}
+
+size_t dispatch_workspace_bytes(int T, int K, int E) {
+    const int64_t R = int64_t(T) * K;
+    const int64_t nb = (R + kRoutesPerBlock - 1) / kRoutesPerBlock;
+    return size_t((nb > 0 ? nb : 1) * E + 16) * sizeof(int32_t);
+}
+
+int32_t* dispatch_live_tiles(void* workspace, int T, int K, int E) {
+    const int64_t R = int64_t(T) * K;
+    const int64_t nb = (R + kRoutesPerBlock - 1) / kRoutesPerBlock;
+    return static_cast<int32_t*>(workspace) + (nb > 0 ? nb : 1) * E;
+}
+
+hipError_t dispatch_launch(hipStream_t st, const DispatchArgs& a) {
+    const int R = a.T * a.K;
+    const int nb = (R + kRoutesPerBlock - 1) / kRoutesPerBlock;
+    int32_t* bcount = static_cast<int32_t*>(a.workspace);
+    int32_t* ntiles = bcount + int64_t(nb > 0 ? nb : 1) * a.E;
+    if (nb > 0)
+        hipLaunchKernelGGL(disp_count, dim3(nb), dim3(kDispThreads), size_t(a.E) * 4, st, a.ids, R,
+                           a.E, bcount);
+    hipLaunchKernelGGL(disp_scan, dim3(1), dim3(1024), 0, st, bcount, nb, a.E, a.counts, a.offsets,
+                       a.tile_e, a.tile_mb, a.tmax, a.mc, ntiles);
+    if (nb > 0)
+        hipLaunchKernelGGL(disp_rank, dim3(nb), dim3(kDispThreads), 0, st, a.ids, R, a.E, a.K,
+                           bcount, a.inverse, a.perm_token);
+    if (a.xperm && a.T > 0) {
+        if (a.hidden_bf16)
+            hipLaunchKernelGGL(disp_permute<true>, dim3(a.T), dim3(kDispThreads), 0, st, a.hidden,
+                               a.inverse, a.xperm, a.xrow, a.H, a.K);
+        else
+            hipLaunchKernelGGL(disp_permute<false>, dim3(a.T), dim3(kDispThreads), 0, st, a.hidden,
+                               a.inverse, a.xperm, a.xrow, a.H, a.K);
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- combine
+
+// dst[t][d] = fma chain over slots of w * src[inverse][d] (+ gate * shared).
+// One block per token, 4 columns per thread.
+template <bool SRC_BF16>
+__global__ __launch_bounds__(kDispThreads) void combine_kernel(
+    const void* __restrict__ src, const int32_t* __restrict__ inverse,
+    const float* __restrict__ rw, const void* __restrict__ shared_src, int shared_bf16,
+    const float* __restrict__ gate, float* __restrict__ dst, int H, int K) {
+    const int t = blockIdx.x;
+    int p[16];
+    float w[16];
+    for (int s = 0; s < K; ++s) { p[s] = inverse[int64_t(t) * K + s]; w[s] = rw[int64_t(t) * K + s]; }
+    const float g = gate ? gate[t] : 1.0f;
+    for (int d = threadIdx.x * 4; d < H; d += blockDim.x * 4) {
+        float v0 = 0.0f, v1 = 0.0f, v2 = 0.0f, v3 = 0.0f;
+        for (int s = 0; s < K; ++s) {
+            if (p[s] < 0) continue;
+            float a0, a1, a2, a3;
+            if constexpr (SRC_BF16) {
+                const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(src) +
+                                                                int64_t(p[s]) * H + d);
+                a0 = bits_f(u.x << 16); a1 = bits_f(u.x & 0xFFFF0000u);
+                a2 = bits_f(u.y << 16); a3 = bits_f(u.y & 0xFFFF0000u);
+            } else {
+                const float4 f = *reinterpret_cast<const float4*>(static_cast<const float*>(src) +
+                                                                  int64_t(p[s]) * H + d);
+                a0 = f.x; a1 = f.y; a2 = f.z; a3 = f.w;
+            }
+            v0 = __builtin_fmaf(w[s], a0, v0);
+            v1 = __builtin_fmaf(w[s], a1, v1);
+            v2 = __builtin_fmaf(w[s], a2, v2);
+            v3 = __builtin_fmaf(w[s], a3, v3);
+        }
+        if (shared_src) {
+            float a0, a1, a2, a3;
+            if (shared_bf16) {
+                const uint2 u = *reinterpret_cast<const uint2*>(
+                    static_cast<const uint16_t*>(shared_src) + int64_t(t) * H + d);
+                a0 = bits_f(u.x << 16); a1 = bits_f(u.x & 0xFFFF0000u);
+                a2 = bits_f(u.y << 16); a3 = bits_f(u.y & 0xFFFF0000u);
+            } else {
+                const float4 f = *reinterpret_cast<const float4*>(
+                    static_cast<const float*>(shared_src) + int64_t(t) * H + d);
+                a0 = f.x; a1 = f.y; a2 = f.z; a3 = f.w;
+            }
+            v0 = __builtin_fmaf(g, a0, v0);
+            v1 = __builtin_fmaf(g, a1, v1);
+            v2 = __builtin_fmaf(g, a2, v2);
+            v3 = __builtin_fmaf(g, a3, v3);
+        }
+        *reinterpret_cast<float4*>(dst + int64_t(t) * H + d) = make_float4(v0, v1, v2, v3);
+    }
+}
+
+hipError_t combine_launch(hipStream_t st, const CombineArgs& a) {
+    if (a.T <= 0) return hipSuccess;
+    if (a.src_bf16)
+        hipLaunchKernelGGL(combine_kernel<true>, dim3(a.T), dim3(kDispThreads), 0, st, a.src,
+                           a.inverse, a.rw, a.shared_src, a.shared_bf16, a.gate, a.dst, a.H, a.K);
+    else
+        hipLaunchKernelGGL(combine_kernel<false>, dim3(a.T), dim3(kDispThreads), 0, st, a.src,
+                           a.inverse, a.rw, a.shared_src, a.shared_bf16, a.gate, a.dst, a.H, a.K);
+    return hipGetLastError();
+}
+
+}  // namespace grim

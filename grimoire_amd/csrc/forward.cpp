@@ -1,0 +1,252 @@
+// forward.cpp -- grimoire_moe_forward: the whole MoE block of one layer.
+//
+// The engine's per-layer sequence (src/grimoire.cpp:15362-15500 decode,
+// :22743-23300 prefill) behind one call, all on one stream, no host sync:
+//
+//   GEMV regime (decode, T*K small):
+//     router GEMV -> top-k -> gate_up(+shared, +gate) -> down(+shared)
+//   GEMM regime (prefill / verify):
+//     router GEMM -> top-k -> dispatch (counts, scan, stable permutation,
+//     bf16 rows) -> [shared gate] -> grouped gate_up+SwiGLU (MFMA, shared
+//     expert as extra tiles) -> grouped down (MFMA, fp32 rows) -> combine
+//     (slot-order fma chain + gate * shared)
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+
+#include "../../include/grimoire_moe.h"
+#include "common.hpp"
+#include "dispatch.hpp"
+#include "gemm.hpp"
+#include "gemv.hpp"
+#include "router.hpp"
+
+using namespace grim;
+
+extern "C" int grimoire_moe_gate_up_shared(void*, const grim_moe_layer*, const grim_quant_weight*,
+                                           const uint16_t*, const int32_t*, const float*, float*,
+                                           float*);
+
+namespace {
+
+struct Carve {
+    char* base;
+    size_t off = 0;
+    template <class T>
+    T* take(size_t n) {
+        off = (off + 255) & ~size_t(255);
+        T* p = reinterpret_cast<T*>(base ? base + off : nullptr);
+        off += n * sizeof(T);
+        return p;
+    }
+};
+
+bool use_gemv(const grim_moe_layer* L, int T, int regime) {
+    if (regime == 1) return true;
+    if (regime == 2) return false;
+    return int64_t(T) * L->cfg.top_k <= 64;
+}
+
+struct Plan {
+    float* logits;
+    int32_t* rex;
+    float* rwt;
+    float* gate;
+    // GEMV
+    float* h;
+    // GEMM
+    void* disp_ws;
+    int32_t *counts, *offsets, *inverse, *tile_e, *tile_mb;
+    int tmax;
+    uint16_t *xperm, *xrow, *hp, *hp_sh;
+    float *yperm, *ysh;
+};
+
+size_t carve(const grim_moe_layer* L, int T, bool gemv, char* base, Plan& p) {
+    const auto& c = L->cfg;
+    const int E = c.num_experts, K = c.top_k, H = c.hidden, I = c.inter;
+    const int64_t R = int64_t(T) * K;
+    const bool sh = L->has_shared;
+    Carve cv{base};
+    p.logits = cv.take<float>(size_t(T) * E);
+    p.rex = cv.take<int32_t>(R);
+    p.rwt = cv.take<float>(R);
+    p.gate = cv.take<float>(T);
+    if (gemv) {
+        p.h = cv.take<float>(size_t(T) * (K + (sh ? 1 : 0)) * I);
+    } else {
+        const size_t dws = dispatch_workspace_bytes(T, K, E);
+        p.disp_ws = cv.take<char>(dws);
+        p.counts = cv.take<int32_t>(E);
+        p.offsets = cv.take<int32_t>(E);
+        p.inverse = cv.take<int32_t>(R);
+        p.tmax = int(E + (R + kGemmBM - 1) / kGemmBM);
+        p.tile_e = cv.take<int32_t>(p.tmax + 4);
+        p.tile_mb = cv.take<int32_t>(p.tmax);
+        p.xperm = cv.take<uint16_t>(R * H);
+        p.xrow = sh ? cv.take<uint16_t>(size_t(T) * H) : nullptr;
+        p.hp = cv.take<uint16_t>(R * 2 * I);
+        p.hp_sh = sh ? cv.take<uint16_t>(size_t(T) * 2 * I) : nullptr;
+        p.yperm = cv.take<float>(R * H);
+        p.ysh = sh ? cv.take<float>(size_t(T) * H) : nullptr;
+    }
+    return cv.off + 256;
+}
+
+}  // namespace
+
+extern "C" size_t grimoire_moe_forward_workspace_bytes(const grim_moe_layer* L, int tokens) {
+    if (!L || tokens <= 0) return 0;
+    Plan p{};
+    const size_t a = carve(L, tokens, true, nullptr, p);
+    const size_t b = carve(L, tokens, false, nullptr, p);
+    return a > b ? a : b;
+}
+
+extern "C" int grimoire_moe_router_logits(void*, const float*, const float*, float*, int, int, int);
+extern "C" int grimoire_moe_router_topk_batched(void*, const float*, int, int, int, int32_t*,
+                                                float*, int);
+extern "C" int grimoire_moe_router_topk_sigmoid(void*, const float*, const uint16_t*, int, int,
+                                                int, int32_t*, float*, int, float);
+extern "C" int grimoire_moe_router_topk_group(void*, const float*, const float*, int, int, int,
+                                              int, int, int32_t*, float*, int, float);
+extern "C" int grimoire_moe_shared_rows(void*, const grim_moe_layer*, const grim_quant_weight*,
+                                        const grim_quant_weight*, const uint16_t*, const int32_t*,
+                                        const float*, const float*, float*, float*, float*, int);
+extern "C" int grimoire_moe_gate_up_batched(void*, const grim_moe_layer*, const int32_t*,
+                                            const float*, float*, int);
+extern "C" int grimoire_moe_down_batched(void*, const grim_moe_layer*, const int32_t*,
+                                         const float*, const float*, float*, int);
+extern "C" int grimoire_moe_route_grouped(void*, const float*, const int32_t*, uint16_t*,
+                                          uint16_t*, int32_t*, int32_t*, int32_t*, int32_t*,
+                                          int32_t*, int, int, int, int, int, int, int32_t*, void*,
+                                          size_t);
+extern "C" const char* grimoire_moe_last_error(void);
+
+static int ferr(int code, const char* msg);
+
+extern "C" int grimoire_moe_forward(void* stream, const grim_moe_layer* L,
+                                    const grim_route_params* rp, const uint16_t* shared_gate_w,
+                                    const float* x, float* y, int tokens, int32_t* out_expert,
+                                    float* out_weight, int regime, void* workspace,
+                                    size_t workspace_bytes) {
+    if (!L || !x || !y) return ferr(GRIM_ERR_ARG, "null layer/x/y");
+    if (tokens <= 0) return GRIM_OK;
+    if (!L->router) return ferr(GRIM_ERR_ARG, "layer has no router");
+    const auto& c = L->cfg;
+    if (L->has_shared && c.shared_inter != c.inter)
+        return ferr(GRIM_ERR_SHAPE, "shared_inter must equal inter");
+    const bool gemv = use_gemv(L, tokens, regime);
+    Plan p{};
+    const size_t need = carve(L, tokens, gemv, nullptr, p);
+    if (!workspace || workspace_bytes < need) return ferr(GRIM_ERR_WORKSPACE, "workspace too small");
+    carve(L, tokens, gemv, static_cast<char*>(workspace), p);
+    if (out_expert) p.rex = out_expert;
+    if (out_weight) p.rwt = out_weight;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+
+    const int E = c.num_experts, K = c.top_k, H = c.hidden, I = c.inter;
+    const int mode = rp ? rp->mode : GRIM_ROUTE_SOFTMAX;
+    if (H % 4) return ferr(GRIM_ERR_SHAPE, "hidden must be a multiple of 4");
+    {
+        const float* rb = (mode == GRIM_ROUTE_SOFTMAX && rp) ? static_cast<const float*>(rp->bias) : nullptr;
+        hipError_t e = router_logits_launch(st, L->router, x, rb, p.logits, tokens, E, H);
+        if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    }
+    int r = GRIM_OK;
+    if (mode == GRIM_ROUTE_SOFTMAX) {
+        TopkArgs a{p.logits, tokens, E, K, 0, c.norm_topk, 1.0f, nullptr, nullptr, 0, 0, p.rex, p.rwt};
+        hipError_t e = topk_launch(st, a);
+        if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    } else if (mode == GRIM_ROUTE_SIGMOID) {
+        r = grimoire_moe_router_topk_sigmoid(stream, p.logits, static_cast<const uint16_t*>(rp->bias),
+                                             tokens, E, K, p.rex, p.rwt, c.norm_topk, rp->scaling);
+    } else if (mode == GRIM_ROUTE_GROUP) {
+        r = grimoire_moe_router_topk_group(stream, p.logits, static_cast<const float*>(rp->bias),
+                                           tokens, E, K, rp->n_group, rp->topk_group, p.rex, p.rwt,
+                                           c.norm_topk, rp->scaling);
+    } else {
+        return ferr(GRIM_ERR_ARG, "unknown route mode");
+    }
+    if (r) return r;
+
+    if (gemv) {
+        if (L->has_shared)
+            return grimoire_moe_shared_rows(stream, L, &L->shared_gate_up, &L->shared_down,
+                                            shared_gate_w, p.rex, p.rwt, x, p.h,
+                                            shared_gate_w ? p.gate : nullptr, y, tokens);
+        r = grimoire_moe_gate_up_batched(stream, L, p.rex, x, p.h, tokens);
+        if (r) return r;
+        return grimoire_moe_down_batched(stream, L, p.rex, p.rwt, p.h, y, tokens);
+    }
+
+    // ---- GEMM regime
+    const int fu = L->gate_up.fmt, fd = L->down.fmt;
+    if (!gemm_format_ok(fu) || !gemm_format_ok(fd))
+        return ferr(GRIM_ERR_FORMAT, "grouped GEMM supports int8, mxfp4 and bf16 weights");
+    if (H % 64 || I % 64) return ferr(GRIM_ERR_SHAPE, "hidden and inter must be multiples of 64");
+    r = grimoire_moe_route_grouped(stream, x, p.rex, p.xperm, p.xrow, p.counts, p.offsets,
+                                   p.inverse, p.tile_e, p.tile_mb, p.tmax, tokens, H, E, kGemmBM, K,
+                                   nullptr, p.disp_ws, dispatch_workspace_bytes(tokens, K, E));
+    if (r) return r;
+    const bool sh = L->has_shared;
+    if (sh && shared_gate_w) {
+        hipError_t e = rowdot_sigmoid_launch(st, x, shared_gate_w, p.gate, tokens, H);
+        if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    }
+    int32_t* live = dispatch_live_tiles(p.disp_ws, tokens, K, E);
+
+    GemmArgs g{};
+    g.w = make_view(L->gate_up);
+    if (sh)
+        g.w_sh = make_view(L->shared_gate_up);
+    g.N = 2 * I;
+    g.K = H;
+    g.I = I;
+    g.swiglu = 1;
+    g.A = p.xperm;
+    g.A_sh = p.xrow;
+    g.out = p.hp;
+    g.out_sh = p.hp_sh;
+    g.offsets = p.offsets;
+    g.counts = p.counts;
+    g.tile_e = p.tile_e;
+    g.tile_mb = p.tile_mb;
+    g.tmax = p.tmax;
+    g.n_tiles_dev = live;
+    g.T_sh = sh ? tokens : 0;
+    if (sh && L->shared_gate_up.fmt != fu) return ferr(GRIM_ERR_FORMAT, "shared format mismatch");
+    hipError_t e = gemm_launch(st, fu, g);
+    if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+
+    GemmArgs d = g;
+    d.w = make_view(L->down);
+    if (sh)
+        d.w_sh = make_view(L->shared_down);
+    d.N = H;
+    d.K = I;
+    d.I = 0;
+    d.swiglu = 0;
+    d.a_pair = 1;
+    d.out_bf16 = 0;
+    d.A = p.hp;
+    d.A_sh = p.hp_sh;
+    d.out = p.yperm;
+    d.out_sh = p.ysh;
+    if (sh && L->shared_down.fmt != fd) return ferr(GRIM_ERR_FORMAT, "shared format mismatch");
+    e = gemm_launch(st, fd, d);
+    if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+
+    CombineArgs cb{p.yperm, 0, p.inverse, p.rwt, p.ysh, 0, (sh && shared_gate_w) ? p.gate : nullptr,
+                   y, tokens, K, H};
+    e = combine_launch(st, cb);
+    if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    return GRIM_OK;
+}
+
+// forward.cpp shares api.cpp's thread-local message through this setter.
+extern "C" __attribute__((visibility("hidden"))) void grimoire_moe_set_error_(const char* msg);
+static int ferr(int code, const char* msg) {
+    grimoire_moe_set_error_(msg);
+    return code;
+}

@@ -1,0 +1,174 @@
+"""Python mirror of the reference's MoE launchers, on torch device tensors.
+
+Same names and argument meaning as the C++ launchers of the reference
+(include/b70/moe.hpp:133-173, src/kernels.hpp:500-590, src/prefill.cpp,
+src/ops.cpp), with a torch stream in place of the SYCL queue.  Every
+function calls libgrimoire_moe.so and raises GrimoireError when the library
+rejects the arguments; nothing here computes on the CPU.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _abi
+from ._abi import check, lib
+from .weights import MoeLayer, Weight
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream=None):
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def _dev(t: torch.Tensor):
+    if not t.is_cuda:
+        raise _abi.GrimoireError("tensor is not on a GPU: the MoE kernels run on the device only")
+
+
+# ------------------------------------------------------------------ router
+
+def router_logits(router: torch.Tensor, x: torch.Tensor, logits: torch.Tensor, stream=None):
+    """gemv_any(d.router, s.h2, s.rlogits) (src/grimoire.cpp:15364)."""
+    _dev(x)
+    T, H = x.shape
+    E = router.shape[0]
+    check(lib().grimoire_moe_router_logits(_stream(stream), _p(router), _p(x), _p(logits), T, E, H),
+          "router_logits")
+
+
+def launch_router_topk(logits, n_experts, top_k, out_expert, out_weight, normalize=True,
+                       stream=None):
+    """launch_router_topk (src/ops.cpp:1205)."""
+    _dev(logits)
+    check(lib().grimoire_moe_router_topk(_stream(stream), _p(logits), n_experts, top_k,
+                                         _p(out_expert), _p(out_weight), int(normalize)),
+          "router_topk")
+
+
+def launch_router_topk_batched(logits, tokens, n_experts, top_k, out_expert, out_weight,
+                               normalize=True, stream=None):
+    """launch_router_topk_batched (src/ops.cpp:1347)."""
+    _dev(logits)
+    check(lib().grimoire_moe_router_topk_batched(_stream(stream), _p(logits), tokens, n_experts,
+                                                 top_k, _p(out_expert), _p(out_weight),
+                                                 int(normalize)), "router_topk_batched")
+
+
+def launch_router_topk_k2(logits, bias_bf16, tokens, n_experts, top_k, out_expert, out_weight,
+                          normalize=True, scaling=1.0, stream=None):
+    """launch_router_topk_k2 (src/ops.cpp:2059): sigmoid + selection-only bias."""
+    _dev(logits)
+    check(lib().grimoire_moe_router_topk_sigmoid(_stream(stream), _p(logits), _p(bias_bf16),
+                                                 tokens, n_experts, top_k, _p(out_expert),
+                                                 _p(out_weight), int(normalize), float(scaling)),
+          "router_topk_sigmoid")
+
+
+def launch_router_topk_group(logits, bias, tokens, n_experts, top_k, n_group, topk_group,
+                             out_expert, out_weight, normalize=True, scaling=1.0, stream=None):
+    """Group-limited sigmoid top-k (no reference counterpart)."""
+    _dev(logits)
+    check(lib().grimoire_moe_router_topk_group(_stream(stream), _p(logits), _p(bias), tokens,
+                                               n_experts, top_k, n_group, topk_group,
+                                               _p(out_expert), _p(out_weight), int(normalize),
+                                               float(scaling)), "router_topk_group")
+
+
+# ----------------------------------------------------- decode expert products
+
+def launch_moe_gate_up_batched(L: MoeLayer, d_expert, x, h, tokens, stream=None):
+    """launch_moe_gate_up(_batched) (src/moe_kernels.cpp:1225, :1372)."""
+    _dev(x)
+    s = L.struct()
+    check(lib().grimoire_moe_gate_up_batched(_stream(stream), s, _p(d_expert), _p(x), _p(h),
+                                             tokens), "gate_up")
+
+
+def launch_moe_down_batched(L: MoeLayer, d_expert, d_weight, h, y, tokens, stream=None):
+    """launch_moe_down(_batched) (src/moe_kernels.cpp:1350, :1394)."""
+    _dev(h)
+    s = L.struct()
+    check(lib().grimoire_moe_down_batched(_stream(stream), s, _p(d_expert), _p(d_weight), _p(h),
+                                          _p(y), tokens), "down")
+
+
+def launch_moe_shared_rows(L: MoeLayer, gate_w, rex, rwt, x, h, gate_out, y, M, stream=None):
+    """launch_moe_shared_rows (src/moe_kernels.cpp:1316)."""
+    _dev(x)
+    s = L.struct()
+    ws = L.shared_gate_up.struct()
+    wd = L.shared_down.struct()
+    check(lib().grimoire_moe_shared_rows(_stream(stream), s, ws, wd, _p(gate_w), _p(rex), _p(rwt),
+                                         _p(x), _p(h), _p(gate_out), _p(y), M), "shared_rows")
+
+
+# ---------------------------------------------------------- dispatch/combine
+
+def route_workspace_bytes(tokens, top_k, num_experts) -> int:
+    return int(lib().grimoire_moe_route_workspace_bytes(tokens, top_k, num_experts))
+
+
+def launch_moe_route_grouped(hidden, topk_ids, xperm, xrow, counts, offsets, inverse, tile_e,
+                             tile_mb, tmax, tokens, hidden_size, num_experts, mc, top_k,
+                             perm_token=None, workspace=None, stream=None):
+    """launch_moe_route_grouped (src/prefill.cpp:2726), deterministic order."""
+    _dev(topk_ids)
+    wsb = route_workspace_bytes(tokens, top_k, num_experts)
+    if workspace is None:
+        workspace = torch.empty(wsb, dtype=torch.uint8, device=topk_ids.device)
+    check(lib().grimoire_moe_route_grouped(_stream(stream), _p(hidden), _p(topk_ids), _p(xperm),
+                                           _p(xrow), _p(counts), _p(offsets), _p(inverse),
+                                           _p(tile_e), _p(tile_mb), tmax, tokens, hidden_size,
+                                           num_experts, mc, top_k, _p(perm_token),
+                                           _p(workspace), workspace.numel()), "route_grouped")
+
+
+def launch_moe_unpermute(src, inverse, route_weight, dst, tokens, top_k, hidden, stream=None):
+    """launch_moe_unpermute(_bf16) (src/prefill.cpp:2654, :2690)."""
+    _dev(src)
+    fn = (lib().grimoire_moe_unpermute_bf16 if src.dtype in (torch.int16, torch.bfloat16)
+          else lib().grimoire_moe_unpermute)
+    check(fn(_stream(stream), _p(src), _p(inverse), _p(route_weight), _p(dst), tokens, top_k,
+             hidden), "unpermute")
+
+
+def grouped_gemm(w: Weight, N, swiglu, A, out, offsets, counts, num_experts, total_rows,
+                 a_pair=False, out_bf16=False, stream=None):
+    """launch_moe_mxfp4_grouped (src/gemm_fast.cpp:2343) for int8/mxfp4/bf16."""
+    _dev(A)
+    check(lib().grimoire_moe_grouped_gemm(_stream(stream), w.struct(), N, int(swiglu), _p(A),
+                                          int(a_pair), _p(out), int(out_bf16), _p(offsets),
+                                          _p(counts), num_experts, total_rows), "grouped_gemm")
+
+
+# ------------------------------------------------------------------- layer
+
+class MoeForward:
+    """One layer's whole MoE block with a preallocated workspace."""
+
+    def __init__(self, L: MoeLayer, max_tokens: int, route: _abi.RouteParams,
+                 regime: int = 0):
+        self.L = L
+        self.struct = L.struct()
+        self.route = route
+        self.regime = regime
+        nbytes = int(lib().grimoire_moe_forward_workspace_bytes(self.struct, max_tokens))
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=L.router.device)
+        self.max_tokens = max_tokens
+
+    def __call__(self, x, y, out_expert=None, out_weight=None, stream=None):
+        _dev(x)
+        T = x.shape[0]
+        if T > self.max_tokens:
+            raise _abi.GrimoireError("more tokens than the workspace was sized for")
+        check(lib().grimoire_moe_forward(_stream(stream), self.struct, self.route,
+                                         _p(self.L.shared_gate_w), _p(x), _p(y), T,
+                                         _p(out_expert), _p(out_weight), self.regime,
+                                         _p(self.workspace), self.workspace.numel()),
+              "moe_forward")

@@ -1,0 +1,353 @@
+/*
+ * grimoire_moe.h -- C ABI of the MI355X (gfx950) mixture-of-experts layer.
+ *
+ * Drop-in for the MoE launchers and bridges of doopeworld/GRIMOIRE.  Every
+ * entry point below names the reference interface it replaces (file:line in
+ * the reference tree).  Differences that apply to all of them:
+ *
+ *   - `sycl::queue&` / `sycl::queue*` becomes `void* stream` (a hipStream_t;
+ *     NULL = the default stream).  Work is ordered by the stream.
+ *   - the returned `sycl::event` becomes an int status: 0 on success, a
+ *     positive hipError_t when a launch failed, GRIM_ERR_* (negative) when
+ *     the arguments were rejected before anything was launched.  The
+ *     reference returns an empty event for an unknown format
+ *     (src/moe_kernels.cpp:1243) and throws std::runtime_error for an
+ *     unsupported grouped shape (src/gemm_fast.cpp:2312); both map to a
+ *     negative status here, with the reason in grimoire_moe_last_error().
+ *   - `const std::vector<sycl::event>& deps` disappears: stream order.
+ *   - No entry point allocates device memory except where stated; scratch
+ *     (h, xperm, tables) is caller-owned exactly as in the reference
+ *     (include/b70/weights.hpp:22-25).
+ *
+ * All pointers are device pointers unless stated otherwise.  Layouts are the
+ * reference's: expert-major packed experts, gate_up [E*2I][H] (gate rows
+ * [e*2I, e*2I+I), up rows [e*2I+I, (e+1)*2I)), down [E*H][I]
+ * (include/b70/moe.hpp:47-56, :100-102).
+ */
+#ifndef GRIMOIRE_MOE_H
+#define GRIMOIRE_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#pragma GCC visibility push(default)
+#endif
+
+/* ------------------------------------------------------------------------
+ * Weight formats.  Codes 0..6 keep the numbering of the reference's
+ * `enum class Fmt` (include/b70/formats.hpp:237-239).  GRIM_FMT_INT4_F16 is
+ * new: GPTQ int4 with the checkpoint's IEEE fp16 group scales kept exactly
+ * (the reference rounds them to bf16 at repack, src/gptq.cpp:65-66).
+ *
+ *   BF16       payload [N][2K]                     scales unused
+ *   INT8       payload [N][K] int8                 scales float [N]
+ *   INT4       payload [N][K/2] (low nibble = even k)
+ *              scales bf16 [N][K/G], zeros u8 [N][K/G]; value (q - z) * s,
+ *              or signed s4 * s when z == 0xff (formats.hpp:483-491);
+ *              zeros == NULL means z = 0.  G = 128 (or 32/64/256, derived
+ *              from row_scales as weights.hpp:80-84 does).
+ *   INT4_F16   as INT4 with fp16 scales; zeros == NULL means the symmetric
+ *              GPTQ zero point 8 (AutoGPTQ's stored 7, plus its +1).
+ *   MXFP4      payload [N][K/2] e2m1 (low nibble = even k),
+ *              scales e8m0 u8 [N][K/32] (formats.hpp:105-126).
+ * ---------------------------------------------------------------------- */
+enum grim_fmt {
+    GRIM_FMT_BF16 = 0,
+    GRIM_FMT_INT8 = 3,
+    GRIM_FMT_INT4 = 4,
+    GRIM_FMT_MXFP4 = 6,
+    GRIM_FMT_INT4_F16 = 64
+};
+
+/* Error codes (negative; positive values are hipError_t). */
+enum grim_status {
+    GRIM_OK = 0,
+    GRIM_ERR_FORMAT = -1,      /* weight format not supported here        */
+    GRIM_ERR_SHAPE = -2,       /* shape outside what the kernels support  */
+    GRIM_ERR_ARG = -3,         /* null pointer or inconsistent argument   */
+    GRIM_ERR_WORKSPACE = -4    /* workspace too small                     */
+};
+
+/* Flat weight view, no ownership: mirrors b70::QuantWeight
+ * (include/b70/weights.hpp:46-126) field for field. */
+typedef struct grim_quant_weight {
+    int32_t fmt;               /* enum grim_fmt                            */
+    int32_t N;                 /* output features                          */
+    int32_t K;                 /* input features                           */
+    int32_t row_scales;        /* scales per row                           */
+    int64_t row_bytes;         /* payload bytes per row                    */
+    const uint8_t* payload;
+    const void* scales;
+    const uint8_t* zeros;
+} grim_quant_weight;
+
+/* b70::MoeConfig (include/b70/moe.hpp:70-77). */
+typedef struct grim_moe_config {
+    int32_t hidden;            /* H */
+    int32_t inter;             /* I */
+    int32_t num_experts;       /* E */
+    int32_t top_k;             /* K <= 16 */
+    int32_t shared_inter;      /* SI, 0 if none */
+    int32_t norm_topk;         /* renormalise the picked weights */
+} grim_moe_config;
+
+/* b70::MoeLayer (include/b70/moe.hpp:85-117). */
+typedef struct grim_moe_layer {
+    grim_moe_config cfg;
+    grim_quant_weight gate_up;          /* [E*2I][H] */
+    grim_quant_weight down;             /* [E*H][I]  */
+    int32_t has_shared;
+    int32_t _pad;
+    grim_quant_weight shared_gate_up;   /* [2*SI][H] */
+    grim_quant_weight shared_down;      /* [H][SI]   */
+    const float* router;                /* fp32 [E][H] */
+} grim_moe_layer;
+
+/* Text of the last argument rejection on this thread ("" if none). */
+const char* grimoire_moe_last_error(void);
+/* Library version string. */
+const char* grimoire_moe_version(void);
+
+/* ------------------------------------------------------------------------
+ * Router
+ * ---------------------------------------------------------------------- */
+
+/* logits[t][e] = sum_k router[e][k] * x[t][k], fp32.  Replaces the router
+ * GEMV gemv_any(d.router, s.h2, s.rlogits) (src/grimoire.cpp:15364) and the
+ * prefill router GEMM (src/grimoire.cpp:22774). */
+int grimoire_moe_router_logits(void* stream, const float* router, const float* x,
+                               float* logits, int tokens, int n_experts, int hidden);
+
+/* Softmax top-k on raw logits for one token: picks = max logit, lowest index
+ * among equals; weights = softmax over the picks in pick order, divided by
+ * their sum when `normalize`, else the unnormalised exp(l - max).
+ * Replaces launch_router_topk (src/ops.cpp:1205-1344). */
+int grimoire_moe_router_topk(void* stream, const float* logits, int n_experts, int top_k,
+                             int32_t* out_expert, float* out_weight, int normalize);
+
+/* The same for `tokens` rows, [T][E] -> [T][K].  As the reference's batched
+ * kernel (src/ops.cpp:1347-1422), normalize == 0 returns the raw logits of
+ * the picks. */
+int grimoire_moe_router_topk_batched(void* stream, const float* logits, int tokens,
+                                     int n_experts, int top_k, int32_t* out_expert,
+                                     float* out_weight, int normalize);
+
+/* Sigmoid scoring with a selection-only bf16 bias (may be NULL): rank on
+ * sigmoid(l) + bias[e], weight = unbiased sigmoid(l), divided by the sum of
+ * the picks when `normalize`, then multiplied by `scaling`.
+ * Replaces launch_router_topk_k2 (src/ops.cpp:2059-2170). */
+int grimoire_moe_router_topk_sigmoid(void* stream, const float* logits,
+                                     const uint16_t* bias_bf16, int tokens, int n_experts,
+                                     int top_k, int32_t* out_expert, float* out_weight,
+                                     int normalize, float scaling);
+
+/* Group-limited sigmoid top-k (DeepSeek-V3 routing; no counterpart in the
+ * reference).  bias is fp32 [E] (may be NULL).  s = sigmoid(l), s' = s + b;
+ * group score = sum of the two largest s' in each of n_group contiguous
+ * groups; keep the topk_group best groups (lower group index wins ties);
+ * pick top_k over s' of the kept experts (lower index wins ties); weight =
+ * s, divided by the sum when `normalize`, times `scaling`. */
+int grimoire_moe_router_topk_group(void* stream, const float* logits, const float* bias,
+                                   int tokens, int n_experts, int top_k, int n_group,
+                                   int topk_group, int32_t* out_expert, float* out_weight,
+                                   int normalize, float scaling);
+
+/* ------------------------------------------------------------------------
+ * Decode / batched-decode expert products (slot form).  h holds
+ * [M][KS][I] fp32, KS = top_k (+1 with the shared expert, whose
+ * intermediate must equal I).  d_expert/d_weight are [M][top_k]; a route
+ * with expert < 0 or weight == 0 is skipped by down.
+ * ---------------------------------------------------------------------- */
+
+/* h[t][s][i] = silu(gate_e[i] . x_t) * (up_e[i] . x_t), e = d_expert[t][s].
+ * Replaces launch_moe_gate_up (src/moe_kernels.cpp:1225). */
+int grimoire_moe_gate_up(void* stream, const grim_moe_layer* L, const int32_t* d_expert,
+                         const float* x, float* h);
+
+/* y[t][o] = sum_s w[t][s] * (down_e[o] . h[t][s]).
+ * Replaces launch_moe_down (src/moe_kernels.cpp:1350). */
+int grimoire_moe_down(void* stream, const grim_moe_layer* L, const int32_t* d_expert,
+                      const float* d_weight, const float* h, float* y);
+
+/* gate_up with the shared expert as slot top_k (ws = [2I][H], same format
+ * as the routed experts); gate_w (bf16 [H], may be NULL) gives
+ * gate_out[t] = sigmoid(x_t . gate_w).
+ * Replaces launch_moe_gate_up_shared (src/moe_kernels.cpp:1246). */
+int grimoire_moe_gate_up_shared(void* stream, const grim_moe_layer* L,
+                                const grim_quant_weight* ws, const uint16_t* gate_w,
+                                const int32_t* d_expert, const float* x, float* h,
+                                float* gate_out);
+
+/* down with the shared expert (wd = [H][I]) weighted by gate_in[t] (1 when
+ * NULL).  Replaces launch_moe_down_shared (src/moe_kernels.cpp:1278). */
+int grimoire_moe_down_shared(void* stream, const grim_moe_layer* L,
+                             const grim_quant_weight* wd, const int32_t* d_expert,
+                             const float* d_weight, const float* gate_in, const float* h,
+                             float* y);
+
+/* M-token forms.  Replace launch_moe_gate_up_batched / launch_moe_down_batched
+ * (src/moe_kernels.cpp:1372, :1394). */
+int grimoire_moe_gate_up_batched(void* stream, const grim_moe_layer* L,
+                                 const int32_t* d_expert, const float* x, float* h,
+                                 int tokens);
+int grimoire_moe_down_batched(void* stream, const grim_moe_layer* L, const int32_t* d_expert,
+                              const float* d_weight, const float* h, float* y, int tokens);
+
+/* Both products for M tokens with the shared expert fused (gate_w may be
+ * NULL).  Replaces launch_moe_shared_rows (src/moe_kernels.cpp:1316). */
+int grimoire_moe_shared_rows(void* stream, const grim_moe_layer* L,
+                             const grim_quant_weight* ws, const grim_quant_weight* wd,
+                             const uint16_t* gate_w, const int32_t* rex, const float* rwt,
+                             const float* x, float* h, float* gate_out, float* y, int M);
+
+/* ------------------------------------------------------------------------
+ * Dispatch (prefill / verify).  The permutation is deterministic and
+ * stable: expert-major, ascending route index r = t*top_k + s, the order
+ * of the reference's host counting sort (src/grimoire.cpp:23162-23170).
+ * The reference's device kernels use atomic arrival order instead
+ * (src/prefill.cpp:2721-2725).
+ * ---------------------------------------------------------------------- */
+
+/* Bytes of device workspace grimoire_moe_route_grouped needs. */
+size_t grimoire_moe_route_workspace_bytes(int tokens, int top_k, int num_experts);
+
+/* counts[E], offsets[E] (exclusive scan), inverse[T*K] = absolute permuted
+ * row of route r, xperm bf16 [T*K][H] = bf16(hidden[t]) at each permuted
+ * row, xrow bf16 [T][H] (may be NULL) = the unpermuted bf16 copy, and the
+ * m-tile table tile_e/tile_mb [tmax] (expert, tile index) padded with -1.
+ * Replaces launch_moe_route_grouped (src/prefill.cpp:2726-2808), whose
+ * TOPK is fixed at 8; here top_k is the trailing argument.  perm_token
+ * (may be NULL) receives the token of each permuted row. */
+int grimoire_moe_route_grouped(void* stream, const float* hidden, const int32_t* topk_ids,
+                               uint16_t* xperm, uint16_t* xrow, int32_t* counts,
+                               int32_t* offsets, int32_t* inverse, int32_t* tile_e,
+                               int32_t* tile_mb, int tmax, int tokens, int hidden_size,
+                               int num_experts, int mc, int top_k, int32_t* perm_token,
+                               void* workspace, size_t workspace_bytes);
+
+/* The same without tile table from bf16 hidden states (vLLM
+ * RowsPerExpertCount / RemapHiddenStates form).  Replaces
+ * launch_moe_remap_bf16_top8 (src/prefill.cpp:2810-2890). */
+int grimoire_moe_remap_bf16(void* stream, const uint16_t* hidden, const int32_t* topk_ids,
+                            uint16_t* remapped, int32_t* rows_per_expert,
+                            int32_t* expert_offsets, int32_t* inverse, int tokens,
+                            int hidden_size, int num_experts, int top_k, void* workspace,
+                            size_t workspace_bytes);
+
+/* dst[t][d] = sum_s w[t,s] * src[inverse[t,s]][d] as an fma chain in slot
+ * order; inverse -1 = route not computed here.  Replaces
+ * launch_moe_unpermute (src/prefill.cpp:2654). */
+int grimoire_moe_unpermute(void* stream, const float* src, const int32_t* inverse,
+                           const float* route_weight, float* dst, int tokens, int top_k,
+                           int hidden);
+/* bf16 source rows.  Replaces launch_moe_unpermute_bf16 (src/prefill.cpp:2690). */
+int grimoire_moe_unpermute_bf16(void* stream, const uint16_t* src, const int32_t* inverse,
+                                const float* route_weight, float* dst, int tokens,
+                                int top_k, int hidden);
+
+/* Combine with the gated shared expert: dst[t] = unpermute(...)[t] +
+ * gate[t] * shared_src[t] (gate NULL = 1).  Replaces the unpermute plus the
+ * shared-expert add of src/grimoire.cpp:23118 and :23247-23283. */
+int grimoire_moe_combine(void* stream, const uint16_t* src, const int32_t* inverse,
+                         const float* route_weight, const uint16_t* shared_src,
+                         const float* gate, float* dst, int tokens, int top_k, int hidden);
+
+/* ------------------------------------------------------------------------
+ * Grouped GEMM on MFMA (prefill).  One launch per projection for all
+ * experts.  A bf16 [R][K] rows grouped by expert (offsets/counts from the
+ * dispatch), W the packed expert weight [E*N][K].
+ *   swiglu != 0: N = 2I; out[r][i] = silu(A_r . gate_e[i]) * (A_r . up_e[i])
+ *                 written as a bf16 pair (hi, lo) with hi + lo = h to
+ *                 within 2^-17 relative: out is uint16_t [R][2][I]
+ *                 (hi row then lo row).
+ *   swiglu == 0: out[r][n] = A_r . W_e[n]; A may be a bf16 pair [R][2][K]
+ *                 (a_pair != 0), out is bf16 [R][N] (out_bf16 != 0) or
+ *                 fp32 [R][N].
+ * Replaces launch_moe_mxfp4_grouped (src/gemm_fast.cpp:2343-2365) and, with
+ * the tile table, gemm_mxfp4_fused_grouped (src/gemm_fast.cpp:1603). */
+int grimoire_moe_grouped_gemm(void* stream, const grim_quant_weight* w, int N, int swiglu,
+                              const uint16_t* A, int a_pair, void* out, int out_bf16,
+                              const int32_t* offsets, const int32_t* counts,
+                              int num_experts, int total_rows);
+
+/* ------------------------------------------------------------------------
+ * Bridges (the vLLM-XPU grouped GEMMs the reference dlopens).  Same
+ * argument lists apart from the queue.  rows_per_expert [ne] gives the
+ * contiguous row blocks of `a`; expert_ids may be NULL (expert i = block
+ * i).  atomic_buffer is accepted and ignored (no persistent tile counter is
+ * needed here).
+ * ---------------------------------------------------------------------- */
+
+/* d[r][n] = a[r] . dequant(b_e)[n], b u8 [E][n][k/2] MXFP4, scales e8m0
+ * [E][n][k/32], a/d bf16.  Replaces grimoire_xe2_grouped_mxfp4_bf16
+ * (src/xe2_grouped_bridge.cpp:135). */
+void grimoire_xe2_grouped_mxfp4_bf16(void* stream, const void* a, const unsigned char* b,
+                                     const unsigned char* scales, void* d, int n, int k,
+                                     const int* rows_per_expert, const int* expert_ids,
+                                     int num_experts, int* atomic_buffer);
+
+/* Signed-s4 weights [E][n][k/2] with bf16 group scales [E][n][k/group].
+ * Declared, never defined, in the reference (src/xe2_grouped_bridge.hpp:22). */
+void grimoire_xe2_grouped_w4a16(void* stream, const void* activations_bf16,
+                                const unsigned char* weights_int4, const void* scales_bf16,
+                                void* outputs_bf16, int n, int k, const int* rows_per_expert,
+                                const int* expert_ids, int num_experts, int group_size,
+                                int* atomic_buffer);
+
+/* Grouped gate_up with SiLU(gate)*up epilogue: weights [E][2n][k/2] MXFP4
+ * (gate rows then up rows), out bf16 [R][n].  Replaces
+ * grimoire_xe2_fused_moe_gate_up_mxfp4_silu_bf16 (src/xe2_fused_moe_bridge.cpp:32-43). */
+void grimoire_xe2_fused_moe_gate_up_mxfp4_silu_bf16(void* stream, const void* activations,
+                                                    const unsigned char* weights,
+                                                    const unsigned char* scales, void* outputs,
+                                                    int n, int k, const int* rows_per_expert,
+                                                    int num_experts, int32_t* atomic_buffer);
+
+/* ------------------------------------------------------------------------
+ * Whole MoE block, the sequence the engine runs per layer
+ * (src/grimoire.cpp:15362-15500 decode, :22743-23300 prefill):
+ * router GEMV -> top-k -> expert products -> combine (+ gated shared).
+ * ---------------------------------------------------------------------- */
+enum grim_route_mode {
+    GRIM_ROUTE_SOFTMAX = 0,    /* softmax top-k (+ renormalise per cfg)   */
+    GRIM_ROUTE_SIGMOID = 1,    /* sigmoid + selection bias (bf16)         */
+    GRIM_ROUTE_GROUP = 2       /* group-limited sigmoid (bias fp32)       */
+};
+
+typedef struct grim_route_params {
+    int32_t mode;              /* enum grim_route_mode                     */
+    int32_t n_group;           /* GROUP only                               */
+    int32_t topk_group;        /* GROUP only                               */
+    float scaling;             /* routed scaling factor (1 = none)         */
+    const void* bias;          /* SOFTMAX: router bias fp32 [E] added to the
+                                  logits (logits = W x + b); SIGMOID: bf16
+                                  [E] selection bias; GROUP: fp32 [E]
+                                  selection bias; or NULL */
+} grim_route_params;
+
+/* Workspace bytes for grimoire_moe_forward at `tokens`. */
+size_t grimoire_moe_forward_workspace_bytes(const grim_moe_layer* L, int tokens);
+
+/* y fp32 [T][H] = MoE(x fp32 [T][H]).  shared_gate_w bf16 [H] (may be NULL:
+ * shared expert weight 1, as src/moe_ref.cpp:100-104).  Routing is written
+ * to out_expert/out_weight [T][K] when not NULL.  regime: 0 = choose
+ * (slot GEMV for T*K <= 64, grouped MFMA GEMM otherwise), 1 = GEMV,
+ * 2 = grouped GEMM. */
+int grimoire_moe_forward(void* stream, const grim_moe_layer* L, const grim_route_params* rp,
+                         const uint16_t* shared_gate_w, const float* x, float* y, int tokens,
+                         int32_t* out_expert, float* out_weight, int regime, void* workspace,
+                         size_t workspace_bytes);
+
+#if defined(__GNUC__)
+#pragma GCC visibility pop
+#endif
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GRIMOIRE_MOE_H */

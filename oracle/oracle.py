@@ -1,0 +1,173 @@
+"""ctypes binding of the CPU oracle (TEST INFRASTRUCTURE ONLY).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
+this module.  It wraps
+  oracle/_build/libmoe_oracle.so  -- this repo's C restatement (moe_oracle.c)
+  oracle/_ref/libmoe_ref.so       -- the reference's own src/moe_ref.cpp and
+                                     src/gptq.cpp (built only where the
+                                     reference tree exists)
+Arguments are CPU torch tensors (or numpy arrays) and the ctypes structs of
+include/grimoire_moe.h.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import torch
+
+HERE = Path(__file__).resolve().parent
+ORACLE_SO = HERE / "_build" / "libmoe_oracle.so"
+REF_SO = HERE / "_ref" / "libmoe_ref.so"
+
+P = C.c_void_p
+I32 = C.c_int
+F32 = C.c_float
+
+_orc = None
+_ref = None
+
+
+def build(ref: bool = True) -> None:
+    """Compile the oracle (and oracle/_ref when the reference is present)."""
+    target = "all" if ref else str(ORACLE_SO)
+    subprocess.run(["make", "-s", "-C", str(HERE), target], check=True)
+
+
+def _p(t):
+    if t is None:
+        return None
+    if isinstance(t, np.ndarray):
+        assert t.flags["C_CONTIGUOUS"]
+        return t.ctypes.data
+    assert not t.is_cuda and t.is_contiguous()
+    return t.data_ptr()
+
+
+def orc() -> C.CDLL:
+    global _orc
+    if _orc is None:
+        if not ORACLE_SO.exists():
+            build(ref=False)
+        l = C.CDLL(str(ORACLE_SO))
+        sig = {
+            "orc_f16_to_f32": (F32, [C.c_uint16]),
+            "orc_bf16_to_f32": (F32, [C.c_uint16]),
+            "orc_f32_to_bf16": (C.c_uint16, [F32]),
+            "orc_e8m0_to_f32": (F32, [C.c_uint8]),
+            "orc_e2m1_to_f32": (F32, [C.c_uint8]),
+            "orc_expf": (F32, [F32]),
+            "orc_sigmoid": (F32, [F32]),
+            "orc_qw_at": (F32, [P, I32, I32]),
+            "orc_gptq_at": (F32, [P, P, P, I32, I32, I32, I32, I32]),
+            "orc_route_ref": (None, [P, I32, I32, I32, P, P]),
+            "orc_topk_softmax": (None, [P, I32, I32, I32, I32, I32, P, P]),
+            "orc_topk_sigmoid": (None, [P, P, I32, I32, I32, I32, F32, P, P]),
+            "orc_topk_group": (None, [P, P, I32, I32, I32, I32, I32, I32, F32, P, P]),
+            "orc_router_logits": (None, [P, P, P, I32, I32, I32]),
+            "orc_gate_up": (None, [P, P, P, P, P, P, P, I32]),
+            "orc_down": (None, [P, P, P, P, P, P, P, I32]),
+            "orc_moe_forward": (None, [P, P, P, P, P, P, I32]),
+            "orc_dispatch": (I32, [P, I32, I32, I32, I32, P, P, P, P, P, P, I32]),
+            "orc_unpermute": (None, [P, P, P, P, I32, I32, I32]),
+            "orc_grouped_gemm": (None, [P, I32, I32, P, P, P, P, I32]),
+        }
+        for n, (r, a) in sig.items():
+            f = getattr(l, n)
+            f.restype = r
+            f.argtypes = a
+        _orc = l
+    return _orc
+
+
+def ref():
+    """The reference's own CPU oracle, or None when it was not built."""
+    global _ref
+    if _ref is None:
+        if not REF_SO.exists():
+            return None
+        l = C.CDLL(str(REF_SO))
+        sig = {
+            "ref_qw_at": (F32, [P, I32, I32]),
+            "ref_gptq_at": (F32, [P, P, P, I32, I32, I32, I32, I32]),
+            "ref_route_ref": (None, [P, I32, I32, I32, P, P]),
+            "ref_moe_forward": (None, [P, P, P, P, P, I32]),
+        }
+        for n, (r, a) in sig.items():
+            f = getattr(l, n)
+            f.restype = r
+            f.argtypes = a
+        _ref = l
+    return _ref
+
+
+def byref(s):
+    return C.cast(C.pointer(s), P)
+
+
+# ------------------------------------------------------------ conveniences
+
+def topk_softmax(logits: torch.Tensor, K: int, normalize=True, batched=False):
+    T, E = logits.shape
+    oe = torch.empty((T, K), dtype=torch.int32)
+    ow = torch.empty((T, K), dtype=torch.float32)
+    orc().orc_topk_softmax(_p(logits.contiguous()), T, E, K, int(normalize), int(batched), _p(oe), _p(ow))
+    return oe, ow
+
+
+def topk_sigmoid(logits, bias_bf16, K, normalize=True, scaling=1.0):
+    T, E = logits.shape
+    oe = torch.empty((T, K), dtype=torch.int32)
+    ow = torch.empty((T, K), dtype=torch.float32)
+    orc().orc_topk_sigmoid(_p(logits.contiguous()), _p(bias_bf16), T, E, K, int(normalize),
+                           float(scaling), _p(oe), _p(ow))
+    return oe, ow
+
+
+def topk_group(logits, bias, K, n_group, topk_group, normalize=True, scaling=1.0):
+    T, E = logits.shape
+    oe = torch.empty((T, K), dtype=torch.int32)
+    ow = torch.empty((T, K), dtype=torch.float32)
+    orc().orc_topk_group(_p(logits.contiguous()), _p(bias), T, E, K, n_group, topk_group,
+                         int(normalize), float(scaling), _p(oe), _p(ow))
+    return oe, ow
+
+
+def router_logits(router, x):
+    T, H = x.shape
+    E = router.shape[0]
+    out = torch.empty((T, E), dtype=torch.float32)
+    orc().orc_router_logits(_p(router.contiguous()), _p(x.contiguous()), _p(out), T, E, H)
+    return out
+
+
+def dispatch(ids: torch.Tensor, E: int, mc: int, tmax: int):
+    T, K = ids.shape
+    R = T * K
+    counts = torch.empty(E, dtype=torch.int32)
+    offsets = torch.empty(E, dtype=torch.int32)
+    inverse = torch.empty(R, dtype=torch.int32)
+    perm = torch.full((R,), -1, dtype=torch.int32)
+    te = torch.empty(max(tmax, 1), dtype=torch.int32)
+    tm = torch.empty(max(tmax, 1), dtype=torch.int32)
+    nt = orc().orc_dispatch(_p(ids.contiguous()), T, K, E, mc, _p(counts), _p(offsets),
+                            _p(inverse), _p(perm), _p(te), _p(tm), tmax)
+    return dict(counts=counts, offsets=offsets, inverse=inverse, perm_token=perm,
+                tile_e=te[:tmax], tile_mb=tm[:tmax], n_tiles=nt)
+
+
+def moe_forward(layer_struct, rex, rwt, gate, x):
+    T, H = x.shape
+    y = torch.empty((T, H), dtype=torch.float32)
+    orc().orc_moe_forward(byref(layer_struct), _p(rex.contiguous()), _p(rwt.contiguous()),
+                          _p(gate), _p(x.contiguous()), _p(y), T)
+    return y
+
+
+def unpermute(src, inverse, rw, T, K, H):
+    dst = torch.empty((T, H), dtype=torch.float32)
+    orc().orc_unpermute(_p(src.contiguous()), _p(inverse.contiguous()), _p(rw.contiguous()),
+                        _p(dst), T, K, H)
+    return dst

@@ -1,0 +1,83 @@
+"""The C ABI library loads, exports every function include/grimoire_moe.h
+declares, and rejects bad arguments on the host before any launch.
+CPU only: no call here reaches a kernel."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from grimoire_amd import _abi
+from grimoire_amd.weights import make_int8
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "grimoire_moe.h"
+
+
+def declared():
+    txt = HEADER.read_text()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(grimoire_\w+)\s*\(", txt)))
+
+
+def test_every_declared_symbol_is_exported():
+    lib = _abi.lib()
+    names = declared()
+    assert len(names) >= 25
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_abi.SIGNATURES), set(names) ^ set(_abi.SIGNATURES)
+
+
+def test_version():
+    assert b"gfx950" in _abi.lib().grimoire_moe_version()
+
+
+def _layer(fmt=_abi.FMT_INT8):
+    w = make_int8(8 * 2 * 64, 128)
+    d = make_int8(8 * 128, 64)
+    L = _abi.MoeLayer()
+    L.cfg = _abi.MoeConfig(128, 64, 8, 2, 0, 1)
+    L.gate_up = w.struct()
+    L.gate_up.fmt = fmt
+    L.down = d.struct()
+    return L, (w, d)
+
+
+def test_unknown_format_rejected():
+    L, keep = _layer(fmt=99)
+    st = _abi.lib().grimoire_moe_gate_up(None, L, 1, 1, 1)
+    assert st == _abi.ERR_FORMAT
+    assert b"format" in _abi.lib().grimoire_moe_last_error()
+
+
+def test_shape_rejections():
+    lib = _abi.lib()
+    L, keep = _layer()
+    L.cfg.top_k = 17
+    assert lib.grimoire_moe_gate_up(None, L, 1, 1, 1) == _abi.ERR_SHAPE
+    L.cfg.top_k = 2
+    L.gate_up.K = 100            # K does not match hidden
+    assert lib.grimoire_moe_gate_up(None, L, 1, 1, 1) == _abi.ERR_SHAPE
+    assert lib.grimoire_moe_router_topk(None, 1, 600, 8, 1, 1, 1) == _abi.ERR_SHAPE
+    assert lib.grimoire_moe_router_topk(None, 1, 64, 17, 1, 1, 1) == _abi.ERR_SHAPE
+    assert lib.grimoire_moe_router_topk_group(None, 1, None, 1, 256, 8, 7, 4, 1, 1, 1, 1.0) == _abi.ERR_SHAPE
+    assert lib.grimoire_moe_router_topk_group(None, 1, None, 1, 256, 40, 8, 1, 1, 1, 1, 1.0) == _abi.ERR_SHAPE
+
+
+def test_null_and_workspace_rejections():
+    lib = _abi.lib()
+    L, keep = _layer()
+    assert lib.grimoire_moe_gate_up(None, L, None, 1, 1) == _abi.ERR_ARG
+    assert lib.grimoire_moe_unpermute(None, None, 1, 1, 1, 4, 2, 8) == _abi.ERR_ARG
+    ws = lib.grimoire_moe_route_workspace_bytes(100, 8, 64)
+    assert ws > 0
+    assert lib.grimoire_moe_route_grouped(None, 1, 1, None, None, 1, 1, 1, None, None, 0, 100, 64,
+                                          64, 0, 8, None, 1, ws - 1) == _abi.ERR_WORKSPACE
+    assert lib.grimoire_moe_forward_workspace_bytes(L, 16) > 0
+
+
+def test_zero_tokens_is_a_no_op():
+    lib = _abi.lib()
+    assert lib.grimoire_moe_router_topk_batched(None, None, 0, 64, 8, None, None, 1) == 0
+    assert lib.grimoire_moe_unpermute(None, None, None, None, None, 0, 8, 64) == 0

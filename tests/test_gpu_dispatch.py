@@ -1,0 +1,90 @@
+"""Dispatch and combine on the GPU: counts, offsets, permutation, token map
+and tile table bit-exact against the oracle's stable counting sort; the
+permuted bf16 rows exact; the unpermute fma chain bit-exact."""
+import pytest
+import torch
+
+from oracle import oracle as O
+from grimoire_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _ids(T, K, E, seed, zipf=0.0, invalid=0):
+    g = torch.Generator().manual_seed(seed)
+    if zipf > 0:
+        p = torch.arange(1, E + 1, dtype=torch.float64) ** -zipf
+        ids = torch.stack([torch.multinomial(p, K, replacement=False, generator=g) for _ in range(T)])
+    else:
+        ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+    ids = ids.int()
+    if invalid:
+        idx = torch.randint(0, T * K, (invalid,), generator=g)
+        ids.view(-1)[idx] = -1
+    return ids.contiguous()
+
+
+@pytest.mark.parametrize("T,K,E,mc,zipf,invalid", [
+    (1, 8, 128, 128, 0.0, 0),
+    (16, 4, 64, 128, 0.0, 0),
+    (300, 10, 512, 128, 1.2, 0),       # several count blocks, skewed
+    (4096, 10, 512, 128, 1.2, 0),      # C4 size
+    (77, 6, 33, 16, 0.0, 5),           # odd sizes, routes not computed here
+    (1000, 3, 2000, 64, 0.0, 0),       # more experts than scan threads
+])
+def test_dispatch_bit_exact(gpu, T, K, E, mc, zipf, invalid):
+    print(f"dispatch T={T} K={K} E={E} mc={mc} zipf={zipf} invalid={invalid}", flush=True)
+    ids = _ids(T, K, E, T + E, zipf, invalid)
+    H = 64
+    x = torch.randn(T, H)
+    R = T * K
+    tmax = E + (R + mc - 1) // mc
+    d = gpu
+    counts = torch.empty(E, dtype=torch.int32, device=d)
+    offsets = torch.empty(E, dtype=torch.int32, device=d)
+    inverse = torch.empty(R, dtype=torch.int32, device=d)
+    perm = torch.full((R,), -7, dtype=torch.int32, device=d)
+    te = torch.empty(tmax, dtype=torch.int32, device=d)
+    tm = torch.empty(tmax, dtype=torch.int32, device=d)
+    xperm = torch.zeros(R, H, dtype=torch.int16, device=d)
+    xrow = torch.empty(T, H, dtype=torch.int16, device=d)
+    ops.launch_moe_route_grouped(x.to(d), ids.to(d), xperm, xrow, counts, offsets, inverse, te, tm,
+                                 tmax, T, H, E, mc, K, perm_token=perm)
+    torch.cuda.synchronize()
+    want = O.dispatch(ids, E, mc, tmax)
+    assert torch.equal(counts.cpu(), want["counts"])
+    assert torch.equal(offsets.cpu(), want["offsets"])
+    assert torch.equal(inverse.cpu(), want["inverse"])
+    nvalid = int(want["counts"].sum())
+    assert torch.equal(perm.cpu()[:nvalid], want["perm_token"][:nvalid])
+    assert torch.equal(te.cpu(), want["tile_e"])
+    nt = want["n_tiles"]
+    assert torch.equal(tm.cpu()[:nt], want["tile_mb"][:nt])
+    xb = x.bfloat16().view(torch.int16)
+    assert torch.equal(xrow.cpu(), xb)
+    inv = want["inverse"]
+    for r in range(0, R, max(1, R // 500)):
+        if inv[r] >= 0:
+            assert torch.equal(xperm.cpu()[inv[r]], xb[r // K])
+
+
+@pytest.mark.parametrize("T,K,H", [(1, 8, 2048), (33, 10, 2048), (5, 4, 2880)])
+def test_unpermute_bit_exact(gpu, T, K, H):
+    print(f"unpermute T={T} K={K} H={H}", flush=True)
+    R = T * K
+    src = torch.randn(R, H)
+    inv = torch.randperm(R).int()
+    inv[::7] = -1
+    rw = torch.rand(R)
+    out = torch.empty(T, H, device=gpu)
+    ops.launch_moe_unpermute(src.to(gpu), inv.to(gpu), rw.to(gpu), out, T, K, H)
+    torch.cuda.synchronize()
+    want = O.unpermute(src, inv, rw, T, K, H)
+    assert torch.equal(out.cpu(), want)
+    # bf16 rows
+    sb = src.bfloat16()
+    out2 = torch.empty(T, H, device=gpu)
+    ops.launch_moe_unpermute(sb.view(torch.int16).to(gpu), inv.to(gpu), rw.to(gpu), out2, T, K, H)
+    torch.cuda.synchronize()
+    want2 = O.unpermute(sb.float(), inv, rw, T, K, H)
+    assert torch.equal(out2.cpu(), want2)

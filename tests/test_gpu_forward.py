@@ -1,0 +1,113 @@
+"""The whole MoE layer (grimoire_moe_forward) on the GPU against the oracle:
+routing bit-exact on the same logits, outputs within max-abs 2e-2 and
+rel-L2 1e-3.  Full BASELINE sizes where the oracle finishes in seconds;
+sampled tokens and cross-regime agreement where it does not."""
+import pytest
+import torch
+
+from oracle import oracle as O
+from grimoire_amd import _abi, configs, ops
+from tests.helpers import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(wl, device, regime=0, T=None):
+    cfg = wl.cfg
+    Lg = wl.layer if wl.layer.router.is_cuda else wl.layer.to(device)
+    x = wl.x[:T] if T else wl.x
+    T = x.shape[0]
+    xg = x.to(device)
+    bias = None if wl.route_bias is None else wl.route_bias.to(device)
+    fwd = ops.MoeForward(Lg, T, configs.route_params(cfg, bias), regime)
+    y = torch.empty(T, cfg.H, device=device)
+    oe = torch.empty(T, cfg.K, dtype=torch.int32, device=device)
+    ow = torch.empty(T, cfg.K, dtype=torch.float32, device=device)
+    fwd(xg, y, oe, ow)
+    # logits through the same router kernel, for the routing check
+    lg = torch.empty(T, cfg.E, device=device)
+    ops.router_logits(Lg.router, xg, lg)
+    torch.cuda.synchronize()
+    return Lg, y.cpu(), oe.cpu(), ow.cpu(), lg.cpu()
+
+
+def _check_routing(wl, logits, oe, ow):
+    cfg = wl.cfg
+    if cfg.route == _abi.ROUTE_SOFTMAX:
+        l = logits if wl.route_bias is None else logits + wl.route_bias.cpu()
+        we, ww = O.topk_softmax(l.contiguous(), cfg.K, True)
+    elif cfg.route == _abi.ROUTE_GROUP:
+        we, ww = O.topk_group(logits, wl.route_bias.cpu().contiguous(), cfg.K, cfg.n_group,
+                              cfg.topk_group, True, cfg.scaling)
+    else:
+        we, ww = O.topk_sigmoid(logits, wl.route_bias.cpu().contiguous(), cfg.K, True, cfg.scaling)
+    assert torch.equal(oe, we), "routing indices differ from the oracle"
+    assert torch.equal(ow, ww), "routing weights differ from the oracle"
+
+
+def _oracle_y(wl_cpu_layer, x, oe, ow, gate_w):
+    s = wl_cpu_layer.struct()
+    gate = None
+    if wl_cpu_layer.has_shared and gate_w is not None:
+        gw = (gate_w.to(torch.int32) << 16).view(torch.float32)
+        gate = torch.sigmoid(x.double() @ gw.double()).float().contiguous()
+    return O.moe_forward(s, oe, ow, gate, x)
+
+
+@pytest.mark.parametrize("name", ["c1", "c2"])
+def test_forward_full_size_decode(gpu, name):
+    print(f"forward {name} full size", flush=True)
+    wl = configs.make_workload(configs.CONFIGS[name], "cpu", seed=1)
+    Lg, y, oe, ow, logits = _run(wl, gpu)
+    _check_routing(wl, logits, oe, ow)
+    yo = _oracle_y(wl.layer, wl.x, oe, ow, None)
+    assert_close(y, yo, what=name)
+
+
+def test_forward_c3_full_size(gpu):
+    print("forward c3 full size (mxfp4, zipf)", flush=True)
+    wl = configs.make_workload(configs.CONFIGS["c3"], "cpu", seed=2)
+    Lg, y, oe, ow, logits = _run(wl, gpu)
+    _check_routing(wl, logits, oe, ow)
+    yo = _oracle_y(wl.layer, wl.x, oe, ow, None)
+    assert_close(y, yo, what="c3")
+
+
+@pytest.mark.parametrize("regime", [1, 2])
+def test_forward_c4_scaled_both_regimes(gpu, regime):
+    print(f"forward c4 scaled regime={regime}", flush=True)
+    cfg = configs.scaled(configs.CONFIGS["c4"], T=96, H=1024, E=64, I=256)
+    wl = configs.make_workload(cfg, "cpu", seed=3)
+    Lg, y, oe, ow, logits = _run(wl, gpu, regime=regime)
+    _check_routing(wl, logits, oe, ow)
+    gate = None
+    yo = _oracle_y(wl.layer, wl.x, oe, ow, wl.layer.shared_gate_w)
+    assert_close(y, yo, what=f"c4 scaled regime {regime}")
+
+
+def test_forward_c5_scaled(gpu):
+    print("forward c5 scaled (group-limited sigmoid, mxfp4, shared)", flush=True)
+    cfg = configs.scaled(configs.CONFIGS["c5"], T=32, H=1024, E=64, I=256)
+    wl = configs.make_workload(cfg, "cpu", seed=4)
+    Lg, y, oe, ow, logits = _run(wl, gpu, regime=2)
+    _check_routing(wl, logits, oe, ow)
+    yo = _oracle_y(wl.layer, wl.x, oe, ow, None)
+    assert_close(y, yo, what="c5 scaled")
+
+
+def test_forward_c4_full_size_sampled(gpu):
+    """C4 at full size: routing of all 4096 tokens bit-exact; outputs of a
+    seeded sample of tokens against the oracle; the grouped-GEMM regime
+    agrees with the independent slot-GEMV regime on a token subset."""
+    print("forward c4 full size", flush=True)
+    cfg = configs.CONFIGS["c4"]
+    wl = configs.make_workload(cfg, "cpu", seed=5)
+    Lg, y, oe, ow, logits = _run(wl, gpu, regime=2)
+    _check_routing(wl, logits, oe, ow)
+    idx = torch.randperm(cfg.T, generator=torch.Generator().manual_seed(0))[:12]
+    yo = _oracle_y(wl.layer, wl.x[idx].contiguous(), oe[idx].contiguous(), ow[idx].contiguous(),
+                   wl.layer.shared_gate_w)
+    assert_close(y[idx], yo, what="c4 sampled tokens")
+    Lg2, y2, oe2, ow2, _ = _run(configs.Workload(cfg, Lg, wl.x, wl.route_bias), gpu, regime=1, T=64)
+    assert torch.equal(oe2, oe[:64])
+    assert_close(y[:64], y2, what="c4 gemm vs gemv regime")

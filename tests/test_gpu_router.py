@@ -1,0 +1,83 @@
+"""Router parity on the GPU: logits to tolerance, top-k bit-exact against
+the oracle on the same fp32 logits buffer (indices AND weights)."""
+import pytest
+import torch
+
+from oracle import oracle as O
+from grimoire_amd import ops
+from tests.helpers import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _ties(T, E, seed, scale=2.0):
+    g = torch.Generator().manual_seed(seed)
+    l = torch.randn(T, E, generator=g) * scale
+    l[:, 5] = l[:, 3]
+    l[:, E - 1] = l[:, 0]
+    l[::2, 7] = l[::2, 2]
+    l[1::3, :] = l[1::3, :].round()          # many exact ties
+    return l.contiguous()
+
+
+@pytest.mark.parametrize("T,E,H", [(1, 128, 2048), (7, 64, 2048), (32, 256, 7168), (33, 512, 2048),
+                                   (300, 96, 512)])
+def test_router_logits(gpu, T, E, H):
+    print(f"router_logits T={T} E={E} H={H}", flush=True)
+    g = torch.Generator().manual_seed(T + E)
+    W = torch.randn(E, H, generator=g) * 0.02
+    x = torch.randn(T, H, generator=g).bfloat16().float()
+    out = torch.empty(T, E, device=gpu)
+    ops.router_logits(W.to(gpu), x.to(gpu), out)
+    torch.cuda.synchronize()
+    want = O.router_logits(W, x)
+    assert (out.cpu() - want).abs().max() < 1e-4
+    assert rel_l2(out.cpu(), want) < 1e-5
+
+
+@pytest.mark.parametrize("T,E,K", [(1, 128, 8), (1, 256, 8), (5, 64, 4), (40, 512, 10), (3, 20, 16),
+                                   (9, 300, 7)])
+@pytest.mark.parametrize("normalize", [True, False])
+def test_topk_softmax_bit_exact(gpu, T, E, K, normalize):
+    print(f"topk softmax T={T} E={E} K={K} norm={normalize}", flush=True)
+    l = _ties(T, E, E * K)
+    oe = torch.empty(T, K, dtype=torch.int32, device=gpu)
+    ow = torch.empty(T, K, dtype=torch.float32, device=gpu)
+    if T == 1:
+        ops.launch_router_topk(l.to(gpu), E, K, oe, ow, normalize)
+        we, ww = O.topk_softmax(l, K, normalize, batched=False)
+    else:
+        ops.launch_router_topk_batched(l.to(gpu), T, E, K, oe, ow, normalize)
+        we, ww = O.topk_softmax(l, K, normalize, batched=True)
+    torch.cuda.synchronize()
+    assert torch.equal(oe.cpu(), we)
+    assert torch.equal(ow.cpu(), ww), (ow.cpu() - ww).abs().max()
+
+
+@pytest.mark.parametrize("T,E,K,scaling", [(1, 128, 8, 1.0), (16, 100, 8, 2.5), (32, 512, 16, 1.0)])
+def test_topk_sigmoid_bit_exact(gpu, T, E, K, scaling):
+    print(f"topk sigmoid T={T} E={E} K={K}", flush=True)
+    l = _ties(T, E, 3 + E)
+    bias = (torch.randn(E) * 0.05).bfloat16().view(torch.int16).contiguous()
+    oe = torch.empty(T, K, dtype=torch.int32, device=gpu)
+    ow = torch.empty(T, K, dtype=torch.float32, device=gpu)
+    ops.launch_router_topk_k2(l.to(gpu), bias.to(gpu), T, E, K, oe, ow, True, scaling)
+    torch.cuda.synchronize()
+    we, ww = O.topk_sigmoid(l, bias, K, True, scaling)
+    assert torch.equal(oe.cpu(), we)
+    assert torch.equal(ow.cpu(), ww)
+
+
+@pytest.mark.parametrize("T,E,K,ng,kg", [(32, 256, 8, 8, 4), (5, 64, 6, 8, 3), (4, 512, 8, 16, 4),
+                                         (3, 64, 4, 1, 1)])
+def test_topk_group_bit_exact(gpu, T, E, K, ng, kg):
+    print(f"topk group T={T} E={E} K={K} groups {kg}/{ng}", flush=True)
+    l = _ties(T, E, 17 + E, scale=1.0)
+    bias = (torch.randn(E) * 1e-3).contiguous()
+    oe = torch.empty(T, K, dtype=torch.int32, device=gpu)
+    ow = torch.empty(T, K, dtype=torch.float32, device=gpu)
+    ops.launch_router_topk_group(l.to(gpu), bias.to(gpu), T, E, K, ng, kg, oe, ow, True, 2.5)
+    torch.cuda.synchronize()
+    we, ww = O.topk_group(l, bias, K, ng, kg, True, 2.5)
+    assert torch.equal(oe.cpu(), we)
+    assert torch.equal(ow.cpu(), ww)
