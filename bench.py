@@ -64,6 +64,31 @@ class Timer:
         return self.a.elapsed_time(self.b)
 
 
+def _graph(fn, stream):
+    """Capture fn() (kernel launches on `stream`) into a HIP graph."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        fn()
+    return g
+
+
+def _replay(g, stream, n=1):
+    """Replay on `stream` (a graph launches on the current stream)."""
+    with torch.cuda.stream(stream):
+        for _ in range(n):
+            g.replay()
+
+
+def check_handoff(fwds):
+    """The single-launch decode keeps its hand-off counters in the first
+    words of each workspace: all zero between calls, word 64 = a timeout."""
+    for f in fwds:
+        ctr = f.workspace[: 4 * 4224].view(torch.int32)
+        if int(ctr[64]) != 0 or int(torch.count_nonzero(ctr)) != 0:
+            raise RuntimeError(f"fused decode hand-off failed: timeout code {int(ctr[64])}, "
+                               f"{int(torch.count_nonzero(ctr))} non-zero counters")
+
+
 def decode_bench(steps, warmup, dev, stream):
     cfg = configs.CONFIGS["c2"]
     layers = [configs.make_layer(cfg, dev, seed=100 + i) for i in range(LAYERS)]
@@ -77,39 +102,51 @@ def decode_bench(steps, warmup, dev, stream):
         for f, y, oe, ow in zip(fwds, ys, oes, ows):
             f(x, y, oe, ow, stream=stream)
 
+    # eager once (routing for the byte count), then the step as one graph
     with torch.cuda.stream(stream):
-        for _ in range(warmup):
-            step()
-        torch.cuda.synchronize()
-        # algorithmic bytes from the actual routing
-        ebytes = layers[0].expert_bytes()
-        step_bytes = 0.0
-        for oe in oes:
-            distinct = len(set(oe.flatten().tolist()))
-            step_bytes += distinct * ebytes + cfg.E * cfg.H * 4 + 2 * cfg.H * 4
-        torch.cuda.synchronize()
-        with Timer(stream) as tm:
-            for _ in range(steps):
-                step()
-        ms = tm.ms() / steps
-        torch.cuda.synchronize()
+        step()
+    torch.cuda.synchronize()
+    check_handoff(fwds)
+    g_step = _graph(step, stream)
+    ebytes = layers[0].expert_bytes()
+    step_bytes = 0.0
+    for oe in oes:
+        distinct = len(set(oe.flatten().tolist()))
+        step_bytes += distinct * ebytes + cfg.E * cfg.H * 4 + 2 * cfg.H * 4
+    _replay(g_step, stream, warmup)
+    torch.cuda.synchronize()
+    with Timer(stream) as tm:
+        _replay(g_step, stream, steps)
+    ms = tm.ms() / steps
+    check_handoff(fwds)
 
-        # dominant kernel: gate_up, launched alone per layer on this stream
-        h = torch.empty(1, cfg.K, cfg.I, device=dev)
-        gu_bytes = cfg.K * layers[0].gate_up.row_bytes_total() * 2 * cfg.I + cfg.H * 4
-        reps = max(steps, 10)
+    # one layer replayed on its own (its 20.5 MB stay in the 256 MB MALL)
+    g_one = _graph(lambda: fwds[0](x, ys[0], oes[0], ows[0], stream=stream), stream)
+    _replay(g_one, stream, 20)
+    reps1 = 200
+    with Timer(stream) as t1:
+        _replay(g_one, stream, reps1)
+    one_us = t1.ms() * 1e3 / reps1
+
+    # dominant kernel: gate_up, 48 layers' launches captured alone
+    h = torch.empty(1, cfg.K, cfg.I, device=dev)
+    gu_bytes = cfg.K * layers[0].gate_up.row_bytes_total() * 2 * cfg.I + cfg.H * 4
+
+    def gu_only():
         for L, oe in zip(layers, oes):
             ops.launch_moe_gate_up_batched(L, oe, x, h, 1, stream=stream)
-        torch.cuda.synchronize()
-        with Timer(stream) as tg:
-            for _ in range(reps):
-                for L, oe in zip(layers, oes):
-                    ops.launch_moe_gate_up_batched(L, oe, x, h, 1, stream=stream)
-        gu_us = tg.ms() * 1e3 / (reps * LAYERS)
+
+    g_gu = _graph(gu_only, stream)
+    _replay(g_gu, stream)
+    torch.cuda.synchronize()
+    reps = max(steps, 10)
+    with Timer(stream) as tg:
+        _replay(g_gu, stream, reps)
+    gu_us = tg.ms() * 1e3 / (reps * LAYERS)
 
     gbs = step_bytes / (ms * 1e-3) / 1e9
     return dict(cfg=cfg, ms=ms, step_bytes=step_bytes, gbs=gbs, gu_us=gu_us, gu_bytes=gu_bytes,
-                layers=layers, x=x, oes=oes, ows=ows)
+                one_us=one_us, layers=layers, x=x, oes=oes, ows=ows)
 
 
 def prefill_bench(dev, stream, reps=5):
@@ -243,6 +280,7 @@ def main():
         "config": {"workload": "c2: T=1 H=2048 E=128 top-8 softmax I=768 GPTQ int4 g128, "
                                "48 distinct layers", "layers": LAYERS},
         "us_per_layer": round(d["ms"] * 1e3 / LAYERS, 2),
+        "us_per_layer_standalone_mall_hot": round(d["one_us"], 2),
         "hbm_frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
         "roofline": {
             "bound": "hbm",

@@ -111,23 +111,25 @@ int gemv_common(void* stream, const grim_moe_layer* L, const grim_quant_weight* 
             return fail(GRIM_ERR_FORMAT, "shared expert format must match routed experts");
     }
     if (gate_w && !gate_out) return fail(GRIM_ERR_ARG, "gate_w without gate_out");
-    if (gemv_lds_bytes(L->gate_up.fmt, c.hidden, c.inter, 0, false) > kMaxLds)
-        return fail(GRIM_ERR_SHAPE, "hidden=%d too large for the decode kernel", c.hidden);
-    GemvArgs a{};
-    a.w = view(L->gate_up);
-    a.ws = wsh ? view(*wsh) : a.w;
+    DecodeArgs a{};
+    a.gu = view(L->gate_up);
+    a.sgu = wsh ? view(*wsh) : a.gu;
+    a.dn = a.sdn = view(L->down);
     a.shared = wsh != nullptr;
-    a.rex = rex;
+    a.rex = const_cast<int32_t*>(rex);
     a.x = x;
     a.h = h;
     a.gate_w = gate_w;
-    a.gate_out = gate_out;
+    a.gate = gate_out;
     a.H = c.hidden;
     a.I = c.inter;
     a.K = c.top_k;
-    a.M = M;
     a.E = c.num_experts;
-    return status(gemv_launch(S(stream), L->gate_up.fmt, a, false));
+    a.M = M;
+    decode_plan(L->gate_up.fmt, a, kRoleGateUp);
+    if (decode_lds_bytes(L->gate_up.fmt, a) > kMaxLds)
+        return fail(GRIM_ERR_SHAPE, "hidden=%d too large for the decode kernel", c.hidden);
+    return status(decode_launch(S(stream), L->gate_up.fmt, a));
 }
 
 int down_common(void* stream, const grim_moe_layer* L, const grim_quant_weight* wd,
@@ -144,24 +146,25 @@ int down_common(void* stream, const grim_moe_layer* L, const grim_quant_weight* 
         if (wd->fmt != L->down.fmt)
             return fail(GRIM_ERR_FORMAT, "shared expert format must match routed experts");
     }
-    const int KS = c.top_k + (wd ? 1 : 0);
-    if (gemv_lds_bytes(L->down.fmt, c.hidden, c.inter, KS, true) > kMaxLds)
-        return fail(GRIM_ERR_SHAPE, "(top_k+shared)*inter too large for the decode kernel");
-    GemvArgs a{};
-    a.w = view(L->down);
-    a.ws = wd ? view(*wd) : a.w;
+    DecodeArgs a{};
+    a.gu = a.sgu = view(L->gate_up);
+    a.dn = view(L->down);
+    a.sdn = wd ? view(*wd) : a.dn;
     a.shared = wd != nullptr;
-    a.rex = rex;
-    a.rwt = rwt;
+    a.rex = const_cast<int32_t*>(rex);
+    a.rwt = const_cast<float*>(rwt);
     a.gate_in = gate_in;
     a.h = const_cast<float*>(h);
     a.y = y;
     a.H = c.hidden;
     a.I = c.inter;
     a.K = c.top_k;
-    a.M = M;
     a.E = c.num_experts;
-    return status(gemv_launch(S(stream), L->down.fmt, a, true));
+    a.M = M;
+    decode_plan(L->down.fmt, a, kRoleDown);
+    if (decode_lds_bytes(L->down.fmt, a) > kMaxLds)
+        return fail(GRIM_ERR_SHAPE, "(top_k+shared)*inter too large for the decode kernel");
+    return status(decode_launch(S(stream), L->down.fmt, a));
 }
 
 // Library-held scratch for the bridges, whose signatures carry none.

@@ -80,11 +80,31 @@ __device__ __forceinline__ float silu(float v) {
     return v / (1.0f + det_expf(-v));
 }
 
-// Butterfly sum over aligned groups of LPR lanes (LPR a power of two <= 64).
+// Cross-lane moves inside a 16-lane row (DPP, no LDS traffic).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return __builtin_amdgcn_update_dpp(0u, v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i within 8
+constexpr int kDppMirror = 0x140;     // lane i <-> 15-i within 16
+
+// Sum over aligned groups of LPR lanes (LPR a power of two <= 64); every
+// lane of a group ends with the same value (each step adds a symmetric
+// pair, so the partners compute identical sums).
 template <int LPR>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int m = LPR / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, kWave);
+    if constexpr (LPR >= 2) v += dpp_f<kDppXor1>(v);
+    if constexpr (LPR >= 4) v += dpp_f<kDppXor2>(v);
+    if constexpr (LPR >= 8) v += dpp_f<kDppHalfMirror>(v);
+    if constexpr (LPR >= 16) v += dpp_f<kDppMirror>(v);
+    if constexpr (LPR >= 32) v += __shfl_xor(v, 16, kWave);
+    if constexpr (LPR >= 64) v += __shfl_xor(v, 32, kWave);
     return v;
 }
 

@@ -41,6 +41,9 @@ struct Carve {
     }
 };
 
+// The fused decode launch covers up to this many tokens.
+constexpr int kFusedDecodeMaxTokens = 8;
+
 bool use_gemv(const grim_moe_layer* L, int T, int regime) {
     if (regime == 1) return true;
     if (regime == 2) return false;
@@ -48,6 +51,7 @@ bool use_gemv(const grim_moe_layer* L, int T, int regime) {
 }
 
 struct Plan {
+    int32_t* ctr;   // hand-off counters of the fused decode launch (zero at rest)
     float* logits;
     int32_t* rex;
     float* rwt;
@@ -68,6 +72,7 @@ size_t carve(const grim_moe_layer* L, int T, bool gemv, char* base, Plan& p) {
     const int64_t R = int64_t(T) * K;
     const bool sh = L->has_shared;
     Carve cv{base};
+    p.ctr = cv.take<int32_t>(kDecodeCounterWords);
     p.logits = cv.take<float>(size_t(T) * E);
     p.rex = cv.take<int32_t>(R);
     p.rwt = cv.take<float>(R);
@@ -148,30 +153,81 @@ extern "C" int grimoire_moe_forward(void* stream, const grim_moe_layer* L,
     const int E = c.num_experts, K = c.top_k, H = c.hidden, I = c.inter;
     const int mode = rp ? rp->mode : GRIM_ROUTE_SOFTMAX;
     if (H % 4) return ferr(GRIM_ERR_SHAPE, "hidden must be a multiple of 4");
+    if (mode < GRIM_ROUTE_SOFTMAX || mode > GRIM_ROUTE_GROUP) return ferr(GRIM_ERR_ARG, "unknown route mode");
+    if (mode == GRIM_ROUTE_GROUP &&
+        (!rp || rp->n_group <= 0 || rp->n_group > 64 || E % rp->n_group || rp->topk_group <= 0 ||
+         rp->topk_group > rp->n_group || K > rp->topk_group * (E / rp->n_group)))
+        return ferr(GRIM_ERR_SHAPE, "group-limited routing parameters");
+    if (E > 512 || K > 16) return ferr(GRIM_ERR_SHAPE, "E <= 512 and top_k <= 16");
+    const float* rbias = (mode == GRIM_ROUTE_SOFTMAX && rp) ? static_cast<const float*>(rp->bias) : nullptr;
+    const int topk_mode = mode == GRIM_ROUTE_SOFTMAX ? 0 : (mode == GRIM_ROUTE_SIGMOID ? 2 : 3);
+    const uint16_t* b16 = mode == GRIM_ROUTE_SIGMOID ? static_cast<const uint16_t*>(rp->bias) : nullptr;
+    const float* b32 = mode == GRIM_ROUTE_GROUP ? static_cast<const float*>(rp->bias) : nullptr;
+    const float scaling = (rp && mode != GRIM_ROUTE_SOFTMAX) ? rp->scaling : 1.0f;
+    const bool sh = L->has_shared;
+
+    if (gemv && tokens <= kFusedDecodeMaxTokens) {
+        // one launch: router GEMV -> top-k -> gate_up -> down, handed off on
+        // the device (decode_kernel roles)
+        if (sh && (L->shared_gate_up.fmt != L->gate_up.fmt || L->shared_down.fmt != L->down.fmt))
+            return ferr(GRIM_ERR_FORMAT, "shared expert format must match routed experts");
+        DecodeArgs a{};
+        a.gu = make_view(L->gate_up);
+        a.dn = make_view(L->down);
+        a.sgu = sh ? make_view(L->shared_gate_up) : a.gu;
+        a.sdn = sh ? make_view(L->shared_down) : a.dn;
+        a.shared = sh;
+        a.router = L->router;
+        a.rbias = rbias;
+        a.mode = topk_mode;
+        a.normalize = c.norm_topk;
+        a.scaling = scaling;
+        a.bias16 = b16;
+        a.bias32 = b32;
+        a.n_group = rp ? rp->n_group : 0;
+        a.topk_group = rp ? rp->topk_group : 0;
+        a.logits = p.logits;
+        a.x = x;
+        a.rex = p.rex;
+        a.rwt = p.rwt;
+        a.gate_w = sh ? shared_gate_w : nullptr;
+        a.gate = p.gate;
+        a.gate_in = (sh && shared_gate_w) ? p.gate : nullptr;
+        a.h = p.h;
+        a.y = y;
+        a.H = H;
+        a.I = I;
+        a.K = K;
+        a.E = E;
+        a.M = tokens;
+        a.fused = 1;
+        a.ctr = p.ctr;
+        if (L->gate_up.fmt != L->down.fmt) {
+            // two formats: the roles need one kernel instantiation each
+            return ferr(GRIM_ERR_FORMAT, "fused decode needs gate_up and down in one format");
+        }
+        decode_plan(L->gate_up.fmt, a, kRoleRouter | kRoleGateUp | kRoleDown);
+        if (decode_lds_bytes(L->gate_up.fmt, a) > 160 * 1024)
+            return ferr(GRIM_ERR_SHAPE, "layer too large for the fused decode kernel");
+        hipError_t e = decode_launch(st, L->gate_up.fmt, a);
+        if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+        return GRIM_OK;
+    }
+
     {
-        const float* rb = (mode == GRIM_ROUTE_SOFTMAX && rp) ? static_cast<const float*>(rp->bias) : nullptr;
-        hipError_t e = router_logits_launch(st, L->router, x, rb, p.logits, tokens, E, H);
+        hipError_t e = router_logits_launch(st, L->router, x, rbias, p.logits, tokens, E, H);
         if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
     }
     int r = GRIM_OK;
-    if (mode == GRIM_ROUTE_SOFTMAX) {
-        TopkArgs a{p.logits, tokens, E, K, 0, c.norm_topk, 1.0f, nullptr, nullptr, 0, 0, p.rex, p.rwt};
+    {
+        TopkArgs a{p.logits, tokens, E, K, topk_mode, c.norm_topk, scaling, b16, b32,
+                   rp ? rp->n_group : 0, rp ? rp->topk_group : 0, p.rex, p.rwt};
         hipError_t e = topk_launch(st, a);
         if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
-    } else if (mode == GRIM_ROUTE_SIGMOID) {
-        r = grimoire_moe_router_topk_sigmoid(stream, p.logits, static_cast<const uint16_t*>(rp->bias),
-                                             tokens, E, K, p.rex, p.rwt, c.norm_topk, rp->scaling);
-    } else if (mode == GRIM_ROUTE_GROUP) {
-        r = grimoire_moe_router_topk_group(stream, p.logits, static_cast<const float*>(rp->bias),
-                                           tokens, E, K, rp->n_group, rp->topk_group, p.rex, p.rwt,
-                                           c.norm_topk, rp->scaling);
-    } else {
-        return ferr(GRIM_ERR_ARG, "unknown route mode");
     }
-    if (r) return r;
 
     if (gemv) {
-        if (L->has_shared)
+        if (sh)
             return grimoire_moe_shared_rows(stream, L, &L->shared_gate_up, &L->shared_down,
                                             shared_gate_w, p.rex, p.rwt, x, p.h,
                                             shared_gate_w ? p.gate : nullptr, y, tokens);
@@ -189,7 +245,6 @@ extern "C" int grimoire_moe_forward(void* stream, const grim_moe_layer* L,
                                    p.inverse, p.tile_e, p.tile_mb, p.tmax, tokens, H, E, kGemmBM, K,
                                    nullptr, p.disp_ws, dispatch_workspace_bytes(tokens, K, E));
     if (r) return r;
-    const bool sh = L->has_shared;
     if (sh && shared_gate_w) {
         hipError_t e = rowdot_sigmoid_launch(st, x, shared_gate_w, p.gate, tokens, H);
         if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));

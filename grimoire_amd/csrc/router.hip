@@ -1,188 +1,26 @@
 // router.hip -- router projection and top-k selection.
 //
-// Top-k runs one wavefront per token with every score in VGPRs (lane l owns
-// experts [l*V, l*V+V), V = ceil(E/64) <= 8).  Each round packs
-// (order-preserving score bits, ~expert) into one 64-bit key, so a single
-// wave max gives the largest score and, among equal scores, the lowest
-// expert index -- the tie rule of src/ops.cpp:1125-1131.  The weights are
-// then formed serially in pick order with the same operations as the
-// reference kernels (src/ops.cpp:1133-1147, :2126-2135), using det_expf so
-// that the oracle reproduces them bit for bit.
+// The per-wave top-k itself lives in topk.hpp (shared with the fused decode
+// kernel).
 #include "common.hpp"
 #include "router.hpp"
+#include "topk.hpp"
 
 namespace grim {
 
-constexpr int kMaxV = 8;          // E <= 512
 constexpr int kTopkWaves = 4;
 
-__device__ __forceinline__ uint64_t score_key(float v, int e) {
-    if (v != v) return (uint64_t(1) << 32) | uint32_t(~e);   // NaN ranks below everything
-    uint32_t u = f_bits(v + 0.0f);                           // -0 -> +0
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return (uint64_t(u) << 32) | uint32_t(~e);
-}
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
-#pragma unroll
-    for (int m = 32; m > 0; m >>= 1) {
-        const uint64_t o = __shfl_xor(k, m, kWave);
-        k = o > k ? o : k;
-    }
-    return k;
-}
-
-// K rounds of wave argmax over sel[V] (lane-owned), skipping masked
-// entries.  Returns the picks in pick order (uniform across the wave).
-__device__ __forceinline__ void wave_select(const float* sel, bool* taken, int V, int E, int K,
-                                            int lane, int* picks) {
-    for (int s = 0; s < K; ++s) {
-        uint64_t best = 0;
-#pragma unroll
-        for (int j = 0; j < kMaxV; ++j) {
-            const int e = lane * V + j;
-            if (j < V && e < E && !taken[j]) {
-                const uint64_t k = score_key(sel[j], e);
-                best = k > best ? k : best;
-            }
-        }
-        best = wave_max_u64(best);
-        const int e = int(~uint32_t(best));
-        picks[s] = e;
-        const int owner = e / V, j = e - owner * V;
-        if (lane == owner) {
-#pragma unroll
-            for (int jj = 0; jj < kMaxV; ++jj)
-                if (jj == j) taken[jj] = true;
-        }
-    }
-}
-
-// mode 0: softmax (decode semantics); 1: softmax batched semantics
-// (normalize == 0 -> raw logits); 2: sigmoid + bf16 bias; 3: group-limited
-// sigmoid + fp32 bias.
 __global__ __launch_bounds__(kTopkWaves * kWave) void topk_kernel(
     const float* __restrict__ logits, int T, int E, int K, int mode, int normalize,
     float scaling, const uint16_t* __restrict__ bias16, const float* __restrict__ bias32,
     int n_group, int topk_group, int32_t* __restrict__ out_e, float* __restrict__ out_w) {
     __shared__ float gsel[kTopkWaves][512];
     __shared__ float gscore[kTopkWaves][64];
-    const int lane = threadIdx.x & (kWave - 1);
     const int wv = threadIdx.x / kWave;
     const int t = blockIdx.x * kTopkWaves + wv;
     if (t >= T) return;   // whole wave exits together
-    const int V = (E + kWave - 1) / kWave;
-    const float* row = logits + int64_t(t) * E;
-
-    float sc[kMaxV], sel[kMaxV];
-    bool taken[kMaxV];
-#pragma unroll
-    for (int j = 0; j < kMaxV; ++j) {
-        const int e = lane * V + j;
-        taken[j] = false;
-        sc[j] = 0.0f;
-        sel[j] = 0.0f;
-        if (j < V && e < E) {
-            const float l = row[e];
-            if (mode <= 1) {
-                sel[j] = l;
-            } else {
-                sc[j] = det_sigmoid(l);
-                const float b = mode == 2 ? (bias16 ? bf16_to_f32(bias16[e]) : 0.0f)
-                                          : (bias32 ? bias32[e] : 0.0f);
-                sel[j] = sc[j] + b;
-            }
-        }
-    }
-
-    if (mode == 3) {
-        // group scores: sum of the two largest biased scores per group
-        for (int j = 0; j < V; ++j) {
-            const int e = lane * V + j;
-            if (e < E) gsel[wv][e] = sel[j];
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const int gs = E / n_group;
-        if (lane < n_group) {
-            int b1 = -1, b2 = -1;
-            for (int e = lane * gs; e < (lane + 1) * gs; ++e) {
-                const float v = gsel[wv][e];
-                if (b1 < 0 || v > gsel[wv][b1]) { b2 = b1; b1 = e; }
-                else if (b2 < 0 || v > gsel[wv][b2]) b2 = e;
-            }
-            gscore[wv][lane] = gs > 1 ? gsel[wv][b1] + gsel[wv][b2] : gsel[wv][b1];
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        uint64_t keep = 0;
-        for (int j = 0; j < topk_group; ++j) {
-            int best = -1;
-            for (int g = 0; g < n_group; ++g) {
-                if (keep & (uint64_t(1) << g)) continue;
-                if (best < 0 || gscore[wv][g] > gscore[wv][best]) best = g;
-            }
-            keep |= uint64_t(1) << best;
-        }
-#pragma unroll
-        for (int j = 0; j < kMaxV; ++j) {
-            const int e = lane * V + j;
-            if (j < V && e < E) taken[j] = !((keep >> (e / gs)) & 1);
-        }
-    }
-
-    int picks[16];
-    wave_select(sel, taken, V, E, K, lane, picks);
-
-    // gather the picked values (uniform): raw score for softmax, unbiased
-    // sigmoid for the sigmoid modes
-    float v[16];
-    for (int s = 0; s < K; ++s) {
-        const int e = picks[s];
-        const int owner = e / V, j = e - owner * V;
-        float mine = 0.0f;
-#pragma unroll
-        for (int jj = 0; jj < kMaxV; ++jj)
-            if (jj == j) mine = mode <= 1 ? sel[jj] : sc[jj];
-        v[s] = __shfl(mine, owner, kWave);
-    }
-
-    if (lane == 0) {
-        int32_t* oe = out_e + int64_t(t) * K;
-        float* ow = out_w + int64_t(t) * K;
-        if (mode <= 1) {
-            if (mode == 1 && !normalize) {
-                for (int s = 0; s < K; ++s) { oe[s] = picks[s]; ow[s] = v[s]; }
-            } else {
-                float m = v[0];
-                for (int s = 1; s < K; ++s) m = fmaxf(m, v[s]);
-                float sum = 0.0f;
-                float ev[16];
-                for (int s = 0; s < K; ++s) {
-                    ev[s] = det_expf(v[s] - m);
-                    sum += ev[s];
-                }
-                for (int s = 0; s < K; ++s) {
-                    oe[s] = picks[s];
-                    ow[s] = (normalize && sum > 0.0f) ? ev[s] / sum : ev[s];
-                }
-            }
-        } else {
-            float w[16];
-            for (int s = 0; s < K; ++s) w[s] = v[s];
-            if (normalize) {
-                float sum = 0.0f;
-                for (int s = 0; s < K; ++s) sum += w[s];
-                if (sum > 0.0f)
-                    for (int s = 0; s < K; ++s) w[s] /= sum;
-            }
-            if (scaling != 1.0f)
-                for (int s = 0; s < K; ++s) w[s] *= scaling;
-            for (int s = 0; s < K; ++s) { oe[s] = picks[s]; ow[s] = w[s]; }
-        }
-    }
+    topk_wave(logits + int64_t(t) * E, E, K, mode, normalize, scaling, bias16, bias32, n_group,
+              topk_group, out_e + int64_t(t) * K, out_w + int64_t(t) * K, gsel[wv], gscore[wv]);
 }
 
 hipError_t topk_launch(hipStream_t st, const TopkArgs& a) {

@@ -42,6 +42,7 @@ def _p(t):
     if isinstance(t, np.ndarray):
         assert t.flags["C_CONTIGUOUS"]
         return t.ctypes.data
+    # callers must keep `t` referenced until the C call returns
     assert not t.is_cuda and t.is_contiguous()
     return t.data_ptr()
 
@@ -113,7 +114,8 @@ def topk_softmax(logits: torch.Tensor, K: int, normalize=True, batched=False):
     T, E = logits.shape
     oe = torch.empty((T, K), dtype=torch.int32)
     ow = torch.empty((T, K), dtype=torch.float32)
-    orc().orc_topk_softmax(_p(logits.contiguous()), T, E, K, int(normalize), int(batched), _p(oe), _p(ow))
+    lc = logits.contiguous()
+    orc().orc_topk_softmax(_p(lc), T, E, K, int(normalize), int(batched), _p(oe), _p(ow))
     return oe, ow
 
 
@@ -121,7 +123,8 @@ def topk_sigmoid(logits, bias_bf16, K, normalize=True, scaling=1.0):
     T, E = logits.shape
     oe = torch.empty((T, K), dtype=torch.int32)
     ow = torch.empty((T, K), dtype=torch.float32)
-    orc().orc_topk_sigmoid(_p(logits.contiguous()), _p(bias_bf16), T, E, K, int(normalize),
+    lc = logits.contiguous()
+    orc().orc_topk_sigmoid(_p(lc), _p(bias_bf16), T, E, K, int(normalize),
                            float(scaling), _p(oe), _p(ow))
     return oe, ow
 
@@ -130,7 +133,8 @@ def topk_group(logits, bias, K, n_group, topk_group, normalize=True, scaling=1.0
     T, E = logits.shape
     oe = torch.empty((T, K), dtype=torch.int32)
     ow = torch.empty((T, K), dtype=torch.float32)
-    orc().orc_topk_group(_p(logits.contiguous()), _p(bias), T, E, K, n_group, topk_group,
+    lc = logits.contiguous()
+    orc().orc_topk_group(_p(lc), _p(bias), T, E, K, n_group, topk_group,
                          int(normalize), float(scaling), _p(oe), _p(ow))
     return oe, ow
 
@@ -139,7 +143,8 @@ def router_logits(router, x):
     T, H = x.shape
     E = router.shape[0]
     out = torch.empty((T, E), dtype=torch.float32)
-    orc().orc_router_logits(_p(router.contiguous()), _p(x.contiguous()), _p(out), T, E, H)
+    rc, xc = router.contiguous(), x.contiguous()
+    orc().orc_router_logits(_p(rc), _p(xc), _p(out), T, E, H)
     return out
 
 
@@ -152,7 +157,8 @@ def dispatch(ids: torch.Tensor, E: int, mc: int, tmax: int):
     perm = torch.full((R,), -1, dtype=torch.int32)
     te = torch.empty(max(tmax, 1), dtype=torch.int32)
     tm = torch.empty(max(tmax, 1), dtype=torch.int32)
-    nt = orc().orc_dispatch(_p(ids.contiguous()), T, K, E, mc, _p(counts), _p(offsets),
+    ic = ids.contiguous()
+    nt = orc().orc_dispatch(_p(ic), T, K, E, mc, _p(counts), _p(offsets),
                             _p(inverse), _p(perm), _p(te), _p(tm), tmax)
     return dict(counts=counts, offsets=offsets, inverse=inverse, perm_token=perm,
                 tile_e=te[:tmax], tile_mb=tm[:tmax], n_tiles=nt)
@@ -161,13 +167,15 @@ def dispatch(ids: torch.Tensor, E: int, mc: int, tmax: int):
 def moe_forward(layer_struct, rex, rwt, gate, x):
     T, H = x.shape
     y = torch.empty((T, H), dtype=torch.float32)
-    orc().orc_moe_forward(byref(layer_struct), _p(rex.contiguous()), _p(rwt.contiguous()),
-                          _p(gate), _p(x.contiguous()), _p(y), T)
+    # keep every contiguous copy alive for the duration of the call
+    rc, wc, xc = rex.contiguous(), rwt.contiguous(), x.contiguous()
+    gc = None if gate is None else gate.contiguous()
+    orc().orc_moe_forward(byref(layer_struct), _p(rc), _p(wc), _p(gc), _p(xc), _p(y), T)
     return y
 
 
 def unpermute(src, inverse, rw, T, K, H):
     dst = torch.empty((T, H), dtype=torch.float32)
-    orc().orc_unpermute(_p(src.contiguous()), _p(inverse.contiguous()), _p(rw.contiguous()),
-                        _p(dst), T, K, H)
+    sc, ic, wc = src.contiguous(), inverse.contiguous(), rw.contiguous()
+    orc().orc_unpermute(_p(sc), _p(ic), _p(wc), _p(dst), T, K, H)
     return dst

@@ -54,7 +54,7 @@ def test_gate_up_down(gpu, fmt, H, I, E, K, T, shared):
     ids_o = ids.clone()
     ids_o[ids_o < 0] = 0          # gate_up computes a row for every slot
     if shared:
-        ws, wd = L.shared_gate_up.struct(), L.shared_down.struct()
+        ws = L.shared_gate_up.struct()
         O.orc().orc_gate_up(O.byref(s), O.byref(ws), O._p(L.shared_gate_w), O._p(ids_o), O._p(x),
                             O._p(ho), O._p(go), T)
     else:
@@ -63,13 +63,15 @@ def test_gate_up_down(gpu, fmt, H, I, E, K, T, shared):
         assert_close(h.cpu(), ho, what="h")
     else:
         assert_close(h.cpu()[:, 1:], ho[:, 1:], what="h")
+    hc = h.cpu().contiguous()
+    yo = torch.empty(T, H)
     if shared:
         assert (gate.cpu() - go).abs().max() < 1e-5
-        O.orc().orc_down(O.byref(s), O.byref(L.shared_down.struct()), O._p(ids), O._p(w), O._p(go),
-                         O._p(h.cpu().contiguous()), O._p(yo := torch.empty(T, H)), T)
+        wds = L.shared_down.struct()
+        O.orc().orc_down(O.byref(s), O.byref(wds), O._p(ids), O._p(w), O._p(go), O._p(hc),
+                         O._p(yo), T)
     else:
-        O.orc().orc_down(O.byref(s), None, O._p(ids), O._p(w), None, O._p(h.cpu().contiguous()),
-                         O._p(yo := torch.empty(T, H)), T)
+        O.orc().orc_down(O.byref(s), None, O._p(ids), O._p(w), None, O._p(hc), O._p(yo), T)
     assert_close(y.cpu(), yo, what="y (down on the GPU's h)")
     # and the whole layer against the oracle's forward
     yf = O.moe_forward(s, ids, w, go if shared else None, x)
