@@ -79,21 +79,22 @@ def _replay(g, stream, n=1):
             g.replay()
 
 
-def check_handoff(fwds):
-    """The single-launch decode keeps its hand-off counters in the first
-    words of each workspace: all zero between calls, word 64 = a timeout."""
+def check_counters(fwds):
+    """The decode path keeps its router counter in the first words of each
+    workspace: all zero between calls."""
     for f in fwds:
-        ctr = f.workspace[: 4 * 4224].view(torch.int32)
-        if int(ctr[64]) != 0 or int(torch.count_nonzero(ctr)) != 0:
-            raise RuntimeError(f"fused decode hand-off failed: timeout code {int(ctr[64])}, "
-                               f"{int(torch.count_nonzero(ctr))} non-zero counters")
+        ctr = f.workspace[: 4 * _abi.DECODE_COUNTER_WORDS].view(torch.int32)
+        if int(torch.count_nonzero(ctr)) != 0:
+            raise RuntimeError(f"decode router counter not back at zero: "
+                               f"{int(torch.count_nonzero(ctr))} non-zero words")
 
 
-def decode_bench(steps, warmup, dev, stream):
+def decode_bench(steps, warmup, dev, stream, regime=1):
     cfg = configs.CONFIGS["c2"]
     layers = [configs.make_layer(cfg, dev, seed=100 + i) for i in range(LAYERS)]
     x = configs.make_x(cfg, dev, seed=7)
-    fwds = [ops.MoeForward(L, 1, configs.route_params(cfg, None), regime=1) for L in layers]
+    fwds = [ops.MoeForward(L, 1, configs.route_params(cfg, None), regime=regime)
+            for L in layers]
     ys = [torch.empty(1, cfg.H, device=dev) for _ in layers]
     oes = [torch.empty(1, cfg.K, dtype=torch.int32, device=dev) for _ in layers]
     ows = [torch.empty(1, cfg.K, dtype=torch.float32, device=dev) for _ in layers]
@@ -106,7 +107,7 @@ def decode_bench(steps, warmup, dev, stream):
     with torch.cuda.stream(stream):
         step()
     torch.cuda.synchronize()
-    check_handoff(fwds)
+    check_counters(fwds)
     g_step = _graph(step, stream)
     ebytes = layers[0].expert_bytes()
     step_bytes = 0.0
@@ -118,7 +119,7 @@ def decode_bench(steps, warmup, dev, stream):
     with Timer(stream) as tm:
         _replay(g_step, stream, steps)
     ms = tm.ms() / steps
-    check_handoff(fwds)
+    check_counters(fwds)
 
     # one layer replayed on its own (its 20.5 MB stay in the 256 MB MALL)
     g_one = _graph(lambda: fwds[0](x, ys[0], oes[0], ows[0], stream=stream), stream)
@@ -254,6 +255,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode-regime", type=int, default=1, choices=(1, 3),
+                    help="1: router kernel with device top-k, gate_up, down; "
+                         "3: router logits, top-k, gate_up, down as four launches")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -263,7 +267,7 @@ def main():
     _abi.lib()
     stream = torch.cuda.Stream()
     log("decode bench (C2, 48 layers)...")
-    d = decode_bench(a.steps, a.warmup, dev, stream)
+    d = decode_bench(a.steps, a.warmup, dev, stream, a.decode_regime)
     out = {
         "metric": "MoE decode layer HBM GB/s (T=1, C2, 48 layers back to back)",
         "value": round(d["gbs"], 1),

@@ -41,23 +41,24 @@ struct Carve {
     }
 };
 
-// The fused decode launch covers up to this many tokens.
-constexpr int kFusedDecodeMaxTokens = 8;
+// The decode path with device-side routing covers up to this many tokens.
+constexpr int kDecodeMaxTokens = 8;
 
 bool use_gemv(const grim_moe_layer* L, int T, int regime) {
-    if (regime == 1) return true;
+    if (regime == 1 || regime == 3) return true;
     if (regime == 2) return false;
     return int64_t(T) * L->cfg.top_k <= 64;
 }
 
 struct Plan {
-    int32_t* ctr;   // hand-off counters of the fused decode launch (zero at rest)
+    int32_t* ctr;   // decode router counter (zero at rest)
     float* logits;
     int32_t* rex;
     float* rwt;
     float* gate;
     // GEMV
     float* h;
+    uint32_t* hf;   // decode: h in the staged layout
     // GEMM
     void* disp_ws;
     int32_t *counts, *offsets, *inverse, *tile_e, *tile_mb;
@@ -79,6 +80,7 @@ size_t carve(const grim_moe_layer* L, int T, bool gemv, char* base, Plan& p) {
     p.gate = cv.take<float>(T);
     if (gemv) {
         p.h = cv.take<float>(size_t(T) * (K + (sh ? 1 : 0)) * I);
+        p.hf = cv.take<uint32_t>(size_t(T) * fmt_words((K + (sh ? 1 : 0)) * I));
     } else {
         const size_t dws = dispatch_workspace_bytes(T, K, E);
         p.disp_ws = cv.take<char>(dws);
@@ -166,9 +168,9 @@ extern "C" int grimoire_moe_forward(void* stream, const grim_moe_layer* L,
     const float scaling = (rp && mode != GRIM_ROUTE_SOFTMAX) ? rp->scaling : 1.0f;
     const bool sh = L->has_shared;
 
-    if (gemv && tokens <= kFusedDecodeMaxTokens) {
-        // one launch: router GEMV -> top-k -> gate_up -> down, handed off on
-        // the device (decode_kernel roles)
+    if (gemv && regime != 3 && tokens <= kDecodeMaxTokens) {
+        // three launches: router GEMV + top-k (last router item), gate_up
+        // (h written in the staged layout), down
         if (sh && (L->shared_gate_up.fmt != L->gate_up.fmt || L->shared_down.fmt != L->down.fmt))
             return ferr(GRIM_ERR_FORMAT, "shared expert format must match routed experts");
         DecodeArgs a{};
@@ -194,21 +196,22 @@ extern "C" int grimoire_moe_forward(void* stream, const grim_moe_layer* L,
         a.gate = p.gate;
         a.gate_in = (sh && shared_gate_w) ? p.gate : nullptr;
         a.h = p.h;
+        a.hf = p.hf;
         a.y = y;
         a.H = H;
         a.I = I;
         a.K = K;
         a.E = E;
         a.M = tokens;
-        a.fused = 1;
+        a.fmt_h = 1;
         a.ctr = p.ctr;
         if (L->gate_up.fmt != L->down.fmt) {
             // two formats: the roles need one kernel instantiation each
-            return ferr(GRIM_ERR_FORMAT, "fused decode needs gate_up and down in one format");
+            return ferr(GRIM_ERR_FORMAT, "decode needs gate_up and down in one format");
         }
         decode_plan(L->gate_up.fmt, a, kRoleRouter | kRoleGateUp | kRoleDown);
         if (decode_lds_bytes(L->gate_up.fmt, a) > 160 * 1024)
-            return ferr(GRIM_ERR_SHAPE, "layer too large for the fused decode kernel");
+            return ferr(GRIM_ERR_SHAPE, "layer too large for the decode kernels");
         hipError_t e = decode_launch(st, L->gate_up.fmt, a);
         if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
         return GRIM_OK;

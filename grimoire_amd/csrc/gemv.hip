@@ -56,7 +56,7 @@ void decode_plan(int fmt, DecodeArgs& a, int roles) {
     a.lpr_dn = lpr_down(a.I / CH);
     a.gu_rb = (a.I + gu_rows_per_block(a.lpr_gu) - 1) / gu_rows_per_block(a.lpr_gu);
     a.dn_rb = down_rows_per_block(a.lpr_dn, KS);
-    a.NR = (roles & kRoleRouter) ? (a.E + kGemvWaves - 1) / kGemvWaves : 0;
+    a.NR = (roles & kRoleRouter) ? a.E : 0;
     a.NG = (roles & kRoleGateUp) ? a.M * KS * a.gu_rb : 0;
     a.ND = (roles & kRoleDown) ? a.M * ((a.H + a.dn_rb - 1) / a.dn_rb) : 0;
 }

@@ -5,11 +5,10 @@
 
 namespace grim {
 
-// One launch of moe_decode_kernel.  Blocks take roles in this order:
-// NR router blocks (fp32 router GEMV, then top-k by the last of them),
-// NG gate_up blocks (token, slot, row block), ND down blocks (token, row
-// block).  `fused` = the roles of this launch depend on each other and
-// hand off through ctr[] (8 int32, zero before the launch, zero after).
+// Arguments of the decode kernels.  Work items: NR router items (fp32
+// router GEMV, then top-k by the last of them), NG gate_up items (token,
+// slot, row block), ND down items (token, row block); each role is one
+// kernel launch, in that order.
 struct DecodeArgs {
     WView gu, sgu, dn, sdn;
     bool shared;
@@ -29,22 +28,25 @@ struct DecodeArgs {
     const uint16_t* gate_w;   // bf16 [H] or null: gate[t] = sigmoid(x_t . gate_w)
     float* gate;              // [M]
     const float* gate_in;     // down: shared-expert weight per token or null (= 1)
-    float* h;                 // [M][KS][I]
+    float* h;                 // [M][KS][I] (single-role launches)
+    uint32_t* hf;             // fmt_h: h formatted for staging, fmt_words(KS*I) words per token
     float* y;                 // [M][H]
     int H, I, K, E, M;
     // plan (decode_plan)
     int lpr_gu, lpr_dn, gu_rb, dn_rb;
     int NR, NG, ND;
-    int fused;
-    int32_t* ctr;
+    int fmt_h;                // gate_up writes hf, down stages hf (else plain h)
+    int32_t* ctr;             // router item counter (kDecodeCounterWords, zero at rest)
 };
+
+// Words per token of the formatted h (n = KS * I elements):
+// the staged planes, one fp32 sum per group of eight, padded to 16 bytes.
+__host__ __device__ constexpr int fmt_words(int n) { return (n + n / 8 + 3) & ~3; }
 
 constexpr int kRoleRouter = 1, kRoleGateUp = 2, kRoleDown = 4;
 
-// int32 words of the fused launch's hand-off counters (zero at rest):
-// router_done [0], routes_ready [32], timeout [64], h_done and dn_done each
-// 64 cache lines of 32 words from [128].
-constexpr int kDecodeCounterWords = 128 + 2 * 64 * 32;
+// int32 words of the decode counters (zero at rest): the router item count.
+constexpr int kDecodeCounterWords = 32;
 
 void decode_plan(int fmt, DecodeArgs& a, int roles);
 size_t decode_lds_bytes(int fmt, const DecodeArgs& a);

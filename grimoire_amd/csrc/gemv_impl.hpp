@@ -1,24 +1,12 @@
 // gemv_impl.hpp -- the decode / batched-decode MoE kernel (slot form).
 //
-// Work items take three roles: router rows (fp32 router GEMV; the last
-// router item also runs the top-k), gate_up rows (token, slot, row block) and
-// down rows (token, row block).  The standalone launchers run one role per
-// kernel; the decode forward (`fused`) runs two launches, the router kernel
-// and then one kernel holding every gate_up and down item, which hands h
-// over on the device:
-//
-//   - one work-group per item, gate_up items first.  gate_up items never
-//     wait; a down item waits only for gate_up items, whose work-group ids
-//     are all lower, and work-groups are dispatched in id order, so a
-//     waiting down item never holds a slot that a not-yet-dispatched gate_up
-//     item needs;
-//   - hand-off data (logits, routes, h, gate) is written and read with
-//     device-coherent (sc1) accesses, and a producer waits for its own
-//     stores (vmcnt 0) before it counts itself done, so no cache writeback
-//     fence is needed;
-//   - the h counter is spread over 64 cache lines (one same-address atomic
-//     costs ~11 ns on this GPU, a per-block writeback fence ~45 ns); waits
-//     are bounded and record a sticky timeout flag instead of hanging.
+// Work items take three roles, one kernel each: router rows (fp32 router
+// GEMV; the last router item to finish also runs the top-k), gate_up rows
+// (token, slot, row block) and down rows (token, row block).  The decode
+// forward runs the three kernels back to back on one stream; with `fmt_h`
+// the gate_up kernel writes h already in the LDS layout the down kernel
+// stages (formatted once, copied by every down work-group), else h is
+// plain fp32 as the standalone launchers expose it.
 //
 // Arithmetic: weights stream as 16-byte chunks per lane with their scales,
 // all loads of an item issued before the activations are touched.  INT4,
@@ -62,52 +50,14 @@ __device__ __forceinline__ void st_coh(int* p, int v) {
 }
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// counters (int32 offsets inside ctr[])
-constexpr int kCtrRouterDone = 0;
-constexpr int kCtrRoutesReady = 32;
-constexpr int kCtrTimeout = 64;
-constexpr int kCtrHDone = 128;                 // 64 lines of 32 ints
-constexpr int kCtrDnDone = kCtrHDone + 64 * 32;
-constexpr int kSpinLimit = 1 << 16;   // ~0.1 s of polling, then give up
-
-// Timeout codes recorded in ctr[kCtrTimeout] (sticky, never reset here).
-constexpr int kTimeoutRoutes = 1, kTimeoutH = 2;
-
-__device__ __forceinline__ void wait_flag(int* p, int* timeout) {
-    if (threadIdx.x == 0) {
-        int it = 0;
-        while (ld_coh(p) == 0) {
-            __builtin_amdgcn_s_sleep(2);
-            if (++it > kSpinLimit) { st_coh(timeout, kTimeoutRoutes); break; }
-        }
-    }
-    __syncthreads();
-}
-
-// sum of the 64 spread counters at base (one wave)
-__device__ __forceinline__ int spread_sum(const int* base) {
-    const int lane = threadIdx.x & (kWave - 1);
-    return int(group_sum<kWave>(float(ld_coh(base + 32 * lane))));
-}
-
-__device__ __forceinline__ void wait_spread(const int* base, int target, int* timeout) {
-    if (threadIdx.x < kWave) {
-        int it = 0;
-        while (spread_sum(base) < target) {
-            __builtin_amdgcn_s_sleep(2);
-            if (++it > kSpinLimit) {
-                if (threadIdx.x == 0) st_coh(timeout, kTimeoutH);
-                break;
-            }
-        }
-    }
-    __syncthreads();
-}
+// counters (int32 offsets inside ctr[], zero at rest)
+constexpr int kCtrRouterDone = 0;   // router items done; the last one resets it
 
 // ------------------------------------------------------- activation staging
 //
 // Pair formats keep a staged vector of n elements as bf16 pair words:
-//   hi[n/2], lo[n/2] (uint32), then one fp32 sum per chunk.
+//   hi[n/2], lo[n/2] (uint32, each plane in 16-byte quads stored
+//   quad-major, see quad_pos), then one fp32 sum per chunk.
 // INT4 pairs (x[8d+j], x[8d+j+4]) inside each dword d of a chunk, to match
 // the nibble decoder; MXFP4 / BF16 pairs (x[2p], x[2p+1]).  INT8 keeps fp32
 // x[n] then the chunk sums.
@@ -115,7 +65,19 @@ __device__ __forceinline__ void wait_spread(const int* base, int target, int* ti
 template <int F> struct Act {
     static constexpr bool kPair = F != GRIM_FMT_INT8;
     static constexpr bool kInterleave = F == GRIM_FMT_INT4 || F == GRIM_FMT_INT4_F16;
+    // 16-byte quads per chunk in a plane (hi, lo, or the fp32 values)
+    static constexpr int kQuads = (kPair ? Chunk<F>::CH / 2 : Chunk<F>::CH) / 4;
 };
+
+// Quads are stored quad-major: quad d of chunk c at d * nch + c.  Lanes
+// that read consecutive chunks then read consecutive 16-byte LDS slots,
+// free of bank conflicts, where chunk-major storage would put them 64 bytes
+// apart.
+template <int F>
+__device__ __forceinline__ int quad_pos(int k, int nch) {
+    constexpr int Q = Act<F>::kQuads;
+    return (k % Q) * nch + k / Q;
+}
 
 __device__ __forceinline__ uint32_t split_hi_lo(float v, uint32_t& lo) {
     const uint16_t h = f32_to_bf16(v);
@@ -123,73 +85,154 @@ __device__ __forceinline__ uint32_t split_hi_lo(float v, uint32_t& lo) {
     return h;
 }
 
-// Two device-coherent 16-byte loads (sc1: served from the coherence point,
-// never from a stale cache line), for data other work-groups of the same
-// launch wrote.
-__device__ __forceinline__ void ld_coh32(const float* p, float4& a, float4& b) {
-    u32x4 ra, rb;
-    asm volatile("global_load_dwordx4 %0, %2, off sc1\n\t"
-                 "global_load_dwordx4 %1, %2, off offset:16 sc1\n\t"
-                 "s_waitcnt vmcnt(0)"
-                 : "=&v"(ra), "=&v"(rb)
-                 : "v"(p)
-                 : "memory");
-    a = make_float4(bits_f(ra.x), bits_f(ra.y), bits_f(ra.z), bits_f(ra.w));
-    b = make_float4(bits_f(rb.x), bits_f(rb.y), bits_f(rb.z), bits_f(rb.w));
+// Formatted group of eight activations: bf16 pair words hi / lo (INT4:
+// (x[j], x[j+4]) to match the nibble decoder; else adjacent) and the sum
+// of the staged values (hi + lo) in element order.
+template <int F>
+__device__ __forceinline__ float format_group(const float (&v)[8], uint32_t (&hw)[4],
+                                              uint32_t (&lw)[4], int& any_lo) {
+    uint32_t h[8], l[8];
+    float part = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        h[i] = split_hi_lo(v[i], l[i]);
+        part += bits_f(h[i] << 16) + bits_f(l[i] << 16);
+        any_lo |= int(l[i] != 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e0 = Act<F>::kInterleave ? j : 2 * j;
+        const int e1 = Act<F>::kInterleave ? j + 4 : 2 * j + 1;
+        hw[j] = h[e0] | (h[e1] << 16);
+        lw[j] = l[e0] | (l[e1] << 16);
+    }
+    return part;
 }
 
-// Stage src[0..n) (n % CH == 0, n % 8 == 0) into LDS, eight elements per
-// thread; returns whether any lo half is non-zero (block-uniform).  The
-// chunk sums are sums of the staged values (hi + lo), so that the offset
-// correction of the INT4 decoder cancels exactly what the dots added.
-template <int F, bool COH>
+// Chunk sums from per-group sums: the TPC threads of a chunk are aligned
+// lanes; the first of them writes.
+template <int F>
+__device__ __forceinline__ void chunk_sum_out(float part, int g, float* sums) {
+    constexpr int TPC = Chunk<F>::CH / 8;   // threads per chunk (4, 2 or 1)
+    if constexpr (TPC >= 2) part += dpp_f<kDppXor1>(part);
+    if constexpr (TPC >= 4) part += dpp_f<kDppXor2>(part);
+    if (g >= 0 && (g % TPC) == 0) sums[g / TPC] = part;
+}
+
+// Stage src[0..n) (fp32, n % CH == 0, n % 8 == 0) into LDS, eight elements
+// per thread and up to NB groups of eight in flight per thread; returns
+// whether any lo half is non-zero (block-uniform).  The chunk sums are sums
+// of the staged values (hi + lo), so that the offset correction of the INT4
+// decoder cancels exactly what the dots added.
+template <int F, int NB = 2>
 __device__ __forceinline__ bool stage_act(const float* __restrict__ src, int n, uint32_t* lds) {
-    constexpr int CH = Chunk<F>::CH;
-    constexpr int TPC = CH / 8;            // threads per chunk (4, 2 or 1)
     int any_lo = 0;
     float* sums = reinterpret_cast<float*>(lds + n);
-    for (int g0 = 0; g0 < n / 8; g0 += blockDim.x) {
-        const int g = g0 + threadIdx.x;    // group of elements [8g, 8g + 8)
-        float part = 0.0f;
-        if (g < n / 8) {
-            float4 p, q;
-            if (COH) {
-                ld_coh32(src + 8 * g, p, q);
-            } else {
-                p = reinterpret_cast<const float4*>(src)[2 * g];
-                q = reinterpret_cast<const float4*>(src)[2 * g + 1];
+    const int ng = n / 8;
+    const int nch = n / Chunk<F>::CH;
+    const float4* s4 = reinterpret_cast<const float4*>(src);
+    for (int g0 = 0; g0 < ng; g0 += NB * blockDim.x) {
+        float4 p[NB], q[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int g = g0 + b * blockDim.x + threadIdx.x;
+            if (g < ng) { p[b] = s4[2 * g]; q[b] = s4[2 * g + 1]; }
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            if (g0 + b * blockDim.x >= ng) break;   // block-uniform
+            const int gi = g0 + b * blockDim.x + threadIdx.x;
+            const int g = gi < ng ? gi : -1;
+            float part = 0.0f;
+            if (g >= 0) {
+                const float v[8] = {p[b].x, p[b].y, p[b].z, p[b].w, q[b].x, q[b].y, q[b].z, q[b].w};
+                if constexpr (Act<F>::kPair) {
+                    uint32_t hw[4], lw[4];
+                    part = format_group<F>(v, hw, lw, any_lo);
+                    const int qp = quad_pos<F>(g, nch);
+                    reinterpret_cast<u32x4*>(lds)[qp] = u32x4{hw[0], hw[1], hw[2], hw[3]};
+                    reinterpret_cast<u32x4*>(lds + n / 2)[qp] = u32x4{lw[0], lw[1], lw[2], lw[3]};
+                } else {
+                    reinterpret_cast<float4*>(lds)[quad_pos<F>(2 * g, nch)] = p[b];
+                    reinterpret_cast<float4*>(lds)[quad_pos<F>(2 * g + 1, nch)] = q[b];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) part += v[i];
+                }
             }
-            const float v[8] = {p.x, p.y, p.z, p.w, q.x, q.y, q.z, q.w};
-            if constexpr (Act<F>::kPair) {
-                uint32_t h[8], l[8];
+            chunk_sum_out<F>(part, g, sums);
+        }
+    }
+    if constexpr (Act<F>::kPair) any_lo = __syncthreads_or(any_lo);
+    else __syncthreads();
+    return any_lo != 0;
+}
+
+// ------------------------------------------------------ formatted h vectors
+//
+// The gate_up kernel can write h already in the staged LDS layout (words
+// [0, n): the planes, quad-major), followed by one fp32 sum per group of
+// eight (words [n, n + n/8)); a down work-group then stages it by copying,
+// with the chunk sums formed from the group sums by the same DPP steps as
+// stage_act uses, so both paths give the same bits.
+
+// Write group g (eight values) of a formatted vector of n elements at dst.
+template <int F>
+__device__ __forceinline__ void put_group_fmt(uint32_t* dst, int n, int g, const float (&v)[8]) {
+    const int nch = n / Chunk<F>::CH;
+    float part = 0.0f;
+    if constexpr (Act<F>::kPair) {
+        uint32_t hw[4], lw[4];
+        int any = 0;
+        part = format_group<F>(v, hw, lw, any);
+        const int qp = quad_pos<F>(g, nch);
+        reinterpret_cast<u32x4*>(dst)[qp] = u32x4{hw[0], hw[1], hw[2], hw[3]};
+        reinterpret_cast<u32x4*>(dst + n / 2)[qp] = u32x4{lw[0], lw[1], lw[2], lw[3]};
+    } else {
+        reinterpret_cast<float4*>(dst)[quad_pos<F>(2 * g, nch)] = make_float4(v[0], v[1], v[2], v[3]);
+        reinterpret_cast<float4*>(dst)[quad_pos<F>(2 * g + 1, nch)] = make_float4(v[4], v[5], v[6], v[7]);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    h[i] = split_hi_lo(v[i], l[i]);
-                    part += bits_f(h[i] << 16) + bits_f(l[i] << 16);
-                    any_lo |= int(l[i] != 0);
-                }
-                uint32_t hw[4], lw[4];
+        for (int i = 0; i < 8; ++i) part += v[i];
+    }
+    reinterpret_cast<float*>(dst)[n + g] = part;
+}
+
+// Stage a formatted vector of n elements (NB quads per thread in flight);
+// returns whether any lo half is non-zero (block-uniform).
+template <int F, int NB = 4>
+__device__ __forceinline__ bool stage_fmt(const uint32_t* __restrict__ src, int n, uint32_t* lds) {
+    const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
+    const float* ps = reinterpret_cast<const float*>(src) + n;
+    float* sums = reinterpret_cast<float*>(lds + n);
+    const int nq = n / 4, ng = n / 8;
+    const int lo_q = Act<F>::kPair ? n / 8 : nq;   // first quad of the lo plane
+    int any_lo = 0;
+    // groups are half as many as quads: iteration q0 covers groups from q0 / 2
+    for (int q0 = 0; q0 < nq; q0 += NB * blockDim.x) {
+        u32x4 v[NB];
+        float pv[NB / 2];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    // INT4: (x[j], x[j+4]) to match the nibble decoder; else adjacent
-                    const int e0 = Act<F>::kInterleave ? j : 2 * j;
-                    const int e1 = Act<F>::kInterleave ? j + 4 : 2 * j + 1;
-                    hw[j] = h[e0] | (h[e1] << 16);
-                    lw[j] = l[e0] | (l[e1] << 16);
-                }
-                reinterpret_cast<u32x4*>(lds)[g] = u32x4{hw[0], hw[1], hw[2], hw[3]};
-                reinterpret_cast<u32x4*>(lds + n / 2)[g] = u32x4{lw[0], lw[1], lw[2], lw[3]};
-            } else {
-                reinterpret_cast<float4*>(lds)[2 * g] = p;
-                reinterpret_cast<float4*>(lds)[2 * g + 1] = q;
+        for (int b = 0; b < NB; ++b) {
+            const int q = q0 + b * blockDim.x + threadIdx.x;
+            if (q < nq) v[b] = s4[q];
+        }
 #pragma unroll
-                for (int i = 0; i < 8; ++i) part += v[i];
+        for (int c = 0; c < NB / 2; ++c) {
+            const int g = q0 / 2 + c * blockDim.x + threadIdx.x;
+            pv[c] = g < ng ? ps[g] : 0.0f;
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const int q = q0 + b * blockDim.x + threadIdx.x;
+            if (q < nq) {
+                reinterpret_cast<u32x4*>(lds)[q] = v[b];
+                if (q >= lo_q) any_lo |= int((v[b].x | v[b].y | v[b].z | v[b].w) != 0);
             }
         }
-        // chunk sum over the TPC threads of a chunk (aligned lane groups)
-        if constexpr (TPC >= 2) part += dpp_f<kDppXor1>(part);
-        if constexpr (TPC >= 4) part += dpp_f<kDppXor2>(part);
-        if (g < n / 8 && (g % TPC) == 0) sums[g / TPC] = part;
+#pragma unroll
+        for (int c = 0; c < NB / 2; ++c) {
+            const int g = q0 / 2 + c * blockDim.x + threadIdx.x;
+            chunk_sum_out<F>(pv[c], g < ng ? g : -1, sums);
+        }
     }
     if constexpr (Act<F>::kPair) any_lo = __syncthreads_or(any_lo);
     else __syncthreads();
@@ -204,10 +247,12 @@ __host__ __device__ constexpr int act_words(int n) {
 
 // ------------------------------------------------------------- chunk math
 
+// One weight chunk in flight: the raw loads only.  Scales are decoded where
+// the chunk is consumed, so that issuing a load never waits for another.
 struct Pre {
     u32x4 raw;
-    float s;      // INT4: group scale, MXFP4: e8m0 scale, INT8: row scale
-    int z;        // INT4: zero point (0xFF = signed s4)
+    uint32_t sb;   // INT4: bf16/fp16 group-scale bits, MXFP4: e8m0 byte, INT8: fp32 bits
+    uint32_t zb;   // INT4: zero point (0xFF = signed s4)
 };
 
 template <int F>
@@ -215,14 +260,22 @@ __device__ __forceinline__ void prefetch(const WView& w, int64_t row, int c, Pre
     p.raw = load16(w.payload + row * w.row_bytes + int64_t(c) * 16);
     if constexpr (F == GRIM_FMT_INT4 || F == GRIM_FMT_INT4_F16) {
         const int64_t si = row * w.row_scales + ((c * 32) >> w.gshift);
-        const uint16_t sraw = static_cast<const uint16_t*>(w.scales)[si];
-        p.s = F == GRIM_FMT_INT4 ? bf16_to_f32(sraw) : f16_to_f32(sraw);
-        p.z = w.zeros ? int(w.zeros[si]) : w.default_zero;
+        p.sb = static_cast<const uint16_t*>(w.scales)[si];
+        p.zb = w.zeros ? uint32_t(w.zeros[si]) : uint32_t(w.default_zero);
     } else if constexpr (F == GRIM_FMT_MXFP4) {
-        p.s = e8m0_to_f32(static_cast<const uint8_t*>(w.scales)[row * w.row_scales + c]);
+        p.sb = static_cast<const uint8_t*>(w.scales)[row * w.row_scales + c];
     } else if constexpr (F == GRIM_FMT_INT8) {
-        p.s = static_cast<const float*>(w.scales)[row];
+        p.sb = f_bits(static_cast<const float*>(w.scales)[row]);
     }
+}
+
+template <int F>
+__device__ __forceinline__ float pre_scale(const Pre& p) {
+    if constexpr (F == GRIM_FMT_INT4) return bf16_to_f32(uint16_t(p.sb));
+    else if constexpr (F == GRIM_FMT_INT4_F16) return f16_to_f32(uint16_t(p.sb));
+    else if constexpr (F == GRIM_FMT_MXFP4) return e8m0_to_f32(uint8_t(p.sb));
+    else if constexpr (F == GRIM_FMT_INT8) return bits_f(p.sb);
+    else return 1.0f;
 }
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
@@ -245,17 +298,18 @@ struct XChunk {
 template <int F, bool LO>
 __device__ __forceinline__ void load_x(const uint32_t* act, int n, int c, XChunk<F, LO>& x) {
     constexpr int W = XChunk<F, LO>::W;
-    const u32x4* h = reinterpret_cast<const u32x4*>(act + c * W);
+    const int nch = n / Chunk<F>::CH;
+    const u32x4* h = reinterpret_cast<const u32x4*>(act) + c;
 #pragma unroll
     for (int i = 0; i < W / 4; ++i) {
-        const u32x4 v = h[i];
+        const u32x4 v = h[i * nch];
         x.hi[4 * i] = v.x; x.hi[4 * i + 1] = v.y; x.hi[4 * i + 2] = v.z; x.hi[4 * i + 3] = v.w;
     }
     if constexpr (LO) {
-        const u32x4* l = reinterpret_cast<const u32x4*>(act + n / 2 + c * W);
+        const u32x4* l = reinterpret_cast<const u32x4*>(act + n / 2) + c;
 #pragma unroll
         for (int i = 0; i < W / 4; ++i) {
-            const u32x4 v = l[i];
+            const u32x4 v = l[i * nch];
             x.lo[4 * i] = v.x; x.lo[4 * i + 1] = v.y; x.lo[4 * i + 2] = v.z; x.lo[4 * i + 3] = v.w;
         }
     }
@@ -268,7 +322,7 @@ __device__ __forceinline__ float dot_chunk(const Pre& p, const XChunk<F, LO>& x)
     const uint32_t w[4] = {p.raw.x, p.raw.y, p.raw.z, p.raw.w};
     float a0 = 0.0f, a1 = 0.0f;
     if constexpr (F == GRIM_FMT_INT4 || F == GRIM_FMT_INT4_F16) {
-        int z = p.z;
+        int z = int(p.zb);
         uint32_t xm = 0;
         if (z == 0xFF) { xm = 0x88888888u; z = 8; }   // signed s4 -> offset binary
 #pragma unroll
@@ -281,7 +335,7 @@ __device__ __forceinline__ float dot_chunk(const Pre& p, const XChunk<F, LO>& x)
                 if constexpr (LO) a1 = dot2(pr, x.lo[4 * d + j], a1);
             }
         }
-        return p.s * ((a0 + a1) - (128.0f + float(z)) * x.xs);
+        return pre_scale<F>(p) * ((a0 + a1) - (128.0f + float(z)) * x.xs);
     } else if constexpr (F == GRIM_FMT_MXFP4) {
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
@@ -300,7 +354,7 @@ __device__ __forceinline__ float dot_chunk(const Pre& p, const XChunk<F, LO>& x)
                 if constexpr (LO) a1 = dot2(q[b], x.lo[4 * d + b], a1);
             }
         }
-        return (a0 + a1) * p.s;
+        return (a0 + a1) * pre_scale<F>(p);
     } else if constexpr (F == GRIM_FMT_BF16) {
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
@@ -312,35 +366,22 @@ __device__ __forceinline__ float dot_chunk(const Pre& p, const XChunk<F, LO>& x)
         float xv[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) xv[i] = bits_f(x.hi[i]);
-        return p.s * (Chunk<GRIM_FMT_INT8>::dot(p.raw, xv) - 128.0f * x.xs);
+        return pre_scale<F>(p) * (Chunk<GRIM_FMT_INT8>::dot(p.raw, xv) - 128.0f * x.xs);
     }
 }
 
 // ------------------------------------------------------------------ roles
 
-// Router rows: wave w of item b computes expert e = 4b + w for every token;
-// the last router item to finish runs the top-k and raises routes_ready.
+// Router rows: item b computes expert b's logits for every token
+// (router_row); the last router item to finish runs the top-k and raises
+// routes_ready.
 __device__ __forceinline__ void router_item(const DecodeArgs& a, int b, uint32_t* lds) {
-    const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    const int e = b * kGemvWaves + wave;
-    if (e < a.E) {
-        const float* wr = a.router + int64_t(e) * a.H;
-        for (int t = 0; t < a.M; ++t) {
-            const float* xt = a.x + int64_t(t) * a.H;
-            float acc = 0.0f;
-            for (int k = lane * 4; k < a.H; k += kWave * 4) {
-                const float4 wv = *reinterpret_cast<const float4*>(wr + k);
-                const float4 xv = *reinterpret_cast<const float4*>(xt + k);
-                acc = __builtin_fmaf(wv.x, xv.x, acc);
-                acc = __builtin_fmaf(wv.y, xv.y, acc);
-                acc = __builtin_fmaf(wv.z, xv.z, acc);
-                acc = __builtin_fmaf(wv.w, xv.w, acc);
-            }
-            acc = group_sum<kWave>(acc);
-            if (lane == 0) st_coh(a.logits + int64_t(t) * a.E + e, a.rbias ? acc + a.rbias[e] : acc);
-        }
-    }
+    __shared__ float red[4 * kRouterTok];
+    const int e = b;
+    const float s = router_row(a.router + int64_t(e) * a.H, a.x, a.M, a.H, red);
+    if (int(threadIdx.x) < a.M)
+        st_coh(a.logits + int64_t(threadIdx.x) * a.E + e, a.rbias ? s + a.rbias[e] : s);
     wait_stores();
     __syncthreads();
     __shared__ int last;
@@ -354,9 +395,8 @@ __device__ __forceinline__ void router_item(const DecodeArgs& a, int b, uint32_t
             topk_wave<true>(a.logits + int64_t(t) * a.E, a.E, a.K, a.mode, a.normalize, a.scaling,
                             a.bias16, a.bias32, a.n_group, a.topk_group, a.rex + int64_t(t) * a.K,
                             a.rwt + int64_t(t) * a.K, scratch, scratch + 512);
-        wait_stores();
-        __syncthreads();
-        if (threadIdx.x == 0) st_coh(a.ctr + kCtrRoutesReady, 1);
+        // every router item has counted itself: ready for the next launch
+        if (threadIdx.x == 0) st_coh(a.ctr + kCtrRouterDone, 0);
     }
     __syncthreads();
 }
@@ -411,17 +451,11 @@ __device__ __forceinline__ void gate_up_item(const DecodeArgs& a, int j, uint32_
     const float* xt = a.x + int64_t(t) * H;
     float* ht = a.h + (int64_t(t) * KS + slot) * I;
 
-    bool lo_pass = true, staged = false;
-    if (a.fused) {   // stage x while the router is still running
-        lo_pass = stage_act<F, false>(xt, H, lds);
-        staged = true;
-        wait_flag(a.ctr + kCtrRoutesReady, a.ctr + kCtrTimeout);
-    }
     const bool shr = SH && slot >= K;
     int64_t gbase = 0;
     bool active = true;
     if (!shr) {
-        const int e = ld_coh(a.rex + int64_t(t) * K + slot);
+        const int e = a.rex[int64_t(t) * K + slot];
         if (e < 0 || e >= a.E) active = false;   // route not computed here: h = 0
         gbase = int64_t(e) * 2 * I;
     }
@@ -438,17 +472,35 @@ __device__ __forceinline__ void gate_up_item(const DecodeArgs& a, int j, uint32_
             prefetch<F>(v, gbase + I + i, sub, cur[1][r]);
         }
     }
-    if (!staged) lo_pass = stage_act<F, false>(xt, H, lds);   // overlaps the first loads
+    const bool lo_pass = stage_act<F>(xt, H, lds);   // overlaps the first loads
     if (active) {
         if (lo_pass) gate_up_rows<F, LPR, true>(v, gbase, i0, I, C, sub, lds, H, cur, ga, ua);
         else gate_up_rows<F, LPR, false>(v, gbase, i0, I, C, sub, lds, H, cur, ga, ua);
     }
+    __shared__ float hrow[kGemvWaves * kWave / 8 * RU];   // this item's RB rows (fmt_h)
 #pragma unroll
     for (int r = 0; r < RU; ++r) {
         const float g = group_sum<LPR>(ga[r]);
         const float u = group_sum<LPR>(ua[r]);
         const int i = i0 + r;
-        if (sub == 0 && i < I) st_coh(ht + i, active ? silu(g) * u : 0.0f);
+        const float hv = active ? silu(g) * u : 0.0f;
+        if (a.fmt_h) {
+            if (sub == 0) hrow[(wave * GPW + lane / LPR) * RU + r] = i < I ? hv : 0.0f;
+        } else if (sub == 0 && i < I) {
+            ht[i] = hv;
+        }
+    }
+    if (a.fmt_h) {
+        // the RB rows as RB / 8 formatted groups of the token's h vector
+        __syncthreads();
+        const int n = KS * I;
+        const int i8 = rb * RB + 8 * int(threadIdx.x);
+        if (int(threadIdx.x) < RB / 8 && i8 < I) {
+            float hv[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) hv[k] = hrow[8 * threadIdx.x + k];
+            put_group_fmt<F>(a.hf + int64_t(t) * fmt_words(n), n, (slot * I + i8) / 8, hv);
+        }
     }
     // shared_expert_gate: sigmoid(x . gate_w) (src/moe_kernels.cpp:162-172),
     // by the first item of each token
@@ -456,39 +508,46 @@ __device__ __forceinline__ void gate_up_item(const DecodeArgs& a, int j, uint32_
         float acc = 0.0f;
         for (int c = lane; c < H; c += kWave) acc = __builtin_fmaf(bf16_to_f32(a.gate_w[c]), xt[c], acc);
         acc = group_sum<kWave>(acc);
-        if (lane == 0) st_coh(a.gate + t, det_sigmoid(acc));
-    }
-    if (a.fused) {
-        wait_stores();
-        __syncthreads();
-        if (threadIdx.x == 0)
-            __hip_atomic_fetch_add(a.ctr + kCtrHDone + 32 * (j & 63), 1, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) a.gate[t] = det_sigmoid(acc);
     }
     __syncthreads();
+}
+
+// Weight chunks of one batch of down rows: up to kDnBatch chunks per lane
+// for each of its kPairsDN (slot, row) pairs, all requested at once.
+constexpr int kDnBatch = 3;
+
+template <int F, int LPR>
+__device__ __forceinline__ void down_issue(const DecodeArgs& a, const bool* pvalid,
+                                           const bool* pshared, const int64_t* wrow, int C,
+                                           int c0, Pre (&w)[kDnBatch][kPairsDN]) {
+#pragma unroll
+    for (int b = 0; b < kDnBatch; ++b) {
+        const int c = c0 + b * LPR;
+#pragma unroll
+        for (int q = 0; q < kPairsDN; ++q)
+            if (c < C && pvalid[q]) prefetch<F>(pshared[q] ? a.sdn : a.dn, wrow[q], c, w[b][q]);
+    }
 }
 
 template <int F, int LPR, bool LO>
 __device__ __forceinline__ void down_rows(const DecodeArgs& a, const int* pslot, const bool* pvalid,
                                           const bool* pshared, const int64_t* wrow, int C, int sub,
-                                          const uint32_t* act, int n, Pre (&cur)[kPairsDN],
-                                          float* acc) {
-    for (int c = sub; c < C; c += LPR) {
-        Pre nxt[kPairsDN];
-        const int cn = c + LPR;
+                                          const uint32_t* act, int n,
+                                          Pre (&w)[kDnBatch][kPairsDN], float* acc) {
+    for (int c0 = sub; c0 < C; c0 += kDnBatch * LPR) {
+        if (c0 != sub) down_issue<F, LPR>(a, pvalid, pshared, wrow, C, c0, w);
 #pragma unroll
-        for (int q = 0; q < kPairsDN; ++q)
-            if (cn < C && pvalid[q]) prefetch<F>(pshared[q] ? a.sdn : a.dn, wrow[q], cn, nxt[q]);
+        for (int b = 0; b < kDnBatch; ++b) {
+            const int c = c0 + b * LPR;
+            if (c >= C) break;
 #pragma unroll
-        for (int q = 0; q < kPairsDN; ++q) {
-            if (!pvalid[q]) continue;
-            XChunk<F, LO> x;
-            load_x<F, LO>(act, n, pslot[q] * C + c, x);
-            acc[q] += dot_chunk<F, LO>(cur[q], x);
-        }
-        if (cn < C) {
-#pragma unroll
-            for (int q = 0; q < kPairsDN; ++q) cur[q] = nxt[q];
+            for (int q = 0; q < kPairsDN; ++q) {
+                if (!pvalid[q]) continue;
+                XChunk<F, LO> x;
+                load_x<F, LO>(act, n, pslot[q] * C + c, x);
+                acc[q] += dot_chunk<F, LO>(w[b][q], x);
+            }
         }
     }
 }
@@ -511,8 +570,18 @@ __device__ __forceinline__ void down_item(const DecodeArgs& a, int j, uint32_t* 
     const int npairs = KS * RB;
     const int n = KS * I;
     float* part = reinterpret_cast<float*>(lds + act_words<F>(n));   // [KS][RB]
+    __shared__ float slot_w[32];   // routed weight per slot, 0 = skipped
+    __shared__ int slot_e[32];     // expert per slot, -1 = skipped
 
-    if (a.fused) wait_flag(a.ctr + kCtrRoutesReady, a.ctr + kCtrTimeout);
+    // routes come from an earlier launch: plain loads, one round trip
+    if (int(threadIdx.x) < K) {
+        const int e = a.rex[int64_t(t) * K + threadIdx.x];
+        const float rw = a.rwt[int64_t(t) * K + threadIdx.x];
+        const bool ok = e >= 0 && e < E && rw != 0.0f;
+        slot_w[threadIdx.x] = ok ? rw : 0.0f;
+        slot_e[threadIdx.x] = ok ? e : -1;
+    }
+    __syncthreads();
     int pslot[NP], prow[NP];
     int64_t wrow[NP];
     bool pshared[NP], pvalid[NP];
@@ -526,24 +595,23 @@ __device__ __forceinline__ void down_item(const DecodeArgs& a, int j, uint32_t* 
         pshared[q] = SH && pslot[q] >= K;
         wrow[q] = o;
         if (pvalid[q] && !pshared[q]) {
-            const int e = ld_coh(a.rex + int64_t(t) * K + pslot[q]);
-            const float rw = ld_coh(a.rwt + int64_t(t) * K + pslot[q]);
-            if (e < 0 || e >= E || rw == 0.0f) pvalid[q] = false;
+            const int e = slot_e[pslot[q]];
+            if (e < 0) pvalid[q] = false;
             else wrow[q] = int64_t(e) * H + o;
         }
     }
     float acc[NP];
-    Pre cur[NP];
+    Pre w[kDnBatch][NP];
 #pragma unroll
-    for (int q = 0; q < NP; ++q) {
-        acc[q] = 0.0f;
-        if (sub < C && pvalid[q]) prefetch<F>(pshared[q] ? a.sdn : a.dn, wrow[q], sub, cur[q]);
-    }
+    for (int q = 0; q < NP; ++q) acc[q] = 0.0f;
+    down_issue<F, LPR>(a, pvalid, pshared, wrow, C, sub, w);
     // h[t] into LDS while the first weights are in flight
-    if (a.fused) wait_spread(a.ctr + kCtrHDone, a.NG, a.ctr + kCtrTimeout);
-    const bool lo_pass = stage_act<F, true>(a.h + int64_t(t) * n, n, lds);
-    if (lo_pass) down_rows<F, LPR, true>(a, pslot, pvalid, pshared, wrow, C, sub, lds, n, cur, acc);
-    else down_rows<F, LPR, false>(a, pslot, pvalid, pshared, wrow, C, sub, lds, n, cur, acc);
+    float gate_sh = 1.0f;
+    if (SH && a.gate_in && int(threadIdx.x) < RB) gate_sh = a.gate_in[t];
+    const bool lo_pass = a.fmt_h ? stage_fmt<F>(a.hf + int64_t(t) * fmt_words(n), n, lds)
+                                  : stage_act<F, 4>(a.h + int64_t(t) * n, n, lds);
+    if (lo_pass) down_rows<F, LPR, true>(a, pslot, pvalid, pshared, wrow, C, sub, lds, n, w, acc);
+    else down_rows<F, LPR, false>(a, pslot, pvalid, pshared, wrow, C, sub, lds, n, w, acc);
 #pragma unroll
     for (int q = 0; q < NP; ++q) {
         const float v = group_sum<LPR>(acc[q]);
@@ -556,57 +624,24 @@ __device__ __forceinline__ void down_item(const DecodeArgs& a, int j, uint32_t* 
         if (o >= H) continue;
         float total = 0.0f;
         for (int s = 0; s < K; ++s) {
-            const int e = ld_coh(a.rex + int64_t(t) * K + s);
-            const float rw = ld_coh(a.rwt + int64_t(t) * K + s);
-            if (e < 0 || e >= E || rw == 0.0f) continue;
+            const float rw = slot_w[s];
+            if (rw == 0.0f) continue;
             total = __builtin_fmaf(rw, part[s * RB + r], total);
         }
-        if (SH) total = __builtin_fmaf(a.gate_in ? ld_coh(a.gate_in + t) : 1.0f, part[K * RB + r], total);
+        if (SH) total = __builtin_fmaf(gate_sh, part[K * RB + r], total);
         a.y[int64_t(t) * H + o] = total;
-    }
-    if (a.fused) {
-        // count this item done; whoever sees every down item done zeroes the
-        // counters (idempotent), ready for the next launch
-        __syncthreads();
-        __shared__ int prev_dn;
-        if (threadIdx.x == 0)   // the returned value makes the add complete first
-            prev_dn = __hip_atomic_fetch_add(a.ctr + kCtrDnDone + 32 * (j & 63), 1,
-                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
-        if (threadIdx.x < kWave && prev_dn >= 0) {
-            const int done = spread_sum(a.ctr + kCtrDnDone);
-            if (done == a.ND) {
-                const int lane = threadIdx.x;
-                st_coh(a.ctr + kCtrHDone + 32 * lane, 0);
-                st_coh(a.ctr + kCtrDnDone + 32 * lane, 0);
-                if (lane == 0) {
-                    st_coh(a.ctr + kCtrRouterDone, 0);
-                    st_coh(a.ctr + kCtrRoutesReady, 0);
-                }
-            }
-        }
     }
     __syncthreads();
 }
 
-// Router rows + top-k: the first launch of the decode forward (its
-// registers are kept out of the expert kernel below).
+// Router rows + top-k: the first launch of the decode forward.
 template <int F>
 __global__ __launch_bounds__(kGemvThreads) void moe_router_kernel(DecodeArgs a) {
     extern __shared__ uint32_t lds[];
     router_item(a, blockIdx.x, lds);
 }
 
-// gate_up then down items, one work-group per item.
-template <int F, int LPG, int LPD, bool SH>
-__global__ __launch_bounds__(kGemvThreads) void moe_decode_fused(DecodeArgs a) {
-    extern __shared__ uint32_t lds[];
-    const int it = blockIdx.x;
-    if (it < a.NG) gate_up_item<F, LPG, SH>(a, it, lds);
-    else down_item<F, LPD, SH>(a, it - a.NG, lds);
-}
-
-// Single-role kernels of the standalone launchers (routes and h are inputs).
+// The expert kernels: routes (and, for down, h) come from earlier launches.
 template <int F, int LPG, bool SH>
 __global__ __launch_bounds__(kGemvThreads) void moe_gate_up_kernel(DecodeArgs a) {
     extern __shared__ uint32_t lds[];
@@ -621,27 +656,14 @@ __global__ __launch_bounds__(kGemvThreads) void moe_down_kernel(DecodeArgs a) {
 // ------------------------------------------------------------ launching
 
 template <int F, int LPG, int LPD, bool SH>
-inline hipError_t launch_fused(hipStream_t st, const DecodeArgs& a) {
-    const int items = a.NG + a.ND;
-    DecodeArgs ex = a;
-    ex.NR = 0;
-    const size_t lds = decode_lds_bytes(F, ex);
+inline hipError_t launch_t(hipStream_t st, const DecodeArgs& a) {
     if (a.NR) {
         const size_t rl = size_t(kGemvWaves) * (512 + 64) * sizeof(float);
         hipLaunchKernelGGL(moe_router_kernel<F>, dim3(a.NR), dim3(kGemvThreads), rl, st, a);
     }
-    if (items <= 0) return hipGetLastError();
-    hipLaunchKernelGGL((moe_decode_fused<F, LPG, LPD, SH>), dim3(items), dim3(kGemvThreads), lds, st,
-                       a);
-    return hipGetLastError();
-}
-
-template <int F, int LPG, int LPD, bool SH>
-inline hipError_t launch_t(hipStream_t st, const DecodeArgs& a) {
-    if (a.NR + a.NG + a.ND <= 0) return hipSuccess;
-    if (a.fused) return launch_fused<F, LPG, LPD, SH>(st, a);
-    if (a.NR) return hipErrorInvalidValue;   // the router role runs fused only
-    const size_t lds = decode_lds_bytes(F, a);
+    DecodeArgs ex = a;
+    ex.NR = 0;
+    const size_t lds = decode_lds_bytes(F, ex);
     if (a.NG)
         hipLaunchKernelGGL((moe_gate_up_kernel<F, LPG, SH>), dim3(a.NG), dim3(kGemvThreads), lds, st,
                            a);

@@ -33,43 +33,19 @@ hipError_t topk_launch(hipStream_t st, const TopkArgs& a) {
 
 // ---------------------------------------------------------- router logits
 
-// Small T: one wave per expert row, fp32 row chunks streamed with 16-byte
-// loads, up to kRT tokens per block; x read through the cache.
-constexpr int kRT = 8;
+// Small T: one work-group per (expert row, kRouterTok tokens), the row
+// streamed once with 16-byte loads (router_row); x read through the cache.
 __global__ __launch_bounds__(256) void router_gemv(const float* __restrict__ W,
                                                    const float* __restrict__ x,
                                                    const float* __restrict__ bias,
                                                    float* __restrict__ logits, int T, int E,
                                                    int H) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int e = blockIdx.x * 4 + threadIdx.x / kWave;
-    const int t0 = blockIdx.y * kRT;
-    if (e >= E) return;
-    const int nt = T - t0 < kRT ? T - t0 : kRT;
-    float acc[kRT];
-#pragma unroll
-    for (int i = 0; i < kRT; ++i) acc[i] = 0.0f;
-    const float* wr = W + int64_t(e) * H;
-    for (int k = lane * 4; k < H; k += kWave * 4) {
-        const float4 wv = *reinterpret_cast<const float4*>(wr + k);
-#pragma unroll
-        for (int i = 0; i < kRT; ++i) {
-            if (i < nt) {
-                const float4 xv = *reinterpret_cast<const float4*>(x + int64_t(t0 + i) * H + k);
-                acc[i] = __builtin_fmaf(wv.x, xv.x, acc[i]);
-                acc[i] = __builtin_fmaf(wv.y, xv.y, acc[i]);
-                acc[i] = __builtin_fmaf(wv.z, xv.z, acc[i]);
-                acc[i] = __builtin_fmaf(wv.w, xv.w, acc[i]);
-            }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < kRT; ++i) {
-        if (i < nt) {
-            const float s = group_sum<kWave>(acc[i]);
-            if (lane == 0) logits[int64_t(t0 + i) * E + e] = bias ? s + bias[e] : s;
-        }
-    }
+    __shared__ float red[4 * kRouterTok];
+    const int e = blockIdx.x;
+    const int t0 = blockIdx.y * kRouterTok;
+    const int nt = T - t0 < kRouterTok ? T - t0 : kRouterTok;
+    const float s = router_row(W + int64_t(e) * H, x + int64_t(t0) * H, nt, H, red);
+    if (int(threadIdx.x) < nt) logits[int64_t(t0 + threadIdx.x) * E + e] = bias ? s + bias[e] : s;
 }
 
 // Large T: LDS-tiled fp32 GEMM, 64 tokens x 64 experts per block, each
@@ -116,7 +92,7 @@ __global__ __launch_bounds__(256) void router_gemm(const float* __restrict__ W,
 hipError_t router_logits_launch(hipStream_t st, const float* W, const float* x,
                                 const float* bias, float* logits, int T, int E, int H) {
     if (T <= 32 && H % 4 == 0) {
-        dim3 grid((E + 3) / 4, (T + kRT - 1) / kRT);
+        dim3 grid(E, (T + kRouterTok - 1) / kRouterTok);
         hipLaunchKernelGGL(router_gemv, grid, dim3(256), 0, st, W, x, bias, logits, T, E, H);
     } else {
         dim3 grid((E + 63) / 64, (T + 63) / 64);

@@ -2,10 +2,10 @@
 // fused decode kernel.
 //
 // One wavefront per token with every score in VGPRs (lane l owns experts
-// [l*V, l*V+V), V = ceil(E/64) <= 8).  Each round packs (order-preserving
-// score bits, ~expert) into one 64-bit key, so one wave max gives the
-// largest score and, among equal scores, the lowest expert index -- the tie
-// rule of src/ops.cpp:1125-1131.  The weights are then formed in pick order
+// [l*V, l*V+V), V = ceil(E/64) <= 8).  Each round takes the wave max of
+// order-preserving 32-bit score keys, then the lowest expert index holding
+// it (lowest lane by ballot, then its lowest slot) -- the tie rule of
+// src/ops.cpp:1125-1131.  The weights are then formed in pick order
 // with the reference kernels' operations (src/ops.cpp:1133-1147,
 // :2126-2135), using det_expf so that the oracle reproduces them bit for
 // bit.
@@ -16,37 +16,72 @@
 namespace grim {
 
 constexpr int kMaxV = 8;          // E <= 512
+constexpr int kRouterTok = 8;     // tokens per router_row call
 
-__device__ __forceinline__ uint64_t score_key(float v, int e) {
-    if (v != v) return (uint64_t(1) << 32) | uint32_t(~e);   // NaN ranks below everything
-    uint32_t u = f_bits(v + 0.0f);                           // -0 -> +0
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return (uint64_t(u) << 32) | uint32_t(~e);
-}
-
-template <int CTRL>
-__device__ __forceinline__ uint64_t dpp64(uint64_t v) {
-    const uint32_t lo = dpp_u<CTRL>(uint32_t(v)), hi = dpp_u<CTRL>(uint32_t(v >> 32));
-    return (uint64_t(hi) << 32) | lo;
-}
-__device__ __forceinline__ uint64_t max64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-
-// Wave-wide max of a 64-bit key, uniform result: DPP inside each 16-lane
-// row, then the four row results read into scalars.
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
-    k = max64(k, dpp64<kDppXor1>(k));
-    k = max64(k, dpp64<kDppXor2>(k));
-    k = max64(k, dpp64<kDppHalfMirror>(k));
-    k = max64(k, dpp64<kDppMirror>(k));
-    const uint32_t lo = uint32_t(k), hi = uint32_t(k >> 32);
-    uint64_t r = 0;
+// Router logits of one expert row for nt <= kRouterTok tokens by one
+// 256-thread work-group: thread i multiplies elements [4i + 1024m, +4), lanes
+// reduce by DPP, the four waves add in wave order through red (LDS, 32
+// floats).  Thread t < nt returns token t's dot product.  Shared by the
+// router kernel and the decode kernel's router role, so both give the same
+// bits.
+__device__ __forceinline__ float router_row(const float* __restrict__ wr,
+                                            const float* __restrict__ x, int nt, int H,
+                                            float* red) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    float acc[kRouterTok];
 #pragma unroll
-    for (int row = 0; row < 4; ++row) {
-        const uint64_t v = (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(hi), row * 16))) << 32) |
-                           uint32_t(__builtin_amdgcn_readlane(int(lo), row * 16));
-        r = max64(r, v);
+    for (int i = 0; i < kRouterTok; ++i) acc[i] = 0.0f;
+#pragma unroll 2
+    for (int k = threadIdx.x * 4; k < H; k += 1024) {
+        const float4 wv = *reinterpret_cast<const float4*>(wr + k);
+#pragma unroll
+        for (int i = 0; i < kRouterTok; ++i) {
+            if (i < nt) {
+                const float4 xv = *reinterpret_cast<const float4*>(x + int64_t(i) * H + k);
+                acc[i] = __builtin_fmaf(wv.x, xv.x, acc[i]);
+                acc[i] = __builtin_fmaf(wv.y, xv.y, acc[i]);
+                acc[i] = __builtin_fmaf(wv.z, xv.z, acc[i]);
+                acc[i] = __builtin_fmaf(wv.w, xv.w, acc[i]);
+            }
+        }
     }
+#pragma unroll
+    for (int i = 0; i < kRouterTok; ++i) {
+        if (i < nt) {
+            const float v = group_sum<kWave>(acc[i]);
+            if (lane == 0) red[wave * kRouterTok + i] = v;
+        }
+    }
+    __syncthreads();
+    float r = 0.0f;
+    const int t = threadIdx.x;
+    if (t < nt)
+        r = (red[t] + red[kRouterTok + t]) + (red[2 * kRouterTok + t] + red[3 * kRouterTok + t]);
+    __syncthreads();
     return r;
+}
+
+// Order-preserving 32-bit key of a score; 0 marks an empty or taken slot,
+// NaN (1) ranks below every number.
+__device__ __forceinline__ uint32_t score_key(float v) {
+    if (v != v) return 1u;
+    const uint32_t u = f_bits(v + 0.0f);                     // -0 -> +0
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);       // -inf -> 0x007fffff
+}
+
+// Wave-wide max, uniform result: DPP inside each 16-lane row, then the four
+// row results read into scalars.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t k) {
+    k = max(k, dpp_u<kDppXor1>(k));
+    k = max(k, dpp_u<kDppXor2>(k));
+    k = max(k, dpp_u<kDppHalfMirror>(k));
+    k = max(k, dpp_u<kDppMirror>(k));
+    const uint32_t r0 = __builtin_amdgcn_readlane(int(k), 0);
+    const uint32_t r1 = __builtin_amdgcn_readlane(int(k), 16);
+    const uint32_t r2 = __builtin_amdgcn_readlane(int(k), 32);
+    const uint32_t r3 = __builtin_amdgcn_readlane(int(k), 48);
+    return max(max(r0, r1), max(r2, r3));
 }
 
 __device__ __forceinline__ float lane_f(float v, int lane) {
@@ -70,7 +105,7 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ row, int E, 
     const int lane = threadIdx.x & (kWave - 1);
     const int V = (E + kWave - 1) / kWave;
 
-    uint64_t key[kMaxV];
+    uint32_t key[kMaxV];
     float wsrc[kMaxV];
 #pragma unroll
     for (int j = 0; j < kMaxV; ++j) {
@@ -91,7 +126,7 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ row, int E, 
                 sel = sc + b;
                 wsrc[j] = sc;
             }
-            key[j] = score_key(sel, e);
+            key[j] = score_key(sel);
             if (mode == 3) gsel_w[e] = sel;
         }
     }
@@ -130,22 +165,31 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ row, int E, 
         }
     }
 
+    // K rounds of: wave max of the keys, then the lowest expert holding it
+    // (experts are lane-major, so the lowest lane, then its lowest slot)
     int my_pick = -1;
     float my_val = 0.0f;
     for (int s = 0; s < K; ++s) {
-        uint64_t best = 0;
+        uint32_t best = 0;
+#pragma unroll
+        for (int j = 0; j < kMaxV; ++j) best = max(best, key[j]);
+        const uint32_t win = wave_max_u32(best);
+        if (win == 0) break;                      // fewer than K experts left
+        int jl = kMaxV;
         float bval = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kMaxV; ++j)
-            if (key[j] > best) { best = key[j]; bval = wsrc[j]; }
-        const uint64_t win = wave_max_u64(best);
-        const int e = win ? int(~uint32_t(win)) : -1;
-        const int owner = e >= 0 ? e / V : 0;
+        for (int j = kMaxV - 1; j >= 0; --j)
+            if (key[j] == win) { jl = j; bval = wsrc[j]; }
+        const uint64_t bal = __ballot(jl < kMaxV);
+        const int owner = int(__builtin_ctzll(bal));
+        const int jw = __builtin_amdgcn_readlane(jl, owner);
         const float val = lane_f(bval, owner);
+        if (lane == owner) {
 #pragma unroll
-        for (int j = 0; j < kMaxV; ++j)
-            if (key[j] == win) key[j] = 0;
-        if (lane == s) { my_pick = e; my_val = val; }
+            for (int j = 0; j < kMaxV; ++j)
+                if (j == jw) key[j] = 0;
+        }
+        if (lane == s) { my_pick = owner * V + jw; my_val = val; }
     }
 
     // weights, serially in pick order through scalar reads (the reference

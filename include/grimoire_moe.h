@@ -340,7 +340,8 @@ size_t grimoire_moe_forward_workspace_bytes(const grim_moe_layer* L, int tokens)
  * shared expert weight 1, as src/moe_ref.cpp:100-104).  Routing is written
  * to out_expert/out_weight [T][K] when not NULL.  regime: 0 = choose
  * (slot GEMV for T*K <= 64, grouped MFMA GEMM otherwise), 1 = GEMV,
- * 2 = grouped GEMM. */
+ * 2 = grouped GEMM, 3 = GEMV with one launch per stage (no on-device
+ * hand-off between gate_up and down). */
 int grimoire_moe_forward(void* stream, const grim_moe_layer* L, const grim_route_params* rp,
                          const uint16_t* shared_gate_w, const float* x, float* y, int tokens,
                          int32_t* out_expert, float* out_weight, int regime, void* workspace,
