@@ -22,9 +22,6 @@ ROUTE_SOFTMAX = 0
 ROUTE_SIGMOID = 1
 ROUTE_GROUP = 2
 
-# Counters of the decode path: the first int32 words of a
-# grimoire_moe_forward workspace, all zero between calls.
-DECODE_COUNTER_WORDS = 32
 
 ERR_FORMAT, ERR_SHAPE, ERR_ARG, ERR_WORKSPACE = -1, -2, -3, -4
 

@@ -51,7 +51,6 @@ bool use_gemv(const grim_moe_layer* L, int T, int regime) {
 }
 
 struct Plan {
-    int32_t* ctr;   // decode router counter (zero at rest)
     float* logits;
     int32_t* rex;
     float* rwt;
@@ -73,7 +72,6 @@ size_t carve(const grim_moe_layer* L, int T, bool gemv, char* base, Plan& p) {
     const int64_t R = int64_t(T) * K;
     const bool sh = L->has_shared;
     Carve cv{base};
-    p.ctr = cv.take<int32_t>(kDecodeCounterWords);
     p.logits = cv.take<float>(size_t(T) * E);
     p.rex = cv.take<int32_t>(R);
     p.rwt = cv.take<float>(R);
@@ -169,8 +167,8 @@ extern "C" int grimoire_moe_forward(void* stream, const grim_moe_layer* L,
     const bool sh = L->has_shared;
 
     if (gemv && regime != 3 && tokens <= kDecodeMaxTokens) {
-        // three launches: router GEMV + top-k (last router item), gate_up
-        // (h written in the staged layout), down
+        // three launches: router GEMV, gate_up (each item runs its token's
+        // top-k; h written in the staged layout), down
         if (sh && (L->shared_gate_up.fmt != L->gate_up.fmt || L->shared_down.fmt != L->down.fmt))
             return ferr(GRIM_ERR_FORMAT, "shared expert format must match routed experts");
         DecodeArgs a{};
@@ -204,7 +202,7 @@ extern "C" int grimoire_moe_forward(void* stream, const grim_moe_layer* L,
         a.E = E;
         a.M = tokens;
         a.fmt_h = 1;
-        a.ctr = p.ctr;
+        a.route_topk = 1;
         if (L->gate_up.fmt != L->down.fmt) {
             // two formats: the roles need one kernel instantiation each
             return ferr(GRIM_ERR_FORMAT, "decode needs gate_up and down in one format");

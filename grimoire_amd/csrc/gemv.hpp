@@ -6,9 +6,8 @@
 namespace grim {
 
 // Arguments of the decode kernels.  Work items: NR router items (fp32
-// router GEMV, then top-k by the last of them), NG gate_up items (token,
-// slot, row block), ND down items (token, row block); each role is one
-// kernel launch, in that order.
+// router GEMV), NG gate_up items (token, slot, row block), ND down items
+// (token, row block); each role is one kernel launch, in that order.
 struct DecodeArgs {
     WView gu, sgu, dn, sdn;
     bool shared;
@@ -36,7 +35,7 @@ struct DecodeArgs {
     int lpr_gu, lpr_dn, gu_rb, dn_rb;
     int NR, NG, ND;
     int fmt_h;                // gate_up writes hf, down stages hf (else plain h)
-    int32_t* ctr;             // router item counter (kDecodeCounterWords, zero at rest)
+    int route_topk;           // gate_up items compute the top-k from logits (and store rex/rwt)
 };
 
 // Words per token of the formatted h (n = KS * I elements):
@@ -45,8 +44,6 @@ __host__ __device__ constexpr int fmt_words(int n) { return (n + n / 8 + 3) & ~3
 
 constexpr int kRoleRouter = 1, kRoleGateUp = 2, kRoleDown = 4;
 
-// int32 words of the decode counters (zero at rest): the router item count.
-constexpr int kDecodeCounterWords = 32;
 
 void decode_plan(int fmt, DecodeArgs& a, int roles);
 size_t decode_lds_bytes(int fmt, const DecodeArgs& a);

@@ -1,12 +1,13 @@
 // gemv_impl.hpp -- the decode / batched-decode MoE kernel (slot form).
 //
 // Work items take three roles, one kernel each: router rows (fp32 router
-// GEMV; the last router item to finish also runs the top-k), gate_up rows
-// (token, slot, row block) and down rows (token, row block).  The decode
-// forward runs the three kernels back to back on one stream; with `fmt_h`
-// the gate_up kernel writes h already in the LDS layout the down kernel
-// stages (formatted once, copied by every down work-group), else h is
-// plain fp32 as the standalone launchers expose it.
+// GEMV), gate_up rows (token, slot, row block) and down rows (token, row
+// block).  The decode forward runs the three kernels back to back on one
+// stream.  With `route_topk` every gate_up item runs its token's top-k from
+// the logits (one wave, a few hundred cycles) instead of reading routes
+// written by an earlier launch; with `fmt_h` it writes h already in the LDS
+// layout the down kernel stages (formatted once, copied by every down
+// work-group).  The standalone launchers read routes and keep plain fp32 h.
 //
 // Arithmetic: weights stream as 16-byte chunks per lane with their scales,
 // all loads of an item issued before the activations are touched.  INT4,
@@ -35,23 +36,6 @@ constexpr int kPairsDN = 2;       // (slot, row) pairs per down lane group
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 // ------------------------------------------------------------ coherent I/O
-
-__device__ __forceinline__ float ld_coh(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int ld_coh(const int* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_coh(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_coh(int* p, int v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-// counters (int32 offsets inside ctr[], zero at rest)
-constexpr int kCtrRouterDone = 0;   // router items done; the last one resets it
 
 // ------------------------------------------------------- activation staging
 //
@@ -372,33 +356,14 @@ __device__ __forceinline__ float dot_chunk(const Pre& p, const XChunk<F, LO>& x)
 
 // ------------------------------------------------------------------ roles
 
-// Router rows: item b computes expert b's logits for every token
-// (router_row); the last router item to finish runs the top-k and raises
-// routes_ready.
-__device__ __forceinline__ void router_item(const DecodeArgs& a, int b, uint32_t* lds) {
-    const int wave = threadIdx.x / kWave;
+// Router rows: item b computes expert b's logits (plus the softmax router
+// bias) for every token (router_row).
+__device__ __forceinline__ void router_item(const DecodeArgs& a, int b) {
     __shared__ float red[4 * kRouterTok];
     const int e = b;
     const float s = router_row(a.router + int64_t(e) * a.H, a.x, a.M, a.H, red);
     if (int(threadIdx.x) < a.M)
-        st_coh(a.logits + int64_t(threadIdx.x) * a.E + e, a.rbias ? s + a.rbias[e] : s);
-    wait_stores();
-    __syncthreads();
-    __shared__ int last;
-    if (threadIdx.x == 0)
-        last = __hip_atomic_fetch_add(a.ctr + kCtrRouterDone, 1, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT) == a.NR - 1;
-    __syncthreads();
-    if (last) {
-        float* scratch = reinterpret_cast<float*>(lds) + wave * (512 + 64);
-        for (int t = wave; t < a.M; t += kGemvWaves)
-            topk_wave<true>(a.logits + int64_t(t) * a.E, a.E, a.K, a.mode, a.normalize, a.scaling,
-                            a.bias16, a.bias32, a.n_group, a.topk_group, a.rex + int64_t(t) * a.K,
-                            a.rwt + int64_t(t) * a.K, scratch, scratch + 512);
-        // every router item has counted itself: ready for the next launch
-        if (threadIdx.x == 0) st_coh(a.ctr + kCtrRouterDone, 0);
-    }
-    __syncthreads();
+        a.logits[int64_t(threadIdx.x) * a.E + e] = a.rbias ? s + a.rbias[e] : s;
 }
 
 // gate_up rows of one (token, slot, row block): RU (gate, up) row pairs per
@@ -454,7 +419,26 @@ __device__ __forceinline__ void gate_up_item(const DecodeArgs& a, int j, uint32_
     const bool shr = SH && slot >= K;
     int64_t gbase = 0;
     bool active = true;
-    if (!shr) {
+    if (a.route_topk) {
+        // the token's top-k from the router logits of the previous launch,
+        // by wave 0; the first item of the token also stores the routes
+        __shared__ int sel_e[16];
+        __shared__ float sel_w[16];
+        __shared__ float tk_scratch[512 + 64];
+        if (wave == 0 && !shr)
+            topk_wave(a.logits + int64_t(t) * a.E, a.E, K, a.mode, a.normalize, a.scaling, a.bias16,
+                      a.bias32, a.n_group, a.topk_group, sel_e, sel_w, tk_scratch, tk_scratch + 512);
+        __syncthreads();
+        if (slot == 0 && rb == 0 && int(threadIdx.x) < K) {
+            a.rex[int64_t(t) * K + threadIdx.x] = sel_e[threadIdx.x];
+            a.rwt[int64_t(t) * K + threadIdx.x] = sel_w[threadIdx.x];
+        }
+        if (!shr) {
+            const int e = sel_e[slot];
+            if (e < 0 || e >= a.E) active = false;
+            gbase = int64_t(e) * 2 * I;
+        }
+    } else if (!shr) {
         const int e = a.rex[int64_t(t) * K + slot];
         if (e < 0 || e >= a.E) active = false;   // route not computed here: h = 0
         gbase = int64_t(e) * 2 * I;
@@ -634,11 +618,10 @@ __device__ __forceinline__ void down_item(const DecodeArgs& a, int j, uint32_t* 
     __syncthreads();
 }
 
-// Router rows + top-k: the first launch of the decode forward.
+// Router rows: the first launch of the decode forward.
 template <int F>
 __global__ __launch_bounds__(kGemvThreads) void moe_router_kernel(DecodeArgs a) {
-    extern __shared__ uint32_t lds[];
-    router_item(a, blockIdx.x, lds);
+    router_item(a, blockIdx.x);
 }
 
 // The expert kernels: routes (and, for down, h) come from earlier launches.
@@ -657,18 +640,18 @@ __global__ __launch_bounds__(kGemvThreads) void moe_down_kernel(DecodeArgs a) {
 
 template <int F, int LPG, int LPD, bool SH>
 inline hipError_t launch_t(hipStream_t st, const DecodeArgs& a) {
-    if (a.NR) {
-        const size_t rl = size_t(kGemvWaves) * (512 + 64) * sizeof(float);
-        hipLaunchKernelGGL(moe_router_kernel<F>, dim3(a.NR), dim3(kGemvThreads), rl, st, a);
-    }
-    DecodeArgs ex = a;
-    ex.NR = 0;
-    const size_t lds = decode_lds_bytes(F, ex);
+    if (a.NR) hipLaunchKernelGGL(moe_router_kernel<F>, dim3(a.NR), dim3(kGemvThreads), 0, st, a);
+    DecodeArgs gu = a, dn = a;   // LDS of each kernel from its own role
+    gu.NR = 0;
+    gu.ND = 0;
+    dn.NR = 0;
+    dn.NG = 0;
     if (a.NG)
-        hipLaunchKernelGGL((moe_gate_up_kernel<F, LPG, SH>), dim3(a.NG), dim3(kGemvThreads), lds, st,
-                           a);
+        hipLaunchKernelGGL((moe_gate_up_kernel<F, LPG, SH>), dim3(a.NG), dim3(kGemvThreads),
+                           decode_lds_bytes(F, gu), st, a);
     if (a.ND)
-        hipLaunchKernelGGL((moe_down_kernel<F, LPD, SH>), dim3(a.ND), dim3(kGemvThreads), lds, st, a);
+        hipLaunchKernelGGL((moe_down_kernel<F, LPD, SH>), dim3(a.ND), dim3(kGemvThreads),
+                           decode_lds_bytes(F, dn), st, a);
     return hipGetLastError();
 }
 

@@ -159,8 +159,7 @@ class MoeForward:
         self.route = route
         self.regime = regime
         nbytes = int(lib().grimoire_moe_forward_workspace_bytes(self.struct, max_tokens))
-        # zero-filled once: the fused decode launch keeps its counters at zero
-        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=L.router.device)
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=L.router.device)
         self.max_tokens = max_tokens
 
     def __call__(self, x, y, out_expert=None, out_weight=None, stream=None):

@@ -330,10 +330,8 @@ typedef struct grim_route_params {
                                   selection bias; or NULL */
 } grim_route_params;
 
-/* Workspace bytes for grimoire_moe_forward at `tokens`.  The workspace must
- * be zero-filled before its first use (the single-launch decode path keeps
- * hand-off counters in it and leaves them at zero after every call); calls
- * that share one workspace must not overlap. */
+/* Workspace bytes for grimoire_moe_forward at `tokens` (no initial contents
+ * required); calls that share one workspace must not overlap. */
 size_t grimoire_moe_forward_workspace_bytes(const grim_moe_layer* L, int tokens);
 
 /* y fp32 [T][H] = MoE(x fp32 [T][H]).  shared_gate_w bf16 [H] (may be NULL:

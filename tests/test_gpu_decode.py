@@ -1,7 +1,6 @@
-"""The decode forward (router kernel with device-side top-k, gate_up kernel
+"""The decode forward (router kernel, gate_up kernel running the top-k and
 writing h in the staged layout, down kernel): parity with the oracle for
-every routing mode and the shared expert, repeated calls (the router
-counter must return to zero), and HIP-graph replays checked one by one."""
+every routing mode and the shared expert, repeated calls on one workspace, and HIP-graph replays checked one by one."""
 import pytest
 import torch
 
@@ -11,14 +10,6 @@ from tests.helpers import assert_close
 from tests.test_gpu_forward import _check_routing, _oracle_y
 
 pytestmark = pytest.mark.gpu
-
-CTR_WORDS = _abi.DECODE_COUNTER_WORDS
-
-
-def _check_counters(fwd):
-    ctr = fwd.workspace[: 4 * CTR_WORDS].view(torch.int32).cpu()
-    nz = torch.nonzero(ctr).flatten().tolist()
-    assert not nz, f"counters not back at zero: {[(i, int(ctr[i])) for i in nz[:8]]}"
 
 CASES = {
     "c2": configs.CONFIGS["c2"],
@@ -53,7 +44,6 @@ def test_decode_parity(gpu, name):
         fwd(xg, y, oe, ow)
         torch.cuda.synchronize()
         outs.append((y.cpu().clone(), oe.cpu().clone(), ow.cpu().clone()))
-    _check_counters(fwd)
     for y2, e2, w2 in outs[1:]:
         assert torch.equal(y2, outs[0][0]) and torch.equal(e2, outs[0][1]) and torch.equal(w2, outs[0][2])
     yv, oev, owv = outs[0]
@@ -92,4 +82,3 @@ def test_decode_graph_replays(gpu):
                 g.replay()
             torch.cuda.synchronize()
             assert torch.equal(y.cpu(), eager[i]), f"replay {rep} input {i}"
-    _check_counters(fwd)
