@@ -398,7 +398,7 @@ __device__ __forceinline__ void gate_up_rows(const WView& v, int64_t gbase, int 
     }
 }
 
-template <int F, int LPR, bool SH>
+template <int F, int LPR, bool SH, bool RT>
 __device__ __forceinline__ void gate_up_item(const DecodeArgs& a, int j, uint32_t* lds) {
     constexpr int GPW = kWave / LPR;
     constexpr int RU = kRuGU;
@@ -419,7 +419,7 @@ __device__ __forceinline__ void gate_up_item(const DecodeArgs& a, int j, uint32_
     const bool shr = SH && slot >= K;
     int64_t gbase = 0;
     bool active = true;
-    if (a.route_topk) {
+    if constexpr (RT) {
         // the token's top-k from the router logits of the previous launch,
         // by wave 0; the first item of the token also stores the routes
         __shared__ int sel_e[16];
@@ -624,11 +624,13 @@ __global__ __launch_bounds__(kGemvThreads) void moe_router_kernel(DecodeArgs a) 
     router_item(a, blockIdx.x);
 }
 
-// The expert kernels: routes (and, for down, h) come from earlier launches.
-template <int F, int LPG, bool SH>
+// The expert kernels.  gate_up: RT = the items run the top-k from the
+// logits, else they read routes; down reads routes (and h) of earlier
+// launches.
+template <int F, int LPG, bool SH, bool RT>
 __global__ __launch_bounds__(kGemvThreads) void moe_gate_up_kernel(DecodeArgs a) {
     extern __shared__ uint32_t lds[];
-    gate_up_item<F, LPG, SH>(a, blockIdx.x, lds);
+    gate_up_item<F, LPG, SH, RT>(a, blockIdx.x, lds);
 }
 template <int F, int LPD, bool SH>
 __global__ __launch_bounds__(kGemvThreads) void moe_down_kernel(DecodeArgs a) {
@@ -646,8 +648,11 @@ inline hipError_t launch_t(hipStream_t st, const DecodeArgs& a) {
     gu.ND = 0;
     dn.NR = 0;
     dn.NG = 0;
-    if (a.NG)
-        hipLaunchKernelGGL((moe_gate_up_kernel<F, LPG, SH>), dim3(a.NG), dim3(kGemvThreads),
+    if (a.NG && a.route_topk)
+        hipLaunchKernelGGL((moe_gate_up_kernel<F, LPG, SH, true>), dim3(a.NG), dim3(kGemvThreads),
+                           decode_lds_bytes(F, gu), st, a);
+    else if (a.NG)
+        hipLaunchKernelGGL((moe_gate_up_kernel<F, LPG, SH, false>), dim3(a.NG), dim3(kGemvThreads),
                            decode_lds_bytes(F, gu), st, a);
     if (a.ND)
         hipLaunchKernelGGL((moe_down_kernel<F, LPD, SH>), dim3(a.ND), dim3(kGemvThreads),
