@@ -80,6 +80,13 @@ __device__ __forceinline__ float silu(float v) {
     return v / (1.0f + det_expf(-v));
 }
 
+// silu with the hardware exp2 / reciprocal (each ~1 ulp): for epilogues
+// whose outputs are compared to a tolerance, not bit for bit.
+__device__ __forceinline__ float fast_silu(float v) {
+    const float e = __builtin_amdgcn_exp2f(v * -1.44269504088896341f);
+    return v * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
 // Cross-lane moves inside a 16-lane row (DPP, no LDS traffic).
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {

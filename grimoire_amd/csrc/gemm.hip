@@ -3,17 +3,22 @@
 // One launch per projection for all experts (the reference's design,
 // src/gemm_fast.cpp:1603-1800, src/prefill.cpp:2726-2808), written for
 // gfx950:
-//   - block tile 128 rows x 128 columns x 64 K, 256 threads (4 waves), each
-//     wave a 64x64 quadrant as 2x2 v_mfma_f32_32x32x16_bf16 tiles;
-//   - weight tiles are dequantised ONCE per block into LDS as bf16 that
-//     equals the stored weight exactly (int8 codes; e2m1 x e8m0 through the
-//     CDNA4 fp4 converter; bf16 copies); per-output-channel scales (int8)
-//     are applied to the fp32 accumulators in the epilogue, so the MFMA
-//     operands are exact;
-//   - two LDS stages: the next K tile's global loads are in flight while
-//     the current one is multiplied; one barrier per K tile;
-//   - rows come from the dispatch's (expert, m-tile) table (padding entries
-//     -1 exit at once), the shared expert as extra tiles after it.
+//   - block tile 128 rows x 256 columns x 64 K, 256 threads (4 waves), each
+//     wave all 128 rows of its own 64 columns as 4x2
+//     v_mfma_f32_32x32x16_bf16 tiles (each weight column is dequantised by
+//     one wave only; 0.5 KB of LDS reads per MFMA);
+//   - A (activation rows) is staged through LDS (double buffer, register
+//     prefetch two K tiles deep); B (weights) never touches LDS: each lane
+//     loads the 32 K-values of the weight column it multiplies straight into
+//     registers and dequantises them there to bf16 that equals the stored
+//     weight exactly (int8 codes; e2m1 x e8m0 through the CDNA4 fp4
+//     converter; bf16 copies).  LDS traffic is A alone, which is what bounds
+//     this loop.  Per-output-channel scales (int8) are applied to the fp32
+//     accumulators in the epilogue, so the MFMA operands are exact;
+//   - K loop barriers wait for LDS only, never for the prefetched loads;
+//   - persistent XCD-aware grid over (m-tile, column tile) items, rows from
+//     the dispatch's (expert, m-tile) table (padding entries -1 skip), the
+//     shared expert's tiles after it.
 // Epilogues: SwiGLU (gate and up columns of the same h column live in the
 // same lane) writing h as a bf16 pair hi + lo (|lo| <= 2^-9 |h|, so h is
 // kept to ~2^-17 relative), or plain fp32 / bf16 output.  The down
@@ -27,313 +32,448 @@ typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
 
-constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int BM = 128, BN = 256, BK = 64;
 constexpr int LDK = BK + 8;         // LDS row stride in bf16 (144 bytes)
 constexpr int kGemmThreads = 256;
+#ifndef GRIM_GEMM_OCC
+#define GRIM_GEMM_OCC 1
+#endif
 
-template <int F> struct BTile;
-template <> struct BTile<GRIM_FMT_INT8> { static constexpr int CPR = 4; };   // 16B chunks per row
-template <> struct BTile<GRIM_FMT_MXFP4> { static constexpr int CPR = 2; };
-template <> struct BTile<GRIM_FMT_BF16> { static constexpr int CPR = 8; };
+
+// Work-group barrier for LDS hand-offs only: waits for this wave's LDS
+// accesses, not for its global loads (a __syncthreads() fence would also
+// wait for the prefetched tiles still in flight).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
     // exact conversions only (values representable in bf16): truncate
     return (f_bits(a) >> 16) | (f_bits(b) & 0xFFFF0000u);
 }
 
-// Dequantise one 16-byte chunk of B into LDS row `dst` (bf16 elements).
-template <int F>
-__device__ __forceinline__ void store_b_chunk(const u32x4 raw, uint8_t sc, uint16_t* dst);
+// MFMA B fragment (8 bf16, exact) for step ks from a lane's 32 K-values of
+// one weight column: INT8 bytes 8ks..8ks+7; MXFP4 nibbles 8ks..8ks+7
+// (low nibble = even K) times the group's e8m0 scale; BF16 elements
+// 8ks..8ks+7.
+template <int F, int BQ>
+__device__ __forceinline__ bf16x8 b_frag(const u32x4 (&raw)[BQ], uint32_t sc, int ks);
 
 template <>
-__device__ __forceinline__ void store_b_chunk<GRIM_FMT_INT8>(const u32x4 raw, uint8_t,
-                                                             uint16_t* dst) {
-    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-    uint32_t o[8];
+__device__ __forceinline__ bf16x8 b_frag<GRIM_FMT_INT8, 2>(const u32x4 (&raw)[2], uint32_t, int ks) {
+    const u32x4 q = raw[ks >> 1];
+    const uint32_t w0 = (ks & 1) ? q.z : q.x, w1 = (ks & 1) ? q.w : q.y;
+    uint32_t o[4];
+    const uint32_t w[2] = {w0, w1};
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
+    for (int d = 0; d < 2; ++d) {
         const float f0 = float(int8_t(w[d] & 0xFF)), f1 = float(int8_t((w[d] >> 8) & 0xFF));
         const float f2 = float(int8_t((w[d] >> 16) & 0xFF)), f3 = float(int8_t(w[d] >> 24));
         o[2 * d] = pack_bf16(f0, f1);
         o[2 * d + 1] = pack_bf16(f2, f3);
     }
-    u32x4* p = reinterpret_cast<u32x4*>(dst);
-    p[0] = u32x4{o[0], o[1], o[2], o[3]};
-    p[1] = u32x4{o[4], o[5], o[6], o[7]};
+    bf16x8 r;
+    __builtin_memcpy(&r, o, 16);
+    return r;
 }
 
 template <>
-__device__ __forceinline__ void store_b_chunk<GRIM_FMT_MXFP4>(const u32x4 raw, uint8_t sc,
-                                                              uint16_t* dst) {
-    const float s = e8m0_to_f32(sc);
-    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-    uint32_t o[16];
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        const bf16x2v v0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], s, 0);
-        const bf16x2v v1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], s, 1);
-        const bf16x2v v2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], s, 2);
-        const bf16x2v v3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], s, 3);
-        __builtin_memcpy(&o[4 * d + 0], &v0, 4);
-        __builtin_memcpy(&o[4 * d + 1], &v1, 4);
-        __builtin_memcpy(&o[4 * d + 2], &v2, 4);
-        __builtin_memcpy(&o[4 * d + 3], &v3, 4);
-    }
-    u32x4* p = reinterpret_cast<u32x4*>(dst);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+__device__ __forceinline__ bf16x8 b_frag<GRIM_FMT_MXFP4, 1>(const u32x4 (&raw)[1], uint32_t sc, int ks) {
+    const float s = e8m0_to_f32(uint8_t(sc));
+    const uint32_t wd = ks == 0 ? raw[0].x : ks == 1 ? raw[0].y : ks == 2 ? raw[0].z : raw[0].w;
+    const bf16x2v v0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 0);
+    const bf16x2v v1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 1);
+    const bf16x2v v2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 2);
+    const bf16x2v v3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, s, 3);
+    uint32_t o[4];
+    __builtin_memcpy(&o[0], &v0, 4);
+    __builtin_memcpy(&o[1], &v1, 4);
+    __builtin_memcpy(&o[2], &v2, 4);
+    __builtin_memcpy(&o[3], &v3, 4);
+    bf16x8 r;
+    __builtin_memcpy(&r, o, 16);
+    return r;
 }
 
 template <>
-__device__ __forceinline__ void store_b_chunk<GRIM_FMT_BF16>(const u32x4 raw, uint8_t,
-                                                             uint16_t* dst) {
-    *reinterpret_cast<u32x4*>(dst) = raw;
+__device__ __forceinline__ bf16x8 b_frag<GRIM_FMT_BF16, 4>(const u32x4 (&raw)[4], uint32_t, int ks) {
+    bf16x8 r;
+    __builtin_memcpy(&r, &raw[ks], 16);
+    return r;
 }
+
+// The operands of one launch (routed experts, or the shared expert): chosen
+// once per launch so that only one set of pointers is live.
+struct GemmSrc {
+    const uint8_t* payload;
+    const void* scales;
+    int64_t row_bytes;
+    int row_scales;
+    const uint16_t* A;
+    void* out;
+};
 
 template <int F>
-__device__ __forceinline__ float col_scale(const WView& w, int64_t row) {
+__device__ __forceinline__ float col_scale(const GemmSrc& w, int64_t row) {
     if constexpr (F == GRIM_FMT_INT8) return static_cast<const float*>(w.scales)[row];
     return 1.0f;
 }
 
 // One (m-tile, column-tile) of the grouped product.
 template <int F, bool SWIGLU, bool APAIR, bool OUT_BF16>
-__device__ __forceinline__ void gemm_tile(const GemmArgs& g, int ty, int n_routed,
-                                          uint16_t (*As)[APAIR ? 2 : 1][BM * LDK],
-                                          uint16_t (*Bs)[BN * LDK]) {
-    constexpr int CPR = BTile<F>::CPR;
-    constexpr int CH = BK / CPR;              // elements per B chunk
-    constexpr int NBCH = BN * CPR / kGemmThreads;   // B chunks per thread (>= 1)
-    static_assert(BN * CPR % kGemmThreads == 0, "B chunk split");
-
+__device__ __forceinline__ void gemm_tile(const GemmArgs& g, const GemmSrc& w, bool routed, int ty,
+                                          int nt, uint16_t (*As)[APAIR ? 2 : 1][BM * LDK]) {
     // ---- which rows / weights
-    int e, rows_valid;
-    int64_t arow0;
-    const uint16_t* A;
-    WView w;
-    void* out;
-    int64_t wrow0;
-    if (ty < n_routed) {
-        e = g.tile_e[ty];
+    int rows_valid;
+    int64_t arow0, wrow0;
+    if (routed) {
+        // table values are the same for the whole work-group: keep them in
+        // scalar registers (buffer descriptors built from them must be)
+        const int e = __builtin_amdgcn_readfirstlane(g.tile_e[ty]);
         if (e < 0) return;
-        const int mb = g.tile_mb[ty];
-        rows_valid = min(BM, g.counts[e] - mb * BM);
-        arow0 = int64_t(g.offsets[e]) + int64_t(mb) * BM;
-        A = g.A;
-        w = g.w;
-        out = g.out;
+        const int mb = __builtin_amdgcn_readfirstlane(g.tile_mb[ty]);
+        rows_valid = min(BM, __builtin_amdgcn_readfirstlane(g.counts[e]) - mb * BM);
+        arow0 = int64_t(__builtin_amdgcn_readfirstlane(g.offsets[e])) + int64_t(mb) * BM;
         wrow0 = int64_t(e) * g.N;
     } else {
-        const int mb = ty - n_routed;
+        const int mb = ty;
         rows_valid = min(BM, g.T_sh - mb * BM);
         arow0 = int64_t(mb) * BM;
-        A = g.A_sh;
-        w = g.w_sh;
-        out = g.out_sh;
         wrow0 = 0;
     }
+    // uniform per work-group: make that explicit, so descriptors and
+    // offsets built from them stay in scalar registers
+    rows_valid = __builtin_amdgcn_readfirstlane(rows_valid);
+    arow0 = int64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(arow0)))) |
+            (int64_t(__builtin_amdgcn_readfirstlane(int(arow0 >> 32))) << 32);
+    wrow0 = int64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(wrow0)))) |
+            (int64_t(__builtin_amdgcn_readfirstlane(int(wrow0 >> 32))) << 32);
+    const uint16_t* A = w.A;
+    void* out = w.out;
     if (rows_valid <= 0) return;
 
-    const int tid = threadIdx.x;
+    // the thread id is laundered so that per-lane offsets are recomputed in
+    // each tile instead of being hoisted out of the persistent loop (which
+    // keeps dozens of them live across it and spills)
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
     const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
     const int K = g.K;
     const int64_t a_stride = APAIR ? 2 * int64_t(K) : int64_t(K);
 
-    // B rows of this tile: SwiGLU: 64 gate cols then the 64 matching up cols
-    const int nt = blockIdx.x;
-    auto b_row = [&](int n) -> int64_t {
-        int c;
+    // Each wave owns 64 output columns of the 256 (two 32-column MFMA
+    // fragments) for all 128 rows: SwiGLU: the gate and the up column of
+    // 32 h columns; else 64 consecutive columns.  Column of fragment ni for
+    // this lane, and its weight row within the expert's slab:
+    auto out_col = [&](int ni) -> int {
+        if (SWIGLU) return nt * (BN / 2) + wave * 32 + (lane & 31);   // h column
+        return nt * BN + wave * 64 + ni * 32 + (lane & 31);
+    };
+    auto b_row = [&](int ni) -> int {
         if (SWIGLU) {
-            const int hc = min(nt * 64 + (n & 63), g.I - 1);
-            c = n < 64 ? hc : g.I + hc;
-        } else {
-            c = min(nt * BN + n, g.N - 1);
+            const int hc = min(out_col(ni), g.I - 1);
+            return ni == 0 ? hc : g.I + hc;
         }
-        return wrow0 + c;
+        return min(out_col(ni), g.N - 1);
     };
 
-    // ---- global -> register staging
-    u32x4 ra[APAIR ? 2 : 1][4];
-    u32x4 rb[NBCH];
-    uint8_t rs[NBCH];
-    int64_t browv[NBCH];
+    // ---- A (activations) goes through LDS; B (weights) never does: each
+    // lane loads the 32 K-values of its own weight column it multiplies and
+    // dequantises them in registers, so LDS carries A only.  The K order
+    // inside a 64-wide K tile is permuted consistently for A and B: in MFMA
+    // step ks, lane half h supplies K = 32 h + 8 ks + [0, 8).
+    //
+    // Buffer loads off per-tile bases; A rows past rows_valid read as zero
+    // (outside the buffer's range).
+    const int a_row_bytes = int(a_stride) * 2;
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(A + arow0 * a_stride), 0, rows_valid * a_row_bytes, 0x00020000);
+    const int n_slab = SWIGLU ? 2 * g.I : g.N;
+    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(w.payload + wrow0 * w.row_bytes), 0, int(n_slab * w.row_bytes),
+        0x00020000);
+    const __amdgpu_buffer_rsrc_t rS = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(static_cast<const void*>(static_cast<const uint8_t*>(w.scales) +
+                                                   (F == GRIM_FMT_MXFP4 ? wrow0 * w.row_scales : 0))),
+        0, F == GRIM_FMT_MXFP4 ? n_slab * w.row_scales : 0, 0x00020000);
+    const int a_off0 = (tid >> 3) * a_row_bytes + (tid & 7) * 16;   // + 32 rows per chunk
+    const int h = lane >> 5;
+    constexpr int BQ = F == GRIM_FMT_BF16 ? 4 : (F == GRIM_FMT_INT8 ? 2 : 1);   // 16-B loads per lane per column
+    int b_off[2], s_off[2];
 #pragma unroll
-    for (int i = 0; i < NBCH; ++i) browv[i] = b_row((tid + i * kGemmThreads) / CPR);
+    for (int ni = 0; ni < 2; ++ni) {
+        const int n = b_row(ni);
+        const int kb = 32 * h;   // first K of this lane inside a K tile
+        b_off[ni] = n * int(w.row_bytes) + (F == GRIM_FMT_MXFP4 ? kb / 2 : (F == GRIM_FMT_BF16 ? kb * 2 : kb));
+        s_off[ni] = n * w.row_scales + h;
+    }
 
-    auto load_tile = [&](int k0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = tid + i * kGemmThreads;   // 1024 chunks of 8 bf16
-            const int r = c >> 3, kc = (c & 7) * 8;
-            const int rr = r < rows_valid ? r : rows_valid - 1;
-            const uint16_t* p = A + (arow0 + rr) * a_stride + k0 + kc;
-            ra[0][i] = *reinterpret_cast<const u32x4*>(p);
-            if constexpr (APAIR) ra[1][i] = *reinterpret_cast<const u32x4*>(p + K);
-        }
-#pragma unroll
-        for (int i = 0; i < NBCH; ++i) {
-            const int c = tid + i * kGemmThreads;
-            const int kc = (c % CPR) * CH;
-            const int64_t byte_off =
-                F == GRIM_FMT_MXFP4 ? (k0 + kc) / 2 : (F == GRIM_FMT_BF16 ? (k0 + kc) * 2 : k0 + kc);
-            rb[i] = load16(w.payload + browv[i] * w.row_bytes + byte_off);
-            if constexpr (F == GRIM_FMT_MXFP4)
-                rs[i] = static_cast<const uint8_t*>(w.scales)[browv[i] * w.row_scales + (k0 + kc) / 32];
-        }
-    };
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = tid + i * kGemmThreads;
-            const int r = c >> 3, kc = (c & 7) * 8;
-            const bool ok = r < rows_valid;
-            const u32x4 z = {0u, 0u, 0u, 0u};
-            *reinterpret_cast<u32x4*>(&As[buf][0][r * LDK + kc]) = ok ? ra[0][i] : z;
-            if constexpr (APAIR)
-                *reinterpret_cast<u32x4*>(&As[buf][1][r * LDK + kc]) = ok ? ra[1][i] : z;
-        }
-#pragma unroll
-        for (int i = 0; i < NBCH; ++i) {
-            const int c = tid + i * kGemmThreads;
-            const int n = c / CPR, kc = (c % CPR) * CH;
-            store_b_chunk<F>(rb[i], F == GRIM_FMT_MXFP4 ? rs[i] : 0, &Bs[buf][n * LDK + kc]);
-        }
-    };
+    struct StageA { u32x4 a[APAIR ? 2 : 1][4]; };
+    struct StageB { u32x4 b[2][BQ]; uint32_t s[2]; };
+#define GRIM_LOAD_A(R, k0)                                                                      \
+    do {                                                                                        \
+        const int kb_ = (k0) * 2;                                                               \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                         \
+            (R).a[0][i] = __builtin_amdgcn_raw_buffer_load_b128(rA, a_off0 + 32 * i * a_row_bytes, kb_, 0); \
+            if constexpr (APAIR)                                                                \
+                (R).a[1][i] = __builtin_amdgcn_raw_buffer_load_b128(rA, a_off0 + 32 * i * a_row_bytes, \
+                                                                    kb_ + 2 * K, 0);            \
+        }                                                                                       \
+    } while (0)
+#define GRIM_LOAD_B(R, k0)                                                                      \
+    do {                                                                                        \
+        const int kw_ = F == GRIM_FMT_MXFP4 ? (k0) / 2 : (F == GRIM_FMT_BF16 ? (k0) * 2 : (k0)); \
+        _Pragma("unroll") for (int ni = 0; ni < 2; ++ni) {                                      \
+            _Pragma("unroll") for (int q = 0; q < BQ; ++q)                                      \
+                (R).b[ni][q] = __builtin_amdgcn_raw_buffer_load_b128(rB, b_off[ni] + 16 * q, kw_, 0); \
+            if constexpr (F == GRIM_FMT_MXFP4)                                                  \
+                (R).s[ni] = __builtin_amdgcn_raw_buffer_load_b8(rS, s_off[ni], (k0) / 32, 0);    \
+        }                                                                                       \
+    } while (0)
+#define GRIM_STORE_A(R, buf)                                                                    \
+    do {                                                                                        \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                         \
+            const int c_ = tid + i * kGemmThreads;                                              \
+            const int r_ = c_ >> 3, kc_ = (c_ & 7) * 8;                                         \
+            *reinterpret_cast<u32x4*>(&As[buf][0][r_ * LDK + kc_]) = (R).a[0][i];               \
+            if constexpr (APAIR) *reinterpret_cast<u32x4*>(&As[buf][1][r_ * LDK + kc_]) = (R).a[1][i]; \
+        }                                                                                       \
+    } while (0)
 
-    f32x16 acc[2][2];
+    f32x16 acc[4][2];
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
+    for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.0f;
 
-    // column offsets (tile-local) of this wave's two 32-column B fragments
-    const int ncol0 = SWIGLU ? wn * 32 : wn * 64;
-    const int ncol1 = SWIGLU ? 64 + wn * 32 : wn * 64 + 32;
+#define GRIM_MMA_TILE(buf, RB)                                                                  \
+    do {                                                                                        \
+        _Pragma("unroll") for (int ks = 0; ks < BK / 16; ++ks) {                                \
+            const int kk = 32 * h + 8 * ks;                                                     \
+            bf16x8 a[APAIR ? 2 : 1][4], b[2];                                                   \
+            _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) {                                  \
+                const int r = mi * 32 + (lane & 31);                                            \
+                a[0][mi] = *reinterpret_cast<const bf16x8*>(&As[buf][0][r * LDK + kk]);         \
+                if constexpr (APAIR) a[1][mi] = *reinterpret_cast<const bf16x8*>(&As[buf][1][r * LDK + kk]); \
+            }                                                                                   \
+            _Pragma("unroll") for (int ni = 0; ni < 2; ++ni)                                    \
+                b[ni] = b_frag<F>((RB).b[ni], (RB).s[ni], ks);                                  \
+            _Pragma("unroll") for (int mi = 0; mi < 4; ++mi)                                    \
+            _Pragma("unroll") for (int ni = 0; ni < 2; ++ni) {                                  \
+                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][mi], b[ni], acc[mi][ni], 0, 0, 0); \
+                if constexpr (APAIR)                                                            \
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][mi], b[ni], acc[mi][ni], 0, 0, 0); \
+            }                                                                                   \
+            __builtin_amdgcn_sched_barrier(0);                                                  \
+        }                                                                                       \
+    } while (0)
 
+    // Iteration t multiplies LDS A buffer t & 1 with B register set t & 1.
+    // Afterwards B(t + 2) is requested into that set, A(t + 1) moves from
+    // its register set into the other LDS buffer and A(t + 3) is requested
+    // into the freed set, so about two K tiles stay in flight.
     const int nk = K / BK;
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) load_tile((kt + 1) * BK);
-#pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
-            const int kk = ks * 16 + 8 * (lane >> 5);
-            bf16x8 a[APAIR ? 2 : 1][2], b[2];
-#pragma unroll
-            for (int mi = 0; mi < 2; ++mi) {
-                const int r = wm * 64 + mi * 32 + (lane & 31);
-                a[0][mi] = *reinterpret_cast<const bf16x8*>(&As[buf][0][r * LDK + kk]);
-                if constexpr (APAIR) a[1][mi] = *reinterpret_cast<const bf16x8*>(&As[buf][1][r * LDK + kk]);
-            }
-            b[0] = *reinterpret_cast<const bf16x8*>(&Bs[buf][(ncol0 + (lane & 31)) * LDK + kk]);
-            b[1] = *reinterpret_cast<const bf16x8*>(&Bs[buf][(ncol1 + (lane & 31)) * LDK + kk]);
-#pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-                for (int ni = 0; ni < 2; ++ni) {
-                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][mi], b[ni], acc[mi][ni], 0, 0, 0);
-                    if constexpr (APAIR)
-                        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][mi], b[ni], acc[mi][ni], 0, 0, 0);
-                }
+    StageA RA0, RA1;
+    StageB RB0, RB1;
+    GRIM_LOAD_A(RA0, 0);
+    GRIM_LOAD_B(RB0, 0);
+    if (nk > 1) { GRIM_LOAD_A(RA1, BK); GRIM_LOAD_B(RB1, BK); }
+    GRIM_STORE_A(RA0, 0);
+    if (nk > 2) GRIM_LOAD_A(RA0, 2 * BK);
+    lds_barrier();
+    // pairs of K tiles, then an odd last tile: no exit from the middle of
+    // the unrolled pair, so the accumulators stay in one register set
+    int kt = 0;
+    for (; kt + 2 <= nk; kt += 2) {
+        GRIM_MMA_TILE(0, RB0);
+        if (kt + 2 < nk) GRIM_LOAD_B(RB0, (kt + 2) * BK);
+        GRIM_STORE_A(RA1, 1);
+        if (kt + 3 < nk) GRIM_LOAD_A(RA1, (kt + 3) * BK);
+        lds_barrier();
+        GRIM_MMA_TILE(1, RB1);
+        if (kt + 3 < nk) GRIM_LOAD_B(RB1, (kt + 3) * BK);
+        if (kt + 2 < nk) {
+            GRIM_STORE_A(RA0, 0);
+            if (kt + 4 < nk) GRIM_LOAD_A(RA0, (kt + 4) * BK);
         }
-        if (kt + 1 < nk) store_tile(buf ^ 1);
-        __syncthreads();
+        lds_barrier();
     }
+    if (kt < nk) GRIM_MMA_TILE(0, RB0);
+#undef GRIM_LOAD_A
+#undef GRIM_LOAD_B
+#undef GRIM_STORE_A
+#undef GRIM_MMA_TILE
 
-    // ---- epilogue.  acc[mi][ni][v]: row = wm*64 + mi*32 + (v&3) + 4*(lane>>5)
-    // + 8*(v>>2), column = ncol(ni) + (lane&31).
-    const int lc = lane & 31;
+    // ---- epilogue.  acc[mi][ni][v]: row = mi*32 + (v&3) + 4*(lane>>5) +
+    // 8*(v>>2), column = out_col(ni).  Results go through LDS (the A
+    // buffers, free once every wave has left the K loop) so that global
+    // stores are whole 16-byte row segments.
+    lds_barrier();
+    constexpr int SP16 = 128 + 8;   // staging row stride, 16-bit results
+    constexpr int SP32 = 64 + 4;    // staging row stride, 32-bit results
+    uint16_t* st16 = &As[0][0][0];
+    float* st32 = reinterpret_cast<float*>(&As[0][0][0]);
+    static_assert(BM * SP16 * 2 <= 2 * BM * LDK * 2 && BM * SP32 * 4 <= 2 * BM * LDK * 2,
+                  "epilogue staging fits the A buffers");
     if constexpr (SWIGLU) {
-        const int hc = nt * 64 + wn * 32 + lc;
-        if (hc < g.I) {
-            const float sg = col_scale<F>(w, wrow0 + hc);
-            const float su = col_scale<F>(w, wrow0 + g.I + hc);
-            uint16_t* o = static_cast<uint16_t*>(out);
+        // h columns [hc0, hc0 + 128): hi plane, then lo plane
+        const int hc0 = nt * (BN / 2);
+        const int hcl = wave * 32 + (lane & 31);
+        const int hc = hc0 + hcl;
+        const float sg = hc < g.I ? col_scale<F>(w, wrow0 + hc) : 0.0f;
+        const float su = hc < g.I ? col_scale<F>(w, wrow0 + g.I + hc) : 0.0f;
+        uint16_t lo_v[4][16];
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
+        for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int r = wm * 64 + mi * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
-                    if (r < rows_valid) {
-                        const float hv = silu(acc[mi][0][v] * sg) * (acc[mi][1][v] * su);
-                        const uint16_t hi = f32_to_bf16(hv);
-                        const uint16_t lo = f32_to_bf16(hv - bf16_to_f32(hi));
-                        const int64_t base = (arow0 + r) * 2 * int64_t(g.I);
-                        o[base + hc] = hi;
-                        o[base + g.I + hc] = lo;
+            for (int v = 0; v < 16; ++v) {
+                const int r = mi * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
+                const float hv = fast_silu(acc[mi][0][v] * sg) * (acc[mi][1][v] * su);
+                const uint16_t hi = f32_to_bf16(hv);
+                lo_v[mi][v] = f32_to_bf16(hv - bf16_to_f32(hi));
+                st16[r * SP16 + hcl] = hi;
+            }
+        uint16_t* o = static_cast<uint16_t*>(out) + arow0 * 2 * int64_t(g.I);
+#pragma unroll
+        for (int plane = 0; plane < 2; ++plane) {
+            if (plane == 1) {
+                lds_barrier();
+#pragma unroll
+                for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int r = mi * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
+                        st16[r * SP16 + hcl] = lo_v[mi][v];
                     }
-                }
+            }
+            lds_barrier();
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int c = tid + k * kGemmThreads;   // 16-byte chunk: row c/16, part c%16
+                const int r = c >> 4, part = c & 15;
+                const int col = hc0 + part * 8;
+                if (r < rows_valid && col < g.I)
+                    *reinterpret_cast<u32x4*>(o + r * 2 * g.I + plane * g.I + col) =
+                        *reinterpret_cast<const u32x4*>(&st16[r * SP16 + part * 8]);
+            }
         }
     } else {
+        // four passes, one per wave's 64 columns
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
-            const int c = nt * BN + (ni ? ncol1 : ncol0) + lc;
-            if (c >= g.N) continue;
-            const float sc = col_scale<F>(w, wrow0 + c);
+        for (int pw = 0; pw < 4; ++pw) {
+            if (pw) lds_barrier();
+            if (wave == pw) {
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
+                for (int ni = 0; ni < 2; ++ni) {
+                    const int c = out_col(ni);
+                    const float sc = c < g.N ? col_scale<F>(w, wrow0 + c) : 0.0f;
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int r = wm * 64 + mi * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
-                    if (r < rows_valid) {
-                        const float val = acc[mi][ni][v] * sc;
-                        const int64_t idx = (arow0 + r) * int64_t(g.N) + c;
-                        if constexpr (OUT_BF16) static_cast<uint16_t*>(out)[idx] = f32_to_bf16(val);
-                        else static_cast<float*>(out)[idx] = val;
+                    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) {
+                            const int r = mi * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
+                            st32[r * SP32 + ni * 32 + (lane & 31)] = acc[mi][ni][v] * sc;
+                        }
+                }
+            }
+            lds_barrier();
+            const int c0 = nt * BN + pw * 64;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int c = tid + k * kGemmThreads;   // 16-byte fp32 chunk: row c/16, part c%16
+                const int r = c >> 4, part = c & 15;
+                const int col = c0 + part * 4;
+                if (r < rows_valid && col < g.N) {
+                    const float4 v4 = *reinterpret_cast<const float4*>(&st32[r * SP32 + part * 4]);
+                    if constexpr (OUT_BF16) {
+                        uint16_t* o = static_cast<uint16_t*>(out) + arow0 * int64_t(g.N);
+                        const uint32_t w0 = uint32_t(f32_to_bf16(v4.x)) | (uint32_t(f32_to_bf16(v4.y)) << 16);
+                        const uint32_t w1 = uint32_t(f32_to_bf16(v4.z)) | (uint32_t(f32_to_bf16(v4.w)) << 16);
+                        *reinterpret_cast<uint2*>(o + r * g.N + col) = make_uint2(w0, w1);
+                    } else {
+                        float* o = static_cast<float*>(out) + arow0 * int64_t(g.N);
+                        *reinterpret_cast<float4*>(o + r * g.N + col) = v4;
                     }
                 }
+            }
         }
     }
 }
 
-// Grid: x = column tile; y strides over the m-tile entries: the routed
-// table (its live length read from the device), then the shared expert's.
+// Persistent 1-D grid, XCD-aware.  Work-group b runs on XCD b % 8
+// (work-groups are dealt round-robin over the eight XCDs, each with its own
+// L2).  The m-tile list (routed table, expert-major, its live length read
+// from the device; or the shared expert's tiles) is cut into eight
+// contiguous ranges, one per XCD, and an XCD's work-groups walk the
+// (m-tile, column tile) items of its range column-fastest.  So every
+// column tile of an m-tile, and every m-tile of most experts, is computed
+// under one L2: each A row block and each expert's weights are fetched
+// from HBM about once instead of once per XCD.
+constexpr int kXcds = 8;
 template <int F, bool SWIGLU, bool APAIR, bool OUT_BF16>
-__global__ __launch_bounds__(kGemmThreads, 2) void grouped_gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(kGemmThreads, GRIM_GEMM_OCC) void grouped_gemm_kernel(GemmArgs g, int n_col_tiles,
+                                                                              int shared_part) {
     __shared__ __attribute__((aligned(16))) uint16_t As[2][APAIR ? 2 : 1][BM * LDK];
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * LDK];
-    int n_routed = g.n_tiles_dev ? *g.n_tiles_dev : g.tmax;
-    n_routed = n_routed < g.tmax ? n_routed : g.tmax;
-    const int total = n_routed + (g.T_sh > 0 ? (g.T_sh + BM - 1) / BM : 0);
-    for (int ty = blockIdx.y; ty < total; ty += gridDim.y) {
-        gemm_tile<F, SWIGLU, APAIR, OUT_BF16>(g, ty, n_routed, As, Bs);
+    const bool routed = shared_part == 0;
+    const GemmSrc w{routed ? g.w.payload : g.w_sh.payload, routed ? g.w.scales : g.w_sh.scales,
+                    routed ? g.w.row_bytes : g.w_sh.row_bytes, routed ? g.w.row_scales : g.w_sh.row_scales,
+                    routed ? g.A : g.A_sh, routed ? g.out : g.out_sh};
+    int total;
+    if (routed) {
+        total = g.n_tiles_dev ? __builtin_amdgcn_readfirstlane(*g.n_tiles_dev) : g.tmax;
+        total = total < g.tmax ? total : g.tmax;
+    } else {
+        total = (g.T_sh + BM - 1) / BM;
+    }
+    const int xcd = blockIdx.x % kXcds, per_xcd = gridDim.x / kXcds;
+    const int lo = int(int64_t(total) * xcd / kXcds), hi = int(int64_t(total) * (xcd + 1) / kXcds);
+    const int items = (hi - lo) * n_col_tiles;
+    for (int i = blockIdx.x / kXcds; i < items; i += per_xcd) {
+        gemm_tile<F, SWIGLU, APAIR, OUT_BF16>(g, w, routed, lo + i / n_col_tiles, i % n_col_tiles, As);
         __syncthreads();
     }
+}
+
+template <int F, bool SWIGLU, bool APAIR, bool OUT_BF16>
+static hipError_t launch_kernel(hipStream_t st, const GemmArgs& g, int ntiles) {
+    // routed tiles, then (one more launch) the shared expert's
+    // persistent: the resident capacity, a multiple of the XCD count
+    static int grid = 0;
+    if (grid == 0) {
+        int per_cu = 0, dev = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &per_cu, grouped_gemm_kernel<F, SWIGLU, APAIR, OUT_BF16>, kGemmThreads, 0) != hipSuccess ||
+            hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return hipErrorInvalidConfiguration;
+        grid = (per_cu > 0 ? per_cu : 1) * cus;
+        grid = (grid + kXcds - 1) / kXcds * kXcds;
+    }
+    if (g.tmax > 0)
+        hipLaunchKernelGGL((grouped_gemm_kernel<F, SWIGLU, APAIR, OUT_BF16>), dim3(grid),
+                           dim3(kGemmThreads), 0, st, g, ntiles, 0);
+    if (g.T_sh > 0) {
+        const int items = (g.T_sh + BM - 1) / BM * ntiles;
+        const int gs = min(grid, (items + kXcds - 1) / kXcds * kXcds);
+        hipLaunchKernelGGL((grouped_gemm_kernel<F, SWIGLU, APAIR, OUT_BF16>), dim3(gs),
+                           dim3(kGemmThreads), 0, st, g, ntiles, 1);
+    }
+    return hipGetLastError();
 }
 
 template <int F>
 static hipError_t launch_fmt(hipStream_t st, const GemmArgs& g) {
-    const int ntiles = g.swiglu ? (g.I + 63) / 64 : (g.N + BN - 1) / BN;
+    const int ntiles = g.swiglu ? (g.I + BN / 2 - 1) / (BN / 2) : (g.N + BN - 1) / BN;
     const int my_max = g.tmax + (g.T_sh > 0 ? (g.T_sh + BM - 1) / BM : 0);
     if (my_max <= 0 || ntiles <= 0) return hipSuccess;
-    // about four resident blocks per CU over the whole grid
-    int my = (4 * 256 + ntiles - 1) / ntiles;
-    my = my < my_max ? my : my_max;
-    dim3 grid(ntiles, my);
-    if (g.swiglu) {
-        hipLaunchKernelGGL((grouped_gemm_kernel<F, true, false, false>), grid, dim3(kGemmThreads), 0,
-                           st, g);
-    } else if (g.a_pair) {
-        if (g.out_bf16)
-            hipLaunchKernelGGL((grouped_gemm_kernel<F, false, true, true>), grid, dim3(kGemmThreads),
-                               0, st, g);
-        else
-            hipLaunchKernelGGL((grouped_gemm_kernel<F, false, true, false>), grid, dim3(kGemmThreads),
-                               0, st, g);
-    } else {
-        if (g.out_bf16)
-            hipLaunchKernelGGL((grouped_gemm_kernel<F, false, false, true>), grid, dim3(kGemmThreads),
-                               0, st, g);
-        else
-            hipLaunchKernelGGL((grouped_gemm_kernel<F, false, false, false>), grid,
-                               dim3(kGemmThreads), 0, st, g);
-    }
-    return hipGetLastError();
+    if (g.swiglu) return launch_kernel<F, true, false, false>(st, g, ntiles);
+    if (g.a_pair)
+        return g.out_bf16 ? launch_kernel<F, false, true, true>(st, g, ntiles)
+                          : launch_kernel<F, false, true, false>(st, g, ntiles);
+    return g.out_bf16 ? launch_kernel<F, false, false, true>(st, g, ntiles)
+                      : launch_kernel<F, false, false, false>(st, g, ntiles);
 }
 
 bool gemm_format_ok(int fmt) {
