@@ -248,25 +248,48 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, const GemmSrc& w, b
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.0f;
 
+// A fragments of step ks are read from LDS while step ks - 1 multiplies
+// (two fragment sets), so LDS latency hides behind the MFMAs.
+#define GRIM_READ_A(dst, buf, ks)                                                               \
+    _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) {                                          \
+        const int r_ = mi * 32 + (lane & 31), kk_ = 32 * h + 8 * (ks);                          \
+        dst[0][mi] = *reinterpret_cast<const bf16x8*>(&As[buf][0][r_ * LDK + kk_]);             \
+        if constexpr (APAIR) dst[1][mi] = *reinterpret_cast<const bf16x8*>(&As[buf][1][r_ * LDK + kk_]); \
+    }
 #define GRIM_MMA_TILE(buf, RB)                                                                  \
     do {                                                                                        \
+        bf16x8 fa0[APAIR ? 2 : 1][4], fa1[APAIR ? 2 : 1][4], fb0[2], fb1[2];                    \
+        GRIM_READ_A(fa0, buf, 0);                                                               \
+        _Pragma("unroll") for (int ni = 0; ni < 2; ++ni) fb0[ni] = b_frag<F>((RB).b[ni], (RB).s[ni], 0); \
         _Pragma("unroll") for (int ks = 0; ks < BK / 16; ++ks) {                                \
-            const int kk = 32 * h + 8 * ks;                                                     \
-            bf16x8 a[APAIR ? 2 : 1][4], b[2];                                                   \
-            _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) {                                  \
-                const int r = mi * 32 + (lane & 31);                                            \
-                a[0][mi] = *reinterpret_cast<const bf16x8*>(&As[buf][0][r * LDK + kk]);         \
-                if constexpr (APAIR) a[1][mi] = *reinterpret_cast<const bf16x8*>(&As[buf][1][r * LDK + kk]); \
+            if (ks + 1 < BK / 16) {                                                             \
+                if (ks & 1) {                                                                   \
+                    GRIM_READ_A(fa0, buf, ks + 1);                                              \
+                    _Pragma("unroll") for (int ni = 0; ni < 2; ++ni)                            \
+                        fb0[ni] = b_frag<F>((RB).b[ni], (RB).s[ni], ks + 1);                    \
+                } else {                                                                        \
+                    GRIM_READ_A(fa1, buf, ks + 1);                                              \
+                    _Pragma("unroll") for (int ni = 0; ni < 2; ++ni)                            \
+                        fb1[ni] = b_frag<F>((RB).b[ni], (RB).s[ni], ks + 1);                    \
+                }                                                                               \
             }                                                                                   \
-            _Pragma("unroll") for (int ni = 0; ni < 2; ++ni)                                    \
-                b[ni] = b_frag<F>((RB).b[ni], (RB).s[ni], ks);                                  \
             _Pragma("unroll") for (int mi = 0; mi < 4; ++mi)                                    \
             _Pragma("unroll") for (int ni = 0; ni < 2; ++ni) {                                  \
-                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][mi], b[ni], acc[mi][ni], 0, 0, 0); \
-                if constexpr (APAIR)                                                            \
-                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][mi], b[ni], acc[mi][ni], 0, 0, 0); \
+                const bf16x8 bb = (ks & 1) ? fb1[ni] : fb0[ni];                                 \
+                const bf16x8 ah = (ks & 1) ? fa1[0][mi] : fa0[0][mi];                           \
+                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bb, acc[mi][ni], 0, 0, 0); \
+                if constexpr (APAIR) {                                                          \
+                    const bf16x8 al = (ks & 1) ? fa1[1][mi] : fa0[1][mi];                       \
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bb, acc[mi][ni], 0, 0, 0); \
+                }                                                                               \
             }                                                                                   \
-            __builtin_amdgcn_sched_barrier(0);                                                  \
+            /* interleave: the next step's LDS reads and conversions between   */               \
+            /* this step's MFMAs                                                */              \
+            _Pragma("unroll") for (int j = 0; j < 8; ++j) {                                     \
+                __builtin_amdgcn_sched_group_barrier(0x008, APAIR ? 2 : 1, 0);                  \
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                              \
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);                              \
+            }                                                                                   \
         }                                                                                       \
     } while (0)
 
@@ -305,6 +328,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, const GemmSrc& w, b
 #undef GRIM_LOAD_B
 #undef GRIM_STORE_A
 #undef GRIM_MMA_TILE
+#undef GRIM_READ_A
 
     // ---- epilogue.  acc[mi][ni][v]: row = mi*32 + (v&3) + 4*(lane>>5) +
     // 8*(v>>2), column = out_col(ni).  Results go through LDS (the A
