@@ -197,24 +197,46 @@ void* bridge_scratch(size_t bytes) {
     return s.p;
 }
 
-__global__ void tiles_from_counts(const int* __restrict__ rows, int ne, int mc,
-                                  int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-                                  int32_t* __restrict__ tile_e, int32_t* __restrict__ tile_mb,
-                                  int tmax, int32_t* __restrict__ n_tiles) {
-    // single thread: ne is at most a few hundred
-    if (threadIdx.x != 0) return;
-    int off = 0, nt = 0;
-    for (int e = 0; e < ne; ++e) {
+// rows per expert -> counts, exclusive offsets and the (expert, m-block)
+// tile table, by one 1024-thread block: each thread sums a contiguous run
+// of experts, a block scan gives every run its row and tile offsets, then
+// each thread writes its run.
+__global__ __launch_bounds__(1024) void tiles_from_counts(const int* __restrict__ rows, int ne, int mc,
+                                                          int32_t* __restrict__ counts,
+                                                          int32_t* __restrict__ offsets,
+                                                          int32_t* __restrict__ tile_e,
+                                                          int32_t* __restrict__ tile_mb, int tmax,
+                                                          int32_t* __restrict__ n_tiles) {
+    __shared__ int s_rows[1024], s_tiles[1024];
+    const int tid = threadIdx.x;
+    const int per = (ne + 1023) / 1024;
+    const int e0 = tid * per, e1 = min(e0 + per, ne);
+    int rsum = 0, tsum = 0;
+    for (int e = e0; e < e1; ++e) {
+        const int c = rows[e] > 0 ? rows[e] : 0;
+        rsum += c;
+        tsum += (c + mc - 1) / mc;
+    }
+    s_rows[tid] = rsum;
+    s_tiles[tid] = tsum;
+    __syncthreads();
+    for (int d = 1; d < 1024; d <<= 1) {   // inclusive scan
+        const int r = tid >= d ? s_rows[tid - d] : 0, t = tid >= d ? s_tiles[tid - d] : 0;
+        __syncthreads();
+        s_rows[tid] += r;
+        s_tiles[tid] += t;
+        __syncthreads();
+    }
+    int off = s_rows[tid] - rsum, nt = s_tiles[tid] - tsum;
+    for (int e = e0; e < e1; ++e) {
         const int c = rows[e] > 0 ? rows[e] : 0;
         counts[e] = c;
         offsets[e] = off;
         off += c;
-        for (int mb = 0; mb * mc < c; ++mb) {
+        for (int mb = 0; mb * mc < c; ++mb, ++nt)
             if (nt < tmax) { tile_e[nt] = e; tile_mb[nt] = mb; }
-            ++nt;
-        }
     }
-    *n_tiles = nt < tmax ? nt : tmax;
+    if (tid == 1023) *n_tiles = s_tiles[1023] < tmax ? s_tiles[1023] : tmax;
 }
 
 constexpr int kBridgeTileCap = 1 << 16;
@@ -231,7 +253,7 @@ int bridge_common(void* stream, const grim_quant_weight& w, int N, int I, int sw
     int32_t* tile_e = sc + 2 * ne;
     int32_t* tile_mb = tile_e + kBridgeTileCap;
     int32_t* n_tiles = tile_mb + kBridgeTileCap;
-    hipLaunchKernelGGL(tiles_from_counts, dim3(1), dim3(64), 0, S(stream), rows, ne, kGemmBM,
+    hipLaunchKernelGGL(tiles_from_counts, dim3(1), dim3(1024), 0, S(stream), rows, ne, kGemmBM,
                        counts, offsets, tile_e, tile_mb, kBridgeTileCap, n_tiles);
     GemmArgs g{};
     g.w = view(w);
@@ -457,7 +479,7 @@ int grimoire_moe_grouped_gemm(void* stream, const grim_quant_weight* w, int N, i
     int32_t* n_tiles = sc + 2 * tmax;
     int32_t* cnt2 = n_tiles + 4;
     int32_t* off2 = cnt2 + num_experts;
-    hipLaunchKernelGGL(tiles_from_counts, dim3(1), dim3(64), 0, S(stream), counts, num_experts,
+    hipLaunchKernelGGL(tiles_from_counts, dim3(1), dim3(1024), 0, S(stream), counts, num_experts,
                        kGemmBM, cnt2, off2, tile_e, tile_mb, tmax, n_tiles);
     GemmArgs g{};
     g.w = view(*w);
@@ -466,7 +488,7 @@ int grimoire_moe_grouped_gemm(void* stream, const grim_quant_weight* w, int N, i
     g.I = swiglu ? N / 2 : 0;
     g.swiglu = swiglu;
     g.a_pair = a_pair;
-    g.out_bf16 = swiglu ? 1 : out_bf16;
+    g.out_bf16 = swiglu ? 0 : out_bf16;   // SwiGLU: h as bf16 pairs
     g.A = A;
     g.out = out;
     g.offsets = offsets;
@@ -494,10 +516,20 @@ void grimoire_xe2_grouped_w4a16(void* stream, const void* activations_bf16,
                                 void* outputs_bf16, int n, int k, const int* rows_per_expert,
                                 const int* expert_ids, int num_experts, int group_size,
                                 int* atomic_buffer) {
-    (void)stream; (void)activations_bf16; (void)weights_int4; (void)scales_bf16;
-    (void)outputs_bf16; (void)n; (void)k; (void)rows_per_expert; (void)expert_ids;
-    (void)num_experts; (void)group_size; (void)atomic_buffer;
-    fail(GRIM_ERR_FORMAT, "grimoire_xe2_grouped_w4a16: int4 grouped GEMM not built yet");
+    (void)expert_ids;      // rows are grouped in expert order, as the reference
+    (void)atomic_buffer;   // no work counter: the tile table is built on the device
+    if (!activations_bf16 || !weights_int4 || !scales_bf16 || !outputs_bf16 || !rows_per_expert) {
+        fail(GRIM_ERR_ARG, "xe2 w4a16: null pointer");
+        return;
+    }
+    if (n <= 0 || k <= 0 || num_experts <= 0 || group_size <= 0 || group_size % 64 || k % group_size) {
+        fail(GRIM_ERR_SHAPE, "xe2 w4a16: n=%d k=%d group=%d (group a multiple of 64 dividing k)", n,
+             k, group_size);
+        return;
+    }
+    grim_quant_weight w{kGemmFmtS4, num_experts * n, k, k / group_size, k / 2, weights_int4,
+                        scales_bf16, nullptr};
+    bridge_common(stream, w, n, 0, 0, activations_bf16, outputs_bf16, rows_per_expert, num_experts);
 }
 
 void grimoire_xe2_fused_moe_gate_up_mxfp4_silu_bf16(void* stream, const void* activations,
@@ -505,10 +537,14 @@ void grimoire_xe2_fused_moe_gate_up_mxfp4_silu_bf16(void* stream, const void* ac
                                                     const unsigned char* scales, void* outputs,
                                                     int n, int k, const int* rows_per_expert,
                                                     int num_experts, int32_t* atomic_buffer) {
-    (void)atomic_buffer;
-    (void)stream; (void)activations; (void)weights; (void)scales; (void)outputs; (void)n; (void)k;
-    (void)rows_per_expert; (void)num_experts;
-    fail(GRIM_ERR_FORMAT, "fused gate_up bridge: bf16-out SwiGLU epilogue not built yet");
+    (void)atomic_buffer;   // no work counter: the tile table is built on the device
+    grim_quant_weight w{GRIM_FMT_MXFP4, num_experts * 2 * n, k, k / 32, k / 2, weights, scales, nullptr};
+    if (check_weight(&w, "xe2 fused gate_up", int64_t(num_experts) * 2 * n, k) || k % 64 || n % 8) return;
+    if (!activations || !outputs || !rows_per_expert) {
+        fail(GRIM_ERR_ARG, "xe2 fused gate_up: null pointer");
+        return;
+    }
+    bridge_common(stream, w, 2 * n, n, 1, activations, outputs, rows_per_expert, num_experts);
 }
 
 }  // extern "C"

@@ -102,6 +102,22 @@ __device__ __forceinline__ bf16x8 b_frag<GRIM_FMT_BF16, 4>(const u32x4 (&raw)[4]
     return r;
 }
 
+template <>
+__device__ __forceinline__ bf16x8 b_frag<kGemmFmtS4, 1>(const u32x4 (&raw)[1], uint32_t, int ks) {
+    const uint32_t wd = ks == 0 ? raw[0].x : ks == 1 ? raw[0].y : ks == 2 ? raw[0].z : raw[0].w;
+    uint32_t o[4];
+    // (the sbfe builtin is typed unsigned: convert its sign-extended result as int)
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const float f0 = float(int(__builtin_amdgcn_sbfe(int(wd), 8 * d, 4)));       // even K
+        const float f1 = float(int(__builtin_amdgcn_sbfe(int(wd), 8 * d + 4, 4)));   // odd K
+        o[d] = pack_bf16(f0, f1);
+    }
+    bf16x8 r;
+    __builtin_memcpy(&r, o, 16);
+    return r;
+}
+
 // The operands of one launch (routed experts, or the shared expert): chosen
 // once per launch so that only one set of pointers is live.
 struct GemmSrc {
@@ -192,10 +208,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, const GemmSrc& w, b
     const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(w.payload + wrow0 * w.row_bytes), 0, int(n_slab * w.row_bytes),
         0x00020000);
+    // side scales: MXFP4 e8m0 bytes [N][K/32]; S4 bf16 [N][K/G]
+    constexpr int SB = F == GRIM_FMT_MXFP4 ? 1 : (F == kGemmFmtS4 ? 2 : 0);   // bytes per scale
     const __amdgpu_buffer_rsrc_t rS = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void*>(static_cast<const void*>(static_cast<const uint8_t*>(w.scales) +
-                                                   (F == GRIM_FMT_MXFP4 ? wrow0 * w.row_scales : 0))),
-        0, F == GRIM_FMT_MXFP4 ? n_slab * w.row_scales : 0, 0x00020000);
+                                                   wrow0 * w.row_scales * SB)),
+        0, n_slab * w.row_scales * SB, 0x00020000);
+    constexpr bool kGroupScaled = F == kGemmFmtS4;
+    const int group = kGroupScaled ? K / w.row_scales : 64;   // K per scale group
+    const int gk = group / BK;                                 // K tiles per group
     const int a_off0 = (tid >> 3) * a_row_bytes + (tid & 7) * 16;   // + 32 rows per chunk
     const int h = lane >> 5;
     constexpr int BQ = F == GRIM_FMT_BF16 ? 4 : (F == GRIM_FMT_INT8 ? 2 : 1);   // 16-B loads per lane per column
@@ -204,8 +225,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, const GemmSrc& w, b
     for (int ni = 0; ni < 2; ++ni) {
         const int n = b_row(ni);
         const int kb = 32 * h;   // first K of this lane inside a K tile
-        b_off[ni] = n * int(w.row_bytes) + (F == GRIM_FMT_MXFP4 ? kb / 2 : (F == GRIM_FMT_BF16 ? kb * 2 : kb));
-        s_off[ni] = n * w.row_scales + h;
+        b_off[ni] = n * int(w.row_bytes) +
+                    (F == GRIM_FMT_MXFP4 || F == kGemmFmtS4 ? kb / 2 : (F == GRIM_FMT_BF16 ? kb * 2 : kb));
+        s_off[ni] = F == kGemmFmtS4 ? n * w.row_scales * 2 : n * w.row_scales + h;
     }
 
     struct StageA { u32x4 a[APAIR ? 2 : 1][4]; };
@@ -222,12 +244,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, const GemmSrc& w, b
     } while (0)
 #define GRIM_LOAD_B(R, k0)                                                                      \
     do {                                                                                        \
-        const int kw_ = F == GRIM_FMT_MXFP4 ? (k0) / 2 : (F == GRIM_FMT_BF16 ? (k0) * 2 : (k0)); \
+        const int kw_ = F == GRIM_FMT_MXFP4 || F == kGemmFmtS4 ? (k0) / 2                      \
+                        : (F == GRIM_FMT_BF16 ? (k0) * 2 : (k0));                               \
         _Pragma("unroll") for (int ni = 0; ni < 2; ++ni) {                                      \
             _Pragma("unroll") for (int q = 0; q < BQ; ++q)                                      \
                 (R).b[ni][q] = __builtin_amdgcn_raw_buffer_load_b128(rB, b_off[ni] + 16 * q, kw_, 0); \
             if constexpr (F == GRIM_FMT_MXFP4)                                                  \
                 (R).s[ni] = __builtin_amdgcn_raw_buffer_load_b8(rS, s_off[ni], (k0) / 32, 0);    \
+            if constexpr (F == kGemmFmtS4)                                                      \
+                (R).s[ni] = __builtin_amdgcn_raw_buffer_load_b16(rS, s_off[ni], ((k0) / group) * 2, 0); \
         }                                                                                       \
     } while (0)
 #define GRIM_STORE_A(R, buf)                                                                    \
@@ -240,13 +265,20 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, const GemmSrc& w, b
         }                                                                                       \
     } while (0)
 
-    f32x16 acc[4][2];
+    // acc: the tile's sums.  Group-scaled formats multiply codes in gacc and
+    // fold gacc x the group's per-column scale into acc after each group
+    // (each lane's accumulators all belong to the two columns it owns).
+    f32x16 acc[4][2], gacc[4][2];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.0f;
+            for (int v = 0; v < 16; ++v) {
+                acc[mi][ni][v] = 0.0f;
+                gacc[mi][ni][v] = 0.0f;
+            }
+    f32x16 (&mt)[4][2] = kGroupScaled ? gacc : acc;   // the MFMA target
 
 // A fragments of step ks are read from LDS while step ks - 1 multiplies
 // (two fragment sets), so LDS latency hides behind the MFMAs.
@@ -277,10 +309,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, const GemmSrc& w, b
             _Pragma("unroll") for (int ni = 0; ni < 2; ++ni) {                                  \
                 const bf16x8 bb = (ks & 1) ? fb1[ni] : fb0[ni];                                 \
                 const bf16x8 ah = (ks & 1) ? fa1[0][mi] : fa0[0][mi];                           \
-                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bb, acc[mi][ni], 0, 0, 0); \
+                mt[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bb, mt[mi][ni], 0, 0, 0);    \
                 if constexpr (APAIR) {                                                          \
                     const bf16x8 al = (ks & 1) ? fa1[1][mi] : fa0[1][mi];                       \
-                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bb, acc[mi][ni], 0, 0, 0); \
+                    mt[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bb, mt[mi][ni], 0, 0, 0); \
                 }                                                                               \
             }                                                                                   \
             /* interleave: the next step's LDS reads and conversions between   */               \
@@ -289,6 +321,22 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, const GemmSrc& w, b
                 __builtin_amdgcn_sched_group_barrier(0x008, APAIR ? 2 : 1, 0);                  \
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                              \
                 __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);                              \
+            }                                                                                   \
+        }                                                                                       \
+    } while (0)
+
+#define GRIM_FOLD(RB, t)                                                                        \
+    do {                                                                                        \
+        if constexpr (kGroupScaled) {                                                           \
+            if (((t) + 1) % gk == 0) {                                                          \
+                _Pragma("unroll") for (int ni = 0; ni < 2; ++ni) {                              \
+                    const float sc_ = bf16_to_f32(uint16_t((RB).s[ni]));                        \
+                    _Pragma("unroll") for (int mi = 0; mi < 4; ++mi)                            \
+                    _Pragma("unroll") for (int v = 0; v < 16; ++v) {                            \
+                        acc[mi][ni][v] = __builtin_fmaf(sc_, gacc[mi][ni][v], acc[mi][ni][v]);   \
+                        gacc[mi][ni][v] = 0.0f;                                                 \
+                    }                                                                           \
+                }                                                                               \
             }                                                                                   \
         }                                                                                       \
     } while (0)
@@ -311,11 +359,13 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, const GemmSrc& w, b
     int kt = 0;
     for (; kt + 2 <= nk; kt += 2) {
         GRIM_MMA_TILE(0, RB0);
+        GRIM_FOLD(RB0, kt);
         if (kt + 2 < nk) GRIM_LOAD_B(RB0, (kt + 2) * BK);
         GRIM_STORE_A(RA1, 1);
         if (kt + 3 < nk) GRIM_LOAD_A(RA1, (kt + 3) * BK);
         lds_barrier();
         GRIM_MMA_TILE(1, RB1);
+        GRIM_FOLD(RB1, kt + 1);
         if (kt + 3 < nk) GRIM_LOAD_B(RB1, (kt + 3) * BK);
         if (kt + 2 < nk) {
             GRIM_STORE_A(RA0, 0);
@@ -323,11 +373,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, const GemmSrc& w, b
         }
         lds_barrier();
     }
-    if (kt < nk) GRIM_MMA_TILE(0, RB0);
+    if (kt < nk) {
+        GRIM_MMA_TILE(0, RB0);
+        GRIM_FOLD(RB0, kt);
+    }
 #undef GRIM_LOAD_A
 #undef GRIM_LOAD_B
 #undef GRIM_STORE_A
 #undef GRIM_MMA_TILE
+#undef GRIM_FOLD
 #undef GRIM_READ_A
 
     // ---- epilogue.  acc[mi][ni][v]: row = mi*32 + (v&3) + 4*(lane>>5) +
@@ -359,9 +413,13 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, const GemmSrc& w, b
                 lo_v[mi][v] = f32_to_bf16(hv - bf16_to_f32(hi));
                 st16[r * SP16 + hcl] = hi;
             }
-        uint16_t* o = static_cast<uint16_t*>(out) + arow0 * 2 * int64_t(g.I);
+        // h as a bf16 pair plane by plane [R][2][I], or (OUT_BF16) plain
+        // bf16 [R][I] (the hi plane alone)
+        constexpr int kPlanes = OUT_BF16 ? 1 : 2;
+        const int ostride = kPlanes * g.I;
+        uint16_t* o = static_cast<uint16_t*>(out) + arow0 * int64_t(ostride);
 #pragma unroll
-        for (int plane = 0; plane < 2; ++plane) {
+        for (int plane = 0; plane < kPlanes; ++plane) {
             if (plane == 1) {
                 lds_barrier();
 #pragma unroll
@@ -379,7 +437,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, const GemmSrc& w, b
                 const int r = c >> 4, part = c & 15;
                 const int col = hc0 + part * 8;
                 if (r < rows_valid && col < g.I)
-                    *reinterpret_cast<u32x4*>(o + r * 2 * g.I + plane * g.I + col) =
+                    *reinterpret_cast<u32x4*>(o + r * ostride + plane * g.I + col) =
                         *reinterpret_cast<const u32x4*>(&st16[r * SP16 + part * 8]);
             }
         }
@@ -492,7 +550,9 @@ static hipError_t launch_fmt(hipStream_t st, const GemmArgs& g) {
     const int ntiles = g.swiglu ? (g.I + BN / 2 - 1) / (BN / 2) : (g.N + BN - 1) / BN;
     const int my_max = g.tmax + (g.T_sh > 0 ? (g.T_sh + BM - 1) / BM : 0);
     if (my_max <= 0 || ntiles <= 0) return hipSuccess;
-    if (g.swiglu) return launch_kernel<F, true, false, false>(st, g, ntiles);
+    if (g.swiglu)
+        return g.out_bf16 ? launch_kernel<F, true, false, true>(st, g, ntiles)
+                          : launch_kernel<F, true, false, false>(st, g, ntiles);
     if (g.a_pair)
         return g.out_bf16 ? launch_kernel<F, false, true, true>(st, g, ntiles)
                           : launch_kernel<F, false, true, false>(st, g, ntiles);
@@ -501,7 +561,7 @@ static hipError_t launch_fmt(hipStream_t st, const GemmArgs& g) {
 }
 
 bool gemm_format_ok(int fmt) {
-    return fmt == GRIM_FMT_INT8 || fmt == GRIM_FMT_MXFP4 || fmt == GRIM_FMT_BF16;
+    return fmt == GRIM_FMT_INT8 || fmt == GRIM_FMT_MXFP4 || fmt == GRIM_FMT_BF16 || fmt == kGemmFmtS4;
 }
 
 hipError_t gemm_launch(hipStream_t st, int fmt, const GemmArgs& g) {
@@ -509,6 +569,7 @@ hipError_t gemm_launch(hipStream_t st, int fmt, const GemmArgs& g) {
     case GRIM_FMT_INT8: return launch_fmt<GRIM_FMT_INT8>(st, g);
     case GRIM_FMT_MXFP4: return launch_fmt<GRIM_FMT_MXFP4>(st, g);
     case GRIM_FMT_BF16: return launch_fmt<GRIM_FMT_BF16>(st, g);
+    case kGemmFmtS4: return launch_fmt<kGemmFmtS4>(st, g);
     }
     return hipErrorInvalidValue;
 }

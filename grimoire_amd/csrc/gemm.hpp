@@ -24,6 +24,10 @@ struct GemmArgs {
 };
 
 constexpr int kGemmBM = 128;
+// Bridge-only weight format of the grouped GEMM: signed 4-bit codes
+// [N][K/2] (low nibble = even K), bf16 group scales [N][K/G] with G a
+// multiple of 64 (row_scales = K / G).  src/xe2_grouped_bridge.hpp:22.
+constexpr int kGemmFmtS4 = 100;
 
 bool gemm_format_ok(int fmt);
 hipError_t gemm_launch(hipStream_t st, int fmt, const GemmArgs& g);

@@ -172,3 +172,33 @@ class MoeForward:
                                          _p(out_expert), _p(out_weight), self.regime,
                                          _p(self.workspace), self.workspace.numel()),
               "moe_forward")
+
+
+# ------------------------------------------------------------------ bridges
+# Same symbols and argument order as the reference's dlopen'd bridges, with
+# a stream in place of the SYCL queue.  They return nothing (as the
+# reference's); a rejected call leaves its reason in
+# grimoire_moe_last_error() and writes no output.
+
+def xe2_grouped_mxfp4_bf16(a, b, scales, d, n, k, rows_per_expert, num_experts, stream=None):
+    """grimoire_xe2_grouped_mxfp4_bf16 (src/xe2_grouped_bridge.cpp:135)."""
+    _dev(a)
+    lib().grimoire_xe2_grouped_mxfp4_bf16(_stream(stream), _p(a), _p(b), _p(scales), _p(d), n, k,
+                                          _p(rows_per_expert), None, num_experts, None)
+
+
+def xe2_grouped_w4a16(a, b, scales, d, n, k, rows_per_expert, num_experts, group_size,
+                      stream=None):
+    """grimoire_xe2_grouped_w4a16 (src/xe2_grouped_bridge.hpp:22)."""
+    _dev(a)
+    lib().grimoire_xe2_grouped_w4a16(_stream(stream), _p(a), _p(b), _p(scales), _p(d), n, k,
+                                     _p(rows_per_expert), None, num_experts, group_size, None)
+
+
+def xe2_fused_moe_gate_up_mxfp4_silu_bf16(a, b, scales, d, n, k, rows_per_expert, num_experts,
+                                          stream=None):
+    """grimoire_xe2_fused_moe_gate_up_mxfp4_silu_bf16 (src/xe2_fused_moe_bridge.cpp:32)."""
+    _dev(a)
+    lib().grimoire_xe2_fused_moe_gate_up_mxfp4_silu_bf16(_stream(stream), _p(a), _p(b),
+                                                         _p(scales), _p(d), n, k,
+                                                         _p(rows_per_expert), num_experts, None)
