@@ -58,6 +58,7 @@ struct Plan {
     // GEMV
     float* h;
     uint32_t* hf;   // decode: h in the staged layout
+    uint32_t* xf;   // decode: x formatted for the wave-centric gate_up
     // GEMM
     void* disp_ws;
     int32_t *counts, *offsets, *inverse, *tile_e, *tile_mb;
@@ -79,6 +80,7 @@ size_t carve(const grim_moe_layer* L, int T, bool gemv, char* base, Plan& p) {
     if (gemv) {
         p.h = cv.take<float>(size_t(T) * (K + (sh ? 1 : 0)) * I);
         p.hf = cv.take<uint32_t>(size_t(T) * fmt_words((K + (sh ? 1 : 0)) * I));
+        p.xf = cv.take<uint32_t>(size_t(T) * xf_words(H));
     } else {
         const size_t dws = dispatch_workspace_bytes(T, K, E);
         p.disp_ws = cv.take<char>(dws);
@@ -129,6 +131,13 @@ extern "C" int grimoire_moe_route_grouped(void*, const float*, const int32_t*, u
 extern "C" const char* grimoire_moe_last_error(void);
 
 static int ferr(int code, const char* msg);
+
+#ifdef GRIM_TIMING
+static unsigned long long* g_timing = nullptr;
+extern "C" __attribute__((visibility("default"))) void grim_timing_set(void* p) {
+    g_timing = static_cast<unsigned long long*>(p);
+}
+#endif
 
 extern "C" int grimoire_moe_forward(void* stream, const grim_moe_layer* L,
                                     const grim_route_params* rp, const uint16_t* shared_gate_w,
@@ -203,9 +212,23 @@ extern "C" int grimoire_moe_forward(void* stream, const grim_moe_layer* L,
         a.M = tokens;
         a.fmt_h = 1;
         a.route_topk = 1;
+#ifdef GRIM_TIMING
+        a.ts = g_timing;
+#endif
         if (L->gate_up.fmt != L->down.fmt) {
             // two formats: the roles need one kernel instantiation each
             return ferr(GRIM_ERR_FORMAT, "decode needs gate_up and down in one format");
+        }
+        {
+            const int f = L->gate_up.fmt;
+            const bool wave_fmt = f == GRIM_FMT_INT4 || f == GRIM_FMT_INT4_F16 || f == GRIM_FMT_MXFP4;
+            // formatting runs in the router launch: a quad of threads per
+            // chunk, at most 64 chunks per router work-group
+            const int chunks = tokens * (H / 32);
+            if (wave_fmt && H % 32 == 0 && H <= 8192 && I % 8 == 0 && (chunks + E - 1) / E <= 64) {
+                a.xf = p.xf;
+                a.xf_words = xf_words(H);
+            }
         }
         decode_plan(L->gate_up.fmt, a, kRoleRouter | kRoleGateUp | kRoleDown);
         if (decode_lds_bytes(L->gate_up.fmt, a) > 160 * 1024)

@@ -55,7 +55,20 @@ void decode_plan(int fmt, DecodeArgs& a, int roles) {
     a.lpr_gu = lpr_gate_up(a.H / CH);
     a.lpr_dn = lpr_down(a.I / CH);
     a.gu_rb = (a.I + gu_rows_per_block(a.lpr_gu) - 1) / gu_rows_per_block(a.lpr_gu);
+    if (a.xf) {
+        // wave-centric gate_up: 4 waves x RU rows (RU 4 for one chunk iteration, else 2)
+        const int nci = (a.H / 32 + kWave - 1) / kWave;
+        const int rb = kGemvWaves * (nci == 1 ? 4 : 2);
+        a.gu_rb = (a.I + rb - 1) / rb;
+    }
     a.dn_rb = down_rows_per_block(a.lpr_dn, KS);
+    a.dn_wave = 0;
+    if (a.xf && KS <= 8 && a.I % 32 == 0 && a.I <= 4096) {
+        // wave-centric down: 2 * RH rows per work-group, RH 4 for one chunk
+        // iteration (I <= 1024), else 2
+        a.dn_wave = 1;
+        a.dn_rb = (a.I / 32 + 31) / 32 == 1 ? 8 : 4;
+    }
     a.NR = (roles & kRoleRouter) ? a.E : 0;
     a.NG = (roles & kRoleGateUp) ? a.M * KS * a.gu_rb : 0;
     a.ND = (roles & kRoleDown) ? a.M * ((a.H + a.dn_rb - 1) / a.dn_rb) : 0;
@@ -69,8 +82,8 @@ size_t decode_lds_bytes(int fmt, const DecodeArgs& a) {
     auto act = [&](size_t n) { return (n + n / CH) * sizeof(uint32_t); };
     size_t b = 0;
     if (a.NR) b = std::max(b, size_t(kGemvWaves) * (512 + 64) * sizeof(float));
-    if (a.NG) b = std::max(b, act(size_t(a.H)));
-    if (a.ND) b = std::max(b, act(size_t(KS) * a.I) + size_t(KS) * a.dn_rb * sizeof(float));
+    if (a.NG && !a.xf) b = std::max(b, act(size_t(a.H)));
+    if (a.ND && !a.dn_wave) b = std::max(b, act(size_t(KS) * a.I) + size_t(KS) * a.dn_rb * sizeof(float));
     return b;
 }
 

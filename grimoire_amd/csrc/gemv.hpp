@@ -36,11 +36,23 @@ struct DecodeArgs {
     int NR, NG, ND;
     int fmt_h;                // gate_up writes hf, down stages hf (else plain h)
     int route_topk;           // gate_up items compute the top-k from logits (and store rex/rwt)
+    unsigned long long* ts;   // phase timestamps (GRIM_TIMING builds only), else null
+    // wave-centric gate_up (INT4 / MXFP4): the router kernel writes the
+    // activations formatted once (xf, xf_words per token), gate_up lanes read
+    // their chunks from it directly
+    uint32_t* xf;
+    int xf_words;
+    int dn_wave;              // wave-centric down (one wave per slot)
 };
 
 // Words per token of the formatted h (n = KS * I elements):
 // the staged planes, one fp32 sum per group of eight, padded to 16 bytes.
 __host__ __device__ constexpr int fmt_words(int n) { return (n + n / 8 + 3) & ~3; }
+
+// Words per token of the formatted activations for the wave-centric gate_up
+// (32-element chunks, H = 32 * C): hi plane [H/2], lo plane [H/2], then
+// (sum, lo-nonzero flag) per chunk, padded to 16 bytes.
+__host__ __device__ constexpr int xf_words(int H) { return (H + 2 * (H / 32) + 3) & ~3; }
 
 constexpr int kRoleRouter = 1, kRoleGateUp = 2, kRoleDown = 4;
 

@@ -27,6 +27,17 @@
 
 namespace grim {
 
+// Phase timestamps for kernel studies: compiled in only with GRIM_TIMING.
+#ifdef GRIM_TIMING
+#define GRIM_TS(a, role, i)                                                          \
+    do {                                                                             \
+        if ((a).ts && threadIdx.x == 0 && blockIdx.x < 2048)                          \
+            (a).ts[((role) * 2048 + blockIdx.x) * 8 + (i)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define GRIM_TS(a, role, i) do {} while (0)
+#endif
+
 constexpr int kGemvThreads = 256;
 constexpr int kGemvWaves = kGemvThreads / kWave;
 constexpr int kMaxJ = 4;          // chunk iterations prefetched per batch
@@ -223,6 +234,136 @@ __device__ __forceinline__ bool stage_fmt(const uint32_t* __restrict__ src, int 
     return any_lo != 0;
 }
 
+
+// Activation staging split in two halves, so that the global loads can be
+// issued together with the routing loads and the LDS formatting can run
+// while the weight loads are in flight.  kXG groups of eight per thread
+// cover n <= 8192; out-of-range groups reload the thread's first group
+// (clamped address, no branch around the load).
+constexpr int kXG = 4;
+struct XRegs {
+    float4 p[kXG], q[kXG];
+};
+
+__device__ __forceinline__ void x_load(const float* __restrict__ src, int n, XRegs& r) {
+    const int ng = n / 8;
+    const int tid = threadIdx.x;
+    const int g_safe = tid < ng ? tid : ng - 1;
+    const float4* s4 = reinterpret_cast<const float4*>(src);
+#pragma unroll
+    for (int b = 0; b < kXG; ++b) {
+        const int g = tid + b * kGemvThreads;
+        const int gi = g < ng ? g : g_safe;
+        r.p[b] = s4[2 * gi];
+        r.q[b] = s4[2 * gi + 1];
+    }
+}
+
+// Format the loaded groups into LDS (layout of stage_act); returns whether
+// any lo half is non-zero (block-uniform).  Ends with a barrier.
+template <int F>
+__device__ __forceinline__ bool x_store(const XRegs& r, int n, uint32_t* lds) {
+    int any_lo = 0;
+    float* sums = reinterpret_cast<float*>(lds + n);
+    const int ng = n / 8;
+    const int nch = n / Chunk<F>::CH;
+#pragma unroll
+    for (int b = 0; b < kXG; ++b) {
+        if (b * kGemvThreads >= ng) break;   // block-uniform
+        const int gi = b * kGemvThreads + int(threadIdx.x);
+        const int g = gi < ng ? gi : -1;
+        float part = 0.0f;
+        if (g >= 0) {
+            const float v[8] = {r.p[b].x, r.p[b].y, r.p[b].z, r.p[b].w,
+                                r.q[b].x, r.q[b].y, r.q[b].z, r.q[b].w};
+            if constexpr (Act<F>::kPair) {
+                uint32_t hw[4], lw[4];
+                part = format_group<F>(v, hw, lw, any_lo);
+                const int qp = quad_pos<F>(g, nch);
+                reinterpret_cast<u32x4*>(lds)[qp] = u32x4{hw[0], hw[1], hw[2], hw[3]};
+                reinterpret_cast<u32x4*>(lds + n / 2)[qp] = u32x4{lw[0], lw[1], lw[2], lw[3]};
+            } else {
+                reinterpret_cast<float4*>(lds)[quad_pos<F>(2 * g, nch)] = r.p[b];
+                reinterpret_cast<float4*>(lds)[quad_pos<F>(2 * g + 1, nch)] = r.q[b];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) part += v[i];
+            }
+        }
+        chunk_sum_out<F>(part, g, sums);
+    }
+    if constexpr (Act<F>::kPair) any_lo = __syncthreads_or(any_lo);
+    else __syncthreads();
+    return any_lo != 0;
+}
+
+// The formatted h of one token (n elements: nq = n / 4 quads of planes,
+// then n / 8 group sums), same two halves: the first kHQ quads and kHQ / 2
+// sums per thread are loaded up front; h_store writes them and copies any
+// remainder with ordinary loads.
+constexpr int kHQ = 8;
+struct HRegs {
+    u32x4 v[kHQ];
+    float s[kHQ / 2];
+};
+
+__device__ __forceinline__ void h_load(const uint32_t* __restrict__ src, int n, HRegs& r) {
+    const int nq = n / 4, ng = n / 8;
+    const int tid = threadIdx.x;
+    const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
+    const float* ps = reinterpret_cast<const float*>(src) + n;
+    const int q_safe = tid < nq ? tid : nq - 1;
+    const int g_safe = tid < ng ? tid : ng - 1;
+#pragma unroll
+    for (int b = 0; b < kHQ; ++b) {
+        const int q = tid + b * kGemvThreads;
+        r.v[b] = s4[q < nq ? q : q_safe];
+    }
+#pragma unroll
+    for (int c = 0; c < kHQ / 2; ++c) {
+        const int g = tid + c * kGemvThreads;
+        r.s[c] = ps[g < ng ? g : g_safe];
+    }
+}
+
+template <int F>
+__device__ __forceinline__ bool h_store(const HRegs& r, const uint32_t* __restrict__ src, int n,
+                                        uint32_t* lds) {
+    const int nq = n / 4, ng = n / 8;
+    const int lo_q = Act<F>::kPair ? n / 8 : nq;   // first quad of the lo plane
+    const int tid = threadIdx.x;
+    float* sums = reinterpret_cast<float*>(lds + n);
+    int any_lo = 0;
+#pragma unroll
+    for (int b = 0; b < kHQ; ++b) {
+        const int q = tid + b * kGemvThreads;
+        if (q < nq) {
+            reinterpret_cast<u32x4*>(lds)[q] = r.v[b];
+            if (q >= lo_q) any_lo |= int((r.v[b].x | r.v[b].y | r.v[b].z | r.v[b].w) != 0);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < kHQ / 2; ++c) {
+        if (c * kGemvThreads >= ng) break;   // block-uniform
+        const int g = tid + c * kGemvThreads;
+        chunk_sum_out<F>(g < ng ? r.s[c] : 0.0f, g < ng ? g : -1, sums);
+    }
+    // remainder (long h vectors)
+    const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
+    for (int q = kHQ * kGemvThreads + tid; q < nq; q += kGemvThreads) {
+        const u32x4 v = s4[q];
+        reinterpret_cast<u32x4*>(lds)[q] = v;
+        if (q >= lo_q) any_lo |= int((v.x | v.y | v.z | v.w) != 0);
+    }
+    const float* ps = reinterpret_cast<const float*>(src) + n;
+    for (int g0 = (kHQ / 2) * kGemvThreads; g0 < ng; g0 += kGemvThreads) {
+        const int g = g0 + tid;
+        chunk_sum_out<F>(g < ng ? ps[g] : 0.0f, g < ng ? g : -1, sums);
+    }
+    if constexpr (Act<F>::kPair) any_lo = __syncthreads_or(any_lo);
+    else __syncthreads();
+    return any_lo != 0;
+}
+
 template <int F>
 __host__ __device__ constexpr int act_words(int n) {
     // LDS words of a staged vector of n elements (pairs or fp32, + sums)
@@ -245,7 +386,12 @@ __device__ __forceinline__ void prefetch(const WView& w, int64_t row, int c, Pre
     if constexpr (F == GRIM_FMT_INT4 || F == GRIM_FMT_INT4_F16) {
         const int64_t si = row * w.row_scales + ((c * 32) >> w.gshift);
         p.sb = static_cast<const uint16_t*>(w.scales)[si];
-        p.zb = w.zeros ? uint32_t(w.zeros[si]) : uint32_t(w.default_zero);
+        // no branch around the load (a branch makes the compiler wait for
+        // the loads before it): without zeros, read a payload byte and
+        // substitute the default
+        const bool hz = w.zeros != nullptr;
+        const uint32_t zl = (hz ? w.zeros : w.payload)[hz ? si : 0];
+        p.zb = hz ? zl : uint32_t(w.default_zero);
     } else if constexpr (F == GRIM_FMT_MXFP4) {
         p.sb = static_cast<const uint8_t*>(w.scales)[row * w.row_scales + c];
     } else if constexpr (F == GRIM_FMT_INT8) {
@@ -415,25 +561,33 @@ __device__ __forceinline__ void gate_up_item(const DecodeArgs& a, int j, uint32_
     const int i0 = rb * RB + (wave * GPW + lane / LPR) * RU;
     const float* xt = a.x + int64_t(t) * H;
     float* ht = a.h + (int64_t(t) * KS + slot) * I;
+    GRIM_TS(a, 1, 0);
 
-    const bool shr = SH && slot >= K;
+    // (1) everything that does not depend on the routing is requested at
+    // once: the token's activations and (RT) its router logits
+    XRegs xr;
+    x_load(xt, H, xr);
+    const bool shr = SH && slot >= K;   // block-uniform
     int64_t gbase = 0;
     bool active = true;
     if constexpr (RT) {
-        // the token's top-k from the router logits of the previous launch,
-        // by wave 0; the first item of the token also stores the routes
+        // (2) the token's top-k from the router logits of the previous
+        // launch; the first item of the token also stores the routes
         __shared__ int sel_e[16];
         __shared__ float sel_w[16];
         __shared__ float tk_scratch[512 + 64];
-        if (wave == 0 && !shr)
-            topk_wave(a.logits + int64_t(t) * a.E, a.E, K, a.mode, a.normalize, a.scaling, a.bias16,
-                      a.bias32, a.n_group, a.topk_group, sel_e, sel_w, tk_scratch, tk_scratch + 512);
-        __syncthreads();
-        if (slot == 0 && rb == 0 && int(threadIdx.x) < K) {
-            a.rex[int64_t(t) * K + threadIdx.x] = sel_e[threadIdx.x];
-            a.rwt[int64_t(t) * K + threadIdx.x] = sel_w[threadIdx.x];
-        }
         if (!shr) {
+            float lv[kMaxV];
+            if (wave == 0) {
+                topk_load(a.logits + int64_t(t) * a.E, a.E, lv);
+                topk_wave_regs(lv, a.E, K, a.mode, a.normalize, a.scaling, a.bias16, a.bias32,
+                               a.n_group, a.topk_group, sel_e, sel_w, tk_scratch, tk_scratch + 512);
+            }
+            __syncthreads();
+            if (slot == 0 && rb == 0 && int(threadIdx.x) < K) {
+                a.rex[int64_t(t) * K + threadIdx.x] = sel_e[threadIdx.x];
+                a.rwt[int64_t(t) * K + threadIdx.x] = sel_w[threadIdx.x];
+            }
             const int e = sel_e[slot];
             if (e < 0 || e >= a.E) active = false;
             gbase = int64_t(e) * 2 * I;
@@ -443,24 +597,29 @@ __device__ __forceinline__ void gate_up_item(const DecodeArgs& a, int j, uint32_
         if (e < 0 || e >= a.E) active = false;   // route not computed here: h = 0
         gbase = int64_t(e) * 2 * I;
     }
+    GRIM_TS(a, 1, 1);
+    // (3) this item's weights, all requested before anything waits on them
     const WView v = (SH && shr) ? a.sgu : a.gu;
+    if (!active) gbase = 0;   // rows of expert 0 are read and discarded
     float ga[RU], ua[RU];
     Pre cur[2][RU];
 #pragma unroll
     for (int r = 0; r < RU; ++r) {
         ga[r] = 0.0f;
         ua[r] = 0.0f;
-        if (active && sub < C) {
-            const int i = i0 + r < I ? i0 + r : I - 1;
-            prefetch<F>(v, gbase + i, sub, cur[0][r]);
-            prefetch<F>(v, gbase + I + i, sub, cur[1][r]);
-        }
+        const int i = i0 + r < I ? i0 + r : I - 1;
+        const int c = sub < C ? sub : 0;
+        prefetch<F>(v, gbase + i, c, cur[0][r]);
+        prefetch<F>(v, gbase + I + i, c, cur[1][r]);
     }
-    const bool lo_pass = stage_act<F>(xt, H, lds);   // overlaps the first loads
+    // (4) the activations into LDS while the weights are in flight
+    const bool lo_pass = x_store<F>(xr, H, lds);
+    GRIM_TS(a, 1, 2);
     if (active) {
         if (lo_pass) gate_up_rows<F, LPR, true>(v, gbase, i0, I, C, sub, lds, H, cur, ga, ua);
         else gate_up_rows<F, LPR, false>(v, gbase, i0, I, C, sub, lds, H, cur, ga, ua);
     }
+    GRIM_TS(a, 1, 3);
     __shared__ float hrow[kGemvWaves * kWave / 8 * RU];   // this item's RB rows (fmt_h)
 #pragma unroll
     for (int r = 0; r < RU; ++r) {
@@ -494,7 +653,7 @@ __device__ __forceinline__ void gate_up_item(const DecodeArgs& a, int j, uint32_
         acc = group_sum<kWave>(acc);
         if (lane == 0) a.gate[t] = det_sigmoid(acc);
     }
-    __syncthreads();
+    GRIM_TS(a, 1, 4);
 }
 
 // Weight chunks of one batch of down rows: up to kDnBatch chunks per lane
@@ -505,12 +664,15 @@ template <int F, int LPR>
 __device__ __forceinline__ void down_issue(const DecodeArgs& a, const bool* pvalid,
                                            const bool* pshared, const int64_t* wrow, int C,
                                            int c0, Pre (&w)[kDnBatch][kPairsDN]) {
+    // clamped addresses instead of branches around the loads (chunks past
+    // the row end and invalid pairs are loaded and never used)
 #pragma unroll
     for (int b = 0; b < kDnBatch; ++b) {
         const int c = c0 + b * LPR;
+        const int cc = c < C ? c : C - 1;
 #pragma unroll
         for (int q = 0; q < kPairsDN; ++q)
-            if (c < C && pvalid[q]) prefetch<F>(pshared[q] ? a.sdn : a.dn, wrow[q], c, w[b][q]);
+            prefetch<F>(pshared[q] ? a.sdn : a.dn, pvalid[q] ? wrow[q] : 0, cc, w[b][q]);
     }
 }
 
@@ -556,16 +718,24 @@ __device__ __forceinline__ void down_item(const DecodeArgs& a, int j, uint32_t* 
     float* part = reinterpret_cast<float*>(lds + act_words<F>(n));   // [KS][RB]
     __shared__ float slot_w[32];   // routed weight per slot, 0 = skipped
     __shared__ int slot_e[32];     // expert per slot, -1 = skipped
+    GRIM_TS(a, 2, 0);
 
-    // routes come from an earlier launch: plain loads, one round trip
-    if (int(threadIdx.x) < K) {
-        const int e = a.rex[int64_t(t) * K + threadIdx.x];
-        const float rw = a.rwt[int64_t(t) * K + threadIdx.x];
-        const bool ok = e >= 0 && e < E && rw != 0.0f;
-        slot_w[threadIdx.x] = ok ? rw : 0.0f;
-        slot_e[threadIdx.x] = ok ? e : -1;
+    // (1) routes (earlier launch) and the token's h requested together
+    HRegs hr;
+    const uint32_t* hsrc = a.hf + int64_t(t) * fmt_words(n);
+    if (a.fmt_h) h_load(hsrc, n, hr);
+    {
+        const int s = int(threadIdx.x) < K ? int(threadIdx.x) : 0;
+        const int e = a.rex[int64_t(t) * K + s];
+        const float rw = a.rwt[int64_t(t) * K + s];
+        if (int(threadIdx.x) < K) {
+            const bool ok = e >= 0 && e < E && rw != 0.0f;
+            slot_w[threadIdx.x] = ok ? rw : 0.0f;
+            slot_e[threadIdx.x] = ok ? e : -1;
+        }
     }
     __syncthreads();
+    GRIM_TS(a, 2, 1);
     int pslot[NP], prow[NP];
     int64_t wrow[NP];
     bool pshared[NP], pvalid[NP];
@@ -588,12 +758,13 @@ __device__ __forceinline__ void down_item(const DecodeArgs& a, int j, uint32_t* 
     Pre w[kDnBatch][NP];
 #pragma unroll
     for (int q = 0; q < NP; ++q) acc[q] = 0.0f;
+    // (2) the first batch of weights, then h into LDS while they fly
     down_issue<F, LPR>(a, pvalid, pshared, wrow, C, sub, w);
-    // h[t] into LDS while the first weights are in flight
     float gate_sh = 1.0f;
     if (SH && a.gate_in && int(threadIdx.x) < RB) gate_sh = a.gate_in[t];
-    const bool lo_pass = a.fmt_h ? stage_fmt<F>(a.hf + int64_t(t) * fmt_words(n), n, lds)
+    const bool lo_pass = a.fmt_h ? h_store<F>(hr, hsrc, n, lds)
                                   : stage_act<F, 4>(a.h + int64_t(t) * n, n, lds);
+    GRIM_TS(a, 2, 2);
     if (lo_pass) down_rows<F, LPR, true>(a, pslot, pvalid, pshared, wrow, C, sub, lds, n, w, acc);
     else down_rows<F, LPR, false>(a, pslot, pvalid, pshared, wrow, C, sub, lds, n, w, acc);
 #pragma unroll
@@ -602,6 +773,7 @@ __device__ __forceinline__ void down_item(const DecodeArgs& a, int j, uint32_t* 
         const int p = grp + q * G;
         if (sub == 0 && p < npairs) part[pslot[q] * RB + prow[q]] = pvalid[q] ? v : 0.0f;
     }
+    GRIM_TS(a, 2, 3);
     __syncthreads();
     for (int r = threadIdx.x; r < RB; r += blockDim.x) {
         const int o = o_base + r;
@@ -615,13 +787,53 @@ __device__ __forceinline__ void down_item(const DecodeArgs& a, int j, uint32_t* 
         if (SH) total = __builtin_fmaf(gate_sh, part[K * RB + r], total);
         a.y[int64_t(t) * H + o] = total;
     }
-    __syncthreads();
+    GRIM_TS(a, 2, 4);
 }
 
-// Router rows: the first launch of the decode forward.
+}  // namespace grim
+#include "gemv_wave.hpp"
+namespace grim {
+
+template <int F>
+constexpr bool kWaveGateUp = F == GRIM_FMT_INT4 || F == GRIM_FMT_INT4_F16 || F == GRIM_FMT_MXFP4;
+
+// Router rows: the first launch of the decode forward; with xf, the same
+// work-groups also format the activations for the wave-centric gate_up.
 template <int F>
 __global__ __launch_bounds__(kGemvThreads) void moe_router_kernel(DecodeArgs a) {
+    GRIM_TS(a, 0, 0);
+    if constexpr (kWaveGateUp<F>) {
+        if (a.xf && a.M == 1) {
+            // one token: the router row's loads first, the formatting of x
+            // while they fly, then the dot (router_row's arithmetic)
+            __shared__ float red[4 * kRouterTok];
+            const int e = blockIdx.x;
+            const float* wr = a.router + int64_t(e) * a.H;
+            float s;
+            if (a.H <= 2048) {
+                RouterRegs<2> rr;
+                router_row1_load(wr, a.x, a.H, rr);
+                xf_format<F>(a, blockIdx.x);
+                s = router_row1_finish(rr, a.H, red);
+            } else if (a.H <= 4096) {
+                RouterRegs<4> rr;
+                router_row1_load(wr, a.x, a.H, rr);
+                xf_format<F>(a, blockIdx.x);
+                s = router_row1_finish(rr, a.H, red);
+            } else {
+                RouterRegs<8> rr;
+                router_row1_load(wr, a.x, a.H, rr);
+                xf_format<F>(a, blockIdx.x);
+                s = router_row1_finish(rr, a.H, red);
+            }
+            if (threadIdx.x == 0) a.logits[e] = a.rbias ? s + a.rbias[e] : s;
+            GRIM_TS(a, 0, 1);
+            return;
+        }
+        if (a.xf) xf_format<F>(a, blockIdx.x);
+    }
     router_item(a, blockIdx.x);
+    GRIM_TS(a, 0, 1);
 }
 
 // The expert kernels.  gate_up: RT = the items run the top-k from the
@@ -648,13 +860,43 @@ inline hipError_t launch_t(hipStream_t st, const DecodeArgs& a) {
     gu.ND = 0;
     dn.NR = 0;
     dn.NG = 0;
-    if (a.NG && a.route_topk)
+    bool wave_done = false;
+    if constexpr (kWaveGateUp<F>) {
+        if (a.NG && a.xf) {
+            // wave-centric gate_up: NCI chunk iterations of RU rows (4 for one iteration, else 2)
+            const int nci = (a.H / 32 + kWave - 1) / kWave;
+            if (nci == 1)
+                hipLaunchKernelGGL((moe_gate_up_wave_kernel<F, 4, 1, SH>), dim3(a.NG), dim3(kGemvThreads), 0, st, a);
+            else if (nci == 2)
+                hipLaunchKernelGGL((moe_gate_up_wave_kernel<F, 2, 2, SH>), dim3(a.NG), dim3(kGemvThreads), 0, st, a);
+            else
+                hipLaunchKernelGGL((moe_gate_up_wave_kernel<F, 2, 4, SH>), dim3(a.NG), dim3(kGemvThreads), 0, st, a);
+            wave_done = true;
+        }
+    }
+    if (wave_done) {
+    } else if (a.NG && a.route_topk)
         hipLaunchKernelGGL((moe_gate_up_kernel<F, LPG, SH, true>), dim3(a.NG), dim3(kGemvThreads),
                            decode_lds_bytes(F, gu), st, a);
     else if (a.NG)
         hipLaunchKernelGGL((moe_gate_up_kernel<F, LPG, SH, false>), dim3(a.NG), dim3(kGemvThreads),
                            decode_lds_bytes(F, gu), st, a);
-    if (a.ND)
+    bool dn_done = false;
+    if constexpr (kWaveGateUp<F>) {
+        if (a.ND && a.dn_wave) {
+            const int KS = a.K + (SH ? 1 : 0);
+            const int nci = (a.I / 32 + 31) / 32;
+            const dim3 blk(KS * kWave);
+            if (nci == 1)
+                hipLaunchKernelGGL((moe_down_wave_kernel<F, 4, 1, SH>), dim3(a.ND), blk, 0, st, a);
+            else if (nci == 2)
+                hipLaunchKernelGGL((moe_down_wave_kernel<F, 2, 2, SH>), dim3(a.ND), blk, 0, st, a);
+            else
+                hipLaunchKernelGGL((moe_down_wave_kernel<F, 2, 4, SH>), dim3(a.ND), blk, 0, st, a);
+            dn_done = true;
+        }
+    }
+    if (a.ND && !dn_done)
         hipLaunchKernelGGL((moe_down_kernel<F, LPD, SH>), dim3(a.ND), dim3(kGemvThreads),
                            decode_lds_bytes(F, dn), st, a);
     return hipGetLastError();

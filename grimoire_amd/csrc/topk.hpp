@@ -62,6 +62,52 @@ __device__ __forceinline__ float router_row(const float* __restrict__ wr,
     return r;
 }
 
+// router_row for one token in two halves: every load of the row and of x
+// issued up front (NK float4 of each per thread, clamped addresses), then
+// the same FMA order and the same reduction as router_row, so both give the
+// same bits.  NK * 1024 >= H.
+template <int NK>
+struct RouterRegs {
+    float4 w[NK], x[NK];
+};
+
+template <int NK>
+__device__ __forceinline__ void router_row1_load(const float* __restrict__ wr,
+                                                 const float* __restrict__ x, int H,
+                                                 RouterRegs<NK>& r) {
+#pragma unroll
+    for (int m = 0; m < NK; ++m) {
+        const int k = int(threadIdx.x) * 4 + 1024 * m;
+        const int kk = k < H ? k : 0;
+        r.w[m] = *reinterpret_cast<const float4*>(wr + kk);
+        r.x[m] = *reinterpret_cast<const float4*>(x + kk);
+    }
+}
+
+template <int NK>
+__device__ __forceinline__ float router_row1_finish(const RouterRegs<NK>& r, int H, float* red) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    float acc = 0.0f;
+#pragma unroll
+    for (int m = 0; m < NK; ++m) {
+        const int k = int(threadIdx.x) * 4 + 1024 * m;
+        float a2 = __builtin_fmaf(r.w[m].x, r.x[m].x, acc);
+        a2 = __builtin_fmaf(r.w[m].y, r.x[m].y, a2);
+        a2 = __builtin_fmaf(r.w[m].z, r.x[m].z, a2);
+        a2 = __builtin_fmaf(r.w[m].w, r.x[m].w, a2);
+        acc = k < H ? a2 : acc;
+    }
+    const float v = group_sum<kWave>(acc);
+    if (lane == 0) red[wave * kRouterTok] = v;
+    __syncthreads();
+    float res = 0.0f;
+    if (threadIdx.x == 0)
+        res = (red[0] + red[kRouterTok]) + (red[2 * kRouterTok] + red[3 * kRouterTok]);
+    __syncthreads();
+    return res;
+}
+
 // Order-preserving 32-bit key of a score; 0 marks an empty or taken slot,
 // NaN (1) ranks below every number.
 __device__ __forceinline__ uint32_t score_key(float v) {
@@ -88,20 +134,32 @@ __device__ __forceinline__ float lane_f(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-// Top-k of one token by one wave.  mode 0: softmax (decode semantics);
-// 1: softmax batched semantics (normalize == 0 -> raw logits); 2: sigmoid +
-// bf16 bias; 3: group-limited sigmoid + fp32 bias.  Lane s ends holding
-// pick s and writes oe[s], ow[s].  gsel (512 floats) and gscore (64) are
-// this wave's LDS scratch for mode 3.  COHERENT: the logits were written by
-// other work-groups of the same launch, so they are read (and the routes
-// written) with device-coherent accesses.
-template <bool COHERENT = false>
-__device__ __forceinline__ void topk_wave(const float* __restrict__ row, int E, int K, int mode,
-                                          int normalize, float scaling,
-                                          const uint16_t* __restrict__ bias16,
-                                          const float* __restrict__ bias32, int n_group,
-                                          int topk_group, int32_t* __restrict__ oe,
-                                          float* __restrict__ ow, float* gsel_w, float* gscore_w) {
+// The logits of one token as topk_wave holds them: lane l owns experts
+// [l*V, l*V+V), V = ceil(E/64).  Loaded with clamped addresses and no
+// branch, so that the loads can be issued together with others.
+__device__ __forceinline__ void topk_load(const float* __restrict__ row, int E, float (&lv)[kMaxV]) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int V = (E + kWave - 1) / kWave;
+#pragma unroll
+    for (int j = 0; j < kMaxV; ++j) {
+        const int e = lane * V + j;
+        lv[j] = row[(j < V && e < E) ? e : 0];
+    }
+}
+
+// Top-k of one token by one wave from logits held as topk_load leaves
+// them.  mode 0: softmax (decode semantics); 1: softmax batched semantics
+// (normalize == 0 -> raw logits); 2: sigmoid + bf16 bias; 3: group-limited
+// sigmoid + fp32 bias.  Lane s ends holding pick s and writes oe[s],
+// ow[s].  gsel (512 floats) and gscore (64) are this wave's LDS scratch
+// for mode 3.
+__device__ __forceinline__ void topk_wave_regs(const float (&lv)[kMaxV], int E, int K, int mode,
+                                               int normalize, float scaling,
+                                               const uint16_t* __restrict__ bias16,
+                                               const float* __restrict__ bias32, int n_group,
+                                               int topk_group, int32_t* __restrict__ oe,
+                                               float* __restrict__ ow, float* gsel_w,
+                                               float* gscore_w) {
     const int lane = threadIdx.x & (kWave - 1);
     const int V = (E + kWave - 1) / kWave;
 
@@ -113,8 +171,7 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ row, int E, 
         key[j] = 0;
         wsrc[j] = 0.0f;
         if (j < V && e < E) {
-            const float l = COHERENT ? __hip_atomic_load(row + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                     : row[e];
+            const float l = lv[j];
             float sel;
             if (mode <= 1) {
                 sel = l;
@@ -216,15 +273,151 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ row, int E, 
         if (scaling != 1.0f) w *= scaling;
     }
     if (lane < K) {
-        if (COHERENT) {
-            __hip_atomic_store(oe + lane, my_pick, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(ow + lane, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-            oe[lane] = my_pick;
-            ow[lane] = w;
-        }
+        oe[lane] = my_pick;
+        ow[lane] = w;
     }
 }
 
+// Top-k of one token by one wave, reading its logits from memory.
+__device__ __forceinline__ void topk_wave(const float* __restrict__ row, int E, int K, int mode,
+                                          int normalize, float scaling,
+                                          const uint16_t* __restrict__ bias16,
+                                          const float* __restrict__ bias32, int n_group,
+                                          int topk_group, int32_t* __restrict__ oe,
+                                          float* __restrict__ ow, float* gsel_w, float* gscore_w) {
+    float lv[kMaxV];
+    topk_load(row, E, lv);
+    topk_wave_regs(lv, E, K, mode, normalize, scaling, bias16, bias32, n_group, topk_group, oe, ow,
+                   gsel_w, gscore_w);
+}
+
+// ---------------------------------------------------------------------
+// Block-wide top-k by parallel rank counting (modes 0-2), for latency.
+//
+// One wave running K rounds of max-and-ballot is a chain of several
+// hundred dependent instructions (~3 us on MI355X); here the ranks are
+// counted in parallel instead: rank(e) = #experts whose 64-bit key
+// (score key << 32 | ~e: larger score first, lower index on ties, the rule
+// of src/ops.cpp:1125-1131) is larger.  Work item (expert e, segment s of
+// 64 keys) per thread; a wave's 64 lanes share s, so every LDS key read is
+// a broadcast.  The weights are then formed by wave 0 with the operations
+// of topk_wave_regs in the same order (serial sums unrolled over 16 slots
+// without branches), so both give the same routes and the same bits.
+
+struct RankLds {
+    uint64_t key[512];
+    float val[512];
+    int rank[512];
+    int sel_e[16];
+    float sel_v[16];
+};
+
+template <int NT>
+__device__ __forceinline__ void topk_rank_block(const float* __restrict__ row, int E, int K, int mode,
+                                                const uint16_t* __restrict__ bias16, RankLds& L,
+                                                unsigned long long* ts = nullptr) {
+    const int tid = threadIdx.x;
+    const int Ep = (E + 63) & ~63;
+#ifdef GRIM_TIMING
+#define GRIM_TK_TS(i) if (ts && tid == 0) ts[i] = __builtin_amdgcn_s_memrealtime()
+#else
+#define GRIM_TK_TS(i) (void)ts
+#endif
+    // keys and values; padding keys are 0 (never larger than a real key)
+#pragma unroll
+    for (int q = 0; q < 512 / NT; ++q) {
+        const int e = tid + q * NT;
+        if (e < Ep) {
+            const bool ok = e < E;
+            const float l = row[ok ? e : 0];
+            float sel = l, v = l;
+            if (mode == 2) {
+                const float sc = det_sigmoid(l);
+                const float b = bias16 ? bf16_to_f32(bias16[ok ? e : 0]) : 0.0f;
+                sel = sc + b;
+                v = sc;
+            }
+            L.key[e] = ok ? (uint64_t(score_key(sel)) << 32) | uint64_t(0xFFFFFFFFu - uint32_t(e)) : 0;
+            L.val[e] = v;
+            L.rank[e] = 0;
+        }
+    }
+    if (tid < 16) { L.sel_e[tid] = -1; L.sel_v[tid] = 0.0f; }
+    __syncthreads();
+    GRIM_TK_TS(5);
+    // partial ranks over 64-key segments, four independent counters
+    const int nseg = Ep / 64;
+    for (int it = tid; it < Ep * nseg; it += NT) {
+        const int sgm = it / Ep, e = it - sgm * Ep;
+        const uint64_t me = L.key[e];
+        const uint64_t* ks = L.key + 64 * sgm;
+        int c0 = 0, c1 = 0, c2 = 0, c3 = 0;
+#pragma unroll
+        for (int f = 0; f < 64; f += 4) {
+            c0 += int(ks[f] > me);
+            c1 += int(ks[f + 1] > me);
+            c2 += int(ks[f + 2] > me);
+            c3 += int(ks[f + 3] > me);
+        }
+        const int c = (c0 + c1) + (c2 + c3);
+        if (e < E && c) atomicAdd(&L.rank[e], c);
+    }
+    __syncthreads();
+    GRIM_TK_TS(6);
+#pragma unroll
+    for (int q = 0; q < 512 / NT; ++q) {
+        const int e = tid + q * NT;
+        if (e < E) {
+            const int r = L.rank[e];
+            if (r < K && (L.key[e] >> 32) != 0) { L.sel_e[r] = e; L.sel_v[r] = L.val[e]; }
+        }
+    }
+    __syncthreads();
+#undef GRIM_TK_TS
+}
+
+// The routing weights of the picks in L (after topk_rank_block), by one
+// wave: lane s < K writes sel_e[s], sel_w[s].
+__device__ __forceinline__ void topk_rank_weights(const RankLds& L, int K, int mode, int normalize,
+                                                  float scaling, int* sel_e, float* sel_w) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const bool in = lane < K;
+    const int my_pick = lane < 16 ? L.sel_e[lane] : -1;
+    const float my_val = lane < 16 ? L.sel_v[lane] : 0.0f;
+    float w;
+    if (mode <= 1 && !(mode == 1 && !normalize)) {
+        // m = max over the K slots (fmaxf is exact, so any order gives the
+        // serial chain's value)
+        float mx = in ? my_val : -__builtin_inff();
+        mx = fmaxf(mx, dpp_f<kDppXor1>(mx));
+        mx = fmaxf(mx, dpp_f<kDppXor2>(mx));
+        mx = fmaxf(mx, dpp_f<kDppHalfMirror>(mx));
+        mx = fmaxf(mx, dpp_f<kDppMirror>(mx));
+        const float m = lane_f(mx, 0);
+        const float ev = det_expf(my_val - m);
+        float sum = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const float v = lane_f(ev, s);
+            sum += s < K ? v : 0.0f;
+        }
+        w = (normalize && sum > 0.0f) ? ev / sum : ev;
+    } else if (mode <= 1) {
+        w = my_val;
+    } else {
+        w = my_val;
+        if (normalize) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const float v = lane_f(w, s);
+                sum += s < K ? v : 0.0f;
+            }
+            if (sum > 0.0f) w /= sum;
+        }
+        if (scaling != 1.0f) w *= scaling;
+    }
+    if (in) { sel_e[lane] = my_pick; sel_w[lane] = w; }
+}
 
 }  // namespace grim
