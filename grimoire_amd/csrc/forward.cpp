@@ -18,6 +18,7 @@
 #include "common.hpp"
 #include "dispatch.hpp"
 #include "gemm.hpp"
+#include "gemm_i8.hpp"
 #include "gemv.hpp"
 #include "router.hpp"
 
@@ -65,6 +66,9 @@ struct Plan {
     int tmax;
     uint16_t *xperm, *xrow, *hp, *hp_sh;
     float *yperm, *ysh;
+    // INT8 weights: activation limbs for the int8 MFMA
+    int8_t *xq, *xrowq, *hq, *hshq;
+    float *sx, *sxrow, *sh, *shsh, *h32, *h32sh;
 };
 
 size_t carve(const grim_moe_layer* L, int T, bool gemv, char* base, Plan& p) {
@@ -96,6 +100,20 @@ size_t carve(const grim_moe_layer* L, int T, bool gemv, char* base, Plan& p) {
         p.hp_sh = sh ? cv.take<uint16_t>(size_t(T) * 2 * I) : nullptr;
         p.yperm = cv.take<float>(R * H);
         p.ysh = sh ? cv.take<float>(size_t(T) * H) : nullptr;
+        if (L->gate_up.fmt == GRIM_FMT_INT8 && L->down.fmt == GRIM_FMT_INT8) {
+            p.xq = cv.take<int8_t>(R * 2 * H);
+            p.sx = cv.take<float>(R);
+            p.h32 = cv.take<float>(R * I);
+            p.hq = cv.take<int8_t>(R * 2 * I);
+            p.sh = cv.take<float>(R);
+            if (sh) {
+                p.xrowq = cv.take<int8_t>(size_t(T) * 2 * H);
+                p.sxrow = cv.take<float>(T);
+                p.h32sh = cv.take<float>(size_t(T) * I);
+                p.hshq = cv.take<int8_t>(size_t(T) * 2 * I);
+                p.shsh = cv.take<float>(T);
+            }
+        }
     }
     return cv.off + 256;
 }
@@ -138,6 +156,87 @@ extern "C" __attribute__((visibility("default"))) void grim_timing_set(void* p) 
     g_timing = static_cast<unsigned long long*>(p);
 }
 #endif
+
+// GEMM regime for INT8 weights: the activations go to the int8 MFMA as
+// two limbs per row (gemm_i8.hip): routes -> limbs of x at the permuted rows
+// -> gate_up + SwiGLU (h fp32) -> limbs of h -> down -> combine.
+static int forward_gemm_i8(hipStream_t st, const grim_moe_layer* L, const Plan& p, const float* x,
+                           float* y, int tokens, const uint16_t* shared_gate_w) {
+    const auto& c = L->cfg;
+    const int E = c.num_experts, K = c.top_k, H = c.hidden, I = c.inter;
+    const bool sh = L->has_shared;
+    const int64_t R = int64_t(tokens) * K;
+    int r = grimoire_moe_route_grouped(st, x, p.rex, nullptr, nullptr, p.counts, p.offsets,
+                                       p.inverse, p.tile_e, p.tile_mb, p.tmax, tokens, H, E,
+                                       kGemmBM, K, nullptr, p.disp_ws,
+                                       dispatch_workspace_bytes(tokens, K, E));
+    if (r) return r;
+    hipError_t e = quant_permute_launch(st, x, tokens, H, K, p.inverse, p.xq, p.sx,
+                                        sh ? p.xrowq : nullptr, sh ? p.sxrow : nullptr);
+    if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    if (sh && shared_gate_w) {
+        e = rowdot_sigmoid_launch(st, x, shared_gate_w, p.gate, tokens, H);
+        if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    }
+    GemmI8Args g{};
+    g.w = L->gate_up.payload;
+    g.ws = static_cast<const float*>(L->gate_up.scales);
+    g.row_bytes = L->gate_up.row_bytes;
+    if (sh) {
+        g.w_sh = L->shared_gate_up.payload;
+        g.ws_sh = static_cast<const float*>(L->shared_gate_up.scales);
+        g.row_bytes_sh = L->shared_gate_up.row_bytes;
+    }
+    g.N = 2 * I;
+    g.K = H;
+    g.I = I;
+    g.swiglu = 1;
+    g.A = p.xq;
+    g.sa = p.sx;
+    g.A_sh = p.xrowq;
+    g.sa_sh = p.sxrow;
+    g.out = p.h32;
+    g.out_sh = p.h32sh;
+    g.offsets = p.offsets;
+    g.counts = p.counts;
+    g.tile_e = p.tile_e;
+    g.tile_mb = p.tile_mb;
+    g.tmax = p.tmax;
+    g.n_tiles_dev = dispatch_live_tiles(p.disp_ws, tokens, K, E);
+    g.T_sh = sh ? tokens : 0;
+    e = gemm_i8_launch(st, g);
+    if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    // h limbs (rows beyond the routed count are never read)
+    e = quant_rows_launch(st, p.h32, int(R), I, p.hq, p.sh);
+    if (e == hipSuccess && sh) e = quant_rows_launch(st, p.h32sh, tokens, I, p.hshq, p.shsh);
+    if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    GemmI8Args d = g;
+    d.w = L->down.payload;
+    d.ws = static_cast<const float*>(L->down.scales);
+    d.row_bytes = L->down.row_bytes;
+    if (sh) {
+        d.w_sh = L->shared_down.payload;
+        d.ws_sh = static_cast<const float*>(L->shared_down.scales);
+        d.row_bytes_sh = L->shared_down.row_bytes;
+    }
+    d.N = H;
+    d.K = I;
+    d.I = 0;
+    d.swiglu = 0;
+    d.A = p.hq;
+    d.sa = p.sh;
+    d.A_sh = p.hshq;
+    d.sa_sh = p.shsh;
+    d.out = p.yperm;
+    d.out_sh = p.ysh;
+    e = gemm_i8_launch(st, d);
+    if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    CombineArgs cb{p.yperm, 0, p.inverse, p.rwt, p.ysh, 0, (sh && shared_gate_w) ? p.gate : nullptr,
+                   y, tokens, K, H};
+    e = combine_launch(st, cb);
+    if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    return GRIM_OK;
+}
 
 extern "C" int grimoire_moe_forward(void* stream, const grim_moe_layer* L,
                                     const grim_route_params* rp, const uint16_t* shared_gate_w,
@@ -265,6 +364,10 @@ extern "C" int grimoire_moe_forward(void* stream, const grim_moe_layer* L,
     if (!gemm_format_ok(fu) || !gemm_format_ok(fd))
         return ferr(GRIM_ERR_FORMAT, "grouped GEMM supports int8, mxfp4 and bf16 weights");
     if (H % 64 || I % 64) return ferr(GRIM_ERR_SHAPE, "hidden and inter must be multiples of 64");
+    const bool i8 = fu == GRIM_FMT_INT8 && fd == GRIM_FMT_INT8 && p.xq &&
+                    (!sh || (L->shared_gate_up.fmt == fu && L->shared_down.fmt == fd)) &&
+                    gemm_i8_shape_ok(2 * I, H, I, 1) && gemm_i8_shape_ok(H, I, 0, 0) && I <= 4096;
+    if (i8) return forward_gemm_i8(st, L, p, x, y, tokens, shared_gate_w);
     r = grimoire_moe_route_grouped(stream, x, p.rex, p.xperm, p.xrow, p.counts, p.offsets,
                                    p.inverse, p.tile_e, p.tile_mb, p.tmax, tokens, H, E, kGemmBM, K,
                                    nullptr, p.disp_ws, dispatch_workspace_bytes(tokens, K, E));

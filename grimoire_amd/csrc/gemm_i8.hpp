@@ -1,0 +1,46 @@
+// gemm_i8.hpp -- host interface of the INT8 grouped GEMM (int8 MFMA on
+// activation limbs) and its quantisers.
+#pragma once
+
+#include "common.hpp"
+
+namespace grim {
+
+struct GemmI8Args {
+    const uint8_t* w;           // routed experts' int8 codes [E*N][row_bytes]
+    const float* ws;            // per-output-channel scales [E*N]
+    int64_t row_bytes;
+    const uint8_t* w_sh;        // shared expert [N][row_bytes_sh] (T_sh > 0)
+    const float* ws_sh;
+    int64_t row_bytes_sh;
+    int N, K, I;                // N = 2I for SwiGLU
+    int swiglu;
+    const int8_t* A;            // limbs, row r = [K/64][2][64] bytes: per 64-K block the hi
+                                // limb's 64 codes, then the lo limb's
+    const float* sa;            // row scales [R]: a = s * (hi + lo / 254)
+    const int8_t* A_sh;         // shared rows [T_sh], same layout
+    const float* sa_sh;
+    float* out;                 // SwiGLU: h [R][I]; else [R][N]
+    float* out_sh;              // same for the shared rows
+    const int32_t* offsets;     // [E]
+    const int32_t* counts;      // [E]
+    const int32_t* tile_e;      // [tmax], -1 padded (128-row m-tiles)
+    const int32_t* tile_mb;
+    int tmax;
+    const int32_t* n_tiles_dev; // live routed tile count (device) or null = tmax
+    int T_sh;                   // shared-expert rows (0 = none)
+};
+
+bool gemm_i8_shape_ok(int N, int K, int I, int swiglu);
+hipError_t gemm_i8_launch(hipStream_t st, const GemmI8Args& g);
+// src fp32 [rows][n] -> limb rows [rows][n/64][2][64] + scale [rows]
+// (n % 64 == 0, n <= 4096)
+hipError_t quant_rows_launch(hipStream_t st, const float* src, int rows, int n, int8_t* dst,
+                             float* scale);
+// token rows of x fp32 [T][n] -> limbs at their K permuted rows (inverse
+// [T][K]) and, when xrowq is given, at their own row
+hipError_t quant_permute_launch(hipStream_t st, const float* x, int T, int n, int K,
+                                const int32_t* inverse, int8_t* xq, float* sq, int8_t* xrowq,
+                                float* srow);
+
+}  // namespace grim
