@@ -117,13 +117,14 @@ def decode_bench(steps, warmup, dev, stream, regime=1):
         _replay(g_one, stream, reps1)
     one_us = t1.ms() * 1e3 / reps1
 
-    # dominant kernel: gate_up, 48 layers' launches captured alone
-    h = torch.empty(1, cfg.K, cfg.I, device=dev)
+    # dominant kernel: the forward's gate_up launch (top-k + gate_up +
+    # SwiGLU, decode stage 2), 48 layers' launches captured alone, each on
+    # the logits and activations its layer's forward left in its workspace
     gu_bytes = cfg.K * layers[0].gate_up.row_bytes_total() * 2 * cfg.I + cfg.H * 4 + cfg.K * cfg.I * 4
 
     def gu_only():
-        for L, oe in zip(layers, oes):
-            ops.launch_moe_gate_up_batched(L, oe, x, h, 1, stream=stream)
+        for f, y in zip(fwds, ys):
+            f.stage(ops.MoeForward.STAGE_GATE_UP, x, y, stream=stream)
 
     g_gu = _graph(gu_only, stream)
     _replay(g_gu, stream)
@@ -165,7 +166,8 @@ def prefill_bench(dev, stream, reps=5):
             for _ in range(reps):
                 fwd(wl.x, y, oe, ow, stream=stream)
         layer_ms = tm.ms() / reps
-        # the routed grouped GEMMs alone, on the same routing
+        # the routed grouped GEMMs alone, on the same routing: the INT8
+        # experts' path of the forward (activation limbs -> int8 MFMA)
         R = cfg.T * cfg.K
         tmax = cfg.E + (R + 127) // 128
         counts = torch.empty(cfg.E, dtype=torch.int32, device=dev)
@@ -173,24 +175,32 @@ def prefill_bench(dev, stream, reps=5):
         inverse = torch.empty(R, dtype=torch.int32, device=dev)
         te = torch.empty(tmax, dtype=torch.int32, device=dev)
         tmb = torch.empty(tmax, dtype=torch.int32, device=dev)
-        xperm = torch.empty(R, cfg.H, dtype=torch.int16, device=dev)
-        ops.launch_moe_route_grouped(wl.x, oe, xperm, None, counts, offsets, inverse, te, tmb, tmax,
+        ops.launch_moe_route_grouped(wl.x, oe, None, None, counts, offsets, inverse, te, tmb, tmax,
                                      cfg.T, cfg.H, cfg.E, 128, cfg.K, stream=stream)
-        hp = torch.empty(R, 2, cfg.I, dtype=torch.int16, device=dev)
+        rows = torch.empty(R, cfg.H, device=dev)
+        rows[inverse.long()] = wl.x.repeat_interleave(cfg.K, dim=0)
+        xq = torch.empty(R, 2 * cfg.H, dtype=torch.int8, device=dev)
+        xs = torch.empty(R, device=dev)
+        ops.quant_limbs(rows, xq, xs, stream=stream)
+        h = torch.empty(R, cfg.I, device=dev)
+        hq = torch.empty(R, 2 * cfg.I, dtype=torch.int8, device=dev)
+        hs = torch.empty(R, device=dev)
         yp = torch.empty(R, cfg.H, device=dev)
-        ops.grouped_gemm(L.gate_up, 2 * cfg.I, True, xperm, hp, offsets, counts, cfg.E, R, stream=stream)
-        ops.grouped_gemm(L.down, cfg.H, False, hp, yp, offsets, counts, cfg.E, R, a_pair=True,
-                         stream=stream)
+        ops.grouped_gemm_i8(L.gate_up, 2 * cfg.I, True, xq, xs, h, offsets, counts, cfg.E, R,
+                            stream=stream)
+        ops.quant_limbs(h, hq, hs, stream=stream)
+        ops.grouped_gemm_i8(L.down, cfg.H, False, hq, hs, yp, offsets, counts, cfg.E, R,
+                            stream=stream)
         torch.cuda.synchronize()
         with Timer(stream) as tg:
             for _ in range(reps):
-                ops.grouped_gemm(L.gate_up, 2 * cfg.I, True, xperm, hp, offsets, counts, cfg.E, R,
-                                 stream=stream)
+                ops.grouped_gemm_i8(L.gate_up, 2 * cfg.I, True, xq, xs, h, offsets, counts, cfg.E,
+                                    R, stream=stream)
         gu_ms = tg.ms() / reps
         with Timer(stream) as td:
             for _ in range(reps):
-                ops.grouped_gemm(L.down, cfg.H, False, hp, yp, offsets, counts, cfg.E, R,
-                                 a_pair=True, stream=stream)
+                ops.grouped_gemm_i8(L.down, cfg.H, False, hq, hs, yp, offsets, counts, cfg.E, R,
+                                    stream=stream)
         dn_ms = td.ms() / reps
         cnt = counts.cpu()
     touched = int((cnt > 0).sum())
@@ -209,7 +219,7 @@ def prefill_bench(dev, stream, reps=5):
         "gate_up_gemm_tflops": round(gu_flops / (gu_ms * 1e-3) / 1e12, 2),
         "down_gemm_us": round(dn_ms * 1e3, 1),
         "down_gemm_tflops": round(dn_flops / (dn_ms * 1e-3) / 1e12, 2),
-        "down_gemm_mfma_passes": 2,
+        "gemm_arithmetic": "int8 MFMA on two int8 activation limbs per row (2 passes, the cost of one bf16 pass); FLOP/s algorithmic, against the bf16 dense peak",
         "mfma_peak_tflops": BF16_MFMA_PEAK_TFLOPS,
         "gate_up_mfma_frac": round(gu_flops / (gu_ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4),
     }
@@ -295,13 +305,13 @@ def main():
         "hbm_frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "grim::moe_gate_up_kernel<64, 64, false, false> (decode gate_up + SwiGLU, "
-                      "GPTQ int4 fp16 scales, routes given), 48 layers in one graph",
+            "kernel": "grim::moe_gate_up_wave_kernel<64, 4, 1, false> (decode stage 2: top-k + "
+                      "gate_up + SwiGLU, GPTQ int4 fp16 scales), 48 layers in one graph",
             "achieved": round(d["gu_bytes"] / (d["gu_us"] * 1e-6) / 1e9, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(d["gu_bytes"] / (d["gu_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic("moe_gate_up_kernel"),
+            "traffic": measured_traffic("moe_gate_up_wave_kernel"),
             "launch_us": round(d["gu_us"], 3),
             "bytes_per_launch": int(d["gu_bytes"]),
         },

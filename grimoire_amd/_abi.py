@@ -108,11 +108,14 @@ SIGNATURES = {
     "grimoire_moe_unpermute_bf16": (I32, [P, P, P, P, P, I32, I32, I32]),
     "grimoire_moe_combine": (I32, [P, P, P, P, P, P, P, I32, I32, I32]),
     "grimoire_moe_grouped_gemm": (I32, [P, QWP, I32, I32, P, I32, P, I32, P, P, I32, I32]),
+    "grimoire_moe_quant_limbs": (I32, [P, P, I32, I32, P, P]),
+    "grimoire_moe_grouped_gemm_i8": (I32, [P, QWP, I32, I32, P, P, P, P, P, I32, I32]),
     "grimoire_xe2_grouped_mxfp4_bf16": (None, [P, P, P, P, P, I32, I32, P, P, I32, P]),
     "grimoire_xe2_grouped_w4a16": (None, [P, P, P, P, P, I32, I32, P, P, I32, I32, P]),
     "grimoire_xe2_fused_moe_gate_up_mxfp4_silu_bf16": (None, [P, P, P, P, P, I32, I32, P, I32, P]),
     "grimoire_moe_forward_workspace_bytes": (SZ, [LP, I32]),
     "grimoire_moe_forward": (I32, [P, LP, RPP, P, P, P, I32, P, P, I32, P, SZ]),
+    "grimoire_moe_decode_stage": (I32, [P, LP, RPP, P, P, P, I32, I32, P, SZ]),
 }
 
 _lib = None

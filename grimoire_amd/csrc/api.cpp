@@ -16,6 +16,7 @@
 #include "common.hpp"
 #include "dispatch.hpp"
 #include "gemm.hpp"
+#include "gemm_i8.hpp"
 #include "gemv.hpp"
 #include "router.hpp"
 
@@ -455,6 +456,57 @@ int grimoire_moe_combine(void* stream, const uint16_t* src, const int32_t* inver
                          float* dst, int tokens, int top_k, int hidden) {
     CombineArgs a{src, 1, inverse, route_weight, shared_src, 1, gate, dst, tokens, top_k, hidden};
     return combine_common(stream, a);
+}
+
+int grimoire_moe_quant_limbs(void* stream, const float* src, int rows, int n, int8_t* dst,
+                             float* scale) {
+    if (rows <= 0) return GRIM_OK;
+    if (!src || !dst || !scale) return fail(GRIM_ERR_ARG, "null pointer");
+    if (n <= 0 || n % 64 || n > 4096) return fail(GRIM_ERR_SHAPE, "n=%d: a multiple of 64, <= 4096", n);
+    return status(quant_rows_launch(S(stream), src, rows, n, dst, scale));
+}
+
+int grimoire_moe_grouped_gemm_i8(void* stream, const grim_quant_weight* w, int N, int swiglu,
+                                 const int8_t* A, const float* a_scale, float* out,
+                                 const int32_t* offsets, const int32_t* counts, int num_experts,
+                                 int total_rows) {
+    if (!w || !A || !a_scale || !out || !offsets || !counts) return fail(GRIM_ERR_ARG, "null pointer");
+    if (w->fmt != GRIM_FMT_INT8) return fail(GRIM_ERR_FORMAT, "INT8 weights only");
+    int r = check_weight(w, "grouped weight", int64_t(num_experts) * N, w->K);
+    if (r) return r;
+    if (swiglu && N % 2) return fail(GRIM_ERR_SHAPE, "swiglu needs even N");
+    if (!gemm_i8_shape_ok(N, w->K, swiglu ? N / 2 : 0, swiglu))
+        return fail(GRIM_ERR_SHAPE, "K=%d: a multiple of 64 in [192, 8192]", w->K);
+    if (total_rows <= 0) return GRIM_OK;
+    const int tmax = num_experts + (total_rows + kGemmBM - 1) / kGemmBM;
+    const size_t need = size_t(2 * tmax + 4) * sizeof(int32_t);
+    int32_t* sc = static_cast<int32_t*>(bridge_scratch(need + size_t(2 * num_experts) * 4));
+    if (!sc) return fail(GRIM_ERR_WORKSPACE, "scratch allocation failed");
+    int32_t* tile_e = sc;
+    int32_t* tile_mb = sc + tmax;
+    int32_t* n_tiles = sc + 2 * tmax;
+    int32_t* cnt2 = n_tiles + 4;
+    int32_t* off2 = cnt2 + num_experts;
+    hipLaunchKernelGGL(tiles_from_counts, dim3(1), dim3(1024), 0, S(stream), counts, num_experts,
+                       kGemmBM, cnt2, off2, tile_e, tile_mb, tmax, n_tiles);
+    GemmI8Args g{};
+    g.w = w->payload;
+    g.ws = static_cast<const float*>(w->scales);
+    g.row_bytes = w->row_bytes;
+    g.N = N;
+    g.K = w->K;
+    g.I = swiglu ? N / 2 : 0;
+    g.swiglu = swiglu;
+    g.A = A;
+    g.sa = a_scale;
+    g.out = out;
+    g.offsets = offsets;
+    g.counts = counts;
+    g.tile_e = tile_e;
+    g.tile_mb = tile_mb;
+    g.tmax = tmax;
+    g.n_tiles_dev = n_tiles;
+    return status(gemm_i8_launch(S(stream), g));
 }
 
 int grimoire_moe_grouped_gemm(void* stream, const grim_quant_weight* w, int N, int swiglu,

@@ -238,11 +238,37 @@ static int forward_gemm_i8(hipStream_t st, const grim_moe_layer* L, const Plan& 
     return GRIM_OK;
 }
 
+static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_params* rp,
+                        const uint16_t* shared_gate_w, const float* x, float* y, int tokens,
+                        int32_t* out_expert, float* out_weight, int regime, void* workspace,
+                        size_t workspace_bytes, int roles);
+
 extern "C" int grimoire_moe_forward(void* stream, const grim_moe_layer* L,
                                     const grim_route_params* rp, const uint16_t* shared_gate_w,
                                     const float* x, float* y, int tokens, int32_t* out_expert,
                                     float* out_weight, int regime, void* workspace,
                                     size_t workspace_bytes) {
+    return forward_impl(stream, L, rp, shared_gate_w, x, y, tokens, out_expert, out_weight, regime,
+                        workspace, workspace_bytes, kRoleRouter | kRoleGateUp | kRoleDown);
+}
+
+extern "C" int grimoire_moe_decode_stage(void* stream, const grim_moe_layer* L,
+                                         const grim_route_params* rp,
+                                         const uint16_t* shared_gate_w, const float* x, float* y,
+                                         int tokens, int stage, void* workspace,
+                                         size_t workspace_bytes) {
+    if (stage != kRoleRouter && stage != kRoleGateUp && stage != kRoleDown)
+        return ferr(GRIM_ERR_ARG, "stage: 1 router, 2 gate_up, 4 down");
+    if (!L || tokens <= 0 || !use_gemv(L, tokens, 1) || tokens > kDecodeMaxTokens)
+        return ferr(GRIM_ERR_SHAPE, "decode stages cover the single-launch-per-stage decode only");
+    return forward_impl(stream, L, rp, shared_gate_w, x, y, tokens, nullptr, nullptr, 1, workspace,
+                        workspace_bytes, stage);
+}
+
+static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_params* rp,
+                        const uint16_t* shared_gate_w, const float* x, float* y, int tokens,
+                        int32_t* out_expert, float* out_weight, int regime, void* workspace,
+                        size_t workspace_bytes, int roles) {
     if (!L || !x || !y) return ferr(GRIM_ERR_ARG, "null layer/x/y");
     if (tokens <= 0) return GRIM_OK;
     if (!L->router) return ferr(GRIM_ERR_ARG, "layer has no router");
@@ -329,7 +355,7 @@ extern "C" int grimoire_moe_forward(void* stream, const grim_moe_layer* L,
                 a.xf_words = xf_words(H);
             }
         }
-        decode_plan(L->gate_up.fmt, a, kRoleRouter | kRoleGateUp | kRoleDown);
+        decode_plan(L->gate_up.fmt, a, roles);
         if (decode_lds_bytes(L->gate_up.fmt, a) > 160 * 1024)
             return ferr(GRIM_ERR_SHAPE, "layer too large for the decode kernels");
         hipError_t e = decode_launch(st, L->gate_up.fmt, a);

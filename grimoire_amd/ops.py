@@ -147,6 +147,24 @@ def grouped_gemm(w: Weight, N, swiglu, A, out, offsets, counts, num_experts, tot
                                           _p(counts), num_experts, total_rows), "grouped_gemm")
 
 
+def quant_limbs(src, dst, scale, stream=None):
+    """Activation rows fp32 [rows][n] -> two int8 limbs per element (row layout
+    [n/64][2][64]) and one fp32 scale per row: a = s * (hi + lo / 254)."""
+    _dev(src)
+    rows, n = src.shape
+    check(lib().grimoire_moe_quant_limbs(_stream(stream), _p(src), rows, n, _p(dst), _p(scale)),
+          "quant_limbs")
+
+
+def grouped_gemm_i8(w: Weight, N, swiglu, A, a_scale, out, offsets, counts, num_experts,
+                    total_rows, stream=None):
+    """INT8 experts on the int8 MFMA (limb rows from quant_limbs), fp32 out."""
+    _dev(A)
+    check(lib().grimoire_moe_grouped_gemm_i8(_stream(stream), w.struct(), N, int(swiglu), _p(A),
+                                             _p(a_scale), _p(out), _p(offsets), _p(counts),
+                                             num_experts, total_rows), "grouped_gemm_i8")
+
+
 # ------------------------------------------------------------------- layer
 
 class MoeForward:
@@ -172,6 +190,18 @@ class MoeForward:
                                          _p(out_expert), _p(out_weight), self.regime,
                                          _p(self.workspace), self.workspace.numel()),
               "moe_forward")
+
+
+    STAGE_ROUTER, STAGE_GATE_UP, STAGE_DOWN = 1, 2, 4
+
+    def stage(self, which, x, y, stream=None):
+        """One launch of the decode path (grimoire_moe_decode_stage), on what
+        earlier stages or forward calls left in this workspace."""
+        _dev(x)
+        check(lib().grimoire_moe_decode_stage(_stream(stream), self.struct, self.route,
+                                              _p(self.L.shared_gate_w), _p(x), _p(y), x.shape[0],
+                                              which, _p(self.workspace), self.workspace.numel()),
+              "decode_stage")
 
 
 # ------------------------------------------------------------------ bridges

@@ -275,6 +275,27 @@ int grimoire_moe_grouped_gemm(void* stream, const grim_quant_weight* w, int N, i
                               const int32_t* offsets, const int32_t* counts,
                               int num_experts, int total_rows);
 
+/* INT8 weights on the int8 MFMA.  Activation rows are first split into
+ * two int8 limbs under one fp32 scale per row, a = s * (hi + lo / 254),
+ * s = max|row| / 127 (grimoire_moe_quant_limbs); each limb row is stored
+ * [n/64][2][64] bytes (per 64 elements: the hi codes, then the lo codes).
+ * src fp32 [rows][n] (n % 64 == 0, n <= 4096) -> dst [rows][2n], scale [rows].
+ * No reference counterpart: the activation format of the kernel below. */
+int grimoire_moe_quant_limbs(void* stream, const float* src, int rows, int n, int8_t* dst,
+                             float* scale);
+
+/* Grouped GEMM for INT8 weights (w->fmt GRIM_FMT_INT8, fp32 per-row scales)
+ * on limb rows A [R][2K] with scales a_scale [R], grouped by expert as in
+ * grimoire_moe_grouped_gemm; out fp32: swiglu != 0 -> h [R][N/2] =
+ * silu(A_r . gate_e) * (A_r . up_e), else [R][N].  The computation of
+ * launch_moe_mxfp4_grouped (src/gemm_fast.cpp:2343-2365) for the INT8
+ * experts that the reference runs one expert at a time
+ * (src/grimoire.cpp:23214-23229). */
+int grimoire_moe_grouped_gemm_i8(void* stream, const grim_quant_weight* w, int N, int swiglu,
+                                 const int8_t* A, const float* a_scale, float* out,
+                                 const int32_t* offsets, const int32_t* counts, int num_experts,
+                                 int total_rows);
+
 /* ------------------------------------------------------------------------
  * Bridges (the vLLM-XPU grouped GEMMs the reference dlopens).  Same
  * argument lists apart from the queue.  rows_per_expert [ne] gives the
@@ -344,6 +365,19 @@ int grimoire_moe_forward(void* stream, const grim_moe_layer* L, const grim_route
                          const uint16_t* shared_gate_w, const float* x, float* y, int tokens,
                          int32_t* out_expert, float* out_weight, int regime, void* workspace,
                          size_t workspace_bytes);
+
+/* One stage of the decode path of grimoire_moe_forward (regime 1, tokens
+ * <= 8): stage 1 = router logits (and the formatted activations), 2 =
+ * top-k + gate_up + SwiGLU, 4 = down + combine, each reading what the
+ * earlier stages (or an earlier grimoire_moe_forward call on the same
+ * workspace and inputs) left in the workspace.  For timing and tests of a
+ * single launch; the three stages in order equal one forward call.  No
+ * reference counterpart (the reference's launchers are per stage already:
+ * launch_moe_gate_up_shared / launch_moe_down_shared,
+ * include/b70/moe.hpp:133-185). */
+int grimoire_moe_decode_stage(void* stream, const grim_moe_layer* L, const grim_route_params* rp,
+                              const uint16_t* shared_gate_w, const float* x, float* y, int tokens,
+                              int stage, void* workspace, size_t workspace_bytes);
 
 #if defined(__GNUC__)
 #pragma GCC visibility pop

@@ -1,0 +1,134 @@
+"""INT8 grouped GEMM on the int8 MFMA (two activation limbs per row) and its
+limb quantiser, on the GPU.
+
+The quantiser is pinned by its definition: a = s * (hi + lo / 254),
+s = max|row| / 127, |hi|, |lo| <= 127, reconstruction error <= s / 508 (+ fp32 rounding).
+The GEMM is pinned exactly where the limbs are exact (integer rows whose
+largest magnitude is 127: s = 1, lo = 0, so the int32 products are the
+exact dot products) and otherwise against fp64 products of the dequantised
+weights (rel-L2 2e-4: the limb error is ~2^-16 of each row's largest
+value), over ragged expert row counts including empty experts, a single
+row, a full 128-row tile and partial tiles."""
+import pytest
+import torch
+
+from grimoire_amd import ops
+from grimoire_amd.weights import make_int8
+from tests.helpers import dequant, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _decode(q, n):
+    """limb rows [rows][n/64][2][64] -> hi, lo int tensors [rows][n]"""
+    q = q.view(torch.int8).reshape(q.shape[0], n // 64, 2, 64).cpu().to(torch.int32)
+    return q[:, :, 0, :].reshape(-1, n), q[:, :, 1, :].reshape(-1, n)
+
+
+def _limbs(gpu, x):
+    rows, n = x.shape
+    q = torch.empty(rows, 2 * n, dtype=torch.int8, device=gpu)
+    s = torch.empty(rows, device=gpu)
+    ops.quant_limbs(x.to(gpu), q, s)
+    torch.cuda.synchronize()
+    return q, s
+
+
+def test_quant_limbs_definition(gpu):
+    print("quant limbs", flush=True)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(37, 512, generator=g) * torch.logspace(-3, 3, 37).unsqueeze(1)
+    x[5] = 0.0
+    q, s = _limbs(gpu, x)
+    hi, lo = _decode(q, 512)
+    s = s.cpu()
+    assert hi.abs().max() <= 127 and lo.abs().max() <= 127
+    m = x.abs().amax(1)
+    assert torch.allclose(s[m > 0], (m / 127)[m > 0], rtol=1e-6)
+    assert s[5] == 1.0 and hi[5].abs().sum() == 0 and lo[5].abs().sum() == 0
+    rec = s.double().unsqueeze(1) * (hi.double() + lo.double() / 254)
+    err = (rec - x.double()).abs()
+    # s / 508 from the lo rounding, plus the fp32 evaluation of x * (127 /
+    # max) (|y| <= 127: up to 127 * 2^-24 of s)
+    assert (err <= s.double().unsqueeze(1) * (1 / 508 + 2e-5) + 1e-30).all()
+    assert err.max() > 0                               # the limbs are not exact
+
+
+def _counts(E, seed):
+    g = torch.Generator().manual_seed(seed)
+    c = torch.randint(0, 300, (E,), generator=g).int()
+    c[0] = 0
+    c[1] = 128
+    c[2] = 1
+    return c
+
+
+def _dense(A, W, counts, offsets, N):
+    out = torch.zeros(A.shape[0], N, dtype=torch.float64)
+    for e in range(len(counts)):
+        r0, n = int(offsets[e]), int(counts[e])
+        if n:
+            out[r0:r0 + n] = A[r0:r0 + n].double() @ W[e * N:(e + 1) * N].double().T
+    return out
+
+
+def test_gemm_i8_exact_on_exact_limbs(gpu):
+    print("gemm i8 exact limbs", flush=True)
+    E, N, K = 3, 256, 512
+    w = make_int8(E * N, K, seed=5)
+    counts = torch.tensor([130, 0, 77]).int()
+    offsets = (torch.cumsum(counts, 0) - counts).int()
+    R = int(counts.sum())
+    g = torch.Generator().manual_seed(1)
+    A = torch.randint(-127, 128, (R, K), generator=g).float()
+    A[:, 0] = 127.0                       # row max exactly 127: s = 1, lo = 0
+    q, s = _limbs(gpu, A)
+    assert (s.cpu() == 1.0).all()
+    out = torch.full((R, N), float("nan"), device=gpu)
+    ops.grouped_gemm_i8(w.to(gpu), N, False, q, s, out, offsets.to(gpu), counts.to(gpu), E, R)
+    torch.cuda.synchronize()
+    want = _dense(A, dequant(w), counts, offsets, N)
+    assert rel_l2(out.cpu(), want) < 1e-6
+
+
+@pytest.mark.parametrize("N,K", [(256, 512), (320, 2048)])
+def test_gemm_i8_plain_ragged(gpu, N, K):
+    print(f"gemm i8 plain N={N} K={K}", flush=True)
+    E = 5
+    w = make_int8(E * N, K, seed=N + K)
+    counts = _counts(E, K)
+    offsets = (torch.cumsum(counts, 0) - counts).int()
+    R = int(counts.sum())
+    A = torch.randn(R, K).bfloat16().float()
+    q, s = _limbs(gpu, A)
+    out = torch.full((R, N), float("nan"), device=gpu)
+    ops.grouped_gemm_i8(w.to(gpu), N, False, q, s, out, offsets.to(gpu), counts.to(gpu), E, R)
+    torch.cuda.synchronize()
+    want = _dense(A, dequant(w), counts, offsets, N)
+    assert not torch.isnan(out).any()
+    assert rel_l2(out.cpu(), want) < 2e-4
+
+
+def test_gemm_i8_swiglu_then_down(gpu):
+    print("gemm i8 swiglu + down", flush=True)
+    E, I, H = 4, 192, 512
+    wgu = make_int8(E * 2 * I, H, seed=1)
+    wdn = make_int8(E * H, I, seed=2)
+    counts = _counts(E, 3)
+    offsets = (torch.cumsum(counts, 0) - counts).int()
+    R = int(counts.sum())
+    A = torch.randn(R, H).bfloat16().float()
+    q, s = _limbs(gpu, A)
+    h = torch.full((R, I), float("nan"), device=gpu)
+    ops.grouped_gemm_i8(wgu.to(gpu), 2 * I, True, q, s, h, offsets.to(gpu), counts.to(gpu), E, R)
+    torch.cuda.synchronize()
+    gu = _dense(A, dequant(wgu), counts, offsets, 2 * I)
+    g, u = gu[:, :I], gu[:, I:]
+    h_want = g / (1 + torch.exp(-g)) * u
+    assert rel_l2(h.cpu(), h_want) < 2e-4
+    hq, hs = _limbs(gpu, h)
+    y = torch.full((R, H), float("nan"), device=gpu)
+    ops.grouped_gemm_i8(wdn.to(gpu), H, False, hq, hs, y, offsets.to(gpu), counts.to(gpu), E, R)
+    torch.cuda.synchronize()
+    y_want = _dense(h_want.float(), dequant(wdn), counts, offsets, H)
+    assert rel_l2(y.cpu(), y_want) < 5e-4
