@@ -6,11 +6,12 @@
 // atomics:
 //   1. count   each block counts its chunk of routes per expert in LDS and
 //              writes the row bcount[b][E];
-//   2. scan    one block turns bcount into per-(block, expert) bases,
-//              per-expert counts and exclusive offsets, and the m-tile
-//              table (src/prefill.cpp:2770-2782);
+//   2. scan    one block turns bcount into per-(block, expert) bases
+//              inside the expert, per-expert counts and exclusive offsets,
+//              and the m-tile table (src/prefill.cpp:2770-2782);
 //   3. rank    each block ranks its routes inside their expert by counting
 //              earlier routes of the same expert in the block (stable);
+//              row = offsets[e] + block base + rank;
 //   4. permute one block per token writes bf16(x[t]) to its K rows
 //              (src/prefill.cpp:2784-2806).
 #include "common.hpp"
@@ -19,7 +20,7 @@
 namespace grim {
 
 constexpr int kDispThreads = 256;
-constexpr int kRoutesPerBlock = 1024;
+constexpr int kRoutesPerBlock = 256;
 
 __global__ __launch_bounds__(kDispThreads) void disp_count(const int32_t* __restrict__ ids, int R,
                                                            int E, int32_t* __restrict__ bcount) {
@@ -54,11 +55,15 @@ __global__ __launch_bounds__(1024) void disp_scan(int32_t* __restrict__ bcount, 
         const int e = e0 + threadIdx.x;
         int c = 0;
         if (e < E) {
-            // per-block bases inside the expert (block order = route order)
-            for (int b = 0; b < nb; ++b) {
-                const int v = bcount[int64_t(b) * E + e];
-                bcount[int64_t(b) * E + e] = c;
-                c += v;
+            // per-block bases inside the expert (block order = route order);
+            // 16 independent loads in flight per step (clamped, then masked)
+            for (int b0 = 0; b0 < nb; b0 += 16) {
+                int v[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) v[j] = bcount[int64_t(min(b0 + j, nb - 1)) * E + e];
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    if (b0 + j < nb) { bcount[int64_t(b0 + j) * E + e] = c; c += v[j]; }
             }
         }
         const int nt = (mc > 0 && e < E) ? (c + mc - 1) / mc : 0;
@@ -79,7 +84,6 @@ __global__ __launch_bounds__(1024) void disp_scan(int32_t* __restrict__ bcount, 
         if (e < E) {
             counts[e] = c;
             offsets[e] = rbase;
-            for (int b = 0; b < nb; ++b) bcount[int64_t(b) * E + e] += rbase;
             if (tile_e)
                 for (int i = 0; i < nt; ++i)
                     if (tbase + i < tmax) { tile_e[tbase + i] = e; tile_mb[tbase + i] = i; }
@@ -96,35 +100,33 @@ __global__ __launch_bounds__(1024) void disp_scan(int32_t* __restrict__ bcount, 
 __global__ __launch_bounds__(kDispThreads) void disp_rank(const int32_t* __restrict__ ids, int R,
                                                           int E, int K,
                                                           const int32_t* __restrict__ bbase,
+                                                          const int32_t* __restrict__ offsets,
                                                           int32_t* __restrict__ inverse,
                                                           int32_t* __restrict__ perm_token) {
-    __shared__ int32_t le[kRoutesPerBlock];
+    static_assert(kRoutesPerBlock == kDispThreads, "one route per thread");
+    __shared__ __attribute__((aligned(16))) int32_t le[kRoutesPerBlock];
     const int r0 = blockIdx.x * kRoutesPerBlock;
     const int n = R - r0 < kRoutesPerBlock ? R - r0 : kRoutesPerBlock;
-    for (int i = threadIdx.x; i < kRoutesPerBlock; i += blockDim.x) le[i] = i < n ? ids[r0 + i] : -1;
+    const int i = threadIdx.x;
+    le[i] = i < n ? ids[r0 + i] : -1;
     __syncthreads();
-    constexpr int PER = kRoutesPerBlock / kDispThreads;
-    int my_e[PER], rank[PER];
-#pragma unroll
-    for (int j = 0; j < PER; ++j) { my_e[j] = le[threadIdx.x + j * kDispThreads]; rank[j] = 0; }
+    const int my_e = le[i];
     // count earlier routes of the same expert (uniform loop: LDS broadcast)
-    for (int i = 0; i < n; ++i) {
-        const int ei = le[i];
-#pragma unroll
-        for (int j = 0; j < PER; ++j)
-            rank[j] += (i < threadIdx.x + j * kDispThreads && ei == my_e[j]) ? 1 : 0;
+    int rank = 0;
+#pragma unroll 4
+    for (int j = 0; j < kRoutesPerBlock; j += 4) {
+        const int4 q = *reinterpret_cast<const int4*>(&le[j]);
+        rank += (j < i && q.x == my_e) ? 1 : 0;
+        rank += (j + 1 < i && q.y == my_e) ? 1 : 0;
+        rank += (j + 2 < i && q.z == my_e) ? 1 : 0;
+        rank += (j + 3 < i && q.w == my_e) ? 1 : 0;
     }
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        const int i = threadIdx.x + j * kDispThreads;
-        if (i >= n) continue;
-        const int e = my_e[j];
-        const int r = r0 + i;
-        if (e < 0 || e >= E) { inverse[r] = -1; continue; }
-        const int p = bbase[int64_t(blockIdx.x) * E + e] + rank[j];
-        inverse[r] = p;
-        if (perm_token) perm_token[p] = r / K;
-    }
+    if (i >= n) return;
+    const int r = r0 + i;
+    if (my_e < 0 || my_e >= E) { inverse[r] = -1; return; }
+    const int p = offsets[my_e] + bbase[int64_t(blockIdx.x) * E + my_e] + rank;
+    inverse[r] = p;
+    if (perm_token) perm_token[p] = r / K;
 }
 
 // One block per token: bf16 row written to each of its K permuted rows.
@@ -180,7 +182,7 @@ hipError_t dispatch_launch(hipStream_t st, const DispatchArgs& a) {
                        a.tile_e, a.tile_mb, a.tmax, a.mc, ntiles);
     if (nb > 0)
         hipLaunchKernelGGL(disp_rank, dim3(nb), dim3(kDispThreads), 0, st, a.ids, R, a.E, a.K,
-                           bcount, a.inverse, a.perm_token);
+                           bcount, a.offsets, a.inverse, a.perm_token);
     if (a.xperm && a.T > 0) {
         if (a.hidden_bf16)
             hipLaunchKernelGGL(disp_permute<true>, dim3(a.T), dim3(kDispThreads), 0, st, a.hidden,
@@ -195,36 +197,47 @@ hipError_t dispatch_launch(hipStream_t st, const DispatchArgs& a) {
 // ---------------------------------------------------------------- combine
 
 // dst[t][d] = fma chain over slots of w * src[inverse][d] (+ gate * shared).
-// One block per token, 4 columns per thread.
-template <bool SRC_BF16>
+// One block per token, 4 columns per thread.  KT is the slot count the loops
+// are unrolled for (KT == K, or 16 with the slots past K masked), so the
+// slot tables stay in registers and all KT row loads are issued before the
+// first use.  A skipped slot (p < 0, or s >= K) reads row 0 and is masked
+// after the load, not branched around.
+template <bool SRC_BF16, int KT>
 __global__ __launch_bounds__(kDispThreads) void combine_kernel(
     const void* __restrict__ src, const int32_t* __restrict__ inverse,
     const float* __restrict__ rw, const void* __restrict__ shared_src, int shared_bf16,
     const float* __restrict__ gate, float* __restrict__ dst, int H, int K) {
     const int t = blockIdx.x;
-    int p[16];
-    float w[16];
-    for (int s = 0; s < K; ++s) { p[s] = inverse[int64_t(t) * K + s]; w[s] = rw[int64_t(t) * K + s]; }
+    int p[KT];
+    float w[KT];
+#pragma unroll
+    for (int s = 0; s < KT; ++s) {
+        const int sc = s < K ? s : K - 1;
+        p[s] = s < K ? inverse[int64_t(t) * K + sc] : -1;
+        w[s] = rw[int64_t(t) * K + sc];
+    }
     const float g = gate ? gate[t] : 1.0f;
     for (int d = threadIdx.x * 4; d < H; d += blockDim.x * 4) {
         float v0 = 0.0f, v1 = 0.0f, v2 = 0.0f, v3 = 0.0f;
-        for (int s = 0; s < K; ++s) {
-            if (p[s] < 0) continue;
+#pragma unroll
+        for (int s = 0; s < KT; ++s) {
+            const int64_t row = p[s] < 0 ? 0 : p[s];
             float a0, a1, a2, a3;
             if constexpr (SRC_BF16) {
                 const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(src) +
-                                                                int64_t(p[s]) * H + d);
+                                                                row * H + d);
                 a0 = bits_f(u.x << 16); a1 = bits_f(u.x & 0xFFFF0000u);
                 a2 = bits_f(u.y << 16); a3 = bits_f(u.y & 0xFFFF0000u);
             } else {
                 const float4 f = *reinterpret_cast<const float4*>(static_cast<const float*>(src) +
-                                                                  int64_t(p[s]) * H + d);
+                                                                  row * H + d);
                 a0 = f.x; a1 = f.y; a2 = f.z; a3 = f.w;
             }
-            v0 = __builtin_fmaf(w[s], a0, v0);
-            v1 = __builtin_fmaf(w[s], a1, v1);
-            v2 = __builtin_fmaf(w[s], a2, v2);
-            v3 = __builtin_fmaf(w[s], a3, v3);
+            const bool on = p[s] >= 0;
+            v0 = on ? __builtin_fmaf(w[s], a0, v0) : v0;
+            v1 = on ? __builtin_fmaf(w[s], a1, v1) : v1;
+            v2 = on ? __builtin_fmaf(w[s], a2, v2) : v2;
+            v3 = on ? __builtin_fmaf(w[s], a3, v3) : v3;
         }
         if (shared_src) {
             float a0, a1, a2, a3;
@@ -247,14 +260,29 @@ __global__ __launch_bounds__(kDispThreads) void combine_kernel(
     }
 }
 
+template <bool SRC_BF16>
+static void combine_k(hipStream_t st, const CombineArgs& a) {
+#define GRIM_COMBINE(KT)                                                                          \
+    hipLaunchKernelGGL((combine_kernel<SRC_BF16, KT>), dim3(a.T), dim3(kDispThreads), 0, st,      \
+                       a.src, a.inverse, a.rw, a.shared_src, a.shared_bf16, a.gate, a.dst, a.H,   \
+                       a.K)
+    switch (a.K) {
+        case 1: GRIM_COMBINE(1); break;
+        case 2: GRIM_COMBINE(2); break;
+        case 4: GRIM_COMBINE(4); break;
+        case 6: GRIM_COMBINE(6); break;
+        case 8: GRIM_COMBINE(8); break;
+        case 10: GRIM_COMBINE(10); break;
+        default: GRIM_COMBINE(16); break;
+    }
+#undef GRIM_COMBINE
+}
+
 hipError_t combine_launch(hipStream_t st, const CombineArgs& a) {
     if (a.T <= 0) return hipSuccess;
-    if (a.src_bf16)
-        hipLaunchKernelGGL(combine_kernel<true>, dim3(a.T), dim3(kDispThreads), 0, st, a.src,
-                           a.inverse, a.rw, a.shared_src, a.shared_bf16, a.gate, a.dst, a.H, a.K);
-    else
-        hipLaunchKernelGGL(combine_kernel<false>, dim3(a.T), dim3(kDispThreads), 0, st, a.src,
-                           a.inverse, a.rw, a.shared_src, a.shared_bf16, a.gate, a.dst, a.H, a.K);
+    if (a.K <= 0 || a.K > 16) return hipErrorInvalidValue;
+    if (a.src_bf16) combine_k<true>(st, a);
+    else combine_k<false>(st, a);
     return hipGetLastError();
 }
 

@@ -90,66 +90,72 @@ __global__ __launch_bounds__(256) void router_gemm(const float* __restrict__ W,
 }
 
 // Large T on MFMA: fp32 v_mfma_f32_32x32x2f32 (fp32 products and sums, no
-// reduced-precision operands).  Block tile 128 tokens x 128 experts x 32 K,
-// 4 waves of 64 x 64 (2 x 2 MFMA tiles), LDS double buffer with a register
-// prefetch of the next K tile.  Inside a 32-wide K tile lane half h supplies
-// K = 16 h + s in MFMA step s (the same order for x and W), so each lane
-// reads 16 consecutive floats per row with 16-byte LDS loads.
-constexpr int kRtBM = 128, kRtBN = 128, kRtBK = 32, kRtLD = kRtBK + 4;
+// reduced-precision operands).  Block tile (64 MI) tokens x (64 NI) experts x
+// 32 K, 4 waves of (32 MI) x (32 NI) (MI x NI MFMA tiles), LDS double buffer
+// with a register prefetch of the next K tile.  Inside a 32-wide K tile lane
+// half h supplies K = 16 h + s in MFMA step s (the same order for x and W),
+// so each lane reads 16 consecutive floats per row with 16-byte LDS loads.
+// MI = NI = 1 (64 x 64) is the default: T = 4096, E = 512 then gives 512
+// blocks, two per CU, where 128 x 128 tiles would leave half the CUs idle.
+constexpr int kRtBK = 32, kRtLD = kRtBK + 4;
 typedef float f32x16r __attribute__((__vector_size__(16 * sizeof(float))));
 typedef float f32x4n __attribute__((ext_vector_type(4)));   // native vector (HIP's float4 is a struct)
 
-// staging of one K tile: 4 f32x4n of x and 4 of W per thread (row c/8,
-// K offset 4 (c % 8)); rows past T / E repeat the last one
-__device__ __forceinline__ void rt_load(const float* __restrict__ x, const float* __restrict__ W,
-                                        int T, int E, int H, int t0, int e0, int k0,
-                                        f32x4n (&rx)[4], f32x4n (&rw)[4]) {
+// staging of one K tile: ROWS/32 f32x4n per thread from `src` (row c/8,
+// K offset 4 (c % 8)); rows past `n` repeat the last one
+template <int ROWS>
+__device__ __forceinline__ void rt_load(const float* __restrict__ src, int n, int H, int r0,
+                                        int k0, f32x4n (&reg)[ROWS / 32]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < ROWS / 32; ++i) {
         const int c = threadIdx.x + i * 256, r = c >> 3, kc = (c & 7) * 4;
-        const int t = min(t0 + r, T - 1), e = min(e0 + r, E - 1);
-        rx[i] = *reinterpret_cast<const f32x4n*>(x + int64_t(t) * H + k0 + kc);
-        rw[i] = *reinterpret_cast<const f32x4n*>(W + int64_t(e) * H + k0 + kc);
+        const int rr = min(r0 + r, n - 1);
+        reg[i] = *reinterpret_cast<const f32x4n*>(src + int64_t(rr) * H + k0 + kc);
     }
 }
-__device__ __forceinline__ void rt_store(float* xs, float* ws, const f32x4n (&rx)[4],
-                                         const f32x4n (&rw)[4]) {
+template <int ROWS>
+__device__ __forceinline__ void rt_store(float* dst, const f32x4n (&reg)[ROWS / 32]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < ROWS / 32; ++i) {
         const int c = threadIdx.x + i * 256, r = c >> 3, kc = (c & 7) * 4;
-        *reinterpret_cast<f32x4n*>(&xs[r * kRtLD + kc]) = rx[i];
-        *reinterpret_cast<f32x4n*>(&ws[r * kRtLD + kc]) = rw[i];
+        *reinterpret_cast<f32x4n*>(&dst[r * kRtLD + kc]) = reg[i];
     }
 }
+template <int MI, int NI>
 __global__ __launch_bounds__(256) void router_mfma(const float* __restrict__ W,
                                                    const float* __restrict__ x,
                                                    const float* __restrict__ bias,
                                                    float* __restrict__ logits, int T, int E, int H) {
-    __shared__ __attribute__((aligned(16))) float Xs[2][kRtBM * kRtLD];
-    __shared__ __attribute__((aligned(16))) float Ws[2][kRtBN * kRtLD];
+    constexpr int BM = 64 * MI, BN = 64 * NI;
+    __shared__ __attribute__((aligned(16))) float Xs[2][BM * kRtLD];
+    __shared__ __attribute__((aligned(16))) float Ws[2][BN * kRtLD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1, h = lane >> 5;
-    const int t0 = blockIdx.y * kRtBM, e0 = blockIdx.x * kRtBN;
-    // staging: 4 f32x4n of x and 4 of W per thread per K tile (row c/8, k 4*(c%8))
-    f32x4n rx[4], rw[4];
-    f32x16r acc[2][2];
+    const int t0 = blockIdx.y * BM, e0 = blockIdx.x * BN;
+    f32x4n rx[BM / 32], rw[BN / 32];
+    f32x16r acc[MI][NI];
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
+    for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
+        for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.0f;
     const int nk = H / kRtBK;
-    rt_load(x, W, T, E, H, t0, e0, 0, rx, rw);
-    rt_store(Xs[0], Ws[0], rx, rw);
+    rt_load<BM>(x, T, H, t0, 0, rx);
+    rt_load<BN>(W, E, H, e0, 0, rw);
+    rt_store<BM>(Xs[0], rx);
+    rt_store<BN>(Ws[0], rw);
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
         const int buf = kt & 1;
-        if (kt + 1 < nk) rt_load(x, W, T, E, H, t0, e0, (kt + 1) * kRtBK, rx, rw);
-        float av[2][16], bv[2][16];
+        if (kt + 1 < nk) {
+            rt_load<BM>(x, T, H, t0, (kt + 1) * kRtBK, rx);
+            rt_load<BN>(W, E, H, e0, (kt + 1) * kRtBK, rw);
+        }
+        float av[MI][16], bv[NI][16];
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi) {
-            const float* p = &Xs[buf][(wm * 64 + mi * 32 + (lane & 31)) * kRtLD + 16 * h];
+        for (int mi = 0; mi < MI; ++mi) {
+            const float* p = &Xs[buf][(wm * 32 * MI + mi * 32 + (lane & 31)) * kRtLD + 16 * h];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const f32x4n v4 = *reinterpret_cast<const f32x4n*>(p + 4 * q);
@@ -157,8 +163,8 @@ __global__ __launch_bounds__(256) void router_mfma(const float* __restrict__ W,
             }
         }
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
-            const float* p = &Ws[buf][(wn * 64 + ni * 32 + (lane & 31)) * kRtLD + 16 * h];
+        for (int ni = 0; ni < NI; ++ni) {
+            const float* p = &Ws[buf][(wn * 32 * NI + ni * 32 + (lane & 31)) * kRtLD + 16 * h];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const f32x4n v4 = *reinterpret_cast<const f32x4n*>(p + 4 * q);
@@ -168,24 +174,27 @@ __global__ __launch_bounds__(256) void router_mfma(const float* __restrict__ W,
 #pragma unroll
         for (int st = 0; st < 16; ++st)
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
+            for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-                for (int ni = 0; ni < 2; ++ni)
+                for (int ni = 0; ni < NI; ++ni)
                     acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[mi][st], bv[ni][st], acc[mi][ni], 0, 0, 0);
-        if (kt + 1 < nk) rt_store(Xs[buf ^ 1], Ws[buf ^ 1], rx, rw);
+        if (kt + 1 < nk) {
+            rt_store<BM>(Xs[buf ^ 1], rx);
+            rt_store<BN>(Ws[buf ^ 1], rw);
+        }
         __syncthreads();
     }
     // acc[mi][ni][v]: token row (v&3) + 4*(lane>>5) + 8*(v>>2), expert lane&31
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
-        const int e = e0 + wn * 64 + ni * 32 + (lane & 31);
+    for (int ni = 0; ni < NI; ++ni) {
+        const int e = e0 + wn * 32 * NI + ni * 32 + (lane & 31);
         if (e >= E) continue;
         const float b = bias ? bias[e] : 0.0f;
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
+        for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const int t = t0 + wm * 64 + mi * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
+                const int t = t0 + wm * 32 * MI + mi * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
                 if (t < T) logits[int64_t(t) * E + e] = bias ? acc[mi][ni][v] + b : acc[mi][ni][v];
             }
     }
@@ -197,8 +206,8 @@ hipError_t router_logits_launch(hipStream_t st, const float* W, const float* x,
         dim3 grid(E, (T + kRouterTok - 1) / kRouterTok);
         hipLaunchKernelGGL(router_gemv, grid, dim3(256), 0, st, W, x, bias, logits, T, E, H);
     } else if (H % kRtBK == 0) {
-        dim3 grid((E + kRtBN - 1) / kRtBN, (T + kRtBM - 1) / kRtBM);
-        hipLaunchKernelGGL(router_mfma, grid, dim3(256), 0, st, W, x, bias, logits, T, E, H);
+        dim3 grid((E + 63) / 64, (T + 63) / 64);
+        hipLaunchKernelGGL((router_mfma<1, 1>), grid, dim3(256), 0, st, W, x, bias, logits, T, E, H);
     } else {
         dim3 grid((E + 63) / 64, (T + 63) / 64);
         hipLaunchKernelGGL(router_gemm, grid, dim3(256), 0, st, W, x, bias, logits, T, E, H);
