@@ -20,9 +20,11 @@
 // rows are stored [K/64][2][64] so that one K tile of a row is one 128-byte
 // line; every DMA instruction moves whole row segments (A 8 x 128 bytes, B
 // 16 x 64 bytes) into XOR-swizzled slots that keep the fragment reads free
-// of bank conflicts.  Three K tiles are in flight while one is multiplied.
-// Persistent XCD-aware grid over (m-tile, column tile) items, rows from the
-// dispatch's tile table.
+// of bank conflicts.  Three K tiles are in flight while one is multiplied,
+// and the stream runs on across items: a work-group's next item has its
+// first tiles and its scales in LDS before the current one's epilogue,
+// which stores straight from the accumulators.  Persistent XCD-aware grid
+// over (m-tile, column tile) items, rows from the dispatch's tile table.
 #include "common.hpp"
 #include "gemm.hpp"
 #include "gemm_i8.hpp"
@@ -44,12 +46,46 @@ constexpr float kLoScale = 1.0f / 254.0f;
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 #ifdef GRIM_I8_TIMING
-__device__ uint64_t g_i8_wait[4096], g_i8_issue[4096], g_i8_total[4096], g_i8_epi[4096];
+__device__ uint64_t g_i8_total[4096], g_i8_epi[4096];
 #endif
 
 template <int AUX>
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, int voff, int soff) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, soff, 0, AUX);
+}
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+// LDS reads the compiler does not see as such (no wait is inserted for
+// them; the caller waits on lgkmcnt itself)
+__device__ __forceinline__ float lds_f32(int addr) {
+    float v;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+__device__ __forceinline__ f32x4v lds_f32x4(int addr) {
+    f32x4v v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+
+// Lane index from mbcnt: formed where it is needed, so no register holds
+// it (and no spill reload, with its wait on every outstanding load) across
+// the item loop.
+// The value is opaque to the optimiser, so what is derived from it is
+// formed at each call and not hoisted out of the loops.
+__device__ __forceinline__ int lane_id() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
+
+// Scalar load of one int (lgkmcnt, not vmcnt: it does not wait on the
+// vector loads and stores in flight); p must be wave-uniform.
+__device__ __forceinline__ int sload_i32(const int32_t* p) {
+    int v;
+    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+    return v;
 }
 
 struct I8Src {
@@ -61,248 +97,74 @@ struct I8Src {
     float* out;
 };
 
+// One (m-tile, column tile) work item, wave-uniform: its first A row, row
+// count, first weight row and first output column (h column for SwiGLU).
+// The buffer resources built from it bound everything: rows past the
+// expert's count and columns past the slab read as zero, and stores past
+// them are dropped by the hardware.
+struct I8Item {
+    int64_t arow0, wrow;   // wrow: first weight row of the tile (expert base + col0)
+    int rows, col0;
+};
+
 template <bool SWIGLU>
-__device__ __forceinline__ void i8_tile(const GemmI8Args& g, const I8Src& src, bool routed, int ty,
-                                        int nt, uint8_t (*smem)[kQStageBytes]) {
+__device__ __forceinline__ I8Item i8_item(const GemmI8Args& g, bool routed, int ty, int nt) {
     int rows_valid;
     int64_t arow0, wrow0;
+    ty = __builtin_amdgcn_readfirstlane(ty);
     if (routed) {
-        const int e = __builtin_amdgcn_readfirstlane(g.tile_e[ty]);
-        if (e < 0) return;
-        const int mb = __builtin_amdgcn_readfirstlane(g.tile_mb[ty]);
-        rows_valid = min(QBM, __builtin_amdgcn_readfirstlane(g.counts[e]) - mb * QBM);
-        arow0 = int64_t(__builtin_amdgcn_readfirstlane(g.offsets[e])) + int64_t(mb) * QBM;
-        wrow0 = int64_t(e) * g.N;
+        const int e = sload_i32(g.tile_e + ty);
+        const int ec = e < 0 ? 0 : e;
+        const int mb = sload_i32(g.tile_mb + ty);
+        rows_valid = e < 0 ? 0 : min(QBM, sload_i32(g.counts + ec) - mb * QBM);
+        arow0 = int64_t(sload_i32(g.offsets + ec)) + int64_t(mb) * QBM;
+        wrow0 = int64_t(ec) * g.N;
     } else {
         rows_valid = min(QBM, g.T_sh - ty * QBM);
         arow0 = int64_t(ty) * QBM;
         wrow0 = 0;
     }
-    rows_valid = __builtin_amdgcn_readfirstlane(rows_valid);
-    arow0 = int64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(arow0)))) |
-            (int64_t(__builtin_amdgcn_readfirstlane(int(arow0 >> 32))) << 32);
-    wrow0 = int64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(wrow0)))) |
-            (int64_t(__builtin_amdgcn_readfirstlane(int(wrow0 >> 32))) << 32);
-    if (rows_valid <= 0) return;
-
-    int tid = threadIdx.x;
-    asm volatile("" : "+v"(tid));
-    const int lane = tid & 63, wave = tid >> 6;
-    const int K = g.K;
-    const int a_row_bytes = 2 * K;
-    const int n_slab = SWIGLU ? 2 * g.I : g.N;
-    // rows past rows_valid and columns past the slab read as zero
-    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int8_t*>(src.A + arow0 * a_row_bytes), 0, rows_valid * a_row_bytes, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(src.w + wrow0 * src.row_bytes), 0, int(n_slab * src.row_bytes), 0x00020000);
-
-    // Stage layout (one K tile of 64):
-    //   A 16 KiB: row r's 128 bytes (limb hi K 0..63, limb lo K 0..63 as
-    //     eight 16-byte chunks c = 4 limb + K/16) at r * 128, chunk c at
-    //     physical slot c ^ ((r >> 1) & 7);
-    //   B 16 KiB: tile column n's 64 bytes (four chunks c = K/16) at
-    //     16384 + n * 64, chunk c at slot c ^ ((n >> 2) & 3).
-    // The swizzles make every fragment read (32 rows or columns at one
-    // chunk, 16 lanes per LDS cycle) hit 16 distinct 16-byte slots of the
-    // bank window.  Each DMA instruction covers whole row segments: A 8 rows
-    // x 128 bytes, B 16 columns x 64 bytes (lane i: 16 bytes at slot i).
-    // In global memory A rows are [K/64][2][64] bytes (the quantisers write
-    // that layout), B rows are the weight rows as stored.
-    int a_off[4], b_off[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int ja = 4 * wave + j;
-        const int r = 8 * ja + (lane >> 3), pc = lane & 7;
-        a_off[j] = r * a_row_bytes + ((pc ^ ((r >> 1) & 7)) << 4);
-        const int jb = 4 * wave + j;
-        const int col = 16 * jb + (lane >> 2), pcb = lane & 3;
-        const int nsub = col >> 5, x = col & 31;
-        int row;
-        if (SWIGLU) {
-            // h columns [32 w', +32) of wave w' = nsub / 2: gate rows for
-            // nsub even, up rows for nsub odd
-            const int hc = min(nt * (QBN / 2) + (nsub >> 1) * 32 + x, g.I - 1);
-            row = (nsub & 1) ? g.I + hc : hc;
-        } else {
-            row = min(nt * QBN + col, g.N - 1);
-        }
-        b_off[j] = row * int(src.row_bytes) + ((pcb ^ ((col >> 2) & 3)) << 4);
-    }
-    auto issue = [&](int t) {
-        uint8_t* st = smem[t % kQStages];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) dma16<0>(rA, st + (4 * wave + j) * 1024, a_off[j], t * 128);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) dma16<2>(rB, st + 16384 + (4 * wave + j) * 1024, b_off[j], t * QBK);
-    };
-    // fragment read addresses inside a stage
-    int fa_off[2][2][4], fb_off[2][2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        const int ch = 2 * ks + (lane >> 5);
-#pragma unroll
-        for (int l = 0; l < 2; ++l)
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi) {
-                const int r = mi * 32 + (lane & 31);
-                fa_off[ks][l][mi] = r * 128 + (((4 * l + ch) ^ ((r >> 1) & 7)) << 4);
-            }
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
-            const int n = (2 * wave + ni) * 32 + (lane & 31);
-            fb_off[ks][ni] = 16384 + n * 64 + ((ch ^ ((n >> 2) & 3)) << 4);
-        }
-    }
-
-    i32x16 acc[2][4][2];
-#pragma unroll
-    for (int l = 0; l < 2; ++l)
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-            for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) acc[l][mi][ni][v] = 0;
-
-    const int nk = K / QBK;   // >= 3
-    // Iteration t: tile t complete (this wave's loads are counted in order,
-    // 8 per tile; then the barrier covers every wave's), which also retires
-    // every wave's reads of tile t - 1, whose stage then takes tile t + 3;
-    // tile t's 20 fragments are read at once (LDS latency paid once per
-    // tile), then its 32 MFMAs run.
-#pragma unroll
-    for (int p = 0; p < kQStages - 1; ++p)
-        if (p < nk) issue(p);
-    for (int t = 0; t < nk; ++t) {
-#ifdef GRIM_I8_TIMING
-        const uint64_t tw0 = __builtin_amdgcn_s_memtime();
-#endif
-        const int later = min(kQStages - 2, nk - 1 - t);
-        if (later >= 2) asm volatile("s_waitcnt vmcnt(16)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        else if (later == 1) asm volatile("s_waitcnt vmcnt(8)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-#ifdef GRIM_I8_TIMING
-        const uint64_t tw1 = __builtin_amdgcn_s_memtime();
-        g_i8_wait[blockIdx.x * 4 + wave] += tw1 - tw0;
-#endif
-        if (t + kQStages - 1 < nk) issue(t + kQStages - 1);
-#ifdef GRIM_I8_TIMING
-        g_i8_issue[blockIdx.x * 4 + wave] += __builtin_amdgcn_s_memtime() - tw1;
-#endif
-        const uint8_t* st = smem[t % kQStages];
-        i32x4 fb[2][2], fa[2][2][4];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-            for (int ni = 0; ni < 2; ++ni)
-                fb[ks][ni] = *reinterpret_cast<const i32x4*>(st + fb_off[ks][ni]);
-#pragma unroll
-            for (int l = 0; l < 2; ++l)
-#pragma unroll
-                for (int mi = 0; mi < 4; ++mi)
-                    fa[ks][l][mi] = *reinterpret_cast<const i32x4*>(st + fa_off[ks][l][mi]);
-        }
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-                for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-                    for (int l = 0; l < 2; ++l)
-                        acc[l][mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks][l][mi], fb[ks][ni], acc[l][mi][ni], 0, 0, 0);
-    }
-
-#ifdef GRIM_I8_TIMING
-    const uint64_t te0 = __builtin_amdgcn_s_memtime();
-#endif
-    // ---- epilogue.  acc[l][mi][ni][v] is row 32 mi + 8 (v/4) + 4 (l/32) +
-    // v%4, column 32 (2 w + ni) + l%32 of the tile.  The tile goes through
-    // LDS (the ring is idle now) so that global stores are whole rows, 16
-    // bytes per lane; row scales through LDS too.
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    float* srow = reinterpret_cast<float*>(smem[3] + 32768 - QBM * 4);
-    if (tid < QBM) srow[tid] = tid < rows_valid ? src.sa[arow0 + tid] : 0.0f;
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    float* stg = reinterpret_cast<float*>(smem[0]);
-    if constexpr (SWIGLU) {
-        // h [128 rows][128 columns] fp32, row pitch 132 floats
-        constexpr int P = QBN / 2 + 4;
-        const int hcl = wave * 32 + (lane & 31);
-        const int hc = nt * (QBN / 2) + hcl;
-        const float sg = hc < g.I ? src.ws[wrow0 + hc] : 0.0f;
-        const float su = hc < g.I ? src.ws[wrow0 + g.I + hc] : 0.0f;
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int r = mi * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                const float sr = srow[r];
-                const float gv = sr * sg * __builtin_fmaf(float(acc[1][mi][0][v]), kLoScale, float(acc[0][mi][0][v]));
-                const float uv = sr * su * __builtin_fmaf(float(acc[1][mi][1][v]), kLoScale, float(acc[0][mi][1][v]));
-                stg[r * P + hcl] = fast_silu(gv) * uv;
-            }
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        // 128 rows x 32 chunks of 16 bytes: 16 per thread, a row per half-wave
-        const int c0 = nt * (QBN / 2);
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const int c = tid + k * kQThreads;
-            const int r = c >> 5, part = c & 31;
-            const int col = c0 + part * 4;
-            if (r < rows_valid && col < g.I)
-                *reinterpret_cast<float4*>(src.out + (arow0 + r) * g.I + col) =
-                    *reinterpret_cast<const float4*>(&stg[r * P + part * 4]);
-        }
-    } else {
-        // [128 rows][256 columns] fp32 in two halves of 64 rows, pitch 260
-        constexpr int P = QBN + 4;
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            if (half) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-#pragma unroll
-            for (int ni = 0; ni < 2; ++ni) {
-                const int cl = wave * 64 + ni * 32 + (lane & 31);
-                const int n = nt * QBN + cl;
-                const float sc = n < g.N ? src.ws[wrow0 + n] : 0.0f;
-#pragma unroll
-                for (int mh = 0; mh < 2; ++mh) {
-                    const int mi = 2 * half + mh;
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        const int r = mi * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                        stg[(r - 64 * half) * P + cl] =
-                            srow[r] * sc * __builtin_fmaf(float(acc[1][mi][ni][v]), kLoScale, float(acc[0][mi][ni][v]));
-                    }
-                }
-            }
-            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            // 64 rows x 64 chunks of 16 bytes: 16 per thread, a row per wave
-#pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                const int c = tid + k * kQThreads;
-                const int rl = c >> 6, part = c & 63;
-                const int r = 64 * half + rl;
-                const int col = nt * QBN + part * 4;
-                if (r < rows_valid && col < g.N)
-                    *reinterpret_cast<float4*>(src.out + (arow0 + r) * g.N + col) =
-                        *reinterpret_cast<const float4*>(&stg[rl * P + part * 4]);
-            }
-        }
-    }
-    // the ring is refilled by the next tile only after every wave's LDS
-    // reads; its first wait also covers these stores (one in-order counter)
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-#ifdef GRIM_I8_TIMING
-    g_i8_epi[blockIdx.x * 4 + wave] += __builtin_amdgcn_s_memtime() - te0;
-#endif
+    I8Item it;
+    it.col0 = nt * (SWIGLU ? QBN / 2 : QBN);
+    it.rows = max(0, __builtin_amdgcn_readfirstlane(rows_valid));
+    it.arow0 = int64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(arow0)))) |
+               (int64_t(__builtin_amdgcn_readfirstlane(int(arow0 >> 32))) << 32);
+    const int64_t wr = wrow0 + it.col0;
+    it.wrow = int64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(wr)))) |
+              (int64_t(__builtin_amdgcn_readfirstlane(int(wr >> 32))) << 32);
+    return it;
 }
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t i8_rsrc(const void* p, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
+
+// Persistent XCD-aware walk over (m-tile, column tile) items with one
+// continuous stream of K tiles through the 4-stage LDS ring: the last three
+// iterations of an item request the next item's first three tiles (and,
+// ahead of them, its row and column scales), so an item starts with its
+// data already in LDS, and the epilogue stores straight from the
+// accumulators (no LDS, no barrier) while those tiles land.
+//
+// Iteration t of an item: tile t complete -- this wave's loads and stores
+// complete in issue order, so waiting until at most Y operations younger
+// than tile t's last load are outstanding suffices (Y = 16: the two tiles
+// requested after it; plus the previous item's epilogue stores for t < 3;
+// capped at 63, the counter's limit); the barrier then covers every
+// wave's loads and retires every wave's reads of tile t - 1, whose stage
+// takes stream tile t + 3.  Tile t's 20 fragments are read at once, and its
+// 32 MFMAs run with the 8 DMA instructions for tile t + 3 interleaved, one
+// per 4 MFMAs (issued together, the 4 waves' 32 instructions would queue
+// at the texture unit, 16 cycles each, and hold the MFMAs back).  Past the
+// last item the stream requests tiles from an empty buffer (num_records 0:
+// no memory traffic), which keeps every iteration alike.
 template <bool SWIGLU>
 __global__ __launch_bounds__(kQThreads, 1) void grouped_gemm_i8_kernel(GemmI8Args g, int n_col_tiles,
                                                                       int shared_part) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kQStages][kQStageBytes];
+    // per item parity: row scales [128] at 0, column scales at 1024 (plain:
+    // [256]; SwiGLU: gate [128] then up [128])
+    __shared__ __attribute__((aligned(16))) float meta[2][512];
     const bool routed = shared_part == 0;
     const I8Src src{routed ? g.w : g.w_sh, routed ? g.ws : g.ws_sh,
                     routed ? g.row_bytes : g.row_bytes_sh, routed ? g.A : g.A_sh,
@@ -320,13 +182,286 @@ __global__ __launch_bounds__(kQThreads, 1) void grouped_gemm_i8_kernel(GemmI8Arg
     const int xcd = blockIdx.x % kQXcds, per_xcd = gridDim.x / kQXcds;
     const int lo = int(int64_t(total) * xcd / kQXcds), hi = int(int64_t(total) * (xcd + 1) / kQXcds);
     const int items = (hi - lo) * n_col_tiles;
+    int i = blockIdx.x / kQXcds;
+    if (i >= items) return;
 #ifdef GRIM_I8_TIMING
     const uint64_t t0 = __builtin_amdgcn_s_memtime();
 #endif
-    for (int i = blockIdx.x / kQXcds; i < items; i += per_xcd)
-        i8_tile<SWIGLU>(g, src, routed, lo + i / n_col_tiles, i % n_col_tiles, smem);
+
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+    const int K = g.K;
+    const int a_row_bytes = 2 * K;
+
+    // Stage layout (one K tile of 64):
+    //   A 16 KiB: row r's 128 bytes (limb hi K 0..63, limb lo K 0..63 as
+    //     eight 16-byte chunks c = 4 limb + K/16) at r * 128, chunk c at
+    //     physical slot c ^ ((r >> 1) & 7);
+    //   B 16 KiB: tile column n's 64 bytes (four chunks c = K/16) at
+    //     16384 + n * 64, chunk c at slot c ^ ((n >> 2) & 3).
+    // The swizzles make every fragment read (32 rows or columns at one
+    // chunk, 16 lanes per LDS cycle) hit 16 distinct 16-byte slots of the
+    // bank window.  Each DMA instruction covers whole row segments: A 8 rows
+    // x 128 bytes, B 16 columns x 64 bytes (lane i: 16 bytes at slot i).
+    // In global memory A rows are [K/64][2][64] bytes (the quantisers write
+    // that layout), B rows are the weight rows as stored.
+    // Per-lane offsets, formed from an opaque copy of the lane index: once
+    // here and again at every item's start, so that they are not kept live
+    // (and spilled) across the epilogue, whose reloads would make the
+    // compiler wait for every outstanding load before each fragment read.
+    int a_off[4], b_off[4], fa_off[2][2][4], fb_off[2][2];
+#define GRIM_I8_OFFSETS()                                                                         \
+    do {                                                                                          \
+        const int ln = lane_id();                                                                 \
+        _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                           \
+            const int ja = 4 * wave + j;                                                          \
+            const int r = 8 * ja + (ln >> 3), pc = ln & 7;                                        \
+            a_off[j] = r * a_row_bytes + ((pc ^ ((r >> 1) & 7)) << 4);                            \
+            const int col = 16 * ja + (ln >> 2), pcb = ln & 3;                                    \
+            const int nsub = col >> 5, x = col & 31;                                              \
+            /* SwiGLU: h columns [32 w', +32) of wave w' = nsub / 2: gate rows */                 \
+            /* for nsub even, up rows for nsub odd; otherwise the tile's columns */               \
+            const int row = SWIGLU ? ((nsub & 1) ? g.I : 0) + (nsub >> 1) * 32 + x : col;         \
+            b_off[j] = row * int(src.row_bytes) + ((pcb ^ ((col >> 2) & 3)) << 4);                \
+        }                                                                                         \
+        /* fragment read addresses inside a stage */                                              \
+        _Pragma("unroll") for (int ks = 0; ks < 2; ++ks) {                                        \
+            const int ch = 2 * ks + (ln >> 5);                                                    \
+            _Pragma("unroll") for (int l = 0; l < 2; ++l)                                         \
+                _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) {                                \
+                    const int r = mi * 32 + (ln & 31);                                            \
+                    fa_off[ks][l][mi] = r * 128 + (((4 * l + ch) ^ ((r >> 1) & 7)) << 4);         \
+                }                                                                                 \
+            _Pragma("unroll") for (int ni = 0; ni < 2; ++ni) {                                    \
+                const int n = (2 * wave + ni) * 32 + (ln & 31);                                   \
+                fb_off[ks][ni] = 16384 + n * 64 + ((ch ^ ((n >> 2) & 3)) << 4);                   \
+            }                                                                                     \
+        }                                                                                         \
+    } while (0)
+    GRIM_I8_OFFSETS();
+
+    auto tile_of = [&](int ii) { return lo + ii / n_col_tiles; };
+    auto col_of = [&](int ii) { return ii % n_col_tiles; };
+    const int n_slab = SWIGLU ? 2 * g.I : g.N;
+    const int ldo = SWIGLU ? g.I : g.N;
+    // weight rows from the tile's first one; for SwiGLU the up rows follow
+    // I rows later (gate rows past I read up rows: their columns are never
+    // stored).  rows == 0 (past the last item) gives empty buffers.
+    auto rsrc_a = [&](const I8Item& it) { return i8_rsrc(src.A + it.arow0 * a_row_bytes, it.rows * a_row_bytes); };
+    auto rsrc_b = [&](const I8Item& it) {
+        return i8_rsrc(src.w + it.wrow * src.row_bytes,
+                       it.rows > 0 ? int((n_slab - it.col0) * src.row_bytes) : 0);
+    };
+    // scale requests: wave 0 the 128 row scales (lanes 32..63 past the end
+    // read zero into padding), wave 1 the 256 column scales
+    auto request_meta = [&](const I8Item& it, int par) {
+        const int ln = lane_id();
+        if (wave == 0) {
+            dma16<0>(i8_rsrc(src.sa + it.arow0, it.rows * 4), reinterpret_cast<uint8_t*>(&meta[par][0]),
+                     ln * 16, 0);
+        } else if (wave == 1) {
+            const int m_off = (SWIGLU && ln >= 32) ? g.I * 4 + (ln - 32) * 16 : ln * 16;
+            dma16<0>(i8_rsrc(src.ws + it.wrow, it.rows > 0 ? (n_slab - it.col0) * 4 : 0),
+                     reinterpret_cast<uint8_t*>(&meta[par][256]), m_off, 0);
+        }
+    };
+    auto request = [&](const I8Item& it, int stage, int t) {
+        uint8_t* st = smem[stage];
+        const __amdgpu_buffer_rsrc_t ra = rsrc_a(it), rb = rsrc_b(it);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dma16<0>(ra, st + (4 * wave + j) * 1024, a_off[j], t * 128);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            dma16<2>(rb, st + 16384 + (4 * wave + j) * 1024, b_off[j], t * QBK);
+    };
+
+    const int nk = K / QBK;   // >= 3
+    I8Item cur = i8_item<SWIGLU>(g, routed, tile_of(i), col_of(i));
+    request_meta(cur, 0);
+#pragma unroll
+    for (int p = 0; p < kQStages - 1; ++p) request(cur, p, p);
+    I8Item none;
+    none.arow0 = 0; none.wrow = 0; none.rows = 0; none.col0 = 0;
+
+    // LDS byte address of the ring (a C-style cast is the address-space cast)
+    const int smem_base = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)(&smem[0][0])));
+    const int meta_base = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) float*)(&meta[0][0])));
+    int gs = 0, par = 0;
+    bool first = true;
+    i32x16 acc[2][4][2];
+    i32x4 fb[2][2], fa[2][2][4];
+    for (; i < items; i += per_xcd) {
+        GRIM_I8_OFFSETS();
+        const bool more = i + per_xcd < items;
+        const I8Item nxt = more ? i8_item<SWIGLU>(g, routed, tile_of(i + per_xcd), col_of(i + per_xcd))
+                                : none;
+#pragma unroll
+        for (int l = 0; l < 2; ++l)
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[l][mi][ni][v] = 0;
+        // the wait before tile t: vmcnt(63) right after an epilogue (t < 3,
+        // its stores are younger than tile t), else vmcnt(16); one asm block
+        // so that the loop body is not duplicated per case
+#define GRIM_I8_WAIT(after_epi)                                                                   \
+        asm volatile("s_cmp_eq_u32 %0, 0\n\t"                                                    \
+                     "s_cbranch_scc1 .Lgrim_w16_%=\n\t"                                           \
+                     "s_waitcnt vmcnt(63)\n\t"                                                   \
+                     "s_branch .Lgrim_wdone_%=\n"                                                 \
+                     ".Lgrim_w16_%=:\n\t"                                                        \
+                     "s_waitcnt vmcnt(16)\n"                                                      \
+                     ".Lgrim_wdone_%=:\n\t"                                                      \
+                     "s_waitcnt lgkmcnt(0)\n\t"                                                  \
+                     "s_barrier" ::"s"(__builtin_amdgcn_readfirstlane(after_epi)) : "memory", "scc")
+        // Fragment reads are inline asm with explicit lgkmcnt waits tied to
+        // the fragment registers: the compiler cannot tell that they and the
+        // in-flight DMA writes touch different ring stages, and guards a
+        // compiler-visible LDS read with a wait for every outstanding load.
+        // Reads in MFMA order (ks, mi; B then the two limbs); at most 14
+        // outstanding (lgkmcnt holds 15).
+#define GRIM_I8_DSR(dst, addr)                                                                    \
+        asm volatile("ds_read_b128 %0, %1" : "=v"(dst) : "v"(addr))
+#define GRIM_I8_LGKM(n, ks_, mi_)                                                                 \
+        asm volatile("s_waitcnt lgkmcnt(" #n ")"                                                   \
+                     : "+v"(fb[ks_][0]), "+v"(fb[ks_][1]), "+v"(fa[ks_][0][mi_]), "+v"(fa[ks_][1][mi_]))
+#define GRIM_I8_MMA_MI(ks_, mi_)                                                                  \
+        _Pragma("unroll") for (int ni = 0; ni < 2; ++ni)                                          \
+            _Pragma("unroll") for (int l = 0; l < 2; ++l)                                         \
+                acc[l][mi_][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks_][l][mi_], fb[ks_][ni], \
+                                                                        acc[l][mi_][ni], 0, 0, 0)
+#define GRIM_I8_DMA(q)                                                                            \
+        do {                                                                                      \
+            if ((q) < 4) dma16<0>(qa, nx + (4 * wave + (q)) * 1024, a_off[(q) & 3], tu * 128);    \
+            else dma16<2>(qb, nx + 16384 + (4 * wave + (q) - 4) * 1024, b_off[(q) & 3], tu * QBK); \
+        } while (0)
+#define GRIM_I8_ITER(t_, META)                                                                    \
+        do {                                                                                      \
+            const int t = (t_);                                                                   \
+            GRIM_I8_WAIT((t < 3 && !first) ? 1 : 0);                                              \
+            const int sb = ((gs + t) & 3) * kQStageBytes + smem_base;                             \
+            GRIM_I8_DSR(fb[0][0], sb + fb_off[0][0]);                                             \
+            GRIM_I8_DSR(fb[0][1], sb + fb_off[0][1]);                                             \
+            _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) {                                    \
+                GRIM_I8_DSR(fa[0][0][mi], sb + fa_off[0][0][mi]);                                 \
+                GRIM_I8_DSR(fa[0][1][mi], sb + fa_off[0][1][mi]);                                 \
+            }                                                                                     \
+            GRIM_I8_DSR(fb[1][0], sb + fb_off[1][0]);                                             \
+            GRIM_I8_DSR(fb[1][1], sb + fb_off[1][1]);                                             \
+            GRIM_I8_DSR(fa[1][0][0], sb + fa_off[1][0][0]);                                       \
+            GRIM_I8_DSR(fa[1][1][0], sb + fa_off[1][1][0]);                                       \
+            if (META) request_meta(nxt, par ^ 1);                                                 \
+            /* stream tile t + 3: this item's, or the next item's 0, 1, 2 */                      \
+            const int u = t + kQStages - 1;                                                       \
+            const bool own = u < nk;                                                              \
+            const __amdgpu_buffer_rsrc_t qa = rsrc_a(own ? cur : nxt);                            \
+            const __amdgpu_buffer_rsrc_t qb = rsrc_b(own ? cur : nxt);                            \
+            const int tu = own ? u : u - nk;                                                      \
+            uint8_t* nx = smem[(gs + u) & 3];                                                     \
+            GRIM_I8_LGKM(10, 0, 0); GRIM_I8_MMA_MI(0, 0); GRIM_I8_DMA(0);                         \
+            GRIM_I8_LGKM(8, 0, 1);  GRIM_I8_MMA_MI(0, 1); GRIM_I8_DMA(1);                         \
+            GRIM_I8_LGKM(6, 0, 2);  GRIM_I8_MMA_MI(0, 2); GRIM_I8_DMA(2);                         \
+            GRIM_I8_LGKM(4, 0, 3);  GRIM_I8_MMA_MI(0, 3); GRIM_I8_DMA(3);                         \
+            _Pragma("unroll") for (int mi = 1; mi < 4; ++mi) {                                    \
+                GRIM_I8_DSR(fa[1][0][mi], sb + fa_off[1][0][mi]);                                 \
+                GRIM_I8_DSR(fa[1][1][mi], sb + fa_off[1][1][mi]);                                 \
+            }                                                                                     \
+            GRIM_I8_LGKM(6, 1, 0);  GRIM_I8_MMA_MI(1, 0); GRIM_I8_DMA(4);                         \
+            GRIM_I8_LGKM(4, 1, 1);  GRIM_I8_MMA_MI(1, 1); GRIM_I8_DMA(5);                         \
+            GRIM_I8_LGKM(2, 1, 2);  GRIM_I8_MMA_MI(1, 2); GRIM_I8_DMA(6);                         \
+            GRIM_I8_LGKM(0, 1, 3);  GRIM_I8_MMA_MI(1, 3); GRIM_I8_DMA(7);                         \
+        } while (0)
+        // iteration 0 also requests the next item's scales: after its
+        // barrier (every wave is past the epilogue that read that parity)
+        // and before any of the next item's tiles
+        GRIM_I8_ITER(0, true);
+        for (int t1 = 1; t1 < nk; ++t1) GRIM_I8_ITER(t1, false);
+#undef GRIM_I8_ITER
+#undef GRIM_I8_WAIT
+#undef GRIM_I8_DSR
+#undef GRIM_I8_LGKM
+#undef GRIM_I8_MMA_MI
+#undef GRIM_I8_DMA
+
 #ifdef GRIM_I8_TIMING
-    g_i8_total[blockIdx.x * 4 + threadIdx.x / 64] += __builtin_amdgcn_s_memtime() - t0;
+        const uint64_t te0 = __builtin_amdgcn_s_memtime();
+#endif
+        // ---- epilogue.  acc[l][mi][ni][v] is row 32 mi + 8 (v/4) + 4 (l/32)
+        // + v%4, column 32 (2 w + ni) + l%32 of the tile.  Scales from LDS
+        // (landed with tile 0, behind this item's barriers); each store
+        // writes two 128-byte row segments.
+        const __amdgpu_buffer_rsrc_t ro = i8_rsrc(src.out + cur.arow0 * ldo, cur.rows * ldo * 4);
+        // the scales are read by inline asm too (a compiler-visible LDS read
+        // here would wait for the next item's tiles already in flight)
+        const int mb = meta_base + par * 2048;
+        const int ln = lane_id();
+        const int hrow = 4 * (ln >> 5);
+        if constexpr (SWIGLU) {
+            const int hcl = wave * 32 + (ln & 31);
+            float sg = lds_f32(mb + 1024 + hcl * 4), su = lds_f32(mb + 1024 + (128 + hcl) * 4);
+            // per-lane byte offset of (row hrow, this column), opaque so the
+            // 64 row offsets below are formed here and not kept live
+            int base = cur.col0 + hcl < g.I ? (hrow * g.I + cur.col0 + hcl) * 4 : 0x40000000;
+            asm volatile("" : "+v"(base));
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi) {
+                f32x4v s4[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) s4[q] = lds_f32x4(mb + (mi * 32 + 8 * q + hrow) * 4);
+                asm volatile("s_waitcnt lgkmcnt(0)"
+                             : "+v"(s4[0]), "+v"(s4[1]), "+v"(s4[2]), "+v"(s4[3]), "+v"(sg), "+v"(su));
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int v = 4 * q + j;
+                        const float gv = s4[q][j] * sg * __builtin_fmaf(float(acc[1][mi][0][v]), kLoScale, float(acc[0][mi][0][v]));
+                        const float uv = s4[q][j] * su * __builtin_fmaf(float(acc[1][mi][1][v]), kLoScale, float(acc[0][mi][1][v]));
+                        const int off = base + (mi * 32 + 8 * q + j) * g.I * 4;
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, fast_silu(gv) * uv),
+                                                              ro, off, 0, 0);
+                    }
+            }
+        } else {
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                const int cl = wave * 64 + ni * 32 + (ln & 31);
+                float sc = lds_f32(mb + 1024 + cl * 4);
+                int base = cur.col0 + cl < g.N ? (hrow * g.N + cur.col0 + cl) * 4 : 0x40000000;
+                asm volatile("" : "+v"(base));
+#pragma unroll
+                for (int mi = 0; mi < 4; ++mi) {
+                    f32x4v s4[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) s4[q] = lds_f32x4(mb + (mi * 32 + 8 * q + hrow) * 4);
+                    asm volatile("s_waitcnt lgkmcnt(0)"
+                                 : "+v"(s4[0]), "+v"(s4[1]), "+v"(s4[2]), "+v"(s4[3]), "+v"(sc));
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const int v = 4 * q + j;
+                            const float y = s4[q][j] * sc * __builtin_fmaf(float(acc[1][mi][ni][v]), kLoScale, float(acc[0][mi][ni][v]));
+                            const int off = base + (mi * 32 + 8 * q + j) * g.N * 4;
+                            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ro, off, 0, 0);
+                        }
+                }
+            }
+        }
+#ifdef GRIM_I8_TIMING
+        g_i8_epi[blockIdx.x * 4 + wave] += __builtin_amdgcn_s_memtime() - te0;
+#endif
+        gs += nk;
+        par ^= 1;
+        cur = nxt;
+        first = false;
+    }
+#undef GRIM_I8_OFFSETS
+    // drain: the last iterations requested tiles from the empty buffer
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#ifdef GRIM_I8_TIMING
+    g_i8_total[blockIdx.x * 4 + wave] += __builtin_amdgcn_s_memtime() - t0;
 #endif
 }
 
