@@ -6,9 +6,10 @@
 // atomics:
 //   1. count   each block counts its chunk of routes per expert in LDS and
 //              writes the row bcount[b][E];
-//   2. scan    one block turns bcount into per-(block, expert) bases
-//              inside the expert, per-expert counts and exclusive offsets,
-//              and the m-tile table (src/prefill.cpp:2770-2782);
+//   2. scan    a column scan turns bcount into per-(block, expert) bases
+//              inside the expert and per-expert counts; one block then
+//              forms the exclusive offsets and the m-tile table
+//              (src/prefill.cpp:2770-2782);
 //   3. rank    each block ranks its routes inside their expert by counting
 //              earlier routes of the same expert in the block (stable);
 //              row = offsets[e] + block base + rank;
@@ -39,9 +40,39 @@ __global__ __launch_bounds__(kDispThreads) void disp_count(const int32_t* __rest
     for (int e = threadIdx.x; e < E; e += blockDim.x) bcount[int64_t(blockIdx.x) * E + e] = hist[e];
 }
 
-// One block of 1024 threads; expert e is handled by thread e (and e+1024...).
-__global__ __launch_bounds__(1024) void disp_scan(int32_t* __restrict__ bcount, int nb, int E,
-                                                  int32_t* __restrict__ counts,
+// Per-block bases inside each expert: one block per 64 experts, 16 threads
+// per expert each summing a contiguous slice of the count blocks (all its
+// loads in flight together), slices combined in LDS; writes the exclusive
+// bases back into bcount and the expert's total into counts.
+constexpr int kColExperts = 64, kColSlices = 16;
+__global__ __launch_bounds__(kColExperts * kColSlices) void disp_colscan(int32_t* __restrict__ bcount,
+                                                                       int nb, int E,
+                                                                       int32_t* __restrict__ counts) {
+    __shared__ int32_t ssum[kColSlices][kColExperts];
+    const int el = threadIdx.x % kColExperts, sl = threadIdx.x / kColExperts;
+    const int e = blockIdx.x * kColExperts + el;
+    const int per = (nb + kColSlices - 1) / kColSlices;
+    const int b0 = sl * per, b1 = min(nb, b0 + per);
+    int tot = 0;
+    if (e < E)
+        for (int b = b0; b < b1; ++b) tot += bcount[int64_t(b) * E + e];
+    ssum[sl][el] = tot;
+    __syncthreads();
+    int base = 0;
+    for (int k = 0; k < sl; ++k) base += ssum[k][el];
+    if (e < E) {
+        for (int b = b0; b < b1; ++b) {
+            const int v = bcount[int64_t(b) * E + e];
+            bcount[int64_t(b) * E + e] = base;
+            base += v;
+        }
+        if (sl == kColSlices - 1) counts[e] = base;
+    }
+}
+
+// One block of 1024 threads over the expert totals: exclusive offsets, the
+// m-tile table and the live tile count.
+__global__ __launch_bounds__(1024) void disp_scan(int E, int32_t* __restrict__ counts,
                                                   int32_t* __restrict__ offsets,
                                                   int32_t* __restrict__ tile_e,
                                                   int32_t* __restrict__ tile_mb, int tmax, int mc,
@@ -53,19 +84,7 @@ __global__ __launch_bounds__(1024) void disp_scan(int32_t* __restrict__ bcount, 
     __syncthreads();
     for (int e0 = 0; e0 < E; e0 += 1024) {
         const int e = e0 + threadIdx.x;
-        int c = 0;
-        if (e < E) {
-            // per-block bases inside the expert (block order = route order);
-            // 16 independent loads in flight per step (clamped, then masked)
-            for (int b0 = 0; b0 < nb; b0 += 16) {
-                int v[16];
-#pragma unroll
-                for (int j = 0; j < 16; ++j) v[j] = bcount[int64_t(min(b0 + j, nb - 1)) * E + e];
-#pragma unroll
-                for (int j = 0; j < 16; ++j)
-                    if (b0 + j < nb) { bcount[int64_t(b0 + j) * E + e] = c; c += v[j]; }
-            }
-        }
+        const int c = e < E ? counts[e] : 0;
         const int nt = (mc > 0 && e < E) ? (c + mc - 1) / mc : 0;
         part[threadIdx.x] = c;
         tpart[threadIdx.x] = nt;
@@ -82,7 +101,6 @@ __global__ __launch_bounds__(1024) void disp_scan(int32_t* __restrict__ bcount, 
         const int rbase = carry[0] + part[threadIdx.x] - c;
         const int tbase = carry[1] + tpart[threadIdx.x] - nt;
         if (e < E) {
-            counts[e] = c;
             offsets[e] = rbase;
             if (tile_e)
                 for (int i = 0; i < nt; ++i)
@@ -178,8 +196,11 @@ hipError_t dispatch_launch(hipStream_t st, const DispatchArgs& a) {
     if (nb > 0)
         hipLaunchKernelGGL(disp_count, dim3(nb), dim3(kDispThreads), size_t(a.E) * 4, st, a.ids, R,
                            a.E, bcount);
-    hipLaunchKernelGGL(disp_scan, dim3(1), dim3(1024), 0, st, bcount, nb, a.E, a.counts, a.offsets,
-                       a.tile_e, a.tile_mb, a.tmax, a.mc, ntiles);
+    // T > 0 here (the callers return before), so nb >= 1
+    hipLaunchKernelGGL(disp_colscan, dim3((a.E + kColExperts - 1) / kColExperts),
+                       dim3(kColExperts * kColSlices), 0, st, bcount, nb, a.E, a.counts);
+    hipLaunchKernelGGL(disp_scan, dim3(1), dim3(1024), 0, st, a.E, a.counts, a.offsets, a.tile_e,
+                       a.tile_mb, a.tmax, a.mc, ntiles);
     if (nb > 0)
         hipLaunchKernelGGL(disp_rank, dim3(nb), dim3(kDispThreads), 0, st, a.ids, R, a.E, a.K,
                            bcount, a.offsets, a.inverse, a.perm_token);

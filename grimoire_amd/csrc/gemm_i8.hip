@@ -46,7 +46,7 @@ constexpr float kLoScale = 1.0f / 254.0f;
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 #ifdef GRIM_I8_TIMING
-__device__ uint64_t g_i8_total[4096], g_i8_epi[4096];
+__device__ uint64_t g_i8_total[8192], g_i8_epi[8192], g_i8_wait[8192];
 #endif
 
 template <int AUX>
@@ -105,13 +105,16 @@ struct I8Src {
 struct I8Item {
     int64_t arow0, wrow;   // wrow: first weight row of the tile (expert base + col0)
     int rows, col0;
+    int sh;                // 1: a shared-expert item (its own A rows, weights, output)
 };
 
 template <bool SWIGLU>
-__device__ __forceinline__ I8Item i8_item(const GemmI8Args& g, bool routed, int ty, int nt) {
+__device__ __forceinline__ I8Item i8_item(const GemmI8Args& g, int n_routed, int ty, int nt) {
     int rows_valid;
     int64_t arow0, wrow0;
     ty = __builtin_amdgcn_readfirstlane(ty);
+    const bool routed = ty < n_routed;
+    if (!routed) ty -= n_routed;
     if (routed) {
         const int e = sload_i32(g.tile_e + ty);
         const int ec = e < 0 ? 0 : e;
@@ -125,6 +128,7 @@ __device__ __forceinline__ I8Item i8_item(const GemmI8Args& g, bool routed, int 
         wrow0 = 0;
     }
     I8Item it;
+    it.sh = routed ? 0 : 1;
     it.col0 = nt * (SWIGLU ? QBN / 2 : QBN);
     it.rows = max(0, __builtin_amdgcn_readfirstlane(rows_valid));
     it.arow0 = int64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(arow0)))) |
@@ -158,24 +162,31 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t i8_rsrc(const void* p, int byt
 // at the texture unit, 16 cycles each, and hold the MFMAs back).  Past the
 // last item the stream requests tiles from an empty buffer (num_records 0:
 // no memory traffic), which keeps every iteration alike.
-template <bool SWIGLU>
-__global__ __launch_bounds__(kQThreads, 1) void grouped_gemm_i8_kernel(GemmI8Args g, int n_col_tiles,
-                                                                      int shared_part) {
+template <bool SWIGLU, int WM>
+__global__ __launch_bounds__(256 * WM) void grouped_gemm_i8_kernel(GemmI8Args g, int n_col_tiles,
+                                                                  int parts) {
+    // WM = 1: 4 waves, wave w owns tile columns [64w, +64) for all 128 rows;
+    // WM = 2: 8 waves (two per SIMD, so one wave's MFMAs run while the
+    // other waits on its loads or its epilogue), wave w owns columns
+    // [64 (w % 4), +64) for rows [64 (w / 4), +64).
+    constexpr int MIW = 4 / WM;              // 32-row MFMA tiles per wave
+    constexpr int NJ = 4 / WM;               // DMA instructions per wave per K tile, for A and for B
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kQStages][kQStageBytes];
     // per item parity: row scales [128] at 0, column scales at 1024 (plain:
     // [256]; SwiGLU: gate [128] then up [128])
     __shared__ __attribute__((aligned(16))) float meta[2][512];
-    const bool routed = shared_part == 0;
-    const I8Src src{routed ? g.w : g.w_sh, routed ? g.ws : g.ws_sh,
-                    routed ? g.row_bytes : g.row_bytes_sh, routed ? g.A : g.A_sh,
-                    routed ? g.sa : g.sa_sh, routed ? g.out : g.out_sh};
-    int total;
-    if (routed) {
-        total = g.n_tiles_dev ? __builtin_amdgcn_readfirstlane(*g.n_tiles_dev) : g.tmax;
-        total = total < g.tmax ? total : g.tmax;
-    } else {
-        total = (g.T_sh + QBM - 1) / QBM;
+    // parts: 1 = routed m-tiles, 2 = the shared expert's, 3 = both in one
+    // list (routed first; the host fuses them only when the two weight sets
+    // share a row length, which the per-lane weight offsets assume)
+    const I8Src src_r{g.w, g.ws, g.row_bytes, g.A, g.sa, g.out};
+    const I8Src src_s{g.w_sh, g.ws_sh, g.row_bytes_sh, g.A_sh, g.sa_sh, g.out_sh};
+    const int64_t wrb = parts == 2 ? g.row_bytes_sh : g.row_bytes;
+    int n_routed = 0;
+    if (parts & 1) {
+        n_routed = g.n_tiles_dev ? __builtin_amdgcn_readfirstlane(*g.n_tiles_dev) : g.tmax;
+        n_routed = n_routed < g.tmax ? n_routed : g.tmax;
     }
+    const int total = n_routed + ((parts & 2) ? (g.T_sh + QBM - 1) / QBM : 0);
     // work-group b runs on XCD b % 8: each XCD walks a contiguous range of
     // the m-tile list, column tiles fastest, so an expert's weights and an
     // A row block stay under one L2
@@ -189,6 +200,7 @@ __global__ __launch_bounds__(kQThreads, 1) void grouped_gemm_i8_kernel(GemmI8Arg
 #endif
 
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+    const int wn = wave & 3, wm = wave >> 2;
     const int K = g.K;
     const int a_row_bytes = 2 * K;
 
@@ -208,12 +220,12 @@ __global__ __launch_bounds__(kQThreads, 1) void grouped_gemm_i8_kernel(GemmI8Arg
     // here and again at every item's start, so that they are not kept live
     // (and spilled) across the epilogue, whose reloads would make the
     // compiler wait for every outstanding load before each fragment read.
-    int a_off[4], b_off[4], fa_off[2][2][4], fb_off[2][2];
+    int a_off[NJ], b_off[NJ], fa_off[2][2][MIW], fb_off[2][2];
 #define GRIM_I8_OFFSETS()                                                                         \
     do {                                                                                          \
         const int ln = lane_id();                                                                 \
-        _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                           \
-            const int ja = 4 * wave + j;                                                          \
+        _Pragma("unroll") for (int j = 0; j < NJ; ++j) {                                          \
+            const int ja = NJ * wave + j;                                                         \
             const int r = 8 * ja + (ln >> 3), pc = ln & 7;                                        \
             a_off[j] = r * a_row_bytes + ((pc ^ ((r >> 1) & 7)) << 4);                            \
             const int col = 16 * ja + (ln >> 2), pcb = ln & 3;                                    \
@@ -221,18 +233,18 @@ __global__ __launch_bounds__(kQThreads, 1) void grouped_gemm_i8_kernel(GemmI8Arg
             /* SwiGLU: h columns [32 w', +32) of wave w' = nsub / 2: gate rows */                 \
             /* for nsub even, up rows for nsub odd; otherwise the tile's columns */               \
             const int row = SWIGLU ? ((nsub & 1) ? g.I : 0) + (nsub >> 1) * 32 + x : col;         \
-            b_off[j] = row * int(src.row_bytes) + ((pcb ^ ((col >> 2) & 3)) << 4);                \
+            b_off[j] = row * int(wrb) + ((pcb ^ ((col >> 2) & 3)) << 4);                          \
         }                                                                                         \
         /* fragment read addresses inside a stage */                                              \
         _Pragma("unroll") for (int ks = 0; ks < 2; ++ks) {                                        \
             const int ch = 2 * ks + (ln >> 5);                                                    \
             _Pragma("unroll") for (int l = 0; l < 2; ++l)                                         \
-                _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) {                                \
-                    const int r = mi * 32 + (ln & 31);                                            \
+                _Pragma("unroll") for (int mi = 0; mi < MIW; ++mi) {                              \
+                    const int r = (wm * MIW + mi) * 32 + (ln & 31);                               \
                     fa_off[ks][l][mi] = r * 128 + (((4 * l + ch) ^ ((r >> 1) & 7)) << 4);         \
                 }                                                                                 \
             _Pragma("unroll") for (int ni = 0; ni < 2; ++ni) {                                    \
-                const int n = (2 * wave + ni) * 32 + (ln & 31);                                   \
+                const int n = (2 * wn + ni) * 32 + (ln & 31);                                     \
                 fb_off[ks][ni] = 16384 + n * 64 + ((ch ^ ((n >> 2) & 3)) << 4);                   \
             }                                                                                     \
         }                                                                                         \
@@ -246,21 +258,25 @@ __global__ __launch_bounds__(kQThreads, 1) void grouped_gemm_i8_kernel(GemmI8Arg
     // weight rows from the tile's first one; for SwiGLU the up rows follow
     // I rows later (gate rows past I read up rows: their columns are never
     // stored).  rows == 0 (past the last item) gives empty buffers.
-    auto rsrc_a = [&](const I8Item& it) { return i8_rsrc(src.A + it.arow0 * a_row_bytes, it.rows * a_row_bytes); };
+    auto rsrc_a = [&](const I8Item& it) {
+        const int8_t* A = it.sh ? src_s.A : src_r.A;
+        return i8_rsrc(A + it.arow0 * a_row_bytes, it.rows * a_row_bytes);
+    };
     auto rsrc_b = [&](const I8Item& it) {
-        return i8_rsrc(src.w + it.wrow * src.row_bytes,
-                       it.rows > 0 ? int((n_slab - it.col0) * src.row_bytes) : 0);
+        const uint8_t* w = it.sh ? src_s.w : src_r.w;
+        return i8_rsrc(w + it.wrow * wrb, it.rows > 0 ? int((n_slab - it.col0) * wrb) : 0);
     };
     // scale requests: wave 0 the 128 row scales (lanes 32..63 past the end
     // read zero into padding), wave 1 the 256 column scales
     auto request_meta = [&](const I8Item& it, int par) {
         const int ln = lane_id();
         if (wave == 0) {
-            dma16<0>(i8_rsrc(src.sa + it.arow0, it.rows * 4), reinterpret_cast<uint8_t*>(&meta[par][0]),
+            dma16<0>(i8_rsrc((it.sh ? src_s.sa : src_r.sa) + it.arow0, it.rows * 4),
+                     reinterpret_cast<uint8_t*>(&meta[par][0]),
                      ln * 16, 0);
         } else if (wave == 1) {
             const int m_off = (SWIGLU && ln >= 32) ? g.I * 4 + (ln - 32) * 16 : ln * 16;
-            dma16<0>(i8_rsrc(src.ws + it.wrow, it.rows > 0 ? (n_slab - it.col0) * 4 : 0),
+            dma16<0>(i8_rsrc((it.sh ? src_s.ws : src_r.ws) + it.wrow, it.rows > 0 ? (n_slab - it.col0) * 4 : 0),
                      reinterpret_cast<uint8_t*>(&meta[par][256]), m_off, 0);
         }
     };
@@ -268,53 +284,68 @@ __global__ __launch_bounds__(kQThreads, 1) void grouped_gemm_i8_kernel(GemmI8Arg
         uint8_t* st = smem[stage];
         const __amdgpu_buffer_rsrc_t ra = rsrc_a(it), rb = rsrc_b(it);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dma16<0>(ra, st + (4 * wave + j) * 1024, a_off[j], t * 128);
+        for (int j = 0; j < NJ; ++j) dma16<0>(ra, st + (NJ * wave + j) * 1024, a_off[j], t * 128);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            dma16<2>(rb, st + 16384 + (4 * wave + j) * 1024, b_off[j], t * QBK);
+        for (int j = 0; j < NJ; ++j)
+            dma16<2>(rb, st + 16384 + (NJ * wave + j) * 1024, b_off[j], t * QBK);
     };
 
     const int nk = K / QBK;   // >= 3
-    I8Item cur = i8_item<SWIGLU>(g, routed, tile_of(i), col_of(i));
+    I8Item cur = i8_item<SWIGLU>(g, n_routed, tile_of(i), col_of(i));
+    I8Item none;
+    none.arow0 = 0; none.wrow = 0; none.rows = 0; none.col0 = 0; none.sh = 0;
     request_meta(cur, 0);
 #pragma unroll
     for (int p = 0; p < kQStages - 1; ++p) request(cur, p, p);
-    I8Item none;
-    none.arow0 = 0; none.wrow = 0; none.rows = 0; none.col0 = 0;
 
     // LDS byte address of the ring (a C-style cast is the address-space cast)
     const int smem_base = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)(&smem[0][0])));
     const int meta_base = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) float*)(&meta[0][0])));
     int gs = 0, par = 0;
     bool first = true;
-    i32x16 acc[2][4][2];
-    i32x4 fb[2][2], fa[2][2][4];
+#ifdef GRIM_I8_TIMING
+    uint64_t wait_acc = 0, tw0 = 0;
+#define GRIM_I8_TW0 tw0 = __builtin_amdgcn_s_memtime()
+#define GRIM_I8_TW1 wait_acc += __builtin_amdgcn_s_memtime() - tw0
+#else
+#define GRIM_I8_TW0 (void)0
+#define GRIM_I8_TW1 (void)0
+#endif
+    i32x16 acc[2][MIW][2];
+    i32x4 fb[2][2], fa[2][2][MIW];
     for (; i < items; i += per_xcd) {
         GRIM_I8_OFFSETS();
         const bool more = i + per_xcd < items;
-        const I8Item nxt = more ? i8_item<SWIGLU>(g, routed, tile_of(i + per_xcd), col_of(i + per_xcd))
+        const I8Item nxt = more ? i8_item<SWIGLU>(g, n_routed, tile_of(i + per_xcd), col_of(i + per_xcd))
                                 : none;
 #pragma unroll
         for (int l = 0; l < 2; ++l)
 #pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
+            for (int mi = 0; mi < MIW; ++mi)
 #pragma unroll
                 for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
                     for (int v = 0; v < 16; ++v) acc[l][mi][ni][v] = 0;
-        // the wait before tile t: vmcnt(63) right after an epilogue (t < 3,
-        // its stores are younger than tile t), else vmcnt(16); one asm block
-        // so that the loop body is not duplicated per case
+        // The wait before tile t: the operations younger than tile t's last
+        // load are the two later tiles' loads (YT), and right after an
+        // epilogue (t < 3) also its stores (ES per lane); waiting until at
+        // most min(63, that many) are outstanding (63: the counter's limit)
+        // completes tile t.  One asm block, so that the loop body is not
+        // duplicated per case.
+        constexpr int YT = 4 * NJ;
+        constexpr int ES = (SWIGLU ? 1 : 2) * MIW * 16;
+        constexpr int YE = YT + ES < 63 ? YT + ES : 63;
 #define GRIM_I8_WAIT(after_epi)                                                                   \
         asm volatile("s_cmp_eq_u32 %0, 0\n\t"                                                    \
                      "s_cbranch_scc1 .Lgrim_w16_%=\n\t"                                           \
-                     "s_waitcnt vmcnt(63)\n\t"                                                   \
+                     "s_waitcnt vmcnt(%2)\n\t"                                                   \
                      "s_branch .Lgrim_wdone_%=\n"                                                 \
                      ".Lgrim_w16_%=:\n\t"                                                        \
-                     "s_waitcnt vmcnt(16)\n"                                                      \
+                     "s_waitcnt vmcnt(%1)\n"                                                      \
                      ".Lgrim_wdone_%=:\n\t"                                                      \
                      "s_waitcnt lgkmcnt(0)\n\t"                                                  \
-                     "s_barrier" ::"s"(__builtin_amdgcn_readfirstlane(after_epi)) : "memory", "scc")
+                     "s_barrier" ::"s"(__builtin_amdgcn_readfirstlane(after_epi)), "n"(YT), "n"(YE) \
+                     : "memory", "scc")
         // Fragment reads are inline asm with explicit lgkmcnt waits tied to
         // the fragment registers: the compiler cannot tell that they and the
         // in-flight DMA writes touch different ring stages, and guards a
@@ -333,24 +364,37 @@ __global__ __launch_bounds__(kQThreads, 1) void grouped_gemm_i8_kernel(GemmI8Arg
                                                                         acc[l][mi_][ni], 0, 0, 0)
 #define GRIM_I8_DMA(q)                                                                            \
         do {                                                                                      \
-            if ((q) < 4) dma16<0>(qa, nx + (4 * wave + (q)) * 1024, a_off[(q) & 3], tu * 128);    \
-            else dma16<2>(qb, nx + 16384 + (4 * wave + (q) - 4) * 1024, b_off[(q) & 3], tu * QBK); \
+            if ((q) < NJ) dma16<0>(qa, nx + (NJ * wave + (q)) * 1024, a_off[(q) % NJ], tu * 128); \
+            else dma16<2>(qb, nx + 16384 + (NJ * wave + (q) - NJ) * 1024, b_off[(q) % NJ], tu * QBK); \
         } while (0)
 #define GRIM_I8_ITER(t_, META)                                                                    \
         do {                                                                                      \
             const int t = (t_);                                                                   \
+            GRIM_I8_TW0;                                                                          \
             GRIM_I8_WAIT((t < 3 && !first) ? 1 : 0);                                              \
+            GRIM_I8_TW1;                                                                          \
             const int sb = ((gs + t) & 3) * kQStageBytes + smem_base;                             \
-            GRIM_I8_DSR(fb[0][0], sb + fb_off[0][0]);                                             \
-            GRIM_I8_DSR(fb[0][1], sb + fb_off[0][1]);                                             \
-            _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) {                                    \
-                GRIM_I8_DSR(fa[0][0][mi], sb + fa_off[0][0][mi]);                                 \
-                GRIM_I8_DSR(fa[0][1][mi], sb + fa_off[0][1][mi]);                                 \
+            if constexpr (WM == 1) {                                                              \
+                GRIM_I8_DSR(fb[0][0], sb + fb_off[0][0]);                                         \
+                GRIM_I8_DSR(fb[0][1], sb + fb_off[0][1]);                                         \
+                _Pragma("unroll") for (int mi = 0; mi < MIW; ++mi) {                              \
+                    GRIM_I8_DSR(fa[0][0][mi], sb + fa_off[0][0][mi]);                             \
+                    GRIM_I8_DSR(fa[0][1][mi], sb + fa_off[0][1][mi]);                             \
+                }                                                                                 \
+                GRIM_I8_DSR(fb[1][0], sb + fb_off[1][0]);                                         \
+                GRIM_I8_DSR(fb[1][1], sb + fb_off[1][1]);                                         \
+                GRIM_I8_DSR(fa[1][0][0], sb + fa_off[1][0][0]);                                   \
+                GRIM_I8_DSR(fa[1][1][0], sb + fa_off[1][1][0]);                                   \
+            } else {                                                                              \
+                _Pragma("unroll") for (int ks = 0; ks < 2; ++ks) {                                \
+                    GRIM_I8_DSR(fb[ks][0], sb + fb_off[ks][0]);                                   \
+                    GRIM_I8_DSR(fb[ks][1], sb + fb_off[ks][1]);                                   \
+                    _Pragma("unroll") for (int mi = 0; mi < MIW; ++mi) {                          \
+                        GRIM_I8_DSR(fa[ks][0][mi], sb + fa_off[ks][0][mi]);                       \
+                        GRIM_I8_DSR(fa[ks][1][mi], sb + fa_off[ks][1][mi]);                       \
+                    }                                                                             \
+                }                                                                                 \
             }                                                                                     \
-            GRIM_I8_DSR(fb[1][0], sb + fb_off[1][0]);                                             \
-            GRIM_I8_DSR(fb[1][1], sb + fb_off[1][1]);                                             \
-            GRIM_I8_DSR(fa[1][0][0], sb + fa_off[1][0][0]);                                       \
-            GRIM_I8_DSR(fa[1][1][0], sb + fa_off[1][1][0]);                                       \
             if (META) request_meta(nxt, par ^ 1);                                                 \
             /* stream tile t + 3: this item's, or the next item's 0, 1, 2 */                      \
             const int u = t + kQStages - 1;                                                       \
@@ -359,18 +403,26 @@ __global__ __launch_bounds__(kQThreads, 1) void grouped_gemm_i8_kernel(GemmI8Arg
             const __amdgpu_buffer_rsrc_t qb = rsrc_b(own ? cur : nxt);                            \
             const int tu = own ? u : u - nk;                                                      \
             uint8_t* nx = smem[(gs + u) & 3];                                                     \
-            GRIM_I8_LGKM(10, 0, 0); GRIM_I8_MMA_MI(0, 0); GRIM_I8_DMA(0);                         \
-            GRIM_I8_LGKM(8, 0, 1);  GRIM_I8_MMA_MI(0, 1); GRIM_I8_DMA(1);                         \
-            GRIM_I8_LGKM(6, 0, 2);  GRIM_I8_MMA_MI(0, 2); GRIM_I8_DMA(2);                         \
-            GRIM_I8_LGKM(4, 0, 3);  GRIM_I8_MMA_MI(0, 3); GRIM_I8_DMA(3);                         \
-            _Pragma("unroll") for (int mi = 1; mi < 4; ++mi) {                                    \
-                GRIM_I8_DSR(fa[1][0][mi], sb + fa_off[1][0][mi]);                                 \
-                GRIM_I8_DSR(fa[1][1][mi], sb + fa_off[1][1][mi]);                                 \
+            if constexpr (WM == 1) {                                                              \
+                GRIM_I8_LGKM(10, 0, 0); GRIM_I8_MMA_MI(0, 0); GRIM_I8_DMA(0);                     \
+                GRIM_I8_LGKM(8, 0, 1);  GRIM_I8_MMA_MI(0, 1); GRIM_I8_DMA(1);                     \
+                GRIM_I8_LGKM(6, 0, 2);  GRIM_I8_MMA_MI(0, 2); GRIM_I8_DMA(2);                     \
+                GRIM_I8_LGKM(4, 0, 3);  GRIM_I8_MMA_MI(0, 3); GRIM_I8_DMA(3);                     \
+                _Pragma("unroll") for (int mi = 1; mi < MIW; ++mi) {                              \
+                    GRIM_I8_DSR(fa[1][0][mi], sb + fa_off[1][0][mi]);                             \
+                    GRIM_I8_DSR(fa[1][1][mi], sb + fa_off[1][1][mi]);                             \
+                }                                                                                 \
+                GRIM_I8_LGKM(6, 1, 0);  GRIM_I8_MMA_MI(1, 0); GRIM_I8_DMA(4);                     \
+                GRIM_I8_LGKM(4, 1, 1);  GRIM_I8_MMA_MI(1, 1); GRIM_I8_DMA(5);                     \
+                GRIM_I8_LGKM(2, 1, 2);  GRIM_I8_MMA_MI(1, 2); GRIM_I8_DMA(6);                     \
+                GRIM_I8_LGKM(0, 1, 3);  GRIM_I8_MMA_MI(1, 3); GRIM_I8_DMA(7);                     \
+            } else {                                                                              \
+                /* 12 reads in flight: (ks, mi) needs the first 4 / 6 / 10 / 12 */                \
+                GRIM_I8_LGKM(8, 0, 0); GRIM_I8_MMA_MI(0, 0); GRIM_I8_DMA(0);                      \
+                GRIM_I8_LGKM(6, 0, 1); GRIM_I8_MMA_MI(0, 1); GRIM_I8_DMA(1);                      \
+                GRIM_I8_LGKM(2, 1, 0); GRIM_I8_MMA_MI(1, 0); GRIM_I8_DMA(2);                      \
+                GRIM_I8_LGKM(0, 1, 1); GRIM_I8_MMA_MI(1, 1); GRIM_I8_DMA(3);                      \
             }                                                                                     \
-            GRIM_I8_LGKM(6, 1, 0);  GRIM_I8_MMA_MI(1, 0); GRIM_I8_DMA(4);                         \
-            GRIM_I8_LGKM(4, 1, 1);  GRIM_I8_MMA_MI(1, 1); GRIM_I8_DMA(5);                         \
-            GRIM_I8_LGKM(2, 1, 2);  GRIM_I8_MMA_MI(1, 2); GRIM_I8_DMA(6);                         \
-            GRIM_I8_LGKM(0, 1, 3);  GRIM_I8_MMA_MI(1, 3); GRIM_I8_DMA(7);                         \
         } while (0)
         // iteration 0 also requests the next item's scales: after its
         // barrier (every wave is past the epilogue that read that parity)
@@ -391,24 +443,26 @@ __global__ __launch_bounds__(kQThreads, 1) void grouped_gemm_i8_kernel(GemmI8Arg
         // + v%4, column 32 (2 w + ni) + l%32 of the tile.  Scales from LDS
         // (landed with tile 0, behind this item's barriers); each store
         // writes two 128-byte row segments.
-        const __amdgpu_buffer_rsrc_t ro = i8_rsrc(src.out + cur.arow0 * ldo, cur.rows * ldo * 4);
+        const __amdgpu_buffer_rsrc_t ro =
+            i8_rsrc((cur.sh ? src_s.out : src_r.out) + cur.arow0 * ldo, cur.rows * ldo * 4);
         // the scales are read by inline asm too (a compiler-visible LDS read
         // here would wait for the next item's tiles already in flight)
         const int mb = meta_base + par * 2048;
         const int ln = lane_id();
         const int hrow = 4 * (ln >> 5);
+        const int row0 = wm * MIW * 32;       // this wave's first tile row
         if constexpr (SWIGLU) {
-            const int hcl = wave * 32 + (ln & 31);
+            const int hcl = wn * 32 + (ln & 31);
             float sg = lds_f32(mb + 1024 + hcl * 4), su = lds_f32(mb + 1024 + (128 + hcl) * 4);
-            // per-lane byte offset of (row hrow, this column), opaque so the
-            // 64 row offsets below are formed here and not kept live
-            int base = cur.col0 + hcl < g.I ? (hrow * g.I + cur.col0 + hcl) * 4 : 0x40000000;
+            // per-lane byte offset of (row row0 + hrow, this column), opaque so
+            // the row offsets below are formed here and not kept live
+            int base = cur.col0 + hcl < g.I ? ((row0 + hrow) * g.I + cur.col0 + hcl) * 4 : 0x40000000;
             asm volatile("" : "+v"(base));
 #pragma unroll
-            for (int mi = 0; mi < 4; ++mi) {
+            for (int mi = 0; mi < MIW; ++mi) {
                 f32x4v s4[4];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) s4[q] = lds_f32x4(mb + (mi * 32 + 8 * q + hrow) * 4);
+                for (int q = 0; q < 4; ++q) s4[q] = lds_f32x4(mb + (row0 + mi * 32 + 8 * q + hrow) * 4);
                 asm volatile("s_waitcnt lgkmcnt(0)"
                              : "+v"(s4[0]), "+v"(s4[1]), "+v"(s4[2]), "+v"(s4[3]), "+v"(sg), "+v"(su));
 #pragma unroll
@@ -426,15 +480,15 @@ __global__ __launch_bounds__(kQThreads, 1) void grouped_gemm_i8_kernel(GemmI8Arg
         } else {
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni) {
-                const int cl = wave * 64 + ni * 32 + (ln & 31);
+                const int cl = wn * 64 + ni * 32 + (ln & 31);
                 float sc = lds_f32(mb + 1024 + cl * 4);
-                int base = cur.col0 + cl < g.N ? (hrow * g.N + cur.col0 + cl) * 4 : 0x40000000;
+                int base = cur.col0 + cl < g.N ? ((row0 + hrow) * g.N + cur.col0 + cl) * 4 : 0x40000000;
                 asm volatile("" : "+v"(base));
 #pragma unroll
-                for (int mi = 0; mi < 4; ++mi) {
+                for (int mi = 0; mi < MIW; ++mi) {
                     f32x4v s4[4];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) s4[q] = lds_f32x4(mb + (mi * 32 + 8 * q + hrow) * 4);
+                    for (int q = 0; q < 4; ++q) s4[q] = lds_f32x4(mb + (row0 + mi * 32 + 8 * q + hrow) * 4);
                     asm volatile("s_waitcnt lgkmcnt(0)"
                                  : "+v"(s4[0]), "+v"(s4[1]), "+v"(s4[2]), "+v"(s4[3]), "+v"(sc));
 #pragma unroll
@@ -450,7 +504,7 @@ __global__ __launch_bounds__(kQThreads, 1) void grouped_gemm_i8_kernel(GemmI8Arg
             }
         }
 #ifdef GRIM_I8_TIMING
-        g_i8_epi[blockIdx.x * 4 + wave] += __builtin_amdgcn_s_memtime() - te0;
+        g_i8_epi[blockIdx.x * 8 + wave] += __builtin_amdgcn_s_memtime() - te0;
 #endif
         gs += nk;
         par ^= 1;
@@ -458,10 +512,13 @@ __global__ __launch_bounds__(kQThreads, 1) void grouped_gemm_i8_kernel(GemmI8Arg
         first = false;
     }
 #undef GRIM_I8_OFFSETS
+#undef GRIM_I8_TW0
+#undef GRIM_I8_TW1
     // drain: the last iterations requested tiles from the empty buffer
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #ifdef GRIM_I8_TIMING
-    g_i8_total[blockIdx.x * 4 + wave] += __builtin_amdgcn_s_memtime() - t0;
+    g_i8_total[blockIdx.x * 8 + wave] += __builtin_amdgcn_s_memtime() - t0;
+    g_i8_wait[blockIdx.x * 8 + wave] += wait_acc;
 #endif
 }
 
@@ -590,27 +647,37 @@ __global__ __launch_bounds__(256) void quant_permute_kernel(const float* __restr
 
 // ----------------------------------------------------------------- host
 
+constexpr int kI8WM = 2;   // waves along M (2: 8 waves per work-group)
+
 template <bool SWIGLU>
 static hipError_t launch_i8(hipStream_t st, const GemmI8Args& g, int ntiles) {
+    constexpr int threads = 256 * kI8WM;
     static int grid = 0;
     if (grid == 0) {
         int per_cu = 0, dev = 0, cus = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, grouped_gemm_i8_kernel<SWIGLU>,
-                                                         kQThreads, 0) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, grouped_gemm_i8_kernel<SWIGLU, kI8WM>,
+                                                         threads, 0) != hipSuccess ||
             hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             return hipErrorInvalidConfiguration;
         grid = (per_cu > 0 ? per_cu : 1) * cus;
         grid = (grid + kQXcds - 1) / kQXcds * kQXcds;
     }
+    const bool fuse = g.tmax > 0 && g.T_sh > 0 && g.row_bytes == g.row_bytes_sh;
+    if (fuse) {
+        // the shared expert's m-tiles follow the routed ones in one launch
+        hipLaunchKernelGGL((grouped_gemm_i8_kernel<SWIGLU, kI8WM>), dim3(grid), dim3(threads), 0, st, g,
+                           ntiles, 3);
+        return hipGetLastError();
+    }
     if (g.tmax > 0)
-        hipLaunchKernelGGL(grouped_gemm_i8_kernel<SWIGLU>, dim3(grid), dim3(kQThreads), 0, st, g,
-                           ntiles, 0);
+        hipLaunchKernelGGL((grouped_gemm_i8_kernel<SWIGLU, kI8WM>), dim3(grid), dim3(threads), 0, st, g,
+                           ntiles, 1);
     if (g.T_sh > 0) {
         const int items = (g.T_sh + QBM - 1) / QBM * ntiles;
         const int gs = min(grid, (items + kQXcds - 1) / kQXcds * kQXcds);
-        hipLaunchKernelGGL(grouped_gemm_i8_kernel<SWIGLU>, dim3(gs), dim3(kQThreads), 0, st, g,
-                           ntiles, 1);
+        hipLaunchKernelGGL((grouped_gemm_i8_kernel<SWIGLU, kI8WM>), dim3(gs), dim3(threads), 0, st, g,
+                           ntiles, 2);
     }
     return hipGetLastError();
 }
