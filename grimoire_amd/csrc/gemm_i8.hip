@@ -13,8 +13,8 @@
 // exact int32 sums; the epilogue forms s_row * s_col * (hi + lo / 254).
 // Two int8 passes cost what one bf16 pass costs, with no conversion at all.
 //
-// Tile: 128 rows x 256 columns x 64 K, 256 threads; wave w owns columns
-// [64w, 64w + 64) of the tile for all 128 rows (4 x 2 MFMA tiles per limb).
+// Tile: 128 rows x 256 columns x 64 K, 512 threads; wave w owns columns
+// [64 (w % 4), +64) for rows [64 (w / 4), +64) (2 x 2 MFMA tiles per limb).
 // A (limbs) and B (codes) both stream into a 4-stage LDS ring through
 // buffer_load ... lds (16 bytes per lane, no registers involved).  A limb
 // rows are stored [K/64][2][64] so that one K tile of a row is one 128-byte
@@ -37,17 +37,14 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int QBM = 128, QBN = 256, QBK = 64;
+constexpr int kQThreads = 512;
 constexpr int kQStages = 4;
 constexpr int kQStageBytes = 32768;          // A 16 KiB (2 limbs x 4 x 2 fragments), B 16 KiB
-constexpr int kQThreads = 256;
 constexpr int kQXcds = 8;
 constexpr float kLoScale = 1.0f / 254.0f;
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-#ifdef GRIM_I8_TIMING
-__device__ uint64_t g_i8_total[8192], g_i8_epi[8192], g_i8_wait[8192];
-#endif
 
 template <int AUX>
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, int voff, int soff) {
@@ -162,15 +159,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t i8_rsrc(const void* p, int byt
 // at the texture unit, 16 cycles each, and hold the MFMAs back).  Past the
 // last item the stream requests tiles from an empty buffer (num_records 0:
 // no memory traffic), which keeps every iteration alike.
-template <bool SWIGLU, int WM>
-__global__ __launch_bounds__(256 * WM) void grouped_gemm_i8_kernel(GemmI8Args g, int n_col_tiles,
-                                                                  int parts) {
-    // WM = 1: 4 waves, wave w owns tile columns [64w, +64) for all 128 rows;
-    // WM = 2: 8 waves (two per SIMD, so one wave's MFMAs run while the
-    // other waits on its loads or its epilogue), wave w owns columns
-    // [64 (w % 4), +64) for rows [64 (w / 4), +64).
-    constexpr int MIW = 4 / WM;              // 32-row MFMA tiles per wave
-    constexpr int NJ = 4 / WM;               // DMA instructions per wave per K tile, for A and for B
+template <bool SWIGLU>
+__global__ __launch_bounds__(kQThreads) void grouped_gemm_i8_kernel(GemmI8Args g, int n_col_tiles,
+                                                                   int parts) {
+    // 8 waves, two per SIMD: wave w owns tile columns [64 (w % 4), +64) for
+    // rows [64 (w / 4), +64)
+    constexpr int MIW = 2;                   // 32-row MFMA tiles per wave
+    constexpr int NJ = 2;                    // DMA instructions per wave per K tile, for A and for B
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kQStages][kQStageBytes];
     // per item parity: row scales [128] at 0, column scales at 1024 (plain:
     // [256]; SwiGLU: gate [128] then up [128])
@@ -195,9 +190,6 @@ __global__ __launch_bounds__(256 * WM) void grouped_gemm_i8_kernel(GemmI8Args g,
     const int items = (hi - lo) * n_col_tiles;
     int i = blockIdx.x / kQXcds;
     if (i >= items) return;
-#ifdef GRIM_I8_TIMING
-    const uint64_t t0 = __builtin_amdgcn_s_memtime();
-#endif
 
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
     const int wn = wave & 3, wm = wave >> 2;
@@ -303,14 +295,6 @@ __global__ __launch_bounds__(256 * WM) void grouped_gemm_i8_kernel(GemmI8Args g,
     const int meta_base = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) float*)(&meta[0][0])));
     int gs = 0, par = 0;
     bool first = true;
-#ifdef GRIM_I8_TIMING
-    uint64_t wait_acc = 0, tw0 = 0;
-#define GRIM_I8_TW0 tw0 = __builtin_amdgcn_s_memtime()
-#define GRIM_I8_TW1 wait_acc += __builtin_amdgcn_s_memtime() - tw0
-#else
-#define GRIM_I8_TW0 (void)0
-#define GRIM_I8_TW1 (void)0
-#endif
     i32x16 acc[2][MIW][2];
     i32x4 fb[2][2], fa[2][2][MIW];
     for (; i < items; i += per_xcd) {
@@ -350,8 +334,8 @@ __global__ __launch_bounds__(256 * WM) void grouped_gemm_i8_kernel(GemmI8Args g,
         // the fragment registers: the compiler cannot tell that they and the
         // in-flight DMA writes touch different ring stages, and guards a
         // compiler-visible LDS read with a wait for every outstanding load.
-        // Reads in MFMA order (ks, mi; B then the two limbs); at most 14
-        // outstanding (lgkmcnt holds 15).
+        // Reads in MFMA order (ks, mi; B then the two limbs): 12 outstanding
+        // (lgkmcnt holds 15).
 #define GRIM_I8_DSR(dst, addr)                                                                    \
         asm volatile("ds_read_b128 %0, %1" : "=v"(dst) : "v"(addr))
 #define GRIM_I8_LGKM(n, ks_, mi_)                                                                 \
@@ -370,29 +354,14 @@ __global__ __launch_bounds__(256 * WM) void grouped_gemm_i8_kernel(GemmI8Args g,
 #define GRIM_I8_ITER(t_, META)                                                                    \
         do {                                                                                      \
             const int t = (t_);                                                                   \
-            GRIM_I8_TW0;                                                                          \
             GRIM_I8_WAIT((t < 3 && !first) ? 1 : 0);                                              \
-            GRIM_I8_TW1;                                                                          \
             const int sb = ((gs + t) & 3) * kQStageBytes + smem_base;                             \
-            if constexpr (WM == 1) {                                                              \
-                GRIM_I8_DSR(fb[0][0], sb + fb_off[0][0]);                                         \
-                GRIM_I8_DSR(fb[0][1], sb + fb_off[0][1]);                                         \
+            _Pragma("unroll") for (int ks = 0; ks < 2; ++ks) {                                    \
+                GRIM_I8_DSR(fb[ks][0], sb + fb_off[ks][0]);                                       \
+                GRIM_I8_DSR(fb[ks][1], sb + fb_off[ks][1]);                                       \
                 _Pragma("unroll") for (int mi = 0; mi < MIW; ++mi) {                              \
-                    GRIM_I8_DSR(fa[0][0][mi], sb + fa_off[0][0][mi]);                             \
-                    GRIM_I8_DSR(fa[0][1][mi], sb + fa_off[0][1][mi]);                             \
-                }                                                                                 \
-                GRIM_I8_DSR(fb[1][0], sb + fb_off[1][0]);                                         \
-                GRIM_I8_DSR(fb[1][1], sb + fb_off[1][1]);                                         \
-                GRIM_I8_DSR(fa[1][0][0], sb + fa_off[1][0][0]);                                   \
-                GRIM_I8_DSR(fa[1][1][0], sb + fa_off[1][1][0]);                                   \
-            } else {                                                                              \
-                _Pragma("unroll") for (int ks = 0; ks < 2; ++ks) {                                \
-                    GRIM_I8_DSR(fb[ks][0], sb + fb_off[ks][0]);                                   \
-                    GRIM_I8_DSR(fb[ks][1], sb + fb_off[ks][1]);                                   \
-                    _Pragma("unroll") for (int mi = 0; mi < MIW; ++mi) {                          \
-                        GRIM_I8_DSR(fa[ks][0][mi], sb + fa_off[ks][0][mi]);                       \
-                        GRIM_I8_DSR(fa[ks][1][mi], sb + fa_off[ks][1][mi]);                       \
-                    }                                                                             \
+                    GRIM_I8_DSR(fa[ks][0][mi], sb + fa_off[ks][0][mi]);                           \
+                    GRIM_I8_DSR(fa[ks][1][mi], sb + fa_off[ks][1][mi]);                           \
                 }                                                                                 \
             }                                                                                     \
             if (META) request_meta(nxt, par ^ 1);                                                 \
@@ -403,26 +372,11 @@ __global__ __launch_bounds__(256 * WM) void grouped_gemm_i8_kernel(GemmI8Args g,
             const __amdgpu_buffer_rsrc_t qb = rsrc_b(own ? cur : nxt);                            \
             const int tu = own ? u : u - nk;                                                      \
             uint8_t* nx = smem[(gs + u) & 3];                                                     \
-            if constexpr (WM == 1) {                                                              \
-                GRIM_I8_LGKM(10, 0, 0); GRIM_I8_MMA_MI(0, 0); GRIM_I8_DMA(0);                     \
-                GRIM_I8_LGKM(8, 0, 1);  GRIM_I8_MMA_MI(0, 1); GRIM_I8_DMA(1);                     \
-                GRIM_I8_LGKM(6, 0, 2);  GRIM_I8_MMA_MI(0, 2); GRIM_I8_DMA(2);                     \
-                GRIM_I8_LGKM(4, 0, 3);  GRIM_I8_MMA_MI(0, 3); GRIM_I8_DMA(3);                     \
-                _Pragma("unroll") for (int mi = 1; mi < MIW; ++mi) {                              \
-                    GRIM_I8_DSR(fa[1][0][mi], sb + fa_off[1][0][mi]);                             \
-                    GRIM_I8_DSR(fa[1][1][mi], sb + fa_off[1][1][mi]);                             \
-                }                                                                                 \
-                GRIM_I8_LGKM(6, 1, 0);  GRIM_I8_MMA_MI(1, 0); GRIM_I8_DMA(4);                     \
-                GRIM_I8_LGKM(4, 1, 1);  GRIM_I8_MMA_MI(1, 1); GRIM_I8_DMA(5);                     \
-                GRIM_I8_LGKM(2, 1, 2);  GRIM_I8_MMA_MI(1, 2); GRIM_I8_DMA(6);                     \
-                GRIM_I8_LGKM(0, 1, 3);  GRIM_I8_MMA_MI(1, 3); GRIM_I8_DMA(7);                     \
-            } else {                                                                              \
-                /* 12 reads in flight: (ks, mi) needs the first 4 / 6 / 10 / 12 */                \
-                GRIM_I8_LGKM(8, 0, 0); GRIM_I8_MMA_MI(0, 0); GRIM_I8_DMA(0);                      \
-                GRIM_I8_LGKM(6, 0, 1); GRIM_I8_MMA_MI(0, 1); GRIM_I8_DMA(1);                      \
-                GRIM_I8_LGKM(2, 1, 0); GRIM_I8_MMA_MI(1, 0); GRIM_I8_DMA(2);                      \
-                GRIM_I8_LGKM(0, 1, 1); GRIM_I8_MMA_MI(1, 1); GRIM_I8_DMA(3);                      \
-            }                                                                                     \
+            /* 12 reads in flight: (ks, mi) needs the first 4 / 6 / 10 / 12 */                    \
+            GRIM_I8_LGKM(8, 0, 0); GRIM_I8_MMA_MI(0, 0); GRIM_I8_DMA(0);                          \
+            GRIM_I8_LGKM(6, 0, 1); GRIM_I8_MMA_MI(0, 1); GRIM_I8_DMA(1);                          \
+            GRIM_I8_LGKM(2, 1, 0); GRIM_I8_MMA_MI(1, 0); GRIM_I8_DMA(2);                          \
+            GRIM_I8_LGKM(0, 1, 1); GRIM_I8_MMA_MI(1, 1); GRIM_I8_DMA(3);                          \
         } while (0)
         // iteration 0 also requests the next item's scales: after its
         // barrier (every wave is past the epilogue that read that parity)
@@ -436,9 +390,6 @@ __global__ __launch_bounds__(256 * WM) void grouped_gemm_i8_kernel(GemmI8Args g,
 #undef GRIM_I8_MMA_MI
 #undef GRIM_I8_DMA
 
-#ifdef GRIM_I8_TIMING
-        const uint64_t te0 = __builtin_amdgcn_s_memtime();
-#endif
         // ---- epilogue.  acc[l][mi][ni][v] is row 32 mi + 8 (v/4) + 4 (l/32)
         // + v%4, column 32 (2 w + ni) + l%32 of the tile.  Scales from LDS
         // (landed with tile 0, behind this item's barriers); each store
@@ -503,23 +454,14 @@ __global__ __launch_bounds__(256 * WM) void grouped_gemm_i8_kernel(GemmI8Args g,
                 }
             }
         }
-#ifdef GRIM_I8_TIMING
-        g_i8_epi[blockIdx.x * 8 + wave] += __builtin_amdgcn_s_memtime() - te0;
-#endif
         gs += nk;
         par ^= 1;
         cur = nxt;
         first = false;
     }
 #undef GRIM_I8_OFFSETS
-#undef GRIM_I8_TW0
-#undef GRIM_I8_TW1
     // drain: the last iterations requested tiles from the empty buffer
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#ifdef GRIM_I8_TIMING
-    g_i8_total[blockIdx.x * 8 + wave] += __builtin_amdgcn_s_memtime() - t0;
-    g_i8_wait[blockIdx.x * 8 + wave] += wait_acc;
-#endif
 }
 
 // ------------------------------------------------------------ quantisers
@@ -647,16 +589,13 @@ __global__ __launch_bounds__(256) void quant_permute_kernel(const float* __restr
 
 // ----------------------------------------------------------------- host
 
-constexpr int kI8WM = 2;   // waves along M (2: 8 waves per work-group)
-
 template <bool SWIGLU>
 static hipError_t launch_i8(hipStream_t st, const GemmI8Args& g, int ntiles) {
-    constexpr int threads = 256 * kI8WM;
     static int grid = 0;
     if (grid == 0) {
         int per_cu = 0, dev = 0, cus = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, grouped_gemm_i8_kernel<SWIGLU, kI8WM>,
-                                                         threads, 0) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, grouped_gemm_i8_kernel<SWIGLU>,
+                                                         kQThreads, 0) != hipSuccess ||
             hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             return hipErrorInvalidConfiguration;
@@ -666,17 +605,17 @@ static hipError_t launch_i8(hipStream_t st, const GemmI8Args& g, int ntiles) {
     const bool fuse = g.tmax > 0 && g.T_sh > 0 && g.row_bytes == g.row_bytes_sh;
     if (fuse) {
         // the shared expert's m-tiles follow the routed ones in one launch
-        hipLaunchKernelGGL((grouped_gemm_i8_kernel<SWIGLU, kI8WM>), dim3(grid), dim3(threads), 0, st, g,
+        hipLaunchKernelGGL(grouped_gemm_i8_kernel<SWIGLU>, dim3(grid), dim3(kQThreads), 0, st, g,
                            ntiles, 3);
         return hipGetLastError();
     }
     if (g.tmax > 0)
-        hipLaunchKernelGGL((grouped_gemm_i8_kernel<SWIGLU, kI8WM>), dim3(grid), dim3(threads), 0, st, g,
+        hipLaunchKernelGGL(grouped_gemm_i8_kernel<SWIGLU>, dim3(grid), dim3(kQThreads), 0, st, g,
                            ntiles, 1);
     if (g.T_sh > 0) {
         const int items = (g.T_sh + QBM - 1) / QBM * ntiles;
         const int gs = min(grid, (items + kQXcds - 1) / kQXcds * kQXcds);
-        hipLaunchKernelGGL((grouped_gemm_i8_kernel<SWIGLU, kI8WM>), dim3(gs), dim3(threads), 0, st, g,
+        hipLaunchKernelGGL(grouped_gemm_i8_kernel<SWIGLU>, dim3(gs), dim3(kQThreads), 0, st, g,
                            ntiles, 2);
     }
     return hipGetLastError();
