@@ -200,11 +200,138 @@ __global__ __launch_bounds__(256) void router_mfma(const float* __restrict__ W,
     }
 }
 
+// Large T in three bf16 limbs: each fp32 value v splits exactly into
+// hi + mid + lo (hi = bf16(v), mid = bf16(v - hi), lo = bf16(v - hi - mid):
+// 24 significant bits in three 8-bit pieces), and
+//     x . w = sum of xh.wh + xh.wm + xm.wh + xh.wl + xl.wh + xm.wm
+// up to the three products below 2^-23 of the leading one (the size of an
+// fp32 rounding), each product exact in fp32 and accumulated in fp32 by
+// v_mfma_f32_32x32x16_bf16 -- 16x the fp32 MFMA's rate per product, 2.7x
+// for the six.  Tile 64 tokens x 64 experts x 32 K, 4 waves of 32 x 32;
+// the fp32 tiles are split while staged into LDS (three bf16 planes).
+constexpr int kR3BK = 32, kR3LD = kR3BK + 8;   // LDS row pitch in bf16
+typedef __bf16 bf16x8r __attribute__((__vector_size__(8 * sizeof(__bf16))));
+
+// three limbs of 4 values as packed bf16 pairs: limb p -> out[p] (2 words);
+// the bf16 conversions round to nearest even (one instruction per pair)
+typedef __bf16 bf16x2r __attribute__((ext_vector_type(2)));
+typedef float f32x2r __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_bits(bf16x2r v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ f32x2r widen(bf16x2r v) {
+    const uint32_t b = pk_bits(v);
+    return f32x2r{__uint_as_float(b << 16), __uint_as_float(b & 0xFFFF0000u)};
+}
+__device__ __forceinline__ void split3(const f32x4n v, uint32_t (&out)[3][2]) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const f32x2r x = q ? f32x2r{v.z, v.w} : f32x2r{v.x, v.y};
+        const bf16x2r h = __builtin_convertvector(x, bf16x2r);
+        const f32x2r r1 = x - widen(h);
+        const bf16x2r m = __builtin_convertvector(r1, bf16x2r);
+        const f32x2r r2 = r1 - widen(m);
+        const bf16x2r l = __builtin_convertvector(r2, bf16x2r);
+        out[0][q] = pk_bits(h);
+        out[1][q] = pk_bits(m);
+        out[2][q] = pk_bits(l);
+    }
+}
+__device__ __forceinline__ void r3_store(uint16_t* dst, int plane_stride, const f32x4n (&reg)[2]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = threadIdx.x + i * 256, r = c >> 3, kc = (c & 7) * 4;
+        uint32_t w[3][2];
+        split3(reg[i], w);
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+            *reinterpret_cast<uint2*>(&dst[p * plane_stride + r * kR3LD + kc]) = make_uint2(w[p][0], w[p][1]);
+    }
+}
+
+constexpr int kR3Pre = 4;   // K tiles in flight (register sets)
+
+__global__ __launch_bounds__(256) void router_bf16x3(const float* __restrict__ W,
+                                                     const float* __restrict__ x,
+                                                     const float* __restrict__ bias,
+                                                     float* __restrict__ logits, int T, int E, int H) {
+    constexpr int PS = 64 * kR3LD;                    // one plane of one operand
+    __shared__ __attribute__((aligned(16))) uint16_t Xs[2][3 * PS];
+    __shared__ __attribute__((aligned(16))) uint16_t Ws[2][3 * PS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, h = lane >> 5;
+    // blockIdx.x = token block: work-group b runs on XCD b % 8, so the
+    // column blocks of one token block share an XCD (and its L2 copy of x)
+    const int t0 = blockIdx.x * 64, e0 = blockIdx.y * 64;
+    // K tile j is loaded into register set j % kR3Pre, kR3Pre - 1 tiles
+    // ahead of the one being multiplied (the latency of a tile's loads is
+    // several tiles' worth of MFMA time)
+    f32x4n rx[kR3Pre][2], rw[kR3Pre][2];
+    f32x16r acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    const int nk = H / kR3BK;                         // a multiple of kR3Pre
+#pragma unroll
+    for (int j = 0; j < kR3Pre; ++j) {
+        rt_load<64>(x, T, H, t0, j * kR3BK, rx[j]);
+        rt_load<64>(W, E, H, e0, j * kR3BK, rw[j]);
+    }
+    r3_store(Xs[0], PS, rx[0]);
+    r3_store(Ws[0], PS, rw[0]);
+    __syncthreads();
+    for (int k0 = 0; k0 < nk; k0 += kR3Pre) {
+#pragma unroll
+        for (int u = 0; u < kR3Pre; ++u) {
+            const int kt = k0 + u, buf = kt & 1;
+            // tile kt's set is free once it is in LDS: request tile kt + kR3Pre
+            if (kt + kR3Pre < nk) {
+                rt_load<64>(x, T, H, t0, (kt + kR3Pre) * kR3BK, rx[u]);
+                rt_load<64>(W, E, H, e0, (kt + kR3Pre) * kR3BK, rw[u]);
+            }
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                // lane half h supplies K = 16 h + 8 ks .. + 7 (the same for x and W)
+                const int kk = 16 * h + 8 * ks;
+                bf16x8r a[3], b[3];
+#pragma unroll
+                for (int p = 0; p < 3; ++p) {
+                    a[p] = *reinterpret_cast<const bf16x8r*>(&Xs[buf][p * PS + (wm * 32 + (lane & 31)) * kR3LD + kk]);
+                    b[p] = *reinterpret_cast<const bf16x8r*>(&Ws[buf][p * PS + (wn * 32 + (lane & 31)) * kR3LD + kk]);
+                }
+                // smallest products first
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], acc, 0, 0, 0);
+            }
+            if (kt + 1 < nk) {
+                const int un = (u + 1) % kR3Pre;
+                r3_store(Xs[buf ^ 1], PS, rx[un]);
+                r3_store(Ws[buf ^ 1], PS, rw[un]);
+            }
+            __syncthreads();
+        }
+    }
+    // acc[v]: token row (v&3) + 4*(lane>>5) + 8*(v>>2), expert lane&31
+    const int e = e0 + wn * 32 + (lane & 31);
+    if (e < E) {
+        const float bb = bias ? bias[e] : 0.0f;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int t = t0 + wm * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
+            if (t < T) logits[int64_t(t) * E + e] = bias ? acc[v] + bb : acc[v];
+        }
+    }
+}
+
 hipError_t router_logits_launch(hipStream_t st, const float* W, const float* x,
                                 const float* bias, float* logits, int T, int E, int H) {
     if (T <= 32 && H % 4 == 0) {
         dim3 grid(E, (T + kRouterTok - 1) / kRouterTok);
         hipLaunchKernelGGL(router_gemv, grid, dim3(256), 0, st, W, x, bias, logits, T, E, H);
+    } else if (H % (kR3BK * kR3Pre) == 0) {
+        dim3 grid((T + 63) / 64, (E + 63) / 64);
+        hipLaunchKernelGGL(router_bf16x3, grid, dim3(256), 0, st, W, x, bias, logits, T, E, H);
     } else if (H % kRtBK == 0) {
         dim3 grid((E + 63) / 64, (T + 63) / 64);
         hipLaunchKernelGGL((router_mfma<1, 1>), grid, dim3(256), 0, st, W, x, bias, logits, T, E, H);

@@ -20,8 +20,10 @@ def _ties(T, E, seed, scale=2.0):
     return l.contiguous()
 
 
+# T > 32 takes the three-limb bf16 MFMA kernel when H % 128 == 0 (33, 300),
+# the fp32 MFMA kernel when H % 32 == 0 (2080), else the tiled fp32 kernel (100)
 @pytest.mark.parametrize("T,E,H", [(1, 128, 2048), (7, 64, 2048), (32, 256, 7168), (33, 512, 2048),
-                                   (300, 96, 512)])
+                                   (300, 96, 512), (70, 64, 2080), (40, 32, 100)])
 def test_router_logits(gpu, T, E, H):
     print(f"router_logits T={T} E={E} H={H}", flush=True)
     g = torch.Generator().manual_seed(T + E)
