@@ -458,6 +458,21 @@ int grimoire_moe_combine(void* stream, const uint16_t* src, const int32_t* inver
     return combine_common(stream, a);
 }
 
+int grimoire_moe_rmsnorm_residual(void* stream, float* h, const uint16_t* routed,
+                                  const int32_t* inverse, const float* route_weight,
+                                  const float* shared, const uint16_t* weight,
+                                  float weight_offset, float* out, uint16_t* out_bf,
+                                  int tokens, int top_k, int hidden, float eps) {
+    if (tokens <= 0) return GRIM_OK;
+    if (!h || !routed || !inverse || !route_weight || !weight)
+        return fail(GRIM_ERR_ARG, "null pointer");
+    if (top_k <= 0 || top_k > 16) return fail(GRIM_ERR_SHAPE, "top_k=%d", top_k);
+    if (hidden <= 0 || hidden % 4) return fail(GRIM_ERR_SHAPE, "hidden=%d (need %% 4)", hidden);
+    NormArgs a{h, routed, inverse, route_weight, shared, weight, weight_offset, out, out_bf,
+               tokens, top_k, hidden, eps};
+    return status(combine_norm_launch(S(stream), a));
+}
+
 int grimoire_moe_quant_limbs(void* stream, const float* src, int rows, int n, int8_t* dst,
                              float* scale) {
     if (rows <= 0) return GRIM_OK;

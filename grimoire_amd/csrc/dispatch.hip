@@ -307,4 +307,131 @@ hipError_t combine_launch(hipStream_t st, const CombineArgs& a) {
     return hipGetLastError();
 }
 
+// ------------------------------------------------ combine + residual + RMSNorm
+
+// launch_rmsnorm_moe_residual_batched (src/prefill.cpp:1004-1045): per token
+//   v = h + shared, then v = fma(w_s, bf16 routed[inverse[s]], v) in slot
+//   order; h = v; out = v * rsqrt(sum v^2 / H + eps) * (offset + bf16 w).
+// One block per token, 4 columns per thread.  The first kNormRegChunks
+// chunks of v stay in registers between the two passes, so H <= 8192 reads
+// h, shared and the routed rows once and writes h and out once; wider rows
+// re-read their tail of h, which this thread itself wrote.
+constexpr int kNormRegChunks = 8;
+
+template <int KT>
+__device__ __forceinline__ float4 norm_chunk(const float* __restrict__ h,
+                                             const float* __restrict__ sh,
+                                             const uint16_t* __restrict__ routed, const int* p,
+                                             const float* w, int H, int d) {
+    float4 v = *reinterpret_cast<const float4*>(h + d);
+    if (sh) {
+        const float4 a = *reinterpret_cast<const float4*>(sh + d);
+        v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
+    }
+    uint2 u[KT];
+#pragma unroll
+    for (int s = 0; s < KT; ++s) {
+        const int64_t row = p[s] < 0 ? 0 : p[s];
+        u[s] = *reinterpret_cast<const uint2*>(routed + row * H + d);
+    }
+#pragma unroll
+    for (int s = 0; s < KT; ++s) {
+        const bool on = p[s] >= 0;
+        v.x = on ? __builtin_fmaf(w[s], bits_f(u[s].x << 16), v.x) : v.x;
+        v.y = on ? __builtin_fmaf(w[s], bits_f(u[s].x & 0xFFFF0000u), v.y) : v.y;
+        v.z = on ? __builtin_fmaf(w[s], bits_f(u[s].y << 16), v.z) : v.z;
+        v.w = on ? __builtin_fmaf(w[s], bits_f(u[s].y & 0xFFFF0000u), v.w) : v.w;
+    }
+    return v;
+}
+
+__device__ __forceinline__ void norm_store(const NormArgs& a, int64_t base, int d, float4 v,
+                                           float scale) {
+    const uint2 wb = *reinterpret_cast<const uint2*>(a.weight + d);
+    float4 o;
+    o.x = v.x * scale * (a.offset + bits_f(wb.x << 16));
+    o.y = v.y * scale * (a.offset + bits_f(wb.x & 0xFFFF0000u));
+    o.z = v.z * scale * (a.offset + bits_f(wb.y << 16));
+    o.w = v.w * scale * (a.offset + bits_f(wb.y & 0xFFFF0000u));
+    if (a.out) *reinterpret_cast<float4*>(a.out + base + d) = o;
+    if (a.out_bf) {
+        uint2 b;
+        b.x = uint32_t(f32_to_bf16(o.x)) | (uint32_t(f32_to_bf16(o.y)) << 16);
+        b.y = uint32_t(f32_to_bf16(o.z)) | (uint32_t(f32_to_bf16(o.w)) << 16);
+        *reinterpret_cast<uint2*>(a.out_bf + base + d) = b;
+    }
+}
+
+template <int KT>
+__global__ __launch_bounds__(kDispThreads) void combine_norm_kernel(NormArgs a) {
+    const int t = blockIdx.x, H = a.H, K = a.K;
+    const int64_t base = int64_t(t) * H;
+    int p[KT];
+    float w[KT];
+#pragma unroll
+    for (int s = 0; s < KT; ++s) {
+        const int sc = s < K ? s : K - 1;
+        p[s] = s < K ? a.inverse[int64_t(t) * K + sc] : -1;
+        w[s] = a.rw[int64_t(t) * K + sc];
+    }
+    float* ht = a.h + base;
+    const float* sh = a.shared ? a.shared + base : nullptr;
+    const int step = kDispThreads * 4;
+    float4 keep[kNormRegChunks];
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kNormRegChunks; ++c) {
+        const int d = threadIdx.x * 4 + c * step;
+        if (d < H) {
+            keep[c] = norm_chunk<KT>(ht, sh, a.routed, p, w, H, d);
+            *reinterpret_cast<float4*>(ht + d) = keep[c];
+            ss = __builtin_fmaf(keep[c].x, keep[c].x, ss);
+            ss = __builtin_fmaf(keep[c].y, keep[c].y, ss);
+            ss = __builtin_fmaf(keep[c].z, keep[c].z, ss);
+            ss = __builtin_fmaf(keep[c].w, keep[c].w, ss);
+        }
+    }
+    for (int d = threadIdx.x * 4 + kNormRegChunks * step; d < H; d += step) {
+        const float4 v = norm_chunk<KT>(ht, sh, a.routed, p, w, H, d);
+        *reinterpret_cast<float4*>(ht + d) = v;
+        ss = __builtin_fmaf(v.x, v.x, ss);
+        ss = __builtin_fmaf(v.y, v.y, ss);
+        ss = __builtin_fmaf(v.z, v.z, ss);
+        ss = __builtin_fmaf(v.w, v.w, ss);
+    }
+    __shared__ float part[kDispThreads / kWave];
+    ss = group_sum<kWave>(ss);
+    if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = ss;
+    __syncthreads();
+    float total = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kDispThreads / kWave; ++i) total += part[i];
+    const float scale = rsqrtf(total / float(H) + a.eps);
+#pragma unroll
+    for (int c = 0; c < kNormRegChunks; ++c) {
+        const int d = threadIdx.x * 4 + c * step;
+        if (d < H) norm_store(a, base, d, keep[c], scale);
+    }
+    for (int d = threadIdx.x * 4 + kNormRegChunks * step; d < H; d += step)
+        norm_store(a, base, d, *reinterpret_cast<const float4*>(ht + d), scale);
+}
+
+hipError_t combine_norm_launch(hipStream_t st, const NormArgs& a) {
+    if (a.T <= 0) return hipSuccess;
+    if (a.K <= 0 || a.K > 16 || a.H % 4) return hipErrorInvalidValue;
+#define GRIM_NORM(KT) \
+    hipLaunchKernelGGL((combine_norm_kernel<KT>), dim3(a.T), dim3(kDispThreads), 0, st, a)
+    switch (a.K) {
+        case 1: GRIM_NORM(1); break;
+        case 2: GRIM_NORM(2); break;
+        case 4: GRIM_NORM(4); break;
+        case 6: GRIM_NORM(6); break;
+        case 8: GRIM_NORM(8); break;
+        case 10: GRIM_NORM(10); break;
+        default: GRIM_NORM(16); break;
+    }
+#undef GRIM_NORM
+    return hipGetLastError();
+}
+
 }  // namespace grim

@@ -34,10 +34,26 @@ struct CombineArgs {
     int T, K, H;
 };
 
+// Fused combine + residual + RMSNorm (src/prefill.cpp:1004-1045).
+struct NormArgs {
+    float* h;                // [T][H] residual stream, updated in place
+    const uint16_t* routed;  // [R][H] bf16 expert outputs, dispatch order
+    const int32_t* inverse;  // [T*K]
+    const float* rw;         // [T*K]
+    const float* shared;     // [T][H] or null
+    const uint16_t* weight;  // [H] bf16 norm weight
+    float offset;            // added to every norm weight
+    float* out;              // [T][H] or null
+    uint16_t* out_bf;        // [T][H] or null
+    int T, K, H;
+    float eps;
+};
+
 size_t dispatch_workspace_bytes(int T, int K, int E);
 // Where the dispatch leaves the live m-tile count inside its workspace.
 int32_t* dispatch_live_tiles(void* workspace, int T, int K, int E);
 hipError_t dispatch_launch(hipStream_t st, const DispatchArgs& a);
 hipError_t combine_launch(hipStream_t st, const CombineArgs& a);
+hipError_t combine_norm_launch(hipStream_t st, const NormArgs& a);
 
 }  // namespace grim

@@ -138,6 +138,19 @@ def launch_moe_unpermute(src, inverse, route_weight, dst, tokens, top_k, hidden,
              hidden), "unpermute")
 
 
+def launch_rmsnorm_moe_residual_batched(h, routed, inverse, route_weight, shared, weight, out,
+                                        out_bf, tokens, top_k, hidden, eps,
+                                        weight_offset=1.0, stream=None):
+    """launch_rmsnorm_moe_residual_batched (src/prefill.cpp:1004-1045): h += shared +
+    sum_s w_s * routed[inverse]; out = rmsnorm(h) * (weight_offset + weight).  The
+    reference reads weight_offset from its global g_norm_weight_offset (1.0 default)."""
+    _dev(h)
+    check(lib().grimoire_moe_rmsnorm_residual(_stream(stream), _p(h), _p(routed), _p(inverse),
+                                              _p(route_weight), _p(shared), _p(weight),
+                                              float(weight_offset), _p(out), _p(out_bf), tokens,
+                                              top_k, hidden, float(eps)), "rmsnorm_residual")
+
+
 def grouped_gemm(w: Weight, N, swiglu, A, out, offsets, counts, num_experts, total_rows,
                  a_pair=False, out_bf16=False, stream=None):
     """launch_moe_mxfp4_grouped (src/gemm_fast.cpp:2343) for int8/mxfp4/bf16."""

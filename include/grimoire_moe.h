@@ -257,6 +257,21 @@ int grimoire_moe_combine(void* stream, const uint16_t* src, const int32_t* inver
                          const float* route_weight, const uint16_t* shared_src,
                          const float* gate, float* dst, int tokens, int top_k, int hidden);
 
+/* Combine fused with the residual add and the next RMSNorm.  Per token t:
+ * v = h[t] + shared[t] (shared NULL = 0), then v = fma(route_weight[t,s],
+ * routed[inverse[t,s]], v) in slot order (inverse -1 skips the slot);
+ * h[t] = v; out[t] = v * rsqrt(sum(v^2)/hidden + eps) * (weight_offset +
+ * weight) in fp32 and/or bf16 (either output may be NULL).  routed and
+ * weight are bf16; top_k <= 16; hidden % 4 == 0.  Replaces
+ * launch_rmsnorm_moe_residual_batched (src/prefill.cpp:1004-1045), whose
+ * weight offset is the global g_norm_weight_offset
+ * (include/b70/prefill_qk_math.hpp:9-15): pass its value. */
+int grimoire_moe_rmsnorm_residual(void* stream, float* h, const uint16_t* routed,
+                                  const int32_t* inverse, const float* route_weight,
+                                  const float* shared, const uint16_t* weight,
+                                  float weight_offset, float* out, uint16_t* out_bf,
+                                  int tokens, int top_k, int hidden, float eps);
+
 /* ------------------------------------------------------------------------
  * Grouped GEMM on MFMA (prefill).  One launch per projection for all
  * experts.  A bf16 [R][K] rows grouped by expert (offsets/counts from the

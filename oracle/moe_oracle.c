@@ -16,6 +16,8 @@
  *                       per-expert tensors (tests/test_moe.cpp:54-74 idea)
  *   orc_dispatch        invariants of src/grimoire.cpp:23047-23097
  *   orc_unpermute       closed form on one-hot routes
+ *   orc_rmsnorm_moe_residual  orc_unpermute (h = 0, no shared), exact
+ *                       h + shared (all slots skipped), float64 RMSNorm
  *   orc_grouped_gemm    numpy matmul of the dequantised weights
  *   orc_expf            libm expf to within 2 ulp
  */
@@ -500,6 +502,38 @@ void orc_unpermute(const float* src, const int32_t* inverse, const float* route_
             }
             dst[(int64_t)t * hidden + d] = v;
         }
+}
+
+/* src/prefill.cpp:1004-1045 (launch_rmsnorm_moe_residual_batched); the
+ * weight offset is g_norm_weight_offset (include/b70/prefill_qk_math.hpp:14).
+ * ss accumulates as an fma chain in column order (the reference splits it
+ * over work-items; the order only moves the last bits of the scale). */
+void orc_rmsnorm_moe_residual(float* h, const uint16_t* routed, const int32_t* inverse,
+                              const float* route_weight, const float* shared,
+                              const uint16_t* weight, float weight_offset, float* out,
+                              uint16_t* out_bf, int tokens, int top_k, int hidden, float eps) {
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < tokens; ++t) {
+        float* ht = h + (int64_t)t * hidden;
+        float ss = 0.0f;
+        for (int d = 0; d < hidden; ++d) {
+            float v = ht[d] + (shared ? shared[(int64_t)t * hidden + d] : 0.0f);
+            for (int s = 0; s < top_k; ++s) {
+                const int64_t r = (int64_t)t * top_k + s;
+                const int32_t p = inverse[r];
+                if (p >= 0)
+                    v = fmaf(route_weight[r], orc_bf16_to_f32(routed[(int64_t)p * hidden + d]), v);
+            }
+            ht[d] = v;
+            ss = fmaf(v, v, ss);
+        }
+        const float scale = 1.0f / sqrtf(ss / (float)hidden + eps);
+        for (int d = 0; d < hidden; ++d) {
+            const float o = ht[d] * scale * (weight_offset + orc_bf16_to_f32(weight[d]));
+            if (out) out[(int64_t)t * hidden + d] = o;
+            if (out_bf) out_bf[(int64_t)t * hidden + d] = orc_f32_to_bf16(o);
+        }
+    }
 }
 
 /* src/gemm_fast.cpp:1603-1800 contract (EPI 0 / EPI 1) */

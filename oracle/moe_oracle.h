@@ -96,6 +96,15 @@ int orc_dispatch(const int32_t* topk_ids, int tokens, int top_k, int n_experts, 
 void orc_unpermute(const float* src, const int32_t* inverse, const float* route_weight,
                    float* dst, int tokens, int top_k, int hidden);
 
+/* launch_rmsnorm_moe_residual_batched (src/prefill.cpp:1004-1045): h +=
+ * shared + fma chain over slots of w * bf16 routed[inverse]; out (fp32
+ * and/or bf16, either may be NULL) = h * rsqrt(mean h^2 + eps) *
+ * (weight_offset + bf16 weight). */
+void orc_rmsnorm_moe_residual(float* h, const uint16_t* routed, const int32_t* inverse,
+                              const float* route_weight, const float* shared,
+                              const uint16_t* weight, float weight_offset, float* out,
+                              uint16_t* out_bf, int tokens, int top_k, int hidden, float eps);
+
 /* Grouped GEMM (src/gemm_fast.cpp:1603-1800 contract): rows [off_e,
  * off_e+cnt_e) of A (fp32 values) times W_e^T; swiglu gives silu(g)*u over
  * N = 2I. out fp32 [R][N or I]. Double accumulation. */

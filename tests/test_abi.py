@@ -70,6 +70,12 @@ def test_null_and_workspace_rejections():
     L, keep = _layer()
     assert lib.grimoire_moe_gate_up(None, L, None, 1, 1) == _abi.ERR_ARG
     assert lib.grimoire_moe_unpermute(None, None, 1, 1, 1, 4, 2, 8) == _abi.ERR_ARG
+    assert lib.grimoire_moe_rmsnorm_residual(None, 1, 1, 1, 1, None, None, 1.0, 1, None, 4, 2, 8,
+                                             1e-6) == _abi.ERR_ARG
+    assert lib.grimoire_moe_rmsnorm_residual(None, 1, 1, 1, 1, None, 1, 1.0, 1, None, 4, 17, 8,
+                                             1e-6) == _abi.ERR_SHAPE
+    assert lib.grimoire_moe_rmsnorm_residual(None, 1, 1, 1, 1, None, 1, 1.0, 1, None, 4, 8, 6,
+                                             1e-6) == _abi.ERR_SHAPE
     ws = lib.grimoire_moe_route_workspace_bytes(100, 8, 64)
     assert ws > 0
     assert lib.grimoire_moe_route_grouped(None, 1, 1, None, None, 1, 1, 1, None, None, 0, 100, 64,
@@ -81,3 +87,5 @@ def test_zero_tokens_is_a_no_op():
     lib = _abi.lib()
     assert lib.grimoire_moe_router_topk_batched(None, None, 0, 64, 8, None, None, 1) == 0
     assert lib.grimoire_moe_unpermute(None, None, None, None, None, 0, 8, 64) == 0
+    assert lib.grimoire_moe_rmsnorm_residual(None, None, None, None, None, None, None, 1.0, None,
+                                             None, 0, 8, 64, 1e-6) == 0

@@ -88,3 +88,38 @@ def test_unpermute_bit_exact(gpu, T, K, H):
     torch.cuda.synchronize()
     want2 = O.unpermute(sb.float(), inv, rw, T, K, H)
     assert torch.equal(out2.cpu(), want2)
+
+
+@pytest.mark.parametrize("T,K,H,shared,outs", [(1, 8, 2048, True, "both"), (33, 10, 2048, True, "f32"),
+                                               (5, 4, 2880, False, "bf"), (3, 8, 7168, True, "both"),
+                                               (2, 2, 9000, True, "both"), (7, 3, 12, False, "both")])
+def test_rmsnorm_moe_residual(gpu, T, K, H, shared, outs):
+    """launch_rmsnorm_moe_residual_batched (src/prefill.cpp:1004-1045): the residual
+    update is bit-exact (same fma order); the normalised output differs only by the
+    order of the sum of squares and the device rsqrt (rel 1e-5)."""
+    print(f"rmsnorm_moe_residual T={T} K={K} H={H} shared={shared} outs={outs}", flush=True)
+    g = torch.Generator().manual_seed(T * 1000 + H)
+    R, eps, off = T * K, 1e-6, 1.0 if H != 12 else 0.5
+    routed = torch.randn(R, H, generator=g).bfloat16().view(torch.int16)
+    inv = torch.randperm(R, generator=g).int()
+    inv[::5] = -1
+    rw = torch.rand(R, generator=g)
+    h = torch.randn(T, H, generator=g) * 2
+    sh = torch.randn(T, H, generator=g) if shared else None
+    w = (torch.randn(H, generator=g) * 0.2).bfloat16().view(torch.int16)
+    hd = h.to(gpu)
+    out = torch.full((T, H), float("nan"), device=gpu) if outs in ("both", "f32") else None
+    obf = torch.zeros((T, H), dtype=torch.int16, device=gpu) if outs in ("both", "bf") else None
+    ops.launch_rmsnorm_moe_residual_batched(hd, routed.to(gpu), inv.to(gpu), rw.to(gpu),
+                                            None if sh is None else sh.to(gpu), w.to(gpu), out,
+                                            obf, T, K, H, eps, weight_offset=off)
+    torch.cuda.synchronize()
+    hn, want, want_bf = O.rmsnorm_moe_residual(h, routed, inv, rw, sh, w, off, T, K, H, eps)
+    assert torch.equal(hd.cpu(), hn)
+    if out is not None:
+        err = (out.cpu() - want).abs().max().item()
+        assert err <= 1e-5 * want.abs().max().item(), err
+    if obf is not None:
+        # bf16 of values equal to 1e-5 relative: at most one bf16 ulp apart
+        d = (obf.cpu().int() - want_bf.int()).abs()
+        assert d.max().item() <= 1, d.max().item()

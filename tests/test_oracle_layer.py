@@ -184,6 +184,52 @@ def test_unpermute_closed_form():
     assert (out2 - want).abs().max() < 1e-6
 
 
+def _bf16_bits(x):
+    return x.bfloat16().view(torch.int16)
+
+
+def test_rmsnorm_moe_residual_pinned():
+    """launch_rmsnorm_moe_residual_batched (src/prefill.cpp:1004-1045) restated:
+    h = 0 without shared reduces the residual update to the pinned unpermute
+    bit for bit; all slots skipped leaves exactly h + shared; the normalised
+    output matches an independent float64 RMSNorm; out_bf is bf16(out)."""
+    g = torch.Generator().manual_seed(7)
+    T, K, H, eps = 6, 4, 72, 1e-6
+    routed = torch.randn(T * K, H, generator=g)
+    rbits = _bf16_bits(routed)
+    inv = torch.randperm(T * K, generator=g).int()
+    inv[3::5] = -1
+    rw = torch.rand(T * K, generator=g)
+    w = torch.randn(H, generator=g) * 0.1
+    wbits = _bf16_bits(w)
+    zero = torch.zeros(T, H)
+    hn, _, _ = O.rmsnorm_moe_residual(zero, rbits, inv, rw, None, wbits, 1.0, T, K, H, eps)
+    assert torch.equal(hn, O.unpermute(rbits.view(torch.bfloat16).float(), inv, rw, T, K, H))
+
+    h = torch.randn(T, H, generator=g) * 3
+    sh = torch.randn(T, H, generator=g)
+    hn, out, obf = O.rmsnorm_moe_residual(h, rbits, torch.full_like(inv, -1), rw, sh, wbits, 1.0,
+                                          T, K, H, eps)
+    assert torch.equal(hn, h + sh)
+
+    for off in (1.0, 0.0):
+        hn, out, obf = O.rmsnorm_moe_residual(h, rbits, inv, rw, sh, wbits, off, T, K, H, eps)
+        r = rbits.view(torch.bfloat16).double()
+        v = h.double() + sh.double()
+        for s in range(K):
+            p = inv[s::K].long()
+            v = v + torch.where(p[:, None] >= 0, rw[s::K, None].double() * r[p.clamp(min=0)], 0.0)
+        assert (hn.double() - v).abs().max() < 1e-5
+        wd = off + wbits.view(torch.bfloat16).double()
+        want = v / torch.sqrt((v * v).mean(1, keepdim=True) + eps) * wd
+        assert (out.double() - want).abs().max() < 1e-5 * want.abs().max()
+        assert torch.equal(obf, _bf16_bits(out))
+    # unit weights, offset 1: every row has RMS sqrt(ms / (ms + eps))
+    _, out, _ = O.rmsnorm_moe_residual(h, rbits, inv, rw, sh, _bf16_bits(torch.zeros(H)), 1.0,
+                                       T, K, H, 0.0)
+    assert (out.double().pow(2).mean(1).sqrt() - 1.0).abs().max() < 1e-6
+
+
 # -------------------------------------------------------------- expert ffn
 
 def _small_layer(fmt, E=8, H=256, I=128, K=3, shared=False, seed=0):
