@@ -109,6 +109,7 @@ SIGNATURES = {
     "grimoire_moe_combine": (I32, [P, P, P, P, P, P, P, I32, I32, I32]),
     "grimoire_moe_rmsnorm_residual": (I32, [P, P, P, P, P, P, P, F32, P, P, I32, I32, I32,
                                             F32]),
+    "grimoire_rmsnorm_residual": (I32, [P, P, P, P, P, F32, P, P, I32, I32, F32]),
     "grimoire_moe_grouped_gemm": (I32, [P, QWP, I32, I32, P, I32, P, I32, P, P, I32, I32]),
     "grimoire_moe_quant_limbs": (I32, [P, P, I32, I32, P, P]),
     "grimoire_moe_grouped_gemm_i8": (I32, [P, QWP, I32, I32, P, P, P, P, P, I32, I32]),

@@ -468,8 +468,19 @@ int grimoire_moe_rmsnorm_residual(void* stream, float* h, const uint16_t* routed
         return fail(GRIM_ERR_ARG, "null pointer");
     if (top_k <= 0 || top_k > 16) return fail(GRIM_ERR_SHAPE, "top_k=%d", top_k);
     if (hidden <= 0 || hidden % 4) return fail(GRIM_ERR_SHAPE, "hidden=%d (need %% 4)", hidden);
-    NormArgs a{h, routed, inverse, route_weight, shared, weight, weight_offset, out, out_bf,
-               tokens, top_k, hidden, eps};
+    NormArgs a{h, routed, inverse, route_weight, shared, nullptr, weight, weight_offset, out,
+               out_bf, tokens, top_k, hidden, eps};
+    return status(combine_norm_launch(S(stream), a));
+}
+
+int grimoire_rmsnorm_residual(void* stream, float* h, const float* r0, const float* r1,
+                              const uint16_t* weight, float weight_offset, float* out,
+                              uint16_t* out_bf, int tokens, int hidden, float eps) {
+    if (tokens <= 0) return GRIM_OK;
+    if (!h || !weight) return fail(GRIM_ERR_ARG, "null pointer");
+    if (hidden <= 0 || hidden % 4) return fail(GRIM_ERR_SHAPE, "hidden=%d (need %% 4)", hidden);
+    NormArgs a{h, nullptr, nullptr, nullptr, r0, r1, weight, weight_offset, out, out_bf,
+               tokens, 0, hidden, eps};
     return status(combine_norm_launch(S(stream), a));
 }
 

@@ -312,6 +312,8 @@ hipError_t combine_launch(hipStream_t st, const CombineArgs& a) {
 // launch_rmsnorm_moe_residual_batched (src/prefill.cpp:1004-1045): per token
 //   v = h + shared, then v = fma(w_s, bf16 routed[inverse[s]], v) in slot
 //   order; h = v; out = v * rsqrt(sum v^2 / H + eps) * (offset + bf16 w).
+// KT == 0 is launch_rmsnorm_residual_batched (src/prefill.cpp:627-700):
+//   v = (h + r0) + r1, h written back only when a residual was added.
 // One block per token, 4 columns per thread.  The first kNormRegChunks
 // chunks of v stay in registers between the two passes, so H <= 8192 reads
 // h, shared and the routed rows once and writes h and out once; wider rows
@@ -321,6 +323,7 @@ constexpr int kNormRegChunks = 8;
 template <int KT>
 __device__ __forceinline__ float4 norm_chunk(const float* __restrict__ h,
                                              const float* __restrict__ sh,
+                                             const float* __restrict__ sh2,
                                              const uint16_t* __restrict__ routed, const int* p,
                                              const float* w, int H, int d) {
     float4 v = *reinterpret_cast<const float4*>(h + d);
@@ -328,7 +331,11 @@ __device__ __forceinline__ float4 norm_chunk(const float* __restrict__ h,
         const float4 a = *reinterpret_cast<const float4*>(sh + d);
         v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
     }
-    uint2 u[KT];
+    if (sh2) {
+        const float4 a = *reinterpret_cast<const float4*>(sh2 + d);
+        v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
+    }
+    uint2 u[KT > 0 ? KT : 1];
 #pragma unroll
     for (int s = 0; s < KT; ++s) {
         const int64_t row = p[s] < 0 ? 0 : p[s];
@@ -366,8 +373,8 @@ template <int KT>
 __global__ __launch_bounds__(kDispThreads) void combine_norm_kernel(NormArgs a) {
     const int t = blockIdx.x, H = a.H, K = a.K;
     const int64_t base = int64_t(t) * H;
-    int p[KT];
-    float w[KT];
+    int p[KT > 0 ? KT : 1];
+    float w[KT > 0 ? KT : 1];
 #pragma unroll
     for (int s = 0; s < KT; ++s) {
         const int sc = s < K ? s : K - 1;
@@ -376,6 +383,8 @@ __global__ __launch_bounds__(kDispThreads) void combine_norm_kernel(NormArgs a) 
     }
     float* ht = a.h + base;
     const float* sh = a.shared ? a.shared + base : nullptr;
+    const float* sh2 = a.shared2 ? a.shared2 + base : nullptr;
+    const bool write_h = KT > 0 || sh || sh2;
     const int step = kDispThreads * 4;
     float4 keep[kNormRegChunks];
     float ss = 0.0f;
@@ -383,8 +392,8 @@ __global__ __launch_bounds__(kDispThreads) void combine_norm_kernel(NormArgs a) 
     for (int c = 0; c < kNormRegChunks; ++c) {
         const int d = threadIdx.x * 4 + c * step;
         if (d < H) {
-            keep[c] = norm_chunk<KT>(ht, sh, a.routed, p, w, H, d);
-            *reinterpret_cast<float4*>(ht + d) = keep[c];
+            keep[c] = norm_chunk<KT>(ht, sh, sh2, a.routed, p, w, H, d);
+            if (write_h) *reinterpret_cast<float4*>(ht + d) = keep[c];
             ss = __builtin_fmaf(keep[c].x, keep[c].x, ss);
             ss = __builtin_fmaf(keep[c].y, keep[c].y, ss);
             ss = __builtin_fmaf(keep[c].z, keep[c].z, ss);
@@ -392,8 +401,8 @@ __global__ __launch_bounds__(kDispThreads) void combine_norm_kernel(NormArgs a) 
         }
     }
     for (int d = threadIdx.x * 4 + kNormRegChunks * step; d < H; d += step) {
-        const float4 v = norm_chunk<KT>(ht, sh, a.routed, p, w, H, d);
-        *reinterpret_cast<float4*>(ht + d) = v;
+        const float4 v = norm_chunk<KT>(ht, sh, sh2, a.routed, p, w, H, d);
+        if (write_h) *reinterpret_cast<float4*>(ht + d) = v;
         ss = __builtin_fmaf(v.x, v.x, ss);
         ss = __builtin_fmaf(v.y, v.y, ss);
         ss = __builtin_fmaf(v.z, v.z, ss);
@@ -418,10 +427,11 @@ __global__ __launch_bounds__(kDispThreads) void combine_norm_kernel(NormArgs a) 
 
 hipError_t combine_norm_launch(hipStream_t st, const NormArgs& a) {
     if (a.T <= 0) return hipSuccess;
-    if (a.K <= 0 || a.K > 16 || a.H % 4) return hipErrorInvalidValue;
+    if (a.K < 0 || a.K > 16 || a.H % 4) return hipErrorInvalidValue;
 #define GRIM_NORM(KT) \
     hipLaunchKernelGGL((combine_norm_kernel<KT>), dim3(a.T), dim3(kDispThreads), 0, st, a)
     switch (a.K) {
+        case 0: GRIM_NORM(0); break;
         case 1: GRIM_NORM(1); break;
         case 2: GRIM_NORM(2); break;
         case 4: GRIM_NORM(4); break;

@@ -34,13 +34,15 @@ struct CombineArgs {
     int T, K, H;
 };
 
-// Fused combine + residual + RMSNorm (src/prefill.cpp:1004-1045).
+// Fused combine + residual + RMSNorm (src/prefill.cpp:1004-1045); K == 0 is
+// the residual RMSNorm without experts (src/prefill.cpp:627-700).
 struct NormArgs {
     float* h;                // [T][H] residual stream, updated in place
     const uint16_t* routed;  // [R][H] bf16 expert outputs, dispatch order
     const int32_t* inverse;  // [T*K]
     const float* rw;         // [T*K]
     const float* shared;     // [T][H] or null
+    const float* shared2;    // [T][H] or null, added after shared
     const uint16_t* weight;  // [H] bf16 norm weight
     float offset;            // added to every norm weight
     float* out;              // [T][H] or null

@@ -151,6 +151,16 @@ def launch_rmsnorm_moe_residual_batched(h, routed, inverse, route_weight, shared
                                               top_k, hidden, float(eps)), "rmsnorm_residual")
 
 
+def launch_rmsnorm_residual_batched(h, r0, r1, weight, out, tokens, hidden, eps, out_bf=None,
+                                    weight_offset=1.0, stream=None):
+    """launch_rmsnorm_residual_batched (src/prefill.cpp:627-700), ungrouped norms:
+    h = (h + r0) + r1 when either is given; out = rmsnorm(h) * (weight_offset + weight)."""
+    _dev(h)
+    check(lib().grimoire_rmsnorm_residual(_stream(stream), _p(h), _p(r0), _p(r1), _p(weight),
+                                          float(weight_offset), _p(out), _p(out_bf), tokens,
+                                          hidden, float(eps)), "rmsnorm_residual")
+
+
 def grouped_gemm(w: Weight, N, swiglu, A, out, offsets, counts, num_experts, total_rows,
                  a_pair=False, out_bf16=False, stream=None):
     """launch_moe_mxfp4_grouped (src/gemm_fast.cpp:2343) for int8/mxfp4/bf16."""

@@ -272,6 +272,16 @@ int grimoire_moe_rmsnorm_residual(void* stream, float* h, const uint16_t* routed
                                   float weight_offset, float* out, uint16_t* out_bf,
                                   int tokens, int top_k, int hidden, float eps);
 
+/* The residual RMSNorm that feeds the router: v = (h[t] + r0[t]) + r1[t]
+ * (either addend may be NULL; h is written back only when one is given);
+ * out[t] = v * rsqrt(sum(v^2)/hidden + eps) * (weight_offset + weight), fp32
+ * and/or bf16.  hidden % 4 == 0.  Replaces launch_rmsnorm_residual_batched
+ * (src/prefill.cpp:627-700) for ungrouped norms (its grouped-norm branch,
+ * launch_rmsnorm_grouped, is not covered). */
+int grimoire_rmsnorm_residual(void* stream, float* h, const float* r0, const float* r1,
+                              const uint16_t* weight, float weight_offset, float* out,
+                              uint16_t* out_bf, int tokens, int hidden, float eps);
+
 /* ------------------------------------------------------------------------
  * Grouped GEMM on MFMA (prefill).  One launch per projection for all
  * experts.  A bf16 [R][K] rows grouped by expert (offsets/counts from the

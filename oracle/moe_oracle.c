@@ -18,6 +18,8 @@
  *   orc_unpermute       closed form on one-hot routes
  *   orc_rmsnorm_moe_residual  orc_unpermute (h = 0, no shared), exact
  *                       h + shared (all slots skipped), float64 RMSNorm
+ *   orc_rmsnorm_residual  exact (h + r0) + r1, float64 RMSNorm, torch
+ *                       rms_norm
  *   orc_grouped_gemm    numpy matmul of the dequantised weights
  *   orc_expf            libm expf to within 2 ulp
  */
@@ -525,6 +527,30 @@ void orc_rmsnorm_moe_residual(float* h, const uint16_t* routed, const int32_t* i
                     v = fmaf(route_weight[r], orc_bf16_to_f32(routed[(int64_t)p * hidden + d]), v);
             }
             ht[d] = v;
+            ss = fmaf(v, v, ss);
+        }
+        const float scale = 1.0f / sqrtf(ss / (float)hidden + eps);
+        for (int d = 0; d < hidden; ++d) {
+            const float o = ht[d] * scale * (weight_offset + orc_bf16_to_f32(weight[d]));
+            if (out) out[(int64_t)t * hidden + d] = o;
+            if (out_bf) out_bf[(int64_t)t * hidden + d] = orc_f32_to_bf16(o);
+        }
+    }
+}
+
+/* src/prefill.cpp:627-700 (launch_rmsnorm_residual_batched, ungrouped). */
+void orc_rmsnorm_residual(float* h, const float* r0, const float* r1, const uint16_t* weight,
+                          float weight_offset, float* out, uint16_t* out_bf, int tokens,
+                          int hidden, float eps) {
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < tokens; ++t) {
+        float* ht = h + (int64_t)t * hidden;
+        float ss = 0.0f;
+        for (int d = 0; d < hidden; ++d) {
+            float v = ht[d];
+            if (r0) v += r0[(int64_t)t * hidden + d];
+            if (r1) v += r1[(int64_t)t * hidden + d];
+            if (r0 || r1) ht[d] = v;
             ss = fmaf(v, v, ss);
         }
         const float scale = 1.0f / sqrtf(ss / (float)hidden + eps);

@@ -105,6 +105,13 @@ void orc_rmsnorm_moe_residual(float* h, const uint16_t* routed, const int32_t* i
                               const uint16_t* weight, float weight_offset, float* out,
                               uint16_t* out_bf, int tokens, int top_k, int hidden, float eps);
 
+/* launch_rmsnorm_residual_batched (src/prefill.cpp:627-700), ungrouped:
+ * h = (h + r0) + r1 (NULL addends skipped), out = rmsnorm(h) *
+ * (weight_offset + bf16 weight). */
+void orc_rmsnorm_residual(float* h, const float* r0, const float* r1, const uint16_t* weight,
+                          float weight_offset, float* out, uint16_t* out_bf, int tokens,
+                          int hidden, float eps);
+
 /* Grouped GEMM (src/gemm_fast.cpp:1603-1800 contract): rows [off_e,
  * off_e+cnt_e) of A (fp32 values) times W_e^T; swiglu gives silu(g)*u over
  * N = 2I. out fp32 [R][N or I]. Double accumulation. */

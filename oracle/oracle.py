@@ -73,6 +73,7 @@ def orc() -> C.CDLL:
             "orc_moe_forward": (None, [P, P, P, P, P, P, I32]),
             "orc_dispatch": (I32, [P, I32, I32, I32, I32, P, P, P, P, P, P, I32]),
             "orc_unpermute": (None, [P, P, P, P, I32, I32, I32]),
+            "orc_rmsnorm_residual": (None, [P, P, P, P, F32, P, P, I32, I32, F32]),
             "orc_rmsnorm_moe_residual": (None, [P, P, P, P, P, P, F32, P, P, I32, I32, I32,
                                                 F32]),
             "orc_grouped_gemm": (None, [P, I32, I32, P, P, P, P, I32]),
@@ -192,4 +193,17 @@ def rmsnorm_moe_residual(h, routed, inverse, rw, shared, weight, weight_offset, 
     sc = None if shared is None else shared.contiguous()
     orc().orc_rmsnorm_moe_residual(_p(hn), _p(rc), _p(ic), _p(wc), _p(sc), _p(wt),
                                    float(weight_offset), _p(out), _p(obf), T, K, H, float(eps))
+    return hn, out, obf
+
+
+def rmsnorm_residual(h, r0, r1, weight, weight_offset, T, H, eps):
+    """Returns (h_new, out fp32, out_bf as int16 bits); h is not modified."""
+    hn = h.contiguous().clone()
+    out = torch.empty((T, H), dtype=torch.float32)
+    obf = torch.empty((T, H), dtype=torch.int16)
+    a = None if r0 is None else r0.contiguous()
+    b = None if r1 is None else r1.contiguous()
+    wt = weight.contiguous()
+    orc().orc_rmsnorm_residual(_p(hn), _p(a), _p(b), _p(wt), float(weight_offset), _p(out),
+                               _p(obf), T, H, float(eps))
     return hn, out, obf

@@ -89,3 +89,9 @@ def test_zero_tokens_is_a_no_op():
     assert lib.grimoire_moe_unpermute(None, None, None, None, None, 0, 8, 64) == 0
     assert lib.grimoire_moe_rmsnorm_residual(None, None, None, None, None, None, None, 1.0, None,
                                              None, 0, 8, 64, 1e-6) == 0
+    assert lib.grimoire_rmsnorm_residual(None, None, None, None, None, 1.0, None, None, 0, 64,
+                                         1e-6) == 0
+    assert lib.grimoire_rmsnorm_residual(None, 1, None, None, None, 1.0, None, None, 2, 64,
+                                         1e-6) == _abi.ERR_ARG
+    assert lib.grimoire_rmsnorm_residual(None, 1, None, None, 1, 1.0, None, None, 2, 66,
+                                         1e-6) == _abi.ERR_SHAPE

@@ -123,3 +123,27 @@ def test_rmsnorm_moe_residual(gpu, T, K, H, shared, outs):
         # bf16 of values equal to 1e-5 relative: at most one bf16 ulp apart
         d = (obf.cpu().int() - want_bf.int()).abs()
         assert d.max().item() <= 1, d.max().item()
+
+
+@pytest.mark.parametrize("T,H,addends", [(1, 2048, 2), (64, 7168, 1), (3, 9000, 0), (17, 2880, 2)])
+def test_rmsnorm_residual(gpu, T, H, addends):
+    """launch_rmsnorm_residual_batched (src/prefill.cpp:627-700): h bit-exact, out rel 1e-5."""
+    print(f"rmsnorm_residual T={T} H={H} addends={addends}", flush=True)
+    g = torch.Generator().manual_seed(T + H)
+    eps = 1e-6
+    h = torch.randn(T, H, generator=g) * 2
+    r0 = torch.randn(T, H, generator=g) if addends >= 1 else None
+    r1 = torch.randn(T, H, generator=g) if addends >= 2 else None
+    w = (torch.randn(H, generator=g) * 0.2).bfloat16().view(torch.int16)
+    hd = h.to(gpu)
+    out = torch.full((T, H), float("nan"), device=gpu)
+    obf = torch.zeros((T, H), dtype=torch.int16, device=gpu)
+    ops.launch_rmsnorm_residual_batched(hd, None if r0 is None else r0.to(gpu),
+                                        None if r1 is None else r1.to(gpu), w.to(gpu), out, T, H,
+                                        eps, out_bf=obf)
+    torch.cuda.synchronize()
+    hn, want, want_bf = O.rmsnorm_residual(h, r0, r1, w, 1.0, T, H, eps)
+    assert torch.equal(hd.cpu(), hn)
+    err = (out.cpu() - want).abs().max().item()
+    assert err <= 1e-5 * want.abs().max().item(), err
+    assert (obf.cpu().int() - want_bf.int()).abs().max().item() <= 1

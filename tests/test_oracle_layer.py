@@ -230,6 +230,30 @@ def test_rmsnorm_moe_residual_pinned():
     assert (out.double().pow(2).mean(1).sqrt() - 1.0).abs().max() < 1e-6
 
 
+def test_rmsnorm_residual_pinned():
+    """launch_rmsnorm_residual_batched (src/prefill.cpp:627-700) restated: the
+    residual is exactly (h + r0) + r1; the output is torch's rms_norm scaled by
+    offset + bf16 weight; without addends h is left as it was."""
+    g = torch.Generator().manual_seed(11)
+    T, H, eps = 5, 96, 1e-5
+    h = torch.randn(T, H, generator=g) * 2
+    r0 = torch.randn(T, H, generator=g)
+    r1 = torch.randn(T, H, generator=g)
+    wbits = _bf16_bits(torch.randn(H, generator=g) * 0.1)
+    hn, out, obf = O.rmsnorm_residual(h, r0, r1, wbits, 1.0, T, H, eps)
+    assert torch.equal(hn, (h + r0) + r1)
+    wf = 1.0 + wbits.view(torch.bfloat16).double()
+    want = torch.nn.functional.rms_norm(hn.double(), (H,), eps=eps) * wf
+    assert (out.double() - want).abs().max() < 1e-5 * want.abs().max()
+    assert torch.equal(obf, _bf16_bits(out))
+    hn2, out2, _ = O.rmsnorm_residual(h, None, None, wbits, 0.0, T, H, eps)
+    assert torch.equal(hn2, h)
+    want2 = torch.nn.functional.rms_norm(h.double(), (H,), eps=eps) * wbits.view(torch.bfloat16).double()
+    assert (out2.double() - want2).abs().max() < 1e-5 * want2.abs().max()
+    hn3, _, _ = O.rmsnorm_residual(h, None, r1, wbits, 1.0, T, H, eps)
+    assert torch.equal(hn3, h + r1)
+
+
 # -------------------------------------------------------------- expert ffn
 
 def _small_layer(fmt, E=8, H=256, I=128, K=3, shared=False, seed=0):
