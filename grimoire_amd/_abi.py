@@ -76,6 +76,21 @@ class RouteParams(C.Structure):
     ]
 
 
+class ExpertSrc(C.Structure):
+    """grim_expert_src: one checkpoint projection (weight, zeros, scales)."""
+    _fields_ = [
+        ("kind", C.c_int32),
+        ("in_", C.c_int32),
+        ("out", C.c_int32),
+        ("group", C.c_int32),
+        ("weight", C.c_void_p),
+        ("zeros", C.c_void_p),
+        ("scales", C.c_void_p),
+    ]
+
+
+SRC_GPTQ, SRC_MXFP4_PACKED, SRC_INT4_PACKED = 1, 2, 3
+
 P = C.c_void_p
 I32 = C.c_int
 F32 = C.c_float
@@ -110,6 +125,8 @@ SIGNATURES = {
     "grimoire_moe_rmsnorm_residual": (I32, [P, P, P, P, P, P, P, F32, P, P, I32, I32, I32,
                                             F32]),
     "grimoire_rmsnorm_residual": (I32, [P, P, P, P, P, F32, P, P, I32, I32, F32]),
+    "grimoire_moe_ingest_projection": (I32, [P, C.POINTER(ExpertSrc), QWP, I32]),
+    "grimoire_moe_int4_to_signed": (I32, [P, P, SZ, P, SZ, P, SZ, P, SZ, P]),
     "grimoire_moe_grouped_gemm": (I32, [P, QWP, I32, I32, P, I32, P, I32, P, P, I32, I32]),
     "grimoire_moe_quant_limbs": (I32, [P, P, I32, I32, P, P]),
     "grimoire_moe_grouped_gemm_i8": (I32, [P, QWP, I32, I32, P, P, P, P, P, I32, I32]),

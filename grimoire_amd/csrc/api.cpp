@@ -18,6 +18,7 @@
 #include "gemm.hpp"
 #include "gemm_i8.hpp"
 #include "gemv.hpp"
+#include "ingest.hpp"
 #include "router.hpp"
 
 using namespace grim;
@@ -482,6 +483,79 @@ int grimoire_rmsnorm_residual(void* stream, float* h, const float* r0, const flo
     NormArgs a{h, nullptr, nullptr, nullptr, r0, r1, weight, weight_offset, out, out_bf,
                tokens, 0, hidden, eps};
     return status(combine_norm_launch(S(stream), a));
+}
+
+int grimoire_moe_ingest_projection(void* stream, const grim_expert_src* src,
+                                   const grim_quant_weight* dst, int row0) {
+    if (!src || !dst) return fail(GRIM_ERR_ARG, "null src/dst");
+    if (!src->weight || !src->scales || !dst->payload || !dst->scales)
+        return fail(GRIM_ERR_ARG, "null tensor pointer");
+    const int in = src->in, out = src->out;
+    if (in <= 0 || out <= 0 || in % 32) return fail(GRIM_ERR_SHAPE, "in=%d out=%d", in, out);
+    if (dst->K != in) return fail(GRIM_ERR_SHAPE, "dst K=%d, source in=%d", dst->K, in);
+    if (row0 < 0 || int64_t(row0) + out > dst->N)
+        return fail(GRIM_ERR_SHAPE, "rows [%d, %d) outside dst N=%d", row0, row0 + out, dst->N);
+    if (dst->row_bytes != in / 2)
+        return fail(GRIM_ERR_SHAPE, "dst row_bytes=%lld, need %d", (long long)dst->row_bytes, in / 2);
+    hipStream_t st = S(stream);
+    uint8_t* pay = const_cast<uint8_t*>(dst->payload) + int64_t(row0) * dst->row_bytes;
+    if (src->kind == GRIM_SRC_MXFP4_PACKED) {
+        if (dst->fmt != GRIM_FMT_MXFP4) return fail(GRIM_ERR_FORMAT, "MXFP4 source needs MXFP4 dst");
+        if (dst->row_scales != in / 32) return fail(GRIM_ERR_SHAPE, "dst row_scales != in/32");
+        uint8_t* sc = static_cast<uint8_t*>(const_cast<void*>(dst->scales)) +
+                      int64_t(row0) * dst->row_scales;
+        hipError_t e = hipMemcpyAsync(pay, src->weight, size_t(out) * (in / 2), hipMemcpyDefault, st);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(sc, src->scales, size_t(out) * (in / 32), hipMemcpyDefault, st);
+        return status(e);
+    }
+    if (src->kind != GRIM_SRC_GPTQ && src->kind != GRIM_SRC_INT4_PACKED)
+        return fail(GRIM_ERR_FORMAT, "source kind %d", src->kind);
+    const int g = src->group;
+    if (g <= 0 || in % g || in % 8) return fail(GRIM_ERR_SHAPE, "group=%d in=%d", g, in);
+    if (dst->row_scales != in / g) return fail(GRIM_ERR_SHAPE, "dst row_scales != in/group");
+    if (!dst->zeros) return fail(GRIM_ERR_ARG, "dst zeros required");
+    if (out % 8 && (src->kind == GRIM_SRC_GPTQ || src->zeros))
+        return fail(GRIM_ERR_SHAPE, "out=%d not a multiple of 8", out);
+    uint16_t* sc = static_cast<uint16_t*>(const_cast<void*>(dst->scales)) +
+                   int64_t(row0) * dst->row_scales;
+    uint8_t* zr = const_cast<uint8_t*>(dst->zeros) + int64_t(row0) * dst->row_scales;
+    if (src->kind == GRIM_SRC_GPTQ) {
+        if (dst->fmt != GRIM_FMT_INT4 && dst->fmt != GRIM_FMT_INT4_F16)
+            return fail(GRIM_ERR_FORMAT, "GPTQ source needs INT4 or INT4_F16 dst");
+        if (!src->zeros) return fail(GRIM_ERR_ARG, "GPTQ qzeros required");
+        if ((reinterpret_cast<uintptr_t>(pay) | reinterpret_cast<uintptr_t>(src->weight) |
+             reinterpret_cast<uintptr_t>(src->zeros)) & 3)
+            return fail(GRIM_ERR_ARG, "qweight/qzeros/payload rows not 4-byte aligned");
+        IngestGptq a{static_cast<const uint32_t*>(src->weight),
+                     static_cast<const uint32_t*>(src->zeros),
+                     static_cast<const uint16_t*>(src->scales), in, out, g, pay, dst->row_bytes,
+                     sc, zr, dst->row_scales, dst->fmt == GRIM_FMT_INT4_F16 ? 1 : 0};
+        return status(ingest_gptq(st, a));
+    }
+    if (dst->fmt != GRIM_FMT_INT4) return fail(GRIM_ERR_FORMAT, "INT4 source needs INT4 dst");
+    if (src->zeros && (reinterpret_cast<uintptr_t>(src->zeros) & 3))
+        return fail(GRIM_ERR_ARG, "zero points not 4-byte aligned");
+    hipError_t e = hipMemcpyAsync(pay, src->weight, size_t(out) * (in / 2), hipMemcpyDefault, st);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(sc, src->scales, size_t(out) * (in / g) * 2, hipMemcpyDefault, st);
+    if (e == hipSuccess)
+        e = ingest_int4_zeros(st, static_cast<const uint32_t*>(src->zeros), out, in / g, zr,
+                              dst->row_scales);
+    return status(e);
+}
+
+int grimoire_moe_int4_to_signed(void* stream, uint8_t* gu_payload, size_t gu_bytes,
+                                uint8_t* gu_zeros, size_t gu_zero_bytes, uint8_t* dn_payload,
+                                size_t dn_bytes, uint8_t* dn_zeros, size_t dn_zero_bytes,
+                                int32_t* converted) {
+    if (!converted) return fail(GRIM_ERR_ARG, "null converted flag");
+    if ((gu_bytes && !gu_payload) || (gu_zero_bytes && !gu_zeros) || (dn_bytes && !dn_payload) ||
+        (dn_zero_bytes && !dn_zeros))
+        return fail(GRIM_ERR_ARG, "null region with a nonzero size");
+    SignedRegion r[2] = {{gu_payload, int64_t(gu_bytes), gu_zeros, int64_t(gu_zero_bytes)},
+                         {dn_payload, int64_t(dn_bytes), dn_zeros, int64_t(dn_zero_bytes)}};
+    return status(int4_signed(S(stream), r, 2, converted));
 }
 
 int grimoire_moe_quant_limbs(void* stream, const float* src, int rows, int n, int8_t* dst,

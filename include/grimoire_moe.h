@@ -283,6 +283,65 @@ int grimoire_rmsnorm_residual(void* stream, float* h, const float* r0, const flo
                               uint16_t* out_bf, int tokens, int hidden, float eps);
 
 /* ------------------------------------------------------------------------
+ * Expert-weight ingestion: one checkpoint projection [out][in] of one expert
+ * into rows [row0, row0 + out) of a stacked weight, the per-expert staging
+ * of src/grimoire.cpp:8340-8383 (gate at expert*2I, up at expert*2I + I in
+ * gate_up; down at expert*H).
+ *
+ *   GRIM_SRC_GPTQ           weight = qweight int32 [in/8][out] (8 nibbles
+ *                           along in), zeros = qzeros int32 [in/g][out/8]
+ *                           (8 nibbles along out), scales = fp16 [in/g][out]
+ *                           (include/b70/gptq.hpp:21-55).  dst INT4: the
+ *                           repack of gptq_repack_int4 (src/gptq.cpp:56-83),
+ *                           scales rounded to bf16, zeros = stored + 1.
+ *                           dst INT4_F16: the same with the fp16 scales kept.
+ *                           dst->zeros required.
+ *   GRIM_SRC_MXFP4_PACKED   compressed-tensors weight_packed u8 [out][in/2]
+ *                           and weight_scale e8m0 u8 [out][in/32], copied as
+ *                           stored (src/grimoire.cpp:8355-8367).  dst MXFP4.
+ *   GRIM_SRC_INT4_PACKED    compressed-tensors pack-quantized INT4: weight
+ *                           u8 [out][in/2] (offset binary, +8), scales bf16
+ *                           [out][in/g], zeros = weight_zero_point int32
+ *                           [out/8][in/g] (row n in nibble n % 8) or NULL for
+ *                           8 (read_compressed_int4_ref, src/grimoire.cpp:
+ *                           1396-1434).  dst INT4 with dst->zeros.
+ *
+ * GPTQ and INT4 zero-point sources are read by kernels: device memory or
+ * hipHostMalloc'd host memory.  Copied parts go through hipMemcpyAsync and
+ * may be any host or device memory.  dst->row_bytes must be in/2 and
+ * dst->row_scales in/g (in/32 for MXFP4).
+ * ---------------------------------------------------------------------- */
+enum grim_src_kind {
+    GRIM_SRC_GPTQ = 1,
+    GRIM_SRC_MXFP4_PACKED = 2,
+    GRIM_SRC_INT4_PACKED = 3
+};
+
+typedef struct grim_expert_src {
+    int32_t kind;              /* enum grim_src_kind                        */
+    int32_t in;                /* input features (K)                        */
+    int32_t out;               /* output features (N)                       */
+    int32_t group;             /* quantisation group along in (GPTQ, INT4)  */
+    const void* weight;
+    const void* zeros;
+    const void* scales;
+} grim_expert_src;
+
+int grimoire_moe_ingest_projection(void* stream, const grim_expert_src* src,
+                                   const grim_quant_weight* dst, int row0);
+
+/* Signed-s4 conversion of a layer's INT4 experts (src/grimoire.cpp:
+ * 8386-8397): when every zero point in gu_zeros and dn_zeros is 8, XOR
+ * every payload byte with 0x88 (offset binary -> two's complement) and set
+ * every zero point to 0xFF, the "signed s4" marker; otherwise change
+ * nothing.  *converted (device int32) receives 1 or 0.  Either region may
+ * be empty (NULL, 0). */
+int grimoire_moe_int4_to_signed(void* stream, uint8_t* gu_payload, size_t gu_bytes,
+                                uint8_t* gu_zeros, size_t gu_zero_bytes, uint8_t* dn_payload,
+                                size_t dn_bytes, uint8_t* dn_zeros, size_t dn_zero_bytes,
+                                int32_t* converted);
+
+/* ------------------------------------------------------------------------
  * Grouped GEMM on MFMA (prefill).  One launch per projection for all
  * experts.  A bf16 [R][K] rows grouped by expert (offsets/counts from the
  * dispatch), W the packed expert weight [E*N][K].

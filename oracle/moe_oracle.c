@@ -20,6 +20,11 @@
  *                       h + shared (all slots skipped), float64 RMSNorm
  *   orc_rmsnorm_residual  exact (h + r0) + r1, float64 RMSNorm, torch
  *                       rms_norm
+ *   orc_gptq_repack     reference gptq_repack_int4 via oracle/_ref, golden
+ *                       GPTQ probes through orc_qw_at, orc_gptq_at
+ *   orc_int4_zero_unpack  brute-force nibble extraction
+ *   orc_int4_to_signed  dequantised values unchanged (orc_qw_at before and
+ *                       after), untouched when one zero point is not 8
  *   orc_grouped_gemm    numpy matmul of the dequantised weights
  *   orc_expf            libm expf to within 2 ulp
  */
@@ -560,6 +565,53 @@ void orc_rmsnorm_residual(float* h, const float* r0, const float* r1, const uint
             if (out_bf) out_bf[(int64_t)t * hidden + d] = orc_f32_to_bf16(o);
         }
     }
+}
+
+/* gptq_repack_int4 (src/gptq.cpp:56-83): payload [out][in/2] (even k in the
+ * low nibble), zeros [out][in/g] = stored + 1, scales [out][in/g] rounded to
+ * bf16, or the fp16 bits kept when keep_f16. */
+void orc_gptq_repack(const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
+                     int in, int out, int group, int keep_f16, uint8_t* payload,
+                     uint16_t* scales_out, uint8_t* zeros_out) {
+    const int ng = in / group;
+    for (int o = 0; o < out; ++o) {
+        for (int g = 0; g < ng; ++g) {
+            const uint32_t zw = (uint32_t)qzeros[(int64_t)g * (out / 8) + o / 8];
+            zeros_out[(int64_t)o * ng + g] = (uint8_t)(((zw >> ((o & 7) * 4)) & 0xFu) + 1u);
+            const uint16_t s = scales[(int64_t)g * out + o];
+            scales_out[(int64_t)o * ng + g] = keep_f16 ? s : orc_f32_to_bf16(orc_f16_to_f32(s));
+        }
+        uint8_t* row = payload + (int64_t)o * (in / 2);
+        for (int k = 0; k < in; ++k) {
+            const uint32_t w = (uint32_t)qweight[(int64_t)(k / 8) * out + o];
+            const uint8_t q = (uint8_t)((w >> ((k & 7) * 4)) & 0xFu);
+            if (k & 1) row[k / 2] = (uint8_t)(row[k / 2] | (q << 4));
+            else row[k / 2] = q;
+        }
+    }
+}
+
+/* Compressed-tensors INT4 zero points (src/grimoire.cpp:1418-1434):
+ * [out/8][groups] int32, row n in nibble n % 8; NULL = 8 for every group. */
+void orc_int4_zero_unpack(const int32_t* zp, int out, int groups, uint8_t* zeros_out) {
+    for (int n = 0; n < out; ++n)
+        for (int g = 0; g < groups; ++g)
+            zeros_out[(int64_t)n * groups + g] =
+                zp ? (uint8_t)(((uint32_t)zp[(int64_t)(n / 8) * groups + g] >> (4 * (n % 8))) & 0xFu)
+                   : (uint8_t)8;
+}
+
+/* src/grimoire.cpp:8386-8397: all zero points 8 -> payload ^= 0x88,
+ * zeros = 0xFF.  Returns 1 when converted. */
+int orc_int4_to_signed(uint8_t* gu, int64_t gu_bytes, uint8_t* gz, int64_t gz_bytes, uint8_t* dn,
+                       int64_t dn_bytes, uint8_t* dz, int64_t dz_bytes) {
+    for (int64_t i = 0; i < gz_bytes; ++i) if (gz[i] != 8) return 0;
+    for (int64_t i = 0; i < dz_bytes; ++i) if (dz[i] != 8) return 0;
+    for (int64_t i = 0; i < gu_bytes; ++i) gu[i] ^= 0x88;
+    for (int64_t i = 0; i < dn_bytes; ++i) dn[i] ^= 0x88;
+    memset(gz, 0xFF, (size_t)gz_bytes);
+    memset(dz, 0xFF, (size_t)dz_bytes);
+    return 1;
 }
 
 /* src/gemm_fast.cpp:1603-1800 contract (EPI 0 / EPI 1) */

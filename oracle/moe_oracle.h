@@ -112,6 +112,16 @@ void orc_rmsnorm_residual(float* h, const float* r0, const float* r1, const uint
                           float weight_offset, float* out, uint16_t* out_bf, int tokens,
                           int hidden, float eps);
 
+/* gptq_repack_int4 (src/gptq.cpp:56-83); keep_f16 keeps the fp16 scale bits. */
+void orc_gptq_repack(const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
+                     int in, int out, int group, int keep_f16, uint8_t* payload,
+                     uint16_t* scales_out, uint8_t* zeros_out);
+/* compressed-tensors INT4 zero points (src/grimoire.cpp:1418-1434). */
+void orc_int4_zero_unpack(const int32_t* zp, int out, int groups, uint8_t* zeros_out);
+/* signed-s4 conversion (src/grimoire.cpp:8386-8397); 1 when converted. */
+int orc_int4_to_signed(uint8_t* gu, int64_t gu_bytes, uint8_t* gz, int64_t gz_bytes, uint8_t* dn,
+                       int64_t dn_bytes, uint8_t* dz, int64_t dz_bytes);
+
 /* Grouped GEMM (src/gemm_fast.cpp:1603-1800 contract): rows [off_e,
  * off_e+cnt_e) of A (fp32 values) times W_e^T; swiglu gives silu(g)*u over
  * N = 2I. out fp32 [R][N or I]. Double accumulation. */

@@ -73,6 +73,9 @@ def orc() -> C.CDLL:
             "orc_moe_forward": (None, [P, P, P, P, P, P, I32]),
             "orc_dispatch": (I32, [P, I32, I32, I32, I32, P, P, P, P, P, P, I32]),
             "orc_unpermute": (None, [P, P, P, P, I32, I32, I32]),
+            "orc_gptq_repack": (None, [P, P, P, I32, I32, I32, I32, P, P, P]),
+            "orc_int4_zero_unpack": (None, [P, I32, I32, P]),
+            "orc_int4_to_signed": (I32, [P, C.c_int64, P, C.c_int64, P, C.c_int64, P, C.c_int64]),
             "orc_rmsnorm_residual": (None, [P, P, P, P, F32, P, P, I32, I32, F32]),
             "orc_rmsnorm_moe_residual": (None, [P, P, P, P, P, P, F32, P, P, I32, I32, I32,
                                                 F32]),
@@ -96,6 +99,7 @@ def ref():
         sig = {
             "ref_qw_at": (F32, [P, I32, I32]),
             "ref_gptq_at": (F32, [P, P, P, I32, I32, I32, I32, I32]),
+            "ref_gptq_repack_int4": (I32, [P, P, P, I32, I32, I32, P, P, P]),
             "ref_route_ref": (None, [P, I32, I32, I32, P, P]),
             "ref_moe_forward": (None, [P, P, P, P, P, I32]),
         }
@@ -207,3 +211,29 @@ def rmsnorm_residual(h, r0, r1, weight, weight_offset, T, H, eps):
     orc().orc_rmsnorm_residual(_p(hn), _p(a), _p(b), _p(wt), float(weight_offset), _p(out),
                                _p(obf), T, H, float(eps))
     return hn, out, obf
+
+
+def gptq_repack(qweight, qzeros, scales, inn, out, group, keep_f16=False):
+    """numpy int32/int32/uint16 inputs -> (payload u8 [out][in/2], scales
+    int16 bits [out][in/g], zeros u8 [out][in/g])."""
+    ng = inn // group
+    pay = np.zeros((out, inn // 2), dtype=np.uint8)
+    sc = np.zeros((out, ng), dtype=np.uint16)
+    z = np.zeros((out, ng), dtype=np.uint8)
+    qw, qz, s = (np.ascontiguousarray(a) for a in (qweight, qzeros, scales))
+    orc().orc_gptq_repack(_p(qw), _p(qz), _p(s), inn, out, group, int(keep_f16), _p(pay), _p(sc),
+                          _p(z))
+    return pay, sc.view(np.int16), z
+
+
+def int4_zero_unpack(zp, out, groups):
+    z = np.zeros((out, groups), dtype=np.uint8)
+    zc = None if zp is None else np.ascontiguousarray(zp)
+    orc().orc_int4_zero_unpack(_p(zc), out, groups, _p(z))
+    return z
+
+
+def int4_to_signed(gu, gz, dn, dz):
+    """In place on numpy uint8 arrays; returns 1 when converted."""
+    return orc().orc_int4_to_signed(_p(gu), gu.size, _p(gz), gz.size, _p(dn), dn.size, _p(dz),
+                                    dz.size)

@@ -5,6 +5,8 @@
 //
 // TEST INFRASTRUCTURE ONLY: used to pin oracle/moe_oracle.c and as the
 // "reference" CPU baseline of bench.py.  Nothing here is product code.
+#include <cstring>
+
 #include "b70/moe.hpp"
 #include "b70/gptq.hpp"
 #include "../include/grimoire_moe.h"
@@ -36,6 +38,21 @@ float ref_gptq_at(const int32_t* qweight, const int32_t* qzeros, const uint16_t*
     t.qweight = qweight; t.qzeros = qzeros; t.scales = scales;
     t.in = in; t.out = out; t.group = group;
     return gptq_at(t, o, k);
+}
+
+// gptq_repack_int4 (src/gptq.cpp:56-83); returns 0 when it refused the tensor.
+int ref_gptq_repack_int4(const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
+                         int in, int out, int group, uint8_t* payload, uint16_t* scales_out,
+                         uint8_t* zeros_out) {
+    GptqTensor t;
+    t.qweight = qweight; t.qzeros = qzeros; t.scales = scales;
+    t.in = in; t.out = out; t.group = group;
+    PackedWeight p = gptq_repack_int4(t);
+    if (p.payload.empty()) return 0;
+    std::memcpy(payload, p.payload.data(), p.payload.size());
+    std::memcpy(scales_out, p.scales_raw.data(), p.scales_raw.size());
+    std::memcpy(zeros_out, p.zeros.data(), p.zeros.size());
+    return 1;
 }
 
 // route_ref (src/moe_ref.cpp:30-63)

@@ -209,3 +209,79 @@ def test_qw_at_matches_reference(fmt):
             b = r.ref_qw_at(O.byref(s), n, k)
             assert a == b or (math.isnan(a) and math.isnan(b)), (fmt, n, k, a, b)
             assert d[n, k].item() == a
+
+
+# ------------------------------------------------------ expert ingestion
+
+def test_gptq_repack_pinned():
+    """orc_gptq_repack (src/gptq.cpp:56-83) on the golden LCG tensor: byte for
+    byte the reference's own gptq_repack_int4 (when oracle/_ref is built); with
+    the fp16 scales kept, every golden probe and every sampled element equals
+    gptq_at through the INT4_F16 element decode; with bf16 scales, within the
+    bf16 rounding of the scale."""
+    g = json.loads((GOLD / "gptq_probes.json").read_text())
+    out, inn, group = g["out"], g["in"], g["group"]
+    qw, qz, sc = _lcg_tensors(out, inn, group, 12345)
+    pay, scb, z = O.gptq_repack(qw, qz, sc, inn, out, group)
+    r = O.ref()
+    if r is not None:
+        rp = np.zeros_like(pay); rs = np.zeros(scb.shape, np.uint16); rz = np.zeros_like(z)
+        assert r.ref_gptq_repack_int4(qw.ctypes.data, qz.ctypes.data, sc.ctypes.data, inn, out,
+                                      group, rp.ctypes.data, rs.ctypes.data, rz.ctypes.data) == 1
+        assert np.array_equal(pay, rp) and np.array_equal(scb.view(np.uint16), rs)
+        assert np.array_equal(z, rz)
+    pay16, sc16, z16 = O.gptq_repack(qw, qz, sc, inn, out, group, keep_f16=True)
+    assert np.array_equal(pay16, pay) and np.array_equal(z16, z)
+    w16 = Weight(_abi.FMT_INT4_F16, out, inn, torch.from_numpy(pay16), torch.from_numpy(sc16),
+                 torch.from_numpy(z16), inn // group)
+    wb = Weight(_abi.FMT_INT4, out, inn, torch.from_numpy(pay), torch.from_numpy(scb),
+                torch.from_numpy(z), inn // group)
+    s16, sb = w16.struct(), wb.struct()
+    for o, k, want in zip(g["o"], g["k"], g["w"]):
+        assert abs(orc().orc_qw_at(O.byref(s16), o, k) - want) <= 1e-6 * (1 + abs(want))
+    for o in range(0, out, 37):
+        for k in range(0, inn, 29):
+            ref_v = orc().orc_gptq_at(qw.ctypes.data, qz.ctypes.data, sc.ctypes.data, inn, out,
+                                      group, o, k)
+            assert orc().orc_qw_at(O.byref(s16), o, k) == ref_v
+            assert abs(orc().orc_qw_at(O.byref(sb), o, k) - ref_v) <= abs(ref_v) * 2.0 ** -8
+
+
+def test_int4_zero_unpack_brute_force():
+    rng = np.random.default_rng(4)
+    out, groups = 24, 5
+    zp = rng.integers(0, 2 ** 32, (out // 8, groups), dtype=np.uint64).astype(np.uint32)
+    got = O.int4_zero_unpack(zp.view(np.int32), out, groups)
+    for n in range(out):
+        for gi in range(groups):
+            assert got[n, gi] == (int(zp[n // 8, gi]) >> (4 * (n % 8))) & 0xF
+    assert (O.int4_zero_unpack(None, out, groups) == 8).all()
+
+
+def test_int4_to_signed_keeps_values():
+    """src/grimoire.cpp:8386-8397: with every zero point 8 the conversion must
+    not change a single dequantised element; one zero point off 8 and nothing
+    changes at all."""
+    rng = np.random.default_rng(5)
+    N, K, G = 16, 256, 128
+    gu = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    dn = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    sc = torch.from_numpy((rng.standard_normal((N, K // G)) * 0.02).astype(np.float32)).bfloat16()
+    gz = np.full((N, K // G), 8, np.uint8)
+    dz = np.full((N, K // G), 8, np.uint8)
+
+    def vals(p, z):
+        w = Weight(_abi.FMT_INT4, N, K, torch.from_numpy(p), sc.view(torch.int16),
+                   torch.from_numpy(z), K // G)
+        s = w.struct()
+        return [orc().orc_qw_at(O.byref(s), n, k) for n in range(N) for k in range(0, K, 3)]
+
+    before = vals(gu, gz), vals(dn, dz)
+    gu2, gz2, dn2, dz2 = gu.copy(), gz.copy(), dn.copy(), dz.copy()
+    assert O.int4_to_signed(gu2, gz2, dn2, dz2) == 1
+    assert (gz2 == 0xFF).all() and (dz2 == 0xFF).all() and np.array_equal(gu2, gu ^ 0x88)
+    assert (vals(gu2, gz2), vals(dn2, dz2)) == before
+    dz3 = dz.copy(); dz3[3, 1] = 7
+    gu3, gz3, dn3 = gu.copy(), gz.copy(), dn.copy()
+    assert O.int4_to_signed(gu3, gz3, dn3, dz3) == 0
+    assert np.array_equal(gu3, gu) and np.array_equal(gz3, gz) and np.array_equal(dn3, dn)
