@@ -17,7 +17,10 @@ The JSON line also carries:
   cpu_baseline  the reference's own CPU oracle (src/moe_ref.cpp, built into
                 oracle/_ref) on a bounded sample of the same layers;
   prefill       C4 (T=4096, E=512, top-10, int8, shared expert): layer time
-                and grouped-GEMM TFLOPS against the bf16 MFMA peak.
+                and grouped-GEMM TFLOPS against the bf16 MFMA peak;
+  edges         the fused combine + residual + RMSNorm and the residual
+                RMSNorm (C4 shapes) against 8 TB/s, and the GPTQ ingestion
+                of one C2 layer's experts.
 """
 from __future__ import annotations
 
@@ -225,6 +228,80 @@ def prefill_bench(dev, stream, reps=5):
     }
 
 
+def edges_bench(dev, stream, reps=20):
+    """The steps either side of the path, on C4 / C2 shapes: the fused
+    combine + residual + RMSNorm after it, the residual RMSNorm that feeds
+    the router, and the ingestion of one C2 layer's GPTQ experts."""
+    from grimoire_amd import ingest
+    cfg = configs.CONFIGS["c4"]
+    T, K, H = cfg.T, cfg.K, cfg.H
+    R = T * K
+    g = torch.Generator(device=dev).manual_seed(5)
+    routed = torch.randn(R, H, device=dev, generator=g).bfloat16().view(torch.int16)
+    inverse = torch.randperm(R, device=dev, generator=g).int()
+    rw = torch.rand(R, device=dev, generator=g)
+    h = torch.randn(T, H, device=dev, generator=g)
+    shared = torch.randn(T, H, device=dev, generator=g)
+    r1 = torch.randn(T, H, device=dev, generator=g)
+    w = torch.randn(H, device=dev, generator=g).bfloat16().view(torch.int16)
+    out = torch.empty(T, H, device=dev)
+    out_bf = torch.empty(T, H, dtype=torch.int16, device=dev)
+    res = {}
+    with torch.cuda.stream(stream):
+        def timed(fn):
+            fn()
+            torch.cuda.synchronize()
+            with Timer(stream) as t:
+                for _ in range(reps):
+                    fn()
+            return t.ms() / reps
+        ms = timed(lambda: ops.launch_rmsnorm_moe_residual_batched(
+            h, routed, inverse, rw, shared, w, out, out_bf, T, K, H, 1e-6, stream=stream))
+        nbytes = R * H * 2 + R * 8 + 4 * T * H * 4 + T * H * 2 + H * 2
+        res["combine_rmsnorm_residual"] = {
+            "shape": f"T={T} K={K} H={H}, bf16 routed rows, fp32 shared, fp32 + bf16 out",
+            "us": round(ms * 1e3, 1), "bytes": nbytes,
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        ms = timed(lambda: ops.launch_rmsnorm_residual_batched(
+            h, shared, r1, w, out, T, H, 1e-6, out_bf=out_bf, stream=stream))
+        nbytes = 5 * T * H * 4 + T * H * 2 + H * 2
+        res["rmsnorm_residual"] = {
+            "shape": f"T={T} H={H}, two fp32 residuals, fp32 + bf16 out",
+            "us": round(ms * 1e3, 1), "bytes": nbytes,
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        c2 = configs.CONFIGS["c2"]
+        E, H2, I, grp = c2.E, c2.H, c2.I, 128
+
+        def proj(out_f, in_f):
+            return ingest.gptq(
+                torch.randint(-2 ** 31, 2 ** 31 - 1, (in_f // 8, out_f), dtype=torch.int32,
+                              device=dev, generator=g),
+                torch.full((in_f // grp, out_f // 8), 0x77777777, dtype=torch.int32, device=dev),
+                (torch.rand(in_f // grp, out_f, device=dev, generator=g) * 0.02).half()
+                .view(torch.int16), grp)
+        experts = [(proj(I, H2), proj(I, H2), proj(H2, I)) for _ in range(E)]
+        gu, dn = ingest.ingest_experts(experts, dev, stream=stream)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with Timer(stream) as t:
+            for _ in range(3):
+                ingest.ingest_experts(experts, dev, stream=stream)
+        ms = t.ms() / 3
+        host_ms = (time.perf_counter() - t0) * 1e3 / 3
+        src_bytes = sum(p.weight.numel() * 4 + p.zeros.numel() * 4 + p.scales.numel() * 2
+                        for tr in experts for p in tr)
+        dst_bytes = gu.nbytes() + dn.nbytes()
+        res["ingest_gptq_layer"] = {
+            "shape": f"c2 layer: {E} experts x (gate, up [{I}x{H2}], down [{H2}x{I}]) GPTQ g{grp} "
+                     "-> INT4 bf16 scales, device-resident sources",
+            "ms": round(ms, 3), "host_ms": round(host_ms, 3), "bytes": src_bytes + dst_bytes,
+            "gbs": round((src_bytes + dst_bytes) / (ms * 1e-3) / 1e9, 1),
+            "note": "two batched calls (gate+up, down), 64 GPTQ projections per launch"}
+    return res
+
+
 def cpu_baseline(d, budget_s=15.0):
     """The reference's src/moe_ref.cpp (oracle/_ref) on the same layers."""
     try:
@@ -325,6 +402,9 @@ def main():
     if not a.no_prefill:
         log("prefill bench (C4)...")
         out["prefill"] = prefill_bench(dev, stream)
+    if not a.no_prefill:
+        log("edges (fused norms, ingestion)...")
+        out["edges"] = edges_bench(dev, stream)
     if not a.no_cpu:
         log("cpu baseline...")
         out["cpu_baseline"] = cpu_baseline(d)

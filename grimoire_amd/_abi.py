@@ -126,6 +126,7 @@ SIGNATURES = {
                                             F32]),
     "grimoire_rmsnorm_residual": (I32, [P, P, P, P, P, F32, P, P, I32, I32, F32]),
     "grimoire_moe_ingest_projection": (I32, [P, C.POINTER(ExpertSrc), QWP, I32]),
+    "grimoire_moe_ingest_projections": (I32, [P, C.POINTER(ExpertSrc), P, I32, QWP]),
     "grimoire_moe_int4_to_signed": (I32, [P, P, SZ, P, SZ, P, SZ, P, SZ, P]),
     "grimoire_moe_grouped_gemm": (I32, [P, QWP, I32, I32, P, I32, P, I32, P, P, I32, I32]),
     "grimoire_moe_quant_limbs": (I32, [P, P, I32, I32, P, P]),

@@ -485,64 +485,108 @@ int grimoire_rmsnorm_residual(void* stream, float* h, const float* r0, const flo
     return status(combine_norm_launch(S(stream), a));
 }
 
-int grimoire_moe_ingest_projection(void* stream, const grim_expert_src* src,
-                                   const grim_quant_weight* dst, int row0) {
-    if (!src || !dst) return fail(GRIM_ERR_ARG, "null src/dst");
-    if (!src->weight || !src->scales || !dst->payload || !dst->scales)
-        return fail(GRIM_ERR_ARG, "null tensor pointer");
-    const int in = src->in, out = src->out;
+static int ingest_common(void* stream, const grim_expert_src* srcs, const int32_t* row0s, int n,
+                         const grim_quant_weight* dst) {
+    if (n <= 0) return GRIM_OK;
+    if (!srcs || !row0s || !dst) return fail(GRIM_ERR_ARG, "null srcs/row0/dst");
+    if (!dst->payload || !dst->scales) return fail(GRIM_ERR_ARG, "null dst tensor");
+    const grim_expert_src& s0 = srcs[0];
+    const int in = s0.in, out = s0.out, g = s0.group;
     if (in <= 0 || out <= 0 || in % 32) return fail(GRIM_ERR_SHAPE, "in=%d out=%d", in, out);
     if (dst->K != in) return fail(GRIM_ERR_SHAPE, "dst K=%d, source in=%d", dst->K, in);
-    if (row0 < 0 || int64_t(row0) + out > dst->N)
-        return fail(GRIM_ERR_SHAPE, "rows [%d, %d) outside dst N=%d", row0, row0 + out, dst->N);
     if (dst->row_bytes != in / 2)
         return fail(GRIM_ERR_SHAPE, "dst row_bytes=%lld, need %d", (long long)dst->row_bytes, in / 2);
+    for (int i = 0; i < n; ++i) {
+        const grim_expert_src& s = srcs[i];
+        if (s.kind != s0.kind || s.in != in || s.out != out || s.group != g)
+            return fail(GRIM_ERR_SHAPE, "projection %d: kind or shape differs from projection 0", i);
+        if (!s.weight || !s.scales) return fail(GRIM_ERR_ARG, "projection %d: null tensor", i);
+        if (row0s[i] < 0 || int64_t(row0s[i]) + out > dst->N)
+            return fail(GRIM_ERR_SHAPE, "projection %d: rows [%d, %d) outside dst N=%d", i,
+                        row0s[i], row0s[i] + out, dst->N);
+    }
     hipStream_t st = S(stream);
-    uint8_t* pay = const_cast<uint8_t*>(dst->payload) + int64_t(row0) * dst->row_bytes;
-    if (src->kind == GRIM_SRC_MXFP4_PACKED) {
+    uint8_t* pay0 = const_cast<uint8_t*>(dst->payload);
+    if (s0.kind == GRIM_SRC_MXFP4_PACKED) {
         if (dst->fmt != GRIM_FMT_MXFP4) return fail(GRIM_ERR_FORMAT, "MXFP4 source needs MXFP4 dst");
         if (dst->row_scales != in / 32) return fail(GRIM_ERR_SHAPE, "dst row_scales != in/32");
-        uint8_t* sc = static_cast<uint8_t*>(const_cast<void*>(dst->scales)) +
-                      int64_t(row0) * dst->row_scales;
-        hipError_t e = hipMemcpyAsync(pay, src->weight, size_t(out) * (in / 2), hipMemcpyDefault, st);
-        if (e == hipSuccess)
-            e = hipMemcpyAsync(sc, src->scales, size_t(out) * (in / 32), hipMemcpyDefault, st);
-        return status(e);
+        uint8_t* sc0 = static_cast<uint8_t*>(const_cast<void*>(dst->scales));
+        for (int i = 0; i < n; ++i) {
+            hipError_t e = hipMemcpyAsync(pay0 + int64_t(row0s[i]) * dst->row_bytes, srcs[i].weight,
+                                          size_t(out) * (in / 2), hipMemcpyDefault, st);
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(sc0 + int64_t(row0s[i]) * dst->row_scales, srcs[i].scales,
+                                   size_t(out) * (in / 32), hipMemcpyDefault, st);
+            if (e != hipSuccess) return status(e);
+        }
+        return GRIM_OK;
     }
-    if (src->kind != GRIM_SRC_GPTQ && src->kind != GRIM_SRC_INT4_PACKED)
-        return fail(GRIM_ERR_FORMAT, "source kind %d", src->kind);
-    const int g = src->group;
+    if (s0.kind != GRIM_SRC_GPTQ && s0.kind != GRIM_SRC_INT4_PACKED)
+        return fail(GRIM_ERR_FORMAT, "source kind %d", s0.kind);
     if (g <= 0 || in % g || in % 8) return fail(GRIM_ERR_SHAPE, "group=%d in=%d", g, in);
     if (dst->row_scales != in / g) return fail(GRIM_ERR_SHAPE, "dst row_scales != in/group");
     if (!dst->zeros) return fail(GRIM_ERR_ARG, "dst zeros required");
-    if (out % 8 && (src->kind == GRIM_SRC_GPTQ || src->zeros))
-        return fail(GRIM_ERR_SHAPE, "out=%d not a multiple of 8", out);
-    uint16_t* sc = static_cast<uint16_t*>(const_cast<void*>(dst->scales)) +
-                   int64_t(row0) * dst->row_scales;
-    uint8_t* zr = const_cast<uint8_t*>(dst->zeros) + int64_t(row0) * dst->row_scales;
-    if (src->kind == GRIM_SRC_GPTQ) {
+    uint16_t* sc0 = static_cast<uint16_t*>(const_cast<void*>(dst->scales));
+    uint8_t* zr0 = const_cast<uint8_t*>(dst->zeros);
+    if (s0.kind == GRIM_SRC_GPTQ) {
         if (dst->fmt != GRIM_FMT_INT4 && dst->fmt != GRIM_FMT_INT4_F16)
             return fail(GRIM_ERR_FORMAT, "GPTQ source needs INT4 or INT4_F16 dst");
-        if (!src->zeros) return fail(GRIM_ERR_ARG, "GPTQ qzeros required");
-        if ((reinterpret_cast<uintptr_t>(pay) | reinterpret_cast<uintptr_t>(src->weight) |
-             reinterpret_cast<uintptr_t>(src->zeros)) & 3)
-            return fail(GRIM_ERR_ARG, "qweight/qzeros/payload rows not 4-byte aligned");
-        IngestGptq a{static_cast<const uint32_t*>(src->weight),
-                     static_cast<const uint32_t*>(src->zeros),
-                     static_cast<const uint16_t*>(src->scales), in, out, g, pay, dst->row_bytes,
-                     sc, zr, dst->row_scales, dst->fmt == GRIM_FMT_INT4_F16 ? 1 : 0};
-        return status(ingest_gptq(st, a));
+        if (out % 8) return fail(GRIM_ERR_SHAPE, "out=%d not a multiple of 8", out);
+        if (reinterpret_cast<uintptr_t>(pay0) & 3) return fail(GRIM_ERR_ARG, "payload not 4-byte aligned");
+        for (int i = 0; i < n; ++i) {
+            if (!srcs[i].zeros) return fail(GRIM_ERR_ARG, "projection %d: GPTQ qzeros required", i);
+            if ((reinterpret_cast<uintptr_t>(srcs[i].weight) |
+                 reinterpret_cast<uintptr_t>(srcs[i].zeros)) & 3)
+                return fail(GRIM_ERR_ARG, "projection %d: qweight/qzeros not 4-byte aligned", i);
+        }
+        for (int b = 0; b < n; b += kIngBatch) {
+            IngestGptq a{};
+            a.n = n - b < kIngBatch ? n - b : kIngBatch;
+            for (int i = 0; i < a.n; ++i) {
+                a.qweight[i] = static_cast<const uint32_t*>(srcs[b + i].weight);
+                a.qzeros[i] = static_cast<const uint32_t*>(srcs[b + i].zeros);
+                a.scales[i] = static_cast<const uint16_t*>(srcs[b + i].scales);
+                a.row0[i] = row0s[b + i];
+            }
+            a.in = in; a.out = out; a.group = g;
+            a.dst_payload = pay0; a.dst_row_bytes = dst->row_bytes;
+            a.dst_scales = sc0; a.dst_zeros = zr0; a.dst_rs = dst->row_scales;
+            a.keep_f16 = dst->fmt == GRIM_FMT_INT4_F16 ? 1 : 0;
+            const hipError_t e = ingest_gptq(st, a);
+            if (e != hipSuccess) return status(e);
+        }
+        return GRIM_OK;
     }
     if (dst->fmt != GRIM_FMT_INT4) return fail(GRIM_ERR_FORMAT, "INT4 source needs INT4 dst");
-    if (src->zeros && (reinterpret_cast<uintptr_t>(src->zeros) & 3))
-        return fail(GRIM_ERR_ARG, "zero points not 4-byte aligned");
-    hipError_t e = hipMemcpyAsync(pay, src->weight, size_t(out) * (in / 2), hipMemcpyDefault, st);
-    if (e == hipSuccess)
-        e = hipMemcpyAsync(sc, src->scales, size_t(out) * (in / g) * 2, hipMemcpyDefault, st);
-    if (e == hipSuccess)
-        e = ingest_int4_zeros(st, static_cast<const uint32_t*>(src->zeros), out, in / g, zr,
-                              dst->row_scales);
-    return status(e);
+    if (out % 8) return fail(GRIM_ERR_SHAPE, "out=%d not a multiple of 8", out);
+    for (int i = 0; i < n; ++i) {
+        const grim_expert_src& s = srcs[i];
+        if (s.zeros && (reinterpret_cast<uintptr_t>(s.zeros) & 3))
+            return fail(GRIM_ERR_ARG, "projection %d: zero points not 4-byte aligned", i);
+        const int64_t r0 = row0s[i];
+        hipError_t e = hipMemcpyAsync(pay0 + r0 * dst->row_bytes, s.weight, size_t(out) * (in / 2),
+                                      hipMemcpyDefault, st);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(sc0 + r0 * dst->row_scales, s.scales, size_t(out) * (in / g) * 2,
+                               hipMemcpyDefault, st);
+        if (e == hipSuccess)
+            e = ingest_int4_zeros(st, static_cast<const uint32_t*>(s.zeros), out, in / g,
+                                  zr0 + r0 * dst->row_scales, dst->row_scales);
+        if (e != hipSuccess) return status(e);
+    }
+    return GRIM_OK;
+}
+
+int grimoire_moe_ingest_projection(void* stream, const grim_expert_src* src,
+                                   const grim_quant_weight* dst, int row0) {
+    if (!src) return fail(GRIM_ERR_ARG, "null src");
+    const int32_t r = row0;
+    return ingest_common(stream, src, &r, 1, dst);
+}
+
+int grimoire_moe_ingest_projections(void* stream, const grim_expert_src* srcs,
+                                    const int32_t* row0, int n, const grim_quant_weight* dst) {
+    return ingest_common(stream, srcs, row0, n, dst);
 }
 
 int grimoire_moe_int4_to_signed(void* stream, uint8_t* gu_payload, size_t gu_bytes,

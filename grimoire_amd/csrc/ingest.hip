@@ -29,19 +29,27 @@ namespace grim {
 constexpr int kTile = 64;        // words per tile side
 constexpr int kIngThreads = 256;
 
-// out32[(o) * out_stride + r] = in32[r * C + o] for r < R, o < C.
-__global__ __launch_bounds__(kIngThreads) void transpose_u32(const uint32_t* __restrict__ in,
-                                                             int R, int C,
-                                                             uint32_t* __restrict__ out,
-                                                             int64_t out_stride) {
+// Projection z of the batch: out32[o * out_stride + r] = in32[r * C + o]
+// for r < R, o < C, out32 = the payload rows from row0[z].
+__global__ __launch_bounds__(kIngThreads) void transpose_u32(const IngestGptq a) {
     __shared__ uint32_t tile[kTile][kTile + 1];
+    const int z = blockIdx.z;
+    const int R = a.in / 8, C = a.out;
+    const uint32_t* __restrict__ in = a.qweight[z];
+    uint32_t* __restrict__ out =
+        reinterpret_cast<uint32_t*>(a.dst_payload + int64_t(a.row0[z]) * a.dst_row_bytes);
+    const int64_t out_stride = a.dst_row_bytes / 4;
     const int c0 = blockIdx.x * kTile, r0 = blockIdx.y * kTile;
     const int tx = threadIdx.x & (kTile - 1), ty = threadIdx.x / kTile;   // ty in 0..3
+    constexpr int kRows = kTile / (kIngThreads / kTile);   // 16 loads per thread, all in flight
+    uint32_t v[kRows];
 #pragma unroll
-    for (int i = 0; i < kTile; i += kIngThreads / kTile) {
-        const int r = r0 + ty + i, c = c0 + tx;
-        if (r < R && c < C) tile[ty + i][tx] = in[int64_t(r) * C + c];
+    for (int j = 0; j < kRows; ++j) {
+        const int r = r0 + ty + j * (kIngThreads / kTile), c = c0 + tx;
+        v[j] = (r < R && c < C) ? in[int64_t(r) * C + c] : 0u;
     }
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) tile[ty + j * (kIngThreads / kTile)][tx] = v[j];
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kTile; i += kIngThreads / kTile) {
@@ -50,22 +58,20 @@ __global__ __launch_bounds__(kIngThreads) void transpose_u32(const uint32_t* __r
     }
 }
 
-// One thread per (group g, output o), o fastest: reads of the checkpoint
-// rows are coalesced; the [out][groups] writes are short rows.
-__global__ __launch_bounds__(kIngThreads) void gptq_meta(const uint16_t* __restrict__ scales,
-                                                         const uint32_t* __restrict__ qzeros,
-                                                         int out, int groups, int keep_f16,
-                                                         uint16_t* __restrict__ dst_scales,
-                                                         uint8_t* __restrict__ dst_zeros,
-                                                         int dst_rs) {
+// One thread per (group g, output o) of projection blockIdx.y, o fastest:
+// reads of the checkpoint rows are coalesced; the [out][groups] writes are
+// short rows.
+__global__ __launch_bounds__(kIngThreads) void gptq_meta(const IngestGptq a) {
+    const int z = blockIdx.y;
+    const int out = a.out, groups = a.in / a.group;
     const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= int64_t(out) * groups) return;
     const int g = int(i / out), o = int(i % out);
-    const uint16_t s = scales[int64_t(g) * out + o];
-    const uint32_t zw = qzeros[int64_t(g) * (out >> 3) + (o >> 3)];
-    const int64_t d = int64_t(o) * dst_rs + g;
-    dst_scales[d] = keep_f16 ? s : f32_to_bf16(f16_to_f32(s));
-    dst_zeros[d] = uint8_t(((zw >> ((o & 7) * 4)) & 0xFu) + 1u);
+    const uint16_t s = a.scales[z][int64_t(g) * out + o];
+    const uint32_t zw = a.qzeros[z][int64_t(g) * (out >> 3) + (o >> 3)];
+    const int64_t d = int64_t(a.row0[z] + o) * a.dst_rs + g;
+    a.dst_scales[d] = a.keep_f16 ? s : f32_to_bf16(f16_to_f32(s));
+    a.dst_zeros[d] = uint8_t(((zw >> ((o & 7) * 4)) & 0xFu) + 1u);
 }
 
 // compressed-tensors INT4 zero points, or the symmetric 8 when zp == NULL.
@@ -134,14 +140,13 @@ static unsigned stream_blocks(int64_t bytes) {
 }
 
 hipError_t ingest_gptq(hipStream_t st, const IngestGptq& a) {
+    if (a.n <= 0 || a.n > kIngBatch) return hipErrorInvalidValue;
     const int words_r = a.in / 8;   // qweight rows
-    dim3 g1((a.out + kTile - 1) / kTile, (words_r + kTile - 1) / kTile);
-    hipLaunchKernelGGL(transpose_u32, g1, dim3(kIngThreads), 0, st, a.qweight, words_r, a.out,
-                       reinterpret_cast<uint32_t*>(a.dst_payload), a.dst_row_bytes / 4);
-    const int groups = a.in / a.group;
-    hipLaunchKernelGGL(gptq_meta, grid_for(int64_t(a.out) * groups, kIngThreads),
-                       dim3(kIngThreads), 0, st, a.scales, a.qzeros, a.out, groups, a.keep_f16,
-                       a.dst_scales, a.dst_zeros, a.dst_rs);
+    dim3 g1((a.out + kTile - 1) / kTile, (words_r + kTile - 1) / kTile, a.n);
+    hipLaunchKernelGGL(transpose_u32, g1, dim3(kIngThreads), 0, st, a);
+    const int64_t items = int64_t(a.out) * (a.in / a.group);
+    dim3 g2(unsigned((items + kIngThreads - 1) / kIngThreads), a.n);
+    hipLaunchKernelGGL(gptq_meta, g2, dim3(kIngThreads), 0, st, a);
     return hipGetLastError();
 }
 

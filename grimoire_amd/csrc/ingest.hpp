@@ -6,18 +6,21 @@
 
 namespace grim {
 
-// GPTQ triple of one projection into rows [row0, row0 + out) of a stacked
-// INT4 / INT4_F16 weight (src/gptq.cpp:56-83).  All pointers device-visible;
-// dst_* already offset to row0.
+// GPTQ triples of up to kIngBatch projections of one shape into rows
+// [row0[i], row0[i] + out) of one stacked INT4 / INT4_F16 weight
+// (src/gptq.cpp:56-83).  The table travels in the kernel arguments.
+constexpr int kIngBatch = 64;
+
 struct IngestGptq {
-    const uint32_t* qweight;  // [in/8][out]
-    const uint32_t* qzeros;   // [in/group][out/8]
-    const uint16_t* scales;   // fp16 [in/group][out]
-    int in, out, group;
-    uint8_t* dst_payload;     // [out][dst_row_bytes]
+    const uint32_t* qweight[kIngBatch];  // [in/8][out]
+    const uint32_t* qzeros[kIngBatch];   // [in/group][out/8]
+    const uint16_t* scales[kIngBatch];   // fp16 [in/group][out]
+    int32_t row0[kIngBatch];
+    int n, in, out, group;
+    uint8_t* dst_payload;     // [N][dst_row_bytes]
     int64_t dst_row_bytes;    // in / 2
-    uint16_t* dst_scales;     // [out][dst_rs]
-    uint8_t* dst_zeros;       // [out][dst_rs]
+    uint16_t* dst_scales;     // [N][dst_rs]
+    uint8_t* dst_zeros;       // [N][dst_rs]
     int dst_rs;               // in / group
     int keep_f16;             // 1: fp16 bits kept (INT4_F16); 0: bf16 (INT4)
 };

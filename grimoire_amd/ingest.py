@@ -93,6 +93,18 @@ def ingest_projection(src: Projection, dst: Weight, row0: int, stream=None) -> N
           "ingest_projection")
 
 
+def ingest_projections(srcs: Sequence[Projection], dst: Weight, row0: Sequence[int],
+                       stream=None) -> None:
+    """Projections of one kind and shape into one stacked weight, batched
+    (GPTQ: 64 per launch)."""
+    n = len(srcs)
+    arr = (_abi.ExpertSrc * n)(*[p.struct() for p in srcs])
+    rows = (C.c_int32 * n)(*row0)
+    d = dst.struct()
+    check(lib().grimoire_moe_ingest_projections(_stream(stream), arr, C.cast(rows, C.c_void_p), n,
+                                                C.byref(d)), "ingest_projections")
+
+
 def target_format(kind: int, exact_scales: bool = False) -> int:
     """The reference's target for each source: GPTQ -> INT4 with bf16 scales
     (src/gptq.cpp:65-66), or INT4_F16 keeping the fp16 scales exactly."""
@@ -113,14 +125,18 @@ def ingest_experts(experts: Sequence[Tuple[Projection, Projection, Projection]],
     fmt = target_format(g0.kind, exact_scales)
     gate_up = stacked(fmt, E * 2 * I, H, g0.group, device)
     down = stacked(fmt, E * H, I, d0.group, device)
+    gu_src, gu_rows, dn_src, dn_rows = [], [], [], []
     for e, (g, u, d) in enumerate(experts):
         if {g.kind, u.kind, d.kind} != {g0.kind}:
             raise ValueError("expert source kinds differ within the layer")
         if (g.out, g.in_, u.out, u.in_, d.out, d.in_) != (I, H, I, H, H, I):
             raise ValueError(f"expert {e}: projection shapes differ within the layer")
-        ingest_projection(g, gate_up, e * 2 * I, stream)
-        ingest_projection(u, gate_up, e * 2 * I + I, stream)
-        ingest_projection(d, down, e * H, stream)
+        gu_src += [g, u]
+        gu_rows += [e * 2 * I, e * 2 * I + I]
+        dn_src.append(d)
+        dn_rows.append(e * H)
+    ingest_projections(gu_src, gate_up, gu_rows, stream)
+    ingest_projections(dn_src, down, dn_rows, stream)
     return gate_up, down
 
 

@@ -329,6 +329,11 @@ typedef struct grim_expert_src {
 
 int grimoire_moe_ingest_projection(void* stream, const grim_expert_src* src,
                                    const grim_quant_weight* dst, int row0);
+/* n projections of one kind and shape (host arrays src[n], row0[n]) into
+ * the same stacked weight, e.g. every expert's gate and up of a layer:
+ * GPTQ sources go 64 per launch.  Same conversions and rules as above. */
+int grimoire_moe_ingest_projections(void* stream, const grim_expert_src* srcs,
+                                    const int32_t* row0, int n, const grim_quant_weight* dst);
 
 /* Signed-s4 conversion of a layer's INT4 experts (src/grimoire.cpp:
  * 8386-8397): when every zero point in gu_zeros and dn_zeros is 8, XOR
