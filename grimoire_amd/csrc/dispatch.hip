@@ -223,6 +223,18 @@ hipError_t dispatch_launch(hipStream_t st, const DispatchArgs& a) {
 // slot tables stay in registers and all KT row loads are issued before the
 // first use.  A skipped slot (p < 0, or s >= K) reads row 0 and is masked
 // after the load, not branched around.
+template <bool SRC_BF16>
+__device__ __forceinline__ float4 combine_load(const void* src, int64_t row, int H, int d) {
+    if constexpr (SRC_BF16) {
+        const uint2 u =
+            *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(src) + row * H + d);
+        return make_float4(bits_f(u.x << 16), bits_f(u.x & 0xFFFF0000u), bits_f(u.y << 16),
+                           bits_f(u.y & 0xFFFF0000u));
+    } else {
+        return *reinterpret_cast<const float4*>(static_cast<const float*>(src) + row * H + d);
+    }
+}
+
 template <bool SRC_BF16, int KT>
 __global__ __launch_bounds__(kDispThreads) void combine_kernel(
     const void* __restrict__ src, const int32_t* __restrict__ inverse,
@@ -238,46 +250,44 @@ __global__ __launch_bounds__(kDispThreads) void combine_kernel(
         w[s] = rw[int64_t(t) * K + sc];
     }
     const float g = gate ? gate[t] : 1.0f;
-    for (int d = threadIdx.x * 4; d < H; d += blockDim.x * 4) {
-        float v0 = 0.0f, v1 = 0.0f, v2 = 0.0f, v3 = 0.0f;
+    const int step = blockDim.x * 4;
+    // two column blocks per pass: 2*KT row loads in flight per lane (the
+    // second block is clamped to the first when it falls past H)
+    for (int d0 = threadIdx.x * 4; d0 < H; d0 += 2 * step) {
+        const bool two = d0 + step < H;
+        const int d1 = two ? d0 + step : d0;
+        float4 a0[KT], a1[KT];
 #pragma unroll
         for (int s = 0; s < KT; ++s) {
             const int64_t row = p[s] < 0 ? 0 : p[s];
-            float a0, a1, a2, a3;
-            if constexpr (SRC_BF16) {
-                const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(src) +
-                                                                row * H + d);
-                a0 = bits_f(u.x << 16); a1 = bits_f(u.x & 0xFFFF0000u);
-                a2 = bits_f(u.y << 16); a3 = bits_f(u.y & 0xFFFF0000u);
-            } else {
-                const float4 f = *reinterpret_cast<const float4*>(static_cast<const float*>(src) +
-                                                                  row * H + d);
-                a0 = f.x; a1 = f.y; a2 = f.z; a3 = f.w;
-            }
+            a0[s] = combine_load<SRC_BF16>(src, row, H, d0);
+            a1[s] = combine_load<SRC_BF16>(src, row, H, d1);
+        }
+        float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+#pragma unroll
+        for (int s = 0; s < KT; ++s) {
             const bool on = p[s] >= 0;
-            v0 = on ? __builtin_fmaf(w[s], a0, v0) : v0;
-            v1 = on ? __builtin_fmaf(w[s], a1, v1) : v1;
-            v2 = on ? __builtin_fmaf(w[s], a2, v2) : v2;
-            v3 = on ? __builtin_fmaf(w[s], a3, v3) : v3;
+            v0.x = on ? __builtin_fmaf(w[s], a0[s].x, v0.x) : v0.x;
+            v0.y = on ? __builtin_fmaf(w[s], a0[s].y, v0.y) : v0.y;
+            v0.z = on ? __builtin_fmaf(w[s], a0[s].z, v0.z) : v0.z;
+            v0.w = on ? __builtin_fmaf(w[s], a0[s].w, v0.w) : v0.w;
+            v1.x = on ? __builtin_fmaf(w[s], a1[s].x, v1.x) : v1.x;
+            v1.y = on ? __builtin_fmaf(w[s], a1[s].y, v1.y) : v1.y;
+            v1.z = on ? __builtin_fmaf(w[s], a1[s].z, v1.z) : v1.z;
+            v1.w = on ? __builtin_fmaf(w[s], a1[s].w, v1.w) : v1.w;
         }
         if (shared_src) {
-            float a0, a1, a2, a3;
-            if (shared_bf16) {
-                const uint2 u = *reinterpret_cast<const uint2*>(
-                    static_cast<const uint16_t*>(shared_src) + int64_t(t) * H + d);
-                a0 = bits_f(u.x << 16); a1 = bits_f(u.x & 0xFFFF0000u);
-                a2 = bits_f(u.y << 16); a3 = bits_f(u.y & 0xFFFF0000u);
-            } else {
-                const float4 f = *reinterpret_cast<const float4*>(
-                    static_cast<const float*>(shared_src) + int64_t(t) * H + d);
-                a0 = f.x; a1 = f.y; a2 = f.z; a3 = f.w;
-            }
-            v0 = __builtin_fmaf(g, a0, v0);
-            v1 = __builtin_fmaf(g, a1, v1);
-            v2 = __builtin_fmaf(g, a2, v2);
-            v3 = __builtin_fmaf(g, a3, v3);
+            const float4 b0 = shared_bf16 ? combine_load<true>(shared_src, t, H, d0)
+                                          : combine_load<false>(shared_src, t, H, d0);
+            const float4 b1 = shared_bf16 ? combine_load<true>(shared_src, t, H, d1)
+                                          : combine_load<false>(shared_src, t, H, d1);
+            v0.x = __builtin_fmaf(g, b0.x, v0.x); v0.y = __builtin_fmaf(g, b0.y, v0.y);
+            v0.z = __builtin_fmaf(g, b0.z, v0.z); v0.w = __builtin_fmaf(g, b0.w, v0.w);
+            v1.x = __builtin_fmaf(g, b1.x, v1.x); v1.y = __builtin_fmaf(g, b1.y, v1.y);
+            v1.z = __builtin_fmaf(g, b1.z, v1.z); v1.w = __builtin_fmaf(g, b1.w, v1.w);
         }
-        *reinterpret_cast<float4*>(dst + int64_t(t) * H + d) = make_float4(v0, v1, v2, v3);
+        *reinterpret_cast<float4*>(dst + int64_t(t) * H + d0) = v0;
+        if (two) *reinterpret_cast<float4*>(dst + int64_t(t) * H + d1) = v1;
     }
 }
 
