@@ -91,6 +91,30 @@ class ExpertSrc(C.Structure):
 
 SRC_GPTQ, SRC_MXFP4_PACKED, SRC_INT4_PACKED = 1, 2, 3
 
+
+class NvExpertLayout(C.Structure):
+    """grim_nv_expert_layout (b70::NvExpertLayout, include/b70/tiered_moe.hpp:40-60)."""
+    _fields_ = [("H", C.c_int32), ("I", C.c_int32), ("gu_p", C.c_int64), ("gu_s", C.c_int64),
+                ("dn_p", C.c_int64), ("dn_s", C.c_int64), ("gsc", C.c_int64),
+                ("bytes", C.c_int64)]
+
+
+class TieredMoeView(C.Structure):
+    """grim_tiered_moe_view (b70::TieredMoeView)."""
+    _fields_ = [("lay", NvExpertLayout), ("eptr", C.c_void_p), ("E", C.c_int32),
+                ("top_k", C.c_int32)]
+
+
+class HeatParams(C.Structure):
+    """grim_heat_params (b70::ExpertHeatParams, include/b70/expert_heat.hpp)."""
+    _fields_ = [("decay", C.c_float), ("hysteresis", C.c_float), ("min_gain", C.c_float),
+                ("credit_cap", C.c_float), ("moves_per_step", C.c_int32)]
+
+
+class ExpertSwap(C.Structure):
+    _fields_ = [("promote_layer", C.c_int32), ("promote_expert", C.c_int32),
+                ("demote_layer", C.c_int32), ("demote_expert", C.c_int32)]
+
 P = C.c_void_p
 I32 = C.c_int
 F32 = C.c_float
@@ -128,6 +152,16 @@ SIGNATURES = {
     "grimoire_moe_ingest_projection": (I32, [P, C.POINTER(ExpertSrc), QWP, I32]),
     "grimoire_moe_ingest_projections": (I32, [P, C.POINTER(ExpertSrc), P, I32, QWP]),
     "grimoire_moe_int4_to_signed": (I32, [P, P, SZ, P, SZ, P, SZ, P, SZ, P]),
+    "grimoire_tmoe_layout": (I32, [I32, I32, C.POINTER(NvExpertLayout)]),
+    "grimoire_tmoe_gate_up": (I32, [P, C.POINTER(TieredMoeView), P, P, P, I32]),
+    "grimoire_tmoe_down": (I32, [P, C.POINTER(TieredMoeView), P, P, P, P, I32]),
+    "grimoire_tmoe_place": (I32, [P, P, I32, P, P, SZ]),
+    "grimoire_heat_default_params": (None, [C.POINTER(HeatParams)]),
+    "grimoire_heat_create": (P, [I32, I32, C.POINTER(HeatParams)]),
+    "grimoire_heat_destroy": (None, [P]),
+    "grimoire_heat_credit": (None, [P, I32, P, SZ]),
+    "grimoire_heat_get": (F32, [P, I32, I32]),
+    "grimoire_heat_propose": (I32, [P, P, P, C.POINTER(ExpertSwap), I32]),
     "grimoire_moe_grouped_gemm": (I32, [P, QWP, I32, I32, P, I32, P, I32, P, P, I32, I32]),
     "grimoire_moe_quant_limbs": (I32, [P, P, I32, I32, P, P]),
     "grimoire_moe_grouped_gemm_i8": (I32, [P, QWP, I32, I32, P, P, P, P, P, I32, I32]),

@@ -19,6 +19,7 @@
 #include "gemm_i8.hpp"
 #include "gemv.hpp"
 #include "ingest.hpp"
+#include "tiered.hpp"
 #include "router.hpp"
 
 using namespace grim;
@@ -600,6 +601,70 @@ int grimoire_moe_int4_to_signed(void* stream, uint8_t* gu_payload, size_t gu_byt
     SignedRegion r[2] = {{gu_payload, int64_t(gu_bytes), gu_zeros, int64_t(gu_zero_bytes)},
                          {dn_payload, int64_t(dn_bytes), dn_zeros, int64_t(dn_zero_bytes)}};
     return status(int4_signed(S(stream), r, 2, converted));
+}
+
+int grimoire_tmoe_layout(int H, int I, grim_nv_expert_layout* out) {
+    if (!out) return fail(GRIM_ERR_ARG, "null layout");
+    if (H <= 0 || I <= 0 || H % 128 || I % 128)
+        return fail(GRIM_ERR_SHAPE, "H=%d I=%d (need multiples of 128)", H, I);
+    int64_t o = 0;
+    out->H = H; out->I = I;
+    out->gu_p = o; o += int64_t(2) * I * (H / 2);
+    out->gu_s = o; o += int64_t(2) * I * (H / 16);
+    out->dn_p = o; o += int64_t(H) * (I / 2);
+    out->dn_s = o; o += int64_t(H) * (I / 16);
+    out->gsc = o; o += 16;
+    out->bytes = (o + 4095) & ~int64_t(4095);
+    return GRIM_OK;
+}
+
+static int tmoe_args(const grim_tiered_moe_view* v, int M, TmoeArgs& a) {
+    if (!v || !v->eptr) return fail(GRIM_ERR_ARG, "null view / block table");
+    const grim_nv_expert_layout& L = v->lay;
+    grim_nv_expert_layout want;
+    if (grimoire_tmoe_layout(L.H, L.I, &want) != GRIM_OK) return GRIM_ERR_SHAPE;
+    if (want.gu_p != L.gu_p || want.gu_s != L.gu_s || want.dn_p != L.dn_p ||
+        want.dn_s != L.dn_s || want.gsc != L.gsc)
+        return fail(GRIM_ERR_ARG, "block layout differs from grimoire_tmoe_layout(H, I)");
+    if (v->E <= 0 || v->top_k <= 0 || v->top_k > 32)
+        return fail(GRIM_ERR_SHAPE, "E=%d top_k=%d", v->E, v->top_k);
+    if (M < 0) return fail(GRIM_ERR_SHAPE, "M=%d", M);
+    a = TmoeArgs{};
+    a.eptr = v->eptr;
+    a.gu_p = L.gu_p; a.gu_s = L.gu_s; a.dn_p = L.dn_p; a.dn_s = L.dn_s; a.gsc = L.gsc;
+    a.H = L.H; a.I = L.I; a.K = v->top_k; a.E = v->E; a.M = M;
+    return GRIM_OK;
+}
+
+int grimoire_tmoe_gate_up(void* stream, const grim_tiered_moe_view* v, const int32_t* d_expert,
+                          const float* x, float* h, int M) {
+    TmoeArgs a;
+    if (int st = tmoe_args(v, M, a)) return st;
+    if (M == 0) return GRIM_OK;
+    if (!d_expert || !x || !h) return fail(GRIM_ERR_ARG, "null pointer");
+    a.expert = d_expert; a.x = x; a.h = h;
+    return status(tmoe_gate_up(S(stream), a));
+}
+
+int grimoire_tmoe_down(void* stream, const grim_tiered_moe_view* v, const int32_t* d_expert,
+                       const float* d_weight, const float* h, float* y, int M) {
+    TmoeArgs a;
+    if (int st = tmoe_args(v, M, a)) return st;
+    if (M == 0) return GRIM_OK;
+    if (!d_expert || !d_weight || !h || !y) return fail(GRIM_ERR_ARG, "null pointer");
+    a.expert = d_expert; a.weight = d_weight; a.h = const_cast<float*>(h); a.y = y;  // read only
+    return status(tmoe_down(S(stream), a));
+}
+
+int grimoire_tmoe_place(void* stream, const uint8_t** eptr, int e, uint8_t* dst_block,
+                        const uint8_t* src_block, size_t bytes) {
+    if (!eptr || !dst_block || e < 0) return fail(GRIM_ERR_ARG, "null table/block or e < 0");
+    hipStream_t st = S(stream);
+    if (src_block && bytes) {
+        const hipError_t c = hipMemcpyAsync(dst_block, src_block, bytes, hipMemcpyDefault, st);
+        if (c != hipSuccess) return status(c);
+    }
+    return status(tmoe_store(st, eptr, e, dst_block));
 }
 
 int grimoire_moe_quant_limbs(void* stream, const float* src, int rows, int n, int8_t* dst,

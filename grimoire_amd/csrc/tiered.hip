@@ -1,0 +1,278 @@
+// tiered.hip -- NVFP4 routed experts read through a per-layer table of
+// block pointers (include/b70/tiered_moe.hpp, src/tiered_moe.cpp).
+//
+// Every expert is one self-contained block (gate|up payload [2I][H/2],
+// their E4M3 scales [2I][H/16], down payload [H][I/2] and scales [H][I/16],
+// then the three fp32 projection scales {gate, up, down, 0}); the table
+// entry eptr[e] points into device memory or into pinned host memory, and
+// the kernels read both the same way (host blocks over PCIe).  Moving an
+// expert between tiers is one block copy plus one table store.
+//
+// NVFP4 chunk: 16 payload bytes = 32 elements = two 16-element blocks, each
+// with its own E4M3 scale.  Per lane and chunk the two block sums are formed
+// as fma chains over their 16 elements and scaled once each (the scale is a
+// power-of-two-times-small-integer, the same value as scaling every element);
+// the projection's fp32 scale is applied once per row at the end, as in
+// src/tiered_moe.cpp:45-61.  e2m1 pairs decode through the CDNA4 fp4
+// converter (exact in fp32); E4M3 scales by their bit fields.
+//
+// Lane layout: LPR lanes share one weight row, each walking the row's
+// 32-element chunks LPR apart, summed by group_sum<LPR>; a wave holds 64/LPR
+// rows at once.  LPR = the chunk count rounded up to a power of two, at most
+// 64, so a 2048-wide row is one chunk per lane.
+#include "common.hpp"
+#include "tiered.hpp"
+
+namespace grim {
+
+constexpr int kTmThreads = 256;
+
+// E4M3 (OCP, no infinities; 0x7F / 0xFF NaN) -> fp32 (include/b70/formats.hpp:157-169)
+__device__ __forceinline__ float e4m3_f32(uint32_t b) {
+    const uint32_t s = (b & 0x80u) << 24, e = (b >> 3) & 0xFu, m = b & 7u;
+    if (e == 0xFu && m == 7u) return bits_f(0x7FC00000u | s);
+    if (e == 0u) {
+        const float v = float(m) * 0.001953125f;   // m * 2^-9
+        return s ? -v : v;
+    }
+    return bits_f(s | ((e + 120u) << 23) | (m << 20));
+}
+
+// 32 elements (payload words p0..p3, low nibble = even element) against
+// x[0..31]; s2 holds the two block scales (low byte = elements 0..15).
+__device__ __forceinline__ float nv_dot32(uint4 p, uint32_t s2, const float* x) {
+    const uint32_t w[4] = {p.x, p.y, p.z, p.w};
+    float a[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const f32x2 v[4] = {__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 0),
+                            __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 1),
+                            __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 2),
+                            __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 3)};
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            a[d >> 1] = __builtin_fmaf(v[b].x, x[8 * d + 2 * b], a[d >> 1]);
+            a[d >> 1] = __builtin_fmaf(v[b].y, x[8 * d + 2 * b + 1], a[d >> 1]);
+        }
+    }
+    return a[0] * e4m3_f32(s2 & 0xFFu) + a[1] * e4m3_f32((s2 >> 8) & 0xFFu);
+}
+
+__device__ __forceinline__ void load_x32(const float* p, float* x) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float4 v = reinterpret_cast<const float4*>(p)[j];
+        x[4 * j] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
+    }
+}
+
+__device__ __forceinline__ uint32_t load_s2(const uint8_t* p) {
+    return uint32_t(*reinterpret_cast<const uint16_t*>(p));
+}
+
+// gate + up: each lane group owns 2 (gate row, up row) pairs of one
+// (token, slot); h[t][slot*I + i] = silu(g * s_gate) * (u * s_up), 0 for a
+// slot routed to no expert of this table (id < 0 or >= E).
+template <int LPR>
+__global__ __launch_bounds__(kTmThreads) void tmoe_gate_up_kernel(TmoeArgs a) {
+    constexpr int kGroups = kWave / LPR;            // row groups per wave
+    constexpr int kPairs = 2;                       // row pairs per group
+    constexpr int kPerBlock = (kTmThreads / kWave) * kGroups * kPairs;
+    const int H = a.H, I = a.I, K = a.K;
+    const int per_token = (K * I + kPerBlock - 1) / kPerBlock;
+    const int t = blockIdx.x / per_token;
+    const int lane = threadIdx.x & (kWave - 1), sub = lane % LPR;
+    const int group = (threadIdx.x / kWave) * kGroups + lane / LPR;
+    const int r0 = (blockIdx.x % per_token) * kPerBlock + group * kPairs;
+    const uint8_t* gp[kPairs];
+    const uint8_t* gs[kPairs];
+    float sgf[kPairs], suf[kPairs], ga[kPairs], ua[kPairs];
+    bool on[kPairs];
+#pragma unroll
+    for (int r = 0; r < kPairs; ++r) {
+        const int sr = r0 + r;
+        const int slot = sr / I, i = sr % I;
+        const int e = sr < K * I ? a.expert[int64_t(t) * K + slot] : -1;
+        on[r] = e >= 0 && e < a.E;
+        const uint8_t* blk = on[r] ? a.eptr[e] : nullptr;
+        gp[r] = on[r] ? blk + a.gu_p + int64_t(i) * (H / 2) : nullptr;
+        gs[r] = on[r] ? blk + a.gu_s + int64_t(i) * (H / 16) : nullptr;
+        sgf[r] = on[r] ? reinterpret_cast<const float*>(blk + a.gsc)[0] : 0.0f;
+        suf[r] = on[r] ? reinterpret_cast<const float*>(blk + a.gsc)[1] : 0.0f;
+        ga[r] = 0.0f;
+        ua[r] = 0.0f;
+    }
+    const float* xt = a.x + int64_t(t) * H;
+    const int64_t up_p = int64_t(I) * (H / 2), up_s = int64_t(I) * (H / 16);
+    for (int c = sub; c < H / 32; c += LPR) {
+        uint4 pg[kPairs], pu[kPairs];
+        uint32_t sg[kPairs], su[kPairs];
+#pragma unroll
+        for (int r = 0; r < kPairs; ++r) {
+            if (!on[r]) continue;
+            pg[r] = *reinterpret_cast<const uint4*>(gp[r] + c * 16);
+            pu[r] = *reinterpret_cast<const uint4*>(gp[r] + up_p + c * 16);
+            sg[r] = load_s2(gs[r] + c * 2);
+            su[r] = load_s2(gs[r] + up_s + c * 2);
+        }
+        float x[32];
+        load_x32(xt + c * 32, x);
+#pragma unroll
+        for (int r = 0; r < kPairs; ++r) {
+            if (!on[r]) continue;
+            ga[r] += nv_dot32(pg[r], sg[r], x);
+            ua[r] += nv_dot32(pu[r], su[r], x);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kPairs; ++r) {
+        const float g = group_sum<LPR>(ga[r]);
+        const float u = group_sum<LPR>(ua[r]);
+        const int sr = r0 + r;
+        if (sub == 0 && sr < K * I)
+            a.h[int64_t(t) * K * I + sr] = on[r] ? silu(g * sgf[r]) * (u * suf[r]) : 0.0f;
+    }
+}
+
+// down + routing-weighted sum over the K slots in slot order.  The four
+// waves of a work-group share its output rows and split the slots (wave w
+// takes slots w, w+4, ...), so a wave waits on K/4 rounds of weight loads,
+// not K; each (slot, row) dot lands in LDS and one thread per row forms
+// y[t][o] = fma chain over slots of (w_s * s_down) * dot, skipping a slot
+// with id < 0 (or >= E) or weight 0.
+constexpr int kTmMaxK = 32;
+
+template <int LPR>
+__global__ __launch_bounds__(kTmThreads) void tmoe_down_kernel(TmoeArgs a) {
+    constexpr int kWaves = kTmThreads / kWave;
+    constexpr int kGroups = kWave / LPR;
+    constexpr int kRows = 2;
+    constexpr int kPerBlock = kGroups * kRows;      // output rows of a work-group
+    __shared__ float part[kTmMaxK][kPerBlock];
+    const int H = a.H, I = a.I, K = a.K;
+    const int per_token = (H + kPerBlock - 1) / kPerBlock;
+    const int t = blockIdx.x / per_token;
+    const int obase = (blockIdx.x % per_token) * kPerBlock;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1), sub = lane % LPR;
+    const int g = lane / LPR;
+    const int o0 = obase + g * kRows;
+    __shared__ float coef[kTmMaxK];       // w_s * s_down, or NaN for a skipped slot
+    const float* ht = a.h + int64_t(t) * K * I;
+    // this wave's slots: ids, weights, block pointers and down scales all
+    // requested before any of them is used (three short dependent rounds
+    // for every slot at once instead of one chain per slot)
+    constexpr int kSlots = kTmMaxK / kWaves;
+    int ev[kSlots];
+    float rv[kSlots], sdv[kSlots];
+    const uint8_t* bv[kSlots];
+    bool onv[kSlots];
+    // unconditional loads at clamped indices, masked afterwards: no branch
+    // (and no wait) between the requests
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        const int s = wave + j * kWaves;
+        const int64_t sc = int64_t(t) * K + (s < K ? s : K - 1);
+        ev[j] = a.expert[sc];
+        rv[j] = a.weight[sc];
+    }
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        const int s = wave + j * kWaves;
+        onv[j] = s < K && ev[j] >= 0 && ev[j] < a.E && rv[j] != 0.0f;
+        bv[j] = a.eptr[onv[j] ? ev[j] : 0];
+    }
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) sdv[j] = reinterpret_cast<const float*>(bv[j] + a.gsc)[2];
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        const int s = wave + j * kWaves;
+        if (s < K && lane == 0) coef[s] = onv[j] ? rv[j] * sdv[j] : __builtin_nanf("");
+        if (!onv[j]) bv[j] = nullptr;
+    }
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        const int s = wave + j * kWaves;
+        const uint8_t* blk = bv[j];
+        if (!blk) continue;                                  // uniform across the wave
+        float acc[kRows] = {0.0f, 0.0f};
+        for (int c = sub; c < I / 32; c += LPR) {
+            uint4 pv[kRows];
+            uint32_t s2[kRows];
+#pragma unroll
+            for (int r = 0; r < kRows; ++r) {
+                const int o = o0 + r < H ? o0 + r : H - 1;
+                pv[r] = *reinterpret_cast<const uint4*>(blk + a.dn_p + int64_t(o) * (I / 2) + c * 16);
+                s2[r] = load_s2(blk + a.dn_s + int64_t(o) * (I / 16) + c * 2);
+            }
+            float hx[32];
+            load_x32(ht + s * I + c * 32, hx);
+#pragma unroll
+            for (int r = 0; r < kRows; ++r) acc[r] += nv_dot32(pv[r], s2[r], hx);
+        }
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+            const float d = group_sum<LPR>(acc[r]);
+            if (sub == 0) part[s][g * kRows + r] = d;
+        }
+    }
+    __syncthreads();
+    const int row = threadIdx.x;
+    if (row < kPerBlock && obase + row < H) {
+        float total = 0.0f;
+        for (int s = 0; s < K; ++s) {
+            const float c = coef[s];
+            if (c == c) total = __builtin_fmaf(c, part[s][row], total);   // NaN marks a skip
+        }
+        a.y[int64_t(t) * H + obase + row] = total;
+    }
+}
+
+__global__ void tmoe_store_ptr(const uint8_t** table, int e, const uint8_t* p) {
+    if (threadIdx.x == 0) table[e] = p;
+}
+
+static int lanes_for(int chunks) {
+    int l = 1;
+    while (l < chunks && l < kWave) l *= 2;
+    return l;
+}
+
+#define GRIM_TM_LAUNCH(KERNEL, LPR_VAL, GRID)                                                      \
+    hipLaunchKernelGGL((KERNEL<LPR_VAL>), GRID, dim3(kTmThreads), 0, st, a)
+
+#define GRIM_TM_SWITCH(KERNEL, LPR, GRID)                                                          \
+    switch (LPR) {                                                                                 \
+        case 1: GRIM_TM_LAUNCH(KERNEL, 1, GRID); break;                                            \
+        case 2: GRIM_TM_LAUNCH(KERNEL, 2, GRID); break;                                            \
+        case 4: GRIM_TM_LAUNCH(KERNEL, 4, GRID); break;                                            \
+        case 8: GRIM_TM_LAUNCH(KERNEL, 8, GRID); break;                                            \
+        case 16: GRIM_TM_LAUNCH(KERNEL, 16, GRID); break;                                          \
+        case 32: GRIM_TM_LAUNCH(KERNEL, 32, GRID); break;                                          \
+        default: GRIM_TM_LAUNCH(KERNEL, 64, GRID); break;                                          \
+    }
+
+hipError_t tmoe_gate_up(hipStream_t st, const TmoeArgs& a) {
+    if (a.M <= 0) return hipSuccess;
+    const int lpr = lanes_for(a.H / 32);
+    const int per_block = (kTmThreads / kWave) * (kWave / lpr) * 2;
+    const dim3 grid(unsigned(int64_t(a.M) * ((a.K * a.I + per_block - 1) / per_block)));
+    GRIM_TM_SWITCH(tmoe_gate_up_kernel, lpr, grid);
+    return hipGetLastError();
+}
+
+hipError_t tmoe_down(hipStream_t st, const TmoeArgs& a) {
+    if (a.M <= 0) return hipSuccess;
+    if (a.K > kTmMaxK) return hipErrorInvalidValue;
+    const int lpr = lanes_for(a.I / 32);
+    const int per_block = (kWave / lpr) * 2;
+    const dim3 grid(unsigned(int64_t(a.M) * ((a.H + per_block - 1) / per_block)));
+    GRIM_TM_SWITCH(tmoe_down_kernel, lpr, grid);
+    return hipGetLastError();
+}
+
+hipError_t tmoe_store(hipStream_t st, const uint8_t** table, int e, const uint8_t* p) {
+    hipLaunchKernelGGL(tmoe_store_ptr, dim3(1), dim3(kWave), 0, st, table, e, p);
+    return hipGetLastError();
+}
+
+}  // namespace grim

@@ -1,0 +1,99 @@
+"""Tiered NVFP4 experts (include/b70/tiered_moe.hpp, src/tiered_moe.cpp) and
+their placement policy (include/b70/expert_heat.hpp), on torch tensors.
+
+A layer is E self-contained expert blocks (`layout(H, I)` bytes each) and a
+device table of E block pointers.  A block may be a device tensor or a
+pinned host tensor (`torch.empty(..., pin_memory=True)`): the kernels read
+both through the table.  `TieredLayer.place` moves an expert between tiers
+(block copy + table store, in stream order); `Heat` proposes the moves.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import _abi
+from .ops import _dev, _p, _stream, check, lib
+
+
+def layout(H: int, I: int) -> _abi.NvExpertLayout:
+    L = _abi.NvExpertLayout()
+    check(lib().grimoire_tmoe_layout(H, I, C.byref(L)), "tmoe_layout")
+    return L
+
+
+class TieredLayer:
+    """One layer's routed experts behind a device block table."""
+
+    def __init__(self, H: int, I: int, top_k: int, blocks: Sequence[torch.Tensor], device):
+        self.lay = layout(H, I)
+        self.H, self.I, self.K, self.E = H, I, top_k, len(blocks)
+        for b in blocks:
+            if b.dtype != torch.uint8 or b.numel() < self.lay.bytes:
+                raise ValueError("expert block smaller than the layout")
+        self.blocks: List[torch.Tensor] = list(blocks)
+        self.table = torch.tensor([b.data_ptr() for b in blocks], dtype=torch.int64, device=device)
+
+    def view(self) -> _abi.TieredMoeView:
+        return _abi.TieredMoeView(self.lay, self.table.data_ptr(), self.E, self.K)
+
+    def gate_up(self, expert, x, h, stream=None):
+        """launch_tmoe_gate_up: h[M][K*I]."""
+        _dev(x)
+        v = self.view()
+        check(lib().grimoire_tmoe_gate_up(_stream(stream), C.byref(v), _p(expert), _p(x), _p(h),
+                                          x.shape[0]), "tmoe_gate_up")
+
+    def down(self, expert, weight, h, y, stream=None):
+        """launch_tmoe_down: y[M][H]."""
+        _dev(h)
+        v = self.view()
+        check(lib().grimoire_tmoe_down(_stream(stream), C.byref(v), _p(expert), _p(weight), _p(h),
+                                       _p(y), y.shape[0]), "tmoe_down")
+
+    def place(self, e: int, dst: torch.Tensor, stream=None):
+        """Move expert e into `dst` (device or pinned host): copy, then the
+        table store; the old block may be reused once the stream passes."""
+        src = self.blocks[e]
+        check(lib().grimoire_tmoe_place(_stream(stream), self.table.data_ptr(), e, _p(dst), _p(src),
+                                        self.lay.bytes), "tmoe_place")
+        self.blocks[e] = dst
+
+
+class Heat:
+    """grim_heat: decayed routing counts per (layer, expert) and swap proposals."""
+
+    def __init__(self, layers: int, experts: int, params: Optional[_abi.HeatParams] = None):
+        if params is None:
+            params = _abi.HeatParams()
+            lib().grimoire_heat_default_params(C.byref(params))
+        self.L, self.E = layers, experts
+        self._h = lib().grimoire_heat_create(layers, experts, C.byref(params))
+        if not self._h:
+            raise _abi.GrimoireError("grimoire_heat_create failed")
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            lib().grimoire_heat_destroy(h)
+            self._h = None
+
+    def credit(self, layer: int, ids) -> None:
+        ids = torch.as_tensor(ids, dtype=torch.int32).contiguous().cpu()
+        lib().grimoire_heat_credit(self._h, layer, ids.data_ptr(), ids.numel())
+
+    def heat(self, layer: int, expert: int) -> float:
+        return float(lib().grimoire_heat_get(self._h, layer, expert))
+
+    def propose(self, resident, movable=None, max_out: int = 1 << 16):
+        r = torch.as_tensor(resident, dtype=torch.uint8).contiguous().cpu()
+        m = None if movable is None else torch.as_tensor(movable, dtype=torch.uint8).contiguous().cpu()
+        out = (_abi.ExpertSwap * max_out)()
+        n = lib().grimoire_heat_propose(self._h, r.data_ptr(), None if m is None else m.data_ptr(),
+                                        out, max_out)
+        if n < 0:
+            raise _abi.GrimoireError("grimoire_heat_propose failed")
+        return [(s.promote_layer, s.promote_expert, s.demote_layer, s.demote_expert)
+                for s in out[:n]]

@@ -347,6 +347,81 @@ int grimoire_moe_int4_to_signed(void* stream, uint8_t* gu_payload, size_t gu_byt
                                 int32_t* converted);
 
 /* ------------------------------------------------------------------------
+ * Tiered experts (include/b70/tiered_moe.hpp): every routed expert of a
+ * layer is one self-contained NVFP4 block, and a device array of block
+ * pointers (one per expert) is all the kernels need, so a block may sit in
+ * device memory or in pinned host memory (hipHostMalloc; read over PCIe).
+ * Block layout, NvExpertLayout::make (tiered_moe.hpp:40-60):
+ *   gu_p  gate|up payload [2I][H/2] (e2m1, low nibble = even element)
+ *   gu_s  gate|up E4M3 scales [2I][H/16]
+ *   dn_p  down payload [H][I/2];  dn_s  down E4M3 scales [H][I/16]
+ *   gsc   four fp32 {gate, up, down, 0} projection scales (multipliers)
+ *   bytes the block size rounded up to 4096.
+ * ---------------------------------------------------------------------- */
+typedef struct grim_nv_expert_layout {
+    int32_t H, I;
+    int64_t gu_p, gu_s, dn_p, dn_s, gsc, bytes;
+} grim_nv_expert_layout;
+
+/* b70::TieredMoeView (tiered_moe.hpp:63-67). */
+typedef struct grim_tiered_moe_view {
+    grim_nv_expert_layout lay;
+    const uint8_t* const* eptr;  /* device array [E] of block pointers   */
+    int32_t E;
+    int32_t top_k;
+} grim_tiered_moe_view;
+
+/* NvExpertLayout::make; returns GRIM_ERR_SHAPE unless H and I are
+ * multiples of 128 (NvExpertLayout::supported). */
+int grimoire_tmoe_layout(int H, int I, grim_nv_expert_layout* out);
+
+/* h[M][K*I] = silu(x W_gate^T * s_gate) * (x W_up^T * s_up) for each routed
+ * slot; 0 for a slot whose id is < 0 or >= E (another tier's or rank's).
+ * Replaces launch_tmoe_gate_up (src/tiered_moe.cpp:88-176, :292). */
+int grimoire_tmoe_gate_up(void* stream, const grim_tiered_moe_view* v, const int32_t* d_expert,
+                          const float* x, float* h, int M);
+/* y[M][H] = sum over slots in slot order of (w * s_down) * (h_slot W_down^T),
+ * slots with id < 0 or >= E or weight 0 skipped.  Replaces launch_tmoe_down
+ * (src/tiered_moe.cpp:187-278, :300). */
+int grimoire_tmoe_down(void* stream, const grim_tiered_moe_view* v, const int32_t* d_expert,
+                       const float* d_weight, const float* h, float* y, int M);
+
+/* Moves expert e of a layer to another tier: copies `bytes` from src_block
+ * to dst_block (hipMemcpyAsync, any memory) and then stores dst_block into
+ * eptr[e] on the device, in stream order (tiered_moe.hpp:21-22: "one block
+ * copy plus one pointer store").  src_block NULL: pointer store only. */
+int grimoire_tmoe_place(void* stream, const uint8_t** eptr, int e, uint8_t* dst_block,
+                        const uint8_t* src_block, size_t bytes);
+
+/* Expert heat and tier placement (include/b70/expert_heat.hpp). */
+typedef struct grim_heat_params {
+    float decay;               /* per call of a layer, 0.95              */
+    float hysteresis;          /* promote if hot >= cold * h + min_gain  */
+    float min_gain;
+    float credit_cap;          /* most credited selections per call      */
+    int32_t moves_per_step;
+} grim_heat_params;
+
+typedef struct grim_expert_swap {
+    int32_t promote_layer, promote_expert;   /* to device memory */
+    int32_t demote_layer, demote_expert;     /* to pinned host   */
+} grim_expert_swap;
+
+typedef struct grim_heat grim_heat;
+
+void grimoire_heat_default_params(grim_heat_params* p);
+grim_heat* grimoire_heat_create(int layers, int experts, const grim_heat_params* params);
+void grimoire_heat_destroy(grim_heat* s);
+/* ExpertHeat::credit: one call of `layer` with its n routes (host ids). */
+void grimoire_heat_credit(grim_heat* s, int layer, const int32_t* ids, size_t n);
+float grimoire_heat_get(const grim_heat* s, int layer, int expert);
+/* ExpertHeat::propose over host flags resident[L*E] and movable[L*E]
+ * (NULL = all movable); writes at most min(moves_per_step, max_out) swaps,
+ * returns their count. */
+int grimoire_heat_propose(const grim_heat* s, const uint8_t* resident, const uint8_t* movable,
+                          grim_expert_swap* out, int max_out);
+
+/* ------------------------------------------------------------------------
  * Grouped GEMM on MFMA (prefill).  One launch per projection for all
  * experts.  A bf16 [R][K] rows grouped by expert (offsets/counts from the
  * dispatch), W the packed expert weight [E*N][K].

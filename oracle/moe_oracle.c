@@ -23,6 +23,9 @@
  *   orc_gptq_repack     reference gptq_repack_int4 via oracle/_ref, golden
  *                       GPTQ probes through orc_qw_at, orc_gptq_at
  *   orc_int4_zero_unpack  brute-force nibble extraction
+ *   orc_e4m3_to_f32     reference e4m3_to_f32 over all 256 codes via oracle/_ref
+ *   orc_nvfp4_dequant_row  reference nvfp4_dequant_row via oracle/_ref
+ *   orc_tmoe_*          float64 products of the reference-dequantised blocks
  *   orc_int4_to_signed  dequantised values unchanged (orc_qw_at before and
  *                       after), untouched when one zero point is not 8
  *   orc_grouped_gemm    numpy matmul of the dequantised weights
@@ -612,6 +615,110 @@ int orc_int4_to_signed(uint8_t* gu, int64_t gu_bytes, uint8_t* gz, int64_t gz_by
     memset(gz, 0xFF, (size_t)gz_bytes);
     memset(dz, 0xFF, (size_t)dz_bytes);
     return 1;
+}
+
+/* include/b70/formats.hpp:157-169 */
+float orc_e4m3_to_f32(uint8_t b) {
+    const uint32_t s = (uint32_t)(b & 0x80u) << 24;
+    const int e = (b >> 3) & 0xF, m = b & 7;
+    if (e == 0xF && m == 7) return bits_f(0x7FC00000u | s);
+    if (e == 0) {
+        const float v = (float)m * (1.0f / 8.0f) * 0.015625f;
+        return s ? -v : v;
+    }
+    return bits_f(s | ((uint32_t)(e - 7 + 127) << 23) | ((uint32_t)m << 20));
+}
+
+/* nvfp4_dequant_row (include/b70/nvfp4.hpp): mul = 1 multiplies by gscale. */
+void orc_nvfp4_dequant_row(const uint8_t* packed, const uint8_t* scales, float gscale, int K,
+                           float* out, int mul) {
+    for (int k = 0; k < K; ++k) {
+        const uint8_t byte = packed[k >> 1];
+        const uint8_t nib = (k & 1) ? (uint8_t)(byte >> 4) : (uint8_t)(byte & 0x0F);
+        const float blk = orc_e4m3_to_f32(scales[k / 16]);
+        out[k] = mul ? orc_e2m1_to_f32(nib) * blk * gscale : orc_e2m1_to_f32(nib) * blk / gscale;
+    }
+}
+
+/* NvExpertLayout::make (include/b70/tiered_moe.hpp:40-60) */
+void orc_tmoe_layout(int H, int I, int64_t* off /* gu_p gu_s dn_p dn_s gsc bytes */) {
+    int64_t o = 0;
+    off[0] = o; o += (int64_t)2 * I * (H / 2);
+    off[1] = o; o += (int64_t)2 * I * (H / 16);
+    off[2] = o; o += (int64_t)H * (I / 2);
+    off[3] = o; o += (int64_t)H * (I / 16);
+    off[4] = o; o += 16;
+    off[5] = (o + 4095) & ~(int64_t)4095;
+}
+
+/* nv_dot32 (src/tiered_moe.cpp:45-61): two 16-element fma chains, each
+ * scaled by its E4M3 block scale. */
+static float orc_nv_dot32(const uint8_t* p, const uint8_t* s, const float* x) {
+    float a0 = 0.0f, a1 = 0.0f;
+    for (int k = 0; k < 16; ++k) {
+        const uint8_t nib = (k & 1) ? (uint8_t)(p[k >> 1] >> 4) : (uint8_t)(p[k >> 1] & 15);
+        a0 = fmaf(orc_e2m1_to_f32(nib), x[k], a0);
+    }
+    for (int k = 16; k < 32; ++k) {
+        const uint8_t nib = (k & 1) ? (uint8_t)(p[k >> 1] >> 4) : (uint8_t)(p[k >> 1] & 15);
+        a1 = fmaf(orc_e2m1_to_f32(nib), x[k], a1);
+    }
+    return a0 * orc_e4m3_to_f32(s[0]) + a1 * orc_e4m3_to_f32(s[1]);
+}
+
+static float orc_nv_row(const uint8_t* p, const uint8_t* s, const float* x, int K) {
+    float acc = 0.0f;
+    for (int c = 0; c < K / 32; ++c) acc += orc_nv_dot32(p + c * 16, s + c * 2, x + c * 32);
+    return acc;
+}
+
+/* launch_tmoe_gate_up (src/tiered_moe.cpp:88-176): blocks[e] host copies. */
+void orc_tmoe_gate_up(const uint8_t* const* blocks, int H, int I, int K, int E,
+                      const int32_t* expert, const float* x, float* h, int M) {
+    int64_t off[6];
+    orc_tmoe_layout(H, I, off);
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < M; ++t)
+        for (int sr = 0; sr < K * I; ++sr) {
+            const int slot = sr / I, i = sr % I;
+            const int e = expert[(int64_t)t * K + slot];
+            float v = 0.0f;
+            if (e >= 0 && e < E) {
+                const uint8_t* b = blocks[e];
+                const float* g3 = (const float*)(b + off[4]);
+                const float g = orc_nv_row(b + off[0] + (int64_t)i * (H / 2),
+                                           b + off[1] + (int64_t)i * (H / 16), x + (int64_t)t * H, H);
+                const float u = orc_nv_row(b + off[0] + (int64_t)(I + i) * (H / 2),
+                                           b + off[1] + (int64_t)(I + i) * (H / 16),
+                                           x + (int64_t)t * H, H);
+                v = silu_f(g * g3[0]) * (u * g3[1]);
+            }
+            h[(int64_t)t * K * I + sr] = v;
+        }
+}
+
+/* launch_tmoe_down (src/tiered_moe.cpp:187-278) */
+void orc_tmoe_down(const uint8_t* const* blocks, int H, int I, int K, int E,
+                   const int32_t* expert, const float* weight, const float* h, float* y, int M) {
+    int64_t off[6];
+    orc_tmoe_layout(H, I, off);
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < M; ++t)
+        for (int o = 0; o < H; ++o) {
+            float total = 0.0f;
+            for (int s = 0; s < K; ++s) {
+                const int e = expert[(int64_t)t * K + s];
+                const float rw = weight[(int64_t)t * K + s];
+                if (e < 0 || e >= E || rw == 0.0f) continue;
+                const uint8_t* b = blocks[e];
+                const float sd = ((const float*)(b + off[4]))[2];
+                const float acc = orc_nv_row(b + off[2] + (int64_t)o * (I / 2),
+                                             b + off[3] + (int64_t)o * (I / 16),
+                                             h + (int64_t)t * K * I + (int64_t)s * I, I);
+                total = fmaf(rw * sd, acc, total);
+            }
+            y[(int64_t)t * H + o] = total;
+        }
 }
 
 /* src/gemm_fast.cpp:1603-1800 contract (EPI 0 / EPI 1) */

@@ -122,6 +122,17 @@ void orc_int4_zero_unpack(const int32_t* zp, int out, int groups, uint8_t* zeros
 int orc_int4_to_signed(uint8_t* gu, int64_t gu_bytes, uint8_t* gz, int64_t gz_bytes, uint8_t* dn,
                        int64_t dn_bytes, uint8_t* dz, int64_t dz_bytes);
 
+/* Tiered NVFP4 experts (include/b70/nvfp4.hpp, tiered_moe.hpp,
+ * src/tiered_moe.cpp); blocks[e] are host copies of the expert blocks. */
+float orc_e4m3_to_f32(uint8_t b);
+void orc_nvfp4_dequant_row(const uint8_t* packed, const uint8_t* scales, float gscale, int K,
+                           float* out, int mul);
+void orc_tmoe_layout(int H, int I, int64_t* off);
+void orc_tmoe_gate_up(const uint8_t* const* blocks, int H, int I, int K, int E,
+                      const int32_t* expert, const float* x, float* h, int M);
+void orc_tmoe_down(const uint8_t* const* blocks, int H, int I, int K, int E,
+                   const int32_t* expert, const float* weight, const float* h, float* y, int M);
+
 /* Grouped GEMM (src/gemm_fast.cpp:1603-1800 contract): rows [off_e,
  * off_e+cnt_e) of A (fp32 values) times W_e^T; swiglu gives silu(g)*u over
  * N = 2I. out fp32 [R][N or I]. Double accumulation. */

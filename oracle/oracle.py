@@ -73,6 +73,11 @@ def orc() -> C.CDLL:
             "orc_moe_forward": (None, [P, P, P, P, P, P, I32]),
             "orc_dispatch": (I32, [P, I32, I32, I32, I32, P, P, P, P, P, P, I32]),
             "orc_unpermute": (None, [P, P, P, P, I32, I32, I32]),
+            "orc_e4m3_to_f32": (F32, [C.c_uint8]),
+            "orc_nvfp4_dequant_row": (None, [P, P, F32, I32, P, I32]),
+            "orc_tmoe_layout": (None, [I32, I32, P]),
+            "orc_tmoe_gate_up": (None, [P, I32, I32, I32, I32, P, P, P, I32]),
+            "orc_tmoe_down": (None, [P, I32, I32, I32, I32, P, P, P, P, I32]),
             "orc_gptq_repack": (None, [P, P, P, I32, I32, I32, I32, P, P, P]),
             "orc_int4_zero_unpack": (None, [P, I32, I32, P]),
             "orc_int4_to_signed": (I32, [P, C.c_int64, P, C.c_int64, P, C.c_int64, P, C.c_int64]),
@@ -100,6 +105,13 @@ def ref():
             "ref_qw_at": (F32, [P, I32, I32]),
             "ref_gptq_at": (F32, [P, P, P, I32, I32, I32, I32, I32]),
             "ref_gptq_repack_int4": (I32, [P, P, P, I32, I32, I32, P, P, P]),
+            "ref_e4m3_to_f32": (F32, [C.c_uint8]),
+            "ref_nvfp4_dequant_row": (None, [P, P, F32, I32, P, I32]),
+            "ref_heat_create": (P, [I32, I32, F32, F32, F32, F32, I32]),
+            "ref_heat_destroy": (None, [P]),
+            "ref_heat_credit": (None, [P, I32, P, C.c_size_t]),
+            "ref_heat_get": (F32, [P, I32, I32]),
+            "ref_heat_propose": (I32, [P, I32, P, P, P, I32]),
             "ref_route_ref": (None, [P, I32, I32, I32, P, P]),
             "ref_moe_forward": (None, [P, P, P, P, P, I32]),
         }
@@ -237,3 +249,80 @@ def int4_to_signed(gu, gz, dn, dz):
     """In place on numpy uint8 arrays; returns 1 when converted."""
     return orc().orc_int4_to_signed(_p(gu), gu.size, _p(gz), gz.size, _p(dn), dn.size, _p(dz),
                                     dz.size)
+
+
+def tmoe_layout(H, I):
+    off = np.zeros(6, dtype=np.int64)
+    orc().orc_tmoe_layout(H, I, _p(off))
+    return dict(zip(("gu_p", "gu_s", "dn_p", "dn_s", "gsc", "bytes"), (int(v) for v in off)))
+
+
+def _block_table(blocks):
+    bl = [np.ascontiguousarray(b) for b in blocks]
+    tab = (C.c_void_p * len(bl))(*[b.ctypes.data for b in bl])
+    return bl, tab
+
+
+def tmoe_gate_up(blocks, H, I, K, expert, x, M):
+    """blocks: list of uint8 numpy arrays (one per expert)."""
+    keep, tab = _block_table(blocks)
+    h = np.zeros((M, K * I), dtype=np.float32)
+    ex, xc = np.ascontiguousarray(expert, np.int32), np.ascontiguousarray(x, np.float32)
+    orc().orc_tmoe_gate_up(C.cast(tab, C.c_void_p), H, I, K, len(keep), _p(ex), _p(xc), _p(h), M)
+    return h
+
+
+def tmoe_down(blocks, H, I, K, expert, weight, h, M):
+    keep, tab = _block_table(blocks)
+    y = np.zeros((M, H), dtype=np.float32)
+    ex = np.ascontiguousarray(expert, np.int32)
+    wc, hc = np.ascontiguousarray(weight, np.float32), np.ascontiguousarray(h, np.float32)
+    orc().orc_tmoe_down(C.cast(tab, C.c_void_p), H, I, K, len(keep), _p(ex), _p(wc), _p(hc),
+                        _p(y), M)
+    return y
+
+
+class Heat:
+    """ExpertHeat (include/b70/expert_heat.hpp) restated in plain Python, in
+    float32 arithmetic like the reference: credit() decays the layer's row
+    and adds min(1, cap/n) per route; propose() pairs the hottest
+    non-resident with the coldest resident while hot >= cold*hyst + gain."""
+
+    def __init__(self, layers, experts, decay=0.95, hysteresis=1.25, min_gain=1.5,
+                 credit_cap=512.0, moves=32):
+        self.L, self.E = layers, experts
+        f = np.float32
+        self.decay, self.hyst, self.gain, self.cap = f(decay), f(hysteresis), f(min_gain), f(credit_cap)
+        self.moves = moves
+        self.h = np.zeros((layers, experts), dtype=np.float32)
+
+    def credit(self, l, ids):
+        if not 0 <= l < self.L:
+            return
+        row = self.h[l]
+        row *= self.decay
+        n = len(ids)
+        w = self.cap / np.float32(n) if np.float32(n) > self.cap else np.float32(1.0)
+        for e in ids:
+            if 0 <= e < self.E:
+                row[e] = np.float32(row[e] + w)
+
+    def propose(self, resident, movable=None):
+        hot, cold = [], []
+        for l in range(self.L):
+            for e in range(self.E):
+                if movable is not None and not movable[l][e]:
+                    continue
+                x = self.h[l, e]
+                if resident[l][e]:
+                    cold.append((x, l, e))
+                elif x > 0:
+                    hot.append((x, l, e))
+        hot.sort(key=lambda u: (-u[0], u[1], u[2]))
+        cold.sort(key=lambda u: (u[0], u[1], u[2]))
+        out = []
+        for i in range(min(self.moves, len(hot), len(cold))):
+            if not (hot[i][0] >= np.float32(cold[i][0] * self.hyst) + self.gain):
+                break
+            out.append((hot[i][1], hot[i][2], cold[i][1], cold[i][2]))
+        return out

@@ -9,6 +9,8 @@
 
 #include "b70/moe.hpp"
 #include "b70/gptq.hpp"
+#include "b70/nvfp4.hpp"
+#include "b70/expert_heat.hpp"
 #include "../include/grimoire_moe.h"
 
 using namespace b70;
@@ -53,6 +55,46 @@ int ref_gptq_repack_int4(const int32_t* qweight, const int32_t* qzeros, const ui
     std::memcpy(scales_out, p.scales_raw.data(), p.scales_raw.size());
     std::memcpy(zeros_out, p.zeros.data(), p.zeros.size());
     return 1;
+}
+
+// e4m3_to_f32 (include/b70/formats.hpp:157-169)
+float ref_e4m3_to_f32(uint8_t b) { return e4m3_to_f32(b); }
+
+// nvfp4_dequant_row (include/b70/nvfp4.hpp)
+void ref_nvfp4_dequant_row(const uint8_t* packed, const uint8_t* scales, float gscale, int K,
+                           float* out, int mul) {
+    nvfp4_dequant_row(packed, scales, gscale, K, out, mul != 0);
+}
+
+// ExpertHeat (include/b70/expert_heat.hpp)
+void* ref_heat_create(int layers, int experts, float decay, float hysteresis, float min_gain,
+                      float credit_cap, int moves) {
+    ExpertHeatParams p;
+    p.decay = decay; p.hysteresis = hysteresis; p.min_gain = min_gain;
+    p.credit_cap = credit_cap; p.moves_per_step = moves;
+    ExpertHeat* h = new ExpertHeat;
+    h->init(layers, experts, p);
+    return h;
+}
+void ref_heat_destroy(void* h) { delete static_cast<ExpertHeat*>(h); }
+void ref_heat_credit(void* h, int l, const int32_t* ids, size_t n) {
+    static_cast<ExpertHeat*>(h)->credit(l, ids, n);
+}
+float ref_heat_get(void* h, int l, int e) { return static_cast<ExpertHeat*>(h)->heat(l, e); }
+int ref_heat_propose(void* hp, int experts, const uint8_t* resident, const uint8_t* movable,
+                     int32_t* out4, int max_out) {
+    ExpertHeat* h = static_cast<ExpertHeat*>(hp);
+    std::vector<ExpertSwap> sw;
+    h->propose([&](int l, int e) { return resident[size_t(l) * experts + e] != 0; },
+               [&](int l, int e) { return !movable || movable[size_t(l) * experts + e] != 0; }, sw);
+    int n = 0;
+    for (const ExpertSwap& s : sw) {
+        if (n >= max_out) break;
+        out4[4 * n] = s.promote_layer; out4[4 * n + 1] = s.promote_expert;
+        out4[4 * n + 2] = s.demote_layer; out4[4 * n + 3] = s.demote_expert;
+        ++n;
+    }
+    return n;
 }
 
 // route_ref (src/moe_ref.cpp:30-63)
