@@ -20,7 +20,7 @@ The JSON line also carries:
                 and grouped-GEMM TFLOPS against the bf16 MFMA peak;
   edges         the fused combine + residual + RMSNorm and the residual
                 RMSNorm (C4 shapes) against 8 TB/s, and the GPTQ ingestion
-                of one C2 layer's experts.
+                of one C2 layer's experts, and the tiered NVFP4 experts.
 """
 from __future__ import annotations
 
@@ -299,7 +299,41 @@ def edges_bench(dev, stream, reps=20):
             "ms": round(ms, 3), "host_ms": round(host_ms, 3), "bytes": src_bytes + dst_bytes,
             "gbs": round((src_bytes + dst_bytes) / (ms * 1e-3) / 1e9, 1),
             "note": "two batched calls (gate+up, down), 64 GPTQ projections per launch"}
+        res["tiered_nvfp4"] = _tiered_bench(dev, stream, timed)
     return res
+
+
+def _tiered_bench(dev, stream, timed):
+    """Tiered NVFP4 experts at C2 shapes (H=2048, I=768, top-8 of 128): one
+    token's gate_up and down with every block in device memory, then with
+    every block in pinned host memory (read over PCIe)."""
+    from grimoire_amd import tiered
+    H, I, K, E = 2048, 768, 8, 128
+    lay = tiered.layout(H, I)
+    g = torch.Generator(device=dev).manual_seed(9)
+    blocks = [torch.randint(0, 256, (lay.bytes,), dtype=torch.uint8, device=dev, generator=g)
+              for _ in range(E)]
+    for b in blocks:   # E4M3 scales 0x30..0x3F, projection scales 1
+        b[lay.gu_s:lay.gsc].copy_(0x30 + (b[lay.gu_s:lay.gsc] & 15))
+        b[lay.gsc:lay.gsc + 16].copy_(torch.tensor([1.0, 1.0, 1.0, 0.0]).view(torch.uint8))
+    ex = torch.tensor([[3, 17, 40, 55, 77, 90, 101, 127]], dtype=torch.int32, device=dev)
+    w = torch.full((1, K), 1.0 / K, device=dev)
+    x = torch.randn(1, H, device=dev, generator=g)
+    h = torch.empty(1, K * I, device=dev)
+    y = torch.empty(1, H, device=dev)
+    gu_bytes = K * 2 * I * (H // 2 + H // 16)
+    dn_bytes = K * H * (I // 2 + I // 16)
+    out = {"shape": f"T=1 H={H} I={I} top-{K} of {E}, NVFP4 blocks of {lay.bytes} B"}
+    for tier in ("vram", "pinned_host"):
+        bl = blocks if tier == "vram" else [b.cpu().pin_memory() for b in blocks]
+        L = tiered.TieredLayer(H, I, K, bl, dev)
+        gu_ms = timed(lambda: L.gate_up(ex, x, h, stream=stream))
+        dn_ms = timed(lambda: L.down(ex, w, h, y, stream=stream))
+        out[tier] = {"gate_up_us": round(gu_ms * 1e3, 1),
+                     "gate_up_gbs": round(gu_bytes / (gu_ms * 1e-3) / 1e9, 1),
+                     "down_us": round(dn_ms * 1e3, 1),
+                     "down_gbs": round(dn_bytes / (dn_ms * 1e-3) / 1e9, 1)}
+    return out
 
 
 def cpu_baseline(d, budget_s=15.0):
