@@ -156,6 +156,11 @@ SIGNATURES = {
     "grimoire_tmoe_gate_up": (I32, [P, C.POINTER(TieredMoeView), P, P, P, I32]),
     "grimoire_tmoe_down": (I32, [P, C.POINTER(TieredMoeView), P, P, P, P, I32]),
     "grimoire_tmoe_place": (I32, [P, P, I32, P, P, SZ]),
+    "grimoire_tmoe_scratch_bytes": (SZ, [C.POINTER(NvExpertLayout), I32]),
+    "grimoire_tmoe_expert_gemm": (I32, [P, P, C.POINTER(NvExpertLayout), I32, F32, F32, P, P, I32,
+                                        P, SZ]),
+    "grimoire_tmoe_expert_ffn": (I32, [P, P, C.POINTER(NvExpertLayout), F32, F32, F32, P, P, P,
+                                       I32, P, SZ]),
     "grimoire_heat_default_params": (None, [C.POINTER(HeatParams)]),
     "grimoire_heat_create": (P, [I32, I32, C.POINTER(HeatParams)]),
     "grimoire_heat_destroy": (None, [P]),

@@ -656,6 +656,78 @@ int grimoire_tmoe_down(void* stream, const grim_tiered_moe_view* v, const int32_
     return status(tmoe_down(S(stream), a));
 }
 
+size_t grimoire_tmoe_scratch_bytes(const grim_nv_expert_layout* L, int M) {
+    if (!L || M < 0) return 0;
+    const size_t w = size_t(2) * L->I * L->H * 2;            // decoded gate|up (>= down)
+    return w + size_t(M) * 2 * L->I * 4 + 256;
+}
+
+static int tmoe_prefill_check(const uint8_t* block, const grim_nv_expert_layout* L, int M,
+                              const void* A, const void* out, const void* scratch,
+                              size_t scratch_bytes) {
+    if (!block || !L || !A || !out || !scratch) return fail(GRIM_ERR_ARG, "null pointer");
+    grim_nv_expert_layout want;
+    if (grimoire_tmoe_layout(L->H, L->I, &want) != GRIM_OK) return GRIM_ERR_SHAPE;
+    if (want.gu_p != L->gu_p || want.dn_s != L->dn_s || want.gsc != L->gsc)
+        return fail(GRIM_ERR_ARG, "block layout differs from grimoire_tmoe_layout(H, I)");
+    if (M < 0) return fail(GRIM_ERR_SHAPE, "M=%d", M);
+    if (scratch_bytes < grimoire_tmoe_scratch_bytes(L, M))
+        return fail(GRIM_ERR_WORKSPACE, "scratch %zu < %zu bytes", scratch_bytes,
+                    grimoire_tmoe_scratch_bytes(L, M));
+    return GRIM_OK;
+}
+
+// one expert's rows through the grouped bf16 GEMM: counts/offsets at the
+// scratch tail
+static int tmoe_gemm(hipStream_t st, const uint16_t* Wb, int N, int K, const uint16_t* A, float* out,
+                     int M, int32_t* cnt_off) {
+    hipError_t e = tmoe_set_rows(st, cnt_off, M);
+    if (e != hipSuccess) return status(e);
+    grim_quant_weight w{GRIM_FMT_BF16, N, K, 0, int64_t(K) * 2,
+                        reinterpret_cast<const uint8_t*>(Wb), nullptr, nullptr};
+    return grimoire_moe_grouped_gemm(st, &w, N, 0, A, 0, out, 0, cnt_off + 1, cnt_off, 1, M);
+}
+
+int grimoire_tmoe_expert_gemm(void* stream, const uint8_t* block, const grim_nv_expert_layout* L,
+                              int gate_up, float s0, float s1, const uint16_t* A, float* out,
+                              int M, void* scratch, size_t scratch_bytes) {
+    if (int r = tmoe_prefill_check(block, L, M, A, out, scratch, scratch_bytes)) return r;
+    if (M == 0) return GRIM_OK;
+    hipStream_t st = S(stream);
+    const int H = L->H, I = L->I;
+    const int N = gate_up ? 2 * I : H, K = gate_up ? H : I;
+    uint16_t* Wb = static_cast<uint16_t*>(scratch);
+    int32_t* cnt_off = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(scratch) +
+                                                  grimoire_tmoe_scratch_bytes(L, M) - 256);
+    hipError_t e = tmoe_decode_bf16(st, block + (gate_up ? L->gu_p : L->dn_p),
+                                    block + (gate_up ? L->gu_s : L->dn_s), N, K, Wb);
+    if (e != hipSuccess) return status(e);
+    if (int r = tmoe_gemm(st, Wb, N, K, A, out, M, cnt_off)) return r;
+    return status(tmoe_scale_cols(st, out, M, N, gate_up ? I : N, s0, gate_up ? s1 : s0));
+}
+
+int grimoire_tmoe_expert_ffn(void* stream, const uint8_t* block, const grim_nv_expert_layout* L,
+                             float sg, float su, float sd, const uint16_t* A, uint16_t* hbuf,
+                             float* out, int M, void* scratch, size_t scratch_bytes) {
+    if (int r = tmoe_prefill_check(block, L, M, A, out, scratch, scratch_bytes)) return r;
+    if (!hbuf) return fail(GRIM_ERR_ARG, "null hbuf");
+    if (M == 0) return GRIM_OK;
+    hipStream_t st = S(stream);
+    const int H = L->H, I = L->I;
+    uint8_t* sb = static_cast<uint8_t*>(scratch);
+    uint16_t* Wb = reinterpret_cast<uint16_t*>(sb);
+    float* gu = reinterpret_cast<float*>(sb + size_t(2) * I * H * 2);
+    int32_t* cnt_off = reinterpret_cast<int32_t*>(sb + grimoire_tmoe_scratch_bytes(L, M) - 256);
+    hipError_t e = tmoe_decode_bf16(st, block + L->gu_p, block + L->gu_s, 2 * I, H, Wb);
+    if (e != hipSuccess) return status(e);
+    if (int r = tmoe_gemm(st, Wb, 2 * I, H, A, gu, M, cnt_off)) return r;
+    e = tmoe_swiglu(st, gu, M, I, sg, su, hbuf);
+    if (e == hipSuccess) e = tmoe_decode_bf16(st, block + L->dn_p, block + L->dn_s, H, I, Wb);
+    if (e != hipSuccess) return status(e);
+    if (int r = tmoe_gemm(st, Wb, H, I, hbuf, out, M, cnt_off)) return r;
+    return status(tmoe_scale_cols(st, out, M, H, H, sd, sd));
+}
+
 int grimoire_tmoe_place(void* stream, const uint8_t** eptr, int e, uint8_t* dst_block,
                         const uint8_t* src_block, size_t bytes) {
     if (!eptr || !dst_block || e < 0) return fail(GRIM_ERR_ARG, "null table/block or e < 0");

@@ -227,6 +227,97 @@ __global__ __launch_bounds__(kTmThreads) void tmoe_down_kernel(TmoeArgs a) {
     }
 }
 
+// Prefill on one expert block: the block's NVFP4 rows decoded into bf16
+// scratch rows (exact: an e2m1 value times an E4M3 scale has at most 6
+// significant bits), which the grouped bf16 GEMM then reads; the fp32
+// projection scales are applied to the GEMM's fp32 output, as the
+// reference's launch_nvfp4_expert_gemm does (tiered_moe.hpp:83-93).
+__global__ __launch_bounds__(kTmThreads) void nvfp4_to_bf16(const uint8_t* __restrict__ pay,
+                                                            const uint8_t* __restrict__ sc,
+                                                            int N, int K,
+                                                            uint16_t* __restrict__ out) {
+    // one thread per 32-element chunk: 16 payload bytes, two scale bytes
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int cpr = K / 32;
+    if (i >= int64_t(N) * cpr) return;
+    const int n = int(i / cpr), c = int(i % cpr);
+    const uint4 p = *reinterpret_cast<const uint4*>(pay + int64_t(n) * (K / 2) + c * 16);
+    const uint32_t s2 = load_s2(sc + int64_t(n) * (K / 16) + c * 2);
+    const float b0 = e4m3_f32(s2 & 0xFFu), b1 = e4m3_f32((s2 >> 8) & 0xFFu);
+    const uint32_t w[4] = {p.x, p.y, p.z, p.w};
+    uint32_t o[16];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const f32x2 v[4] = {__builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 0),
+                            __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 1),
+                            __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 2),
+                            __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[d], 1.0f, 3)};
+        const float bs = d < 2 ? b0 : b1;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            o[4 * d + b] = uint32_t(f32_to_bf16(v[b].x * bs)) |
+                           (uint32_t(f32_to_bf16(v[b].y * bs)) << 16);
+    }
+    uint4* dst = reinterpret_cast<uint4*>(out + int64_t(n) * K + c * 32);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dst[q] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+}
+
+// out[m][n] *= (n < split ? s0 : s1) over [M][N]
+__global__ __launch_bounds__(kTmThreads) void scale_cols(float* __restrict__ out, int64_t total,
+                                                         int N, int split, float s0, float s1) {
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += int64_t(gridDim.x) * blockDim.x)
+        out[i] *= (int(i % N) < split ? s0 : s1);
+}
+
+// h[m][i] = bf16(silu(s_g * gu[m][i]) * (s_u * gu[m][I + i]))
+__global__ __launch_bounds__(kTmThreads) void swiglu_bf16(const float* __restrict__ gu, int M,
+                                                          int I, float sg, float su,
+                                                          uint16_t* __restrict__ h) {
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < int64_t(M) * I;
+         i += int64_t(gridDim.x) * blockDim.x) {
+        const int64_t m = i / I, c = i % I;
+        const float g = gu[m * 2 * I + c] * sg, u = gu[m * 2 * I + I + c] * su;
+        h[i] = f32_to_bf16(silu(g) * u);
+    }
+}
+
+__global__ void set_rows(int32_t* cnt_off, int M) {
+    if (threadIdx.x == 0) { cnt_off[0] = M; cnt_off[1] = 0; }
+}
+
+static unsigned ew_blocks(int64_t n) {
+    const int64_t b = (n + kTmThreads - 1) / kTmThreads;
+    return unsigned(b < 1 ? 1 : (b > 8192 ? 8192 : b));
+}
+
+hipError_t tmoe_decode_bf16(hipStream_t st, const uint8_t* pay, const uint8_t* sc, int N, int K,
+                            uint16_t* out) {
+    const int64_t items = int64_t(N) * (K / 32);
+    hipLaunchKernelGGL(nvfp4_to_bf16, dim3(unsigned((items + kTmThreads - 1) / kTmThreads)),
+                       dim3(kTmThreads), 0, st, pay, sc, N, K, out);
+    return hipGetLastError();
+}
+
+hipError_t tmoe_scale_cols(hipStream_t st, float* out, int M, int N, int split, float s0, float s1) {
+    hipLaunchKernelGGL(scale_cols, dim3(ew_blocks(int64_t(M) * N)), dim3(kTmThreads), 0, st, out,
+                       int64_t(M) * N, N, split, s0, s1);
+    return hipGetLastError();
+}
+
+hipError_t tmoe_swiglu(hipStream_t st, const float* gu, int M, int I, float sg, float su,
+                       uint16_t* h) {
+    hipLaunchKernelGGL(swiglu_bf16, dim3(ew_blocks(int64_t(M) * I)), dim3(kTmThreads), 0, st, gu,
+                       M, I, sg, su, h);
+    return hipGetLastError();
+}
+
+hipError_t tmoe_set_rows(hipStream_t st, int32_t* cnt_off, int M) {
+    hipLaunchKernelGGL(set_rows, dim3(1), dim3(kWave), 0, st, cnt_off, M);
+    return hipGetLastError();
+}
+
 __global__ void tmoe_store_ptr(const uint8_t** table, int e, const uint8_t* p) {
     if (threadIdx.x == 0) table[e] = p;
 }

@@ -62,6 +62,31 @@ class TieredLayer:
         self.blocks[e] = dst
 
 
+def _scratch(L, M, device):
+    n = int(lib().grimoire_tmoe_scratch_bytes(C.byref(L), M))
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def expert_gemm(block, L, gate_up, s0, s1, A, out, scratch=None, stream=None):
+    """launch_nvfp4_expert_gemm (tiered_moe.hpp:83-93): out fp32 = A (bf16 bits) x W^T."""
+    _dev(A)
+    M = A.shape[0]
+    scratch = _scratch(L, M, A.device) if scratch is None else scratch
+    check(lib().grimoire_tmoe_expert_gemm(_stream(stream), _p(block), C.byref(L), int(gate_up),
+                                          float(s0), float(s1), _p(A), _p(out), M, _p(scratch),
+                                          scratch.numel()), "tmoe_expert_gemm")
+
+
+def expert_ffn(block, L, sg, su, sd, A, hbuf, out, scratch=None, stream=None):
+    """launch_nvfp4_expert_ffn (tiered_moe.hpp:95-107): SwiGLU FFN of one expert."""
+    _dev(A)
+    M = A.shape[0]
+    scratch = _scratch(L, M, A.device) if scratch is None else scratch
+    check(lib().grimoire_tmoe_expert_ffn(_stream(stream), _p(block), C.byref(L), float(sg),
+                                         float(su), float(sd), _p(A), _p(hbuf), _p(out), M,
+                                         _p(scratch), scratch.numel()), "tmoe_expert_ffn")
+
+
 class Heat:
     """grim_heat: decayed routing counts per (layer, expert) and swap proposals."""
 

@@ -393,6 +393,24 @@ int grimoire_tmoe_down(void* stream, const grim_tiered_moe_view* v, const int32_
 int grimoire_tmoe_place(void* stream, const uint8_t** eptr, int e, uint8_t* dst_block,
                         const uint8_t* src_block, size_t bytes);
 
+/* Prefill on one expert block (tiered_moe.hpp:83-107).  The caller's
+ * device scratch holds grimoire_tmoe_scratch_bytes(L, M) bytes (the block
+ * decoded to bf16, the fp32 gate|up rows of the FFN, two counters).
+ *   expert_gemm: out[M][N] fp32 = A[M][K] (bf16 rows) x W^T, W = gate|up
+ *     (gate_up = 1: N = 2I, K = H; columns [0, I) x s0, [I, 2I) x s1) or
+ *     down (N = H, K = I; x s0).  Replaces launch_nvfp4_expert_gemm.
+ *   expert_ffn: hbuf[M][I] = bf16(silu(s_g A W_g^T) * (s_u A W_u^T)),
+ *     out[M][H] = s_d hbuf W_d^T.  Replaces launch_nvfp4_expert_ffn.
+ * The block may be in device or pinned host memory; it is read once, by
+ * the decode into the scratch. */
+size_t grimoire_tmoe_scratch_bytes(const grim_nv_expert_layout* L, int M);
+int grimoire_tmoe_expert_gemm(void* stream, const uint8_t* block, const grim_nv_expert_layout* L,
+                              int gate_up, float s0, float s1, const uint16_t* A, float* out,
+                              int M, void* scratch, size_t scratch_bytes);
+int grimoire_tmoe_expert_ffn(void* stream, const uint8_t* block, const grim_nv_expert_layout* L,
+                             float sg, float su, float sd, const uint16_t* A, uint16_t* hbuf,
+                             float* out, int M, void* scratch, size_t scratch_bytes);
+
 /* Expert heat and tier placement (include/b70/expert_heat.hpp). */
 typedef struct grim_heat_params {
     float decay;               /* per call of a layer, 0.95              */

@@ -74,3 +74,49 @@ def test_tmoe_place_moves_between_tiers(gpu):
     assert not layer.blocks[1].is_cuda
     assert torch.equal(h0, h1) and torch.equal(y0, y1)
     assert torch.equal(layer.blocks[1], torch.from_numpy(blocks_np[1]))
+
+
+@pytest.mark.parametrize("H,I,M,host", [(512, 256, 37, False), (2048, 768, 130, True),
+                                        (1024, 512, 1, False)])
+def test_expert_gemm_and_ffn(gpu, H, I, M, host):
+    """launch_nvfp4_expert_gemm / _ffn (tiered_moe.hpp:83-107) against float64
+    products of the block dequantised by the reference's nvfp4_dequant_row:
+    GEMMs rel-L2 1e-5 (bf16 weights exact, fp32 accumulation); the FFN's
+    bf16 h within 2^-7 relative per element (+1e-5 of the largest), its output
+    rel-L2 1e-4."""
+    from tests.test_oracle_tiered import dequant
+    print(f"expert gemm/ffn H={H} I={I} M={M} host={host}", flush=True)
+    lay = O.tmoe_layout(H, I)
+    rng = np.random.default_rng(M + H)
+    b = make_block(lay, rng)
+    g3 = b[lay["gsc"]:lay["gsc"] + 16].view(np.float32)
+    blk = torch.from_numpy(b)
+    blk = blk.pin_memory() if host else blk.to(gpu)
+    L = tiered.layout(H, I)
+    gu, dn = dequant(b, lay, H, I)            # float64, projection scales applied
+    A = torch.randn(M, H, generator=torch.Generator().manual_seed(3)).bfloat16()
+    Ad = A.view(torch.int16).to(gpu)
+    out = torch.empty(M, 2 * I, device=gpu)
+    tiered.expert_gemm(blk, L, True, float(g3[0]), float(g3[1]), Ad, out)
+    Ah = torch.randn(M, I, generator=torch.Generator().manual_seed(4)).bfloat16()
+    out_d = torch.empty(M, H, device=gpu)
+    tiered.expert_gemm(blk, L, False, float(g3[2]), 0.0, Ah.view(torch.int16).to(gpu), out_d)
+    hb = torch.empty(M, I, dtype=torch.int16, device=gpu)
+    y = torch.empty(M, H, device=gpu)
+    tiered.expert_ffn(blk, L, float(g3[0]), float(g3[1]), float(g3[2]), Ad, hb, y)
+    torch.cuda.synchronize()
+
+    def rel(a, w):
+        return float(np.linalg.norm(a - w) / max(np.linalg.norm(w), 1e-30))
+    want = A.double().numpy() @ gu.T
+    assert rel(out.cpu().double().numpy(), want) < 1e-5
+    want_d = Ah.double().numpy() @ dn.T
+    assert rel(out_d.cpu().double().numpy(), want_d) < 1e-5
+    g, u = want[:, :I], want[:, I:]
+    h64 = g / (1 + np.exp(np.minimum(-g, 700.0))) * u
+    hgot = hb.cpu().view(torch.bfloat16).double().numpy()
+    # bf16 rounding (2^-8 relative, doubled) plus the fp32 accumulation of
+    # g and u, which dominates where they nearly cancel
+    assert np.all(np.abs(hgot - h64) <= np.abs(h64) * 2.0 ** -7 + 1e-5 * np.abs(h64).max())
+    want_y = hgot @ dn.T
+    assert rel(y.cpu().double().numpy(), want_y) < 1e-4
