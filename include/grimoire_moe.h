@@ -308,7 +308,8 @@ int grimoire_rmsnorm_residual(void* stream, float* h, const float* r0, const flo
  *
  * GPTQ and INT4 zero-point sources are read by kernels: device memory or
  * hipHostMalloc'd host memory.  Copied parts go through hipMemcpyAsync and
- * may be any host or device memory.  dst->row_bytes must be in/2 and
+ * may be any host or device memory; every source must stay valid until the
+ * stream has passed the call (synchronise before freeing or reusing it).  dst->row_bytes must be in/2 and
  * dst->row_scales in/g (in/32 for MXFP4).
  * ---------------------------------------------------------------------- */
 enum grim_src_kind {
