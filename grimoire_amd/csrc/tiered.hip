@@ -156,7 +156,8 @@ __global__ __launch_bounds__(kTmThreads) void tmoe_down_kernel(TmoeArgs a) {
     const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1), sub = lane % LPR;
     const int g = lane / LPR;
     const int o0 = obase + g * kRows;
-    __shared__ float coef[kTmMaxK];       // w_s * s_down, or NaN for a skipped slot
+    __shared__ float coef[kTmMaxK];       // w_s * s_down
+    __shared__ int on_slot[kTmMaxK];      // 0: slot skipped
     const float* ht = a.h + int64_t(t) * K * I;
     // this wave's slots: ids, weights, block pointers and down scales all
     // requested before any of them is used (three short dependent rounds
@@ -186,7 +187,10 @@ __global__ __launch_bounds__(kTmThreads) void tmoe_down_kernel(TmoeArgs a) {
 #pragma unroll
     for (int j = 0; j < kSlots; ++j) {
         const int s = wave + j * kWaves;
-        if (s < K && lane == 0) coef[s] = onv[j] ? rv[j] * sdv[j] : __builtin_nanf("");
+        if (s < K && lane == 0) {
+            coef[s] = onv[j] ? rv[j] * sdv[j] : 0.0f;
+            on_slot[s] = onv[j] ? 1 : 0;
+        }
         if (!onv[j]) bv[j] = nullptr;
     }
 #pragma unroll
@@ -220,8 +224,7 @@ __global__ __launch_bounds__(kTmThreads) void tmoe_down_kernel(TmoeArgs a) {
     if (row < kPerBlock && obase + row < H) {
         float total = 0.0f;
         for (int s = 0; s < K; ++s) {
-            const float c = coef[s];
-            if (c == c) total = __builtin_fmaf(c, part[s][row], total);   // NaN marks a skip
+            if (on_slot[s]) total = __builtin_fmaf(coef[s], part[s][row], total);
         }
         a.y[int64_t(t) * H + obase + row] = total;
     }
