@@ -95,3 +95,54 @@ def test_zero_tokens_is_a_no_op():
                                          1e-6) == _abi.ERR_ARG
     assert lib.grimoire_rmsnorm_residual(None, 1, None, None, 1, 1.0, None, None, 2, 66,
                                          1e-6) == _abi.ERR_SHAPE
+
+
+def test_ingest_rejections():
+    """grimoire_moe_ingest_projection{,s}: shape, format and alignment checks
+    happen on the host, before anything is launched."""
+    lib = _abi.lib()
+    P = 1 << 12                                     # a fake, aligned address
+    dst = _abi.QuantWeight(fmt=_abi.FMT_INT4, N=64, K=256, row_scales=2, row_bytes=128,
+                           payload=P, scales=P, zeros=P)
+    src = _abi.ExpertSrc(_abi.SRC_GPTQ, 256, 64, 128, P, P, P)
+    ing = lambda s, d, r: lib.grimoire_moe_ingest_projection(None, C.byref(s), C.byref(d), r)
+    assert ing(src, dst, 8) == _abi.ERR_SHAPE                      # rows past N
+    bad = _abi.ExpertSrc(_abi.SRC_GPTQ, 256, 64, 128, P + 2, P, P)
+    assert ing(bad, dst, 0) == _abi.ERR_ARG                         # misaligned qweight
+    nz = _abi.ExpertSrc(_abi.SRC_GPTQ, 256, 64, 128, P, None, P)
+    assert ing(nz, dst, 0) == _abi.ERR_ARG                          # GPTQ without qzeros
+    mx = _abi.ExpertSrc(_abi.SRC_MXFP4_PACKED, 256, 64, 32, P, None, P)
+    assert ing(mx, dst, 0) == _abi.ERR_FORMAT                       # MXFP4 into INT4
+    g64 = _abi.ExpertSrc(_abi.SRC_GPTQ, 256, 64, 64, P, P, P)
+    assert ing(g64, dst, 0) == _abi.ERR_SHAPE                       # row_scales != in/group
+    two = (_abi.ExpertSrc * 2)(src, _abi.ExpertSrc(_abi.SRC_GPTQ, 256, 32, 128, P, P, P))
+    rows = (C.c_int32 * 2)(0, 0)
+    assert lib.grimoire_moe_ingest_projections(None, two, C.cast(rows, C.c_void_p), 2,
+                                               C.byref(dst)) == _abi.ERR_SHAPE   # shapes differ
+    assert lib.grimoire_moe_ingest_projections(None, two, C.cast(rows, C.c_void_p), 0,
+                                               C.byref(dst)) == 0                # nothing to do
+    assert lib.grimoire_moe_int4_to_signed(None, None, 16, None, 0, None, 0, None, 0,
+                                           P) == _abi.ERR_ARG
+
+
+def test_tiered_rejections():
+    lib = _abi.lib()
+    L = _abi.NvExpertLayout()
+    assert lib.grimoire_tmoe_layout(2048, 768, C.byref(L)) == 0
+    v = _abi.TieredMoeView(L, 1 << 12, 16, 8)
+    assert lib.grimoire_tmoe_gate_up(None, C.byref(v), None, None, None, 0) == 0   # M = 0
+    v.top_k = 33
+    assert lib.grimoire_tmoe_gate_up(None, C.byref(v), 1, 1, 1, 1) == _abi.ERR_SHAPE
+    v.top_k = 8
+    L2 = _abi.NvExpertLayout.from_buffer_copy(L)
+    L2.dn_p += 16                                                   # not the library's layout
+    v2 = _abi.TieredMoeView(L2, 1 << 12, 16, 8)
+    assert lib.grimoire_tmoe_down(None, C.byref(v2), 1, 1, 1, 1, 1) == _abi.ERR_ARG
+    need = lib.grimoire_tmoe_scratch_bytes(C.byref(L), 10)
+    assert need >= 2 * 2 * 768 * 2048 + 10 * 2 * 768 * 4
+    assert lib.grimoire_tmoe_expert_gemm(None, 1, C.byref(L), 1, 1.0, 1.0, 1, 1, 10, 1,
+                                         need - 1) == _abi.ERR_WORKSPACE
+    assert lib.grimoire_heat_create(0, 8, None) is None
+    h = lib.grimoire_heat_create(2, 8, None)
+    assert lib.grimoire_heat_propose(h, None, None, None, 0) == _abi.ERR_ARG
+    lib.grimoire_heat_destroy(h)
