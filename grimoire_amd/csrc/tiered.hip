@@ -142,7 +142,7 @@ __global__ __launch_bounds__(kTmThreads) void tmoe_gate_up_kernel(TmoeArgs a) {
 // with id < 0 (or >= E) or weight 0.
 constexpr int kTmMaxK = 32;
 
-template <int LPR>
+template <int LPR, int KW>
 __global__ __launch_bounds__(kTmThreads) void tmoe_down_kernel(TmoeArgs a) {
     constexpr int kWaves = kTmThreads / kWave;
     constexpr int kGroups = kWave / LPR;
@@ -162,7 +162,7 @@ __global__ __launch_bounds__(kTmThreads) void tmoe_down_kernel(TmoeArgs a) {
     // this wave's slots: ids, weights, block pointers and down scales all
     // requested before any of them is used (three short dependent rounds
     // for every slot at once instead of one chain per slot)
-    constexpr int kSlots = kTmMaxK / kWaves;
+    constexpr int kSlots = KW;             // slots per wave: ceil(K / 4)
     int ev[kSlots];
     float rv[kSlots], sdv[kSlots];
     const uint8_t* bv[kSlots];
@@ -191,32 +191,50 @@ __global__ __launch_bounds__(kTmThreads) void tmoe_down_kernel(TmoeArgs a) {
             coef[s] = onv[j] ? rv[j] * sdv[j] : 0.0f;
             on_slot[s] = onv[j] ? 1 : 0;
         }
-        if (!onv[j]) bv[j] = nullptr;
+    }
+    // the dots: two slots at a time, every weight and h load of both issued
+    // before either is used (a skipped slot reads a valid block, masked)
+    float acc[kSlots][kRows];
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j)
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) acc[j][r] = 0.0f;
+    constexpr int kPair = kSlots < 2 ? 1 : 2;
+    for (int c = sub; c < I / 32; c += LPR) {
+#pragma unroll
+        for (int j0 = 0; j0 < kSlots; j0 += kPair) {
+            uint4 pv[kPair][kRows];
+            uint32_t s2[kPair][kRows];
+            float hx[kPair][32];
+#pragma unroll
+            for (int jj = 0; jj < kPair; ++jj) {
+                const int j = j0 + jj;
+                const int s = wave + j * kWaves;
+                const int sc = s < K ? s : K - 1;
+#pragma unroll
+                for (int r = 0; r < kRows; ++r) {
+                    const int o = o0 + r < H ? o0 + r : H - 1;
+                    pv[jj][r] = *reinterpret_cast<const uint4*>(bv[j] + a.dn_p + int64_t(o) * (I / 2) + c * 16);
+                    s2[jj][r] = load_s2(bv[j] + a.dn_s + int64_t(o) * (I / 16) + c * 2);
+                }
+                load_x32(ht + sc * I + c * 32, hx[jj]);
+            }
+#pragma unroll
+            for (int jj = 0; jj < kPair; ++jj)
+#pragma unroll
+                for (int r = 0; r < kRows; ++r) {
+                    const float d = nv_dot32(pv[jj][r], s2[jj][r], hx[jj]);
+                    acc[j0 + jj][r] += onv[j0 + jj] ? d : 0.0f;
+                }
+        }
     }
 #pragma unroll
     for (int j = 0; j < kSlots; ++j) {
         const int s = wave + j * kWaves;
-        const uint8_t* blk = bv[j];
-        if (!blk) continue;                                  // uniform across the wave
-        float acc[kRows] = {0.0f, 0.0f};
-        for (int c = sub; c < I / 32; c += LPR) {
-            uint4 pv[kRows];
-            uint32_t s2[kRows];
-#pragma unroll
-            for (int r = 0; r < kRows; ++r) {
-                const int o = o0 + r < H ? o0 + r : H - 1;
-                pv[r] = *reinterpret_cast<const uint4*>(blk + a.dn_p + int64_t(o) * (I / 2) + c * 16);
-                s2[r] = load_s2(blk + a.dn_s + int64_t(o) * (I / 16) + c * 2);
-            }
-            float hx[32];
-            load_x32(ht + s * I + c * 32, hx);
-#pragma unroll
-            for (int r = 0; r < kRows; ++r) acc[r] += nv_dot32(pv[r], s2[r], hx);
-        }
 #pragma unroll
         for (int r = 0; r < kRows; ++r) {
-            const float d = group_sum<LPR>(acc[r]);
-            if (sub == 0) part[s][g * kRows + r] = d;
+            const float d = group_sum<LPR>(acc[j][r]);
+            if (onv[j] && sub == 0) part[s][g * kRows + r] = d;
         }
     }
     __syncthreads();
@@ -354,13 +372,33 @@ hipError_t tmoe_gate_up(hipStream_t st, const TmoeArgs& a) {
     return hipGetLastError();
 }
 
+#define GRIM_TMD_LAUNCH(LPR_VAL, KW_VAL)                                                            \
+    hipLaunchKernelGGL((tmoe_down_kernel<LPR_VAL, KW_VAL>), grid, dim3(kTmThreads), 0, st, a)
+#define GRIM_TMD_KW(LPR_VAL)                                                                        \
+    switch (kw) {                                                                                  \
+        case 1: GRIM_TMD_LAUNCH(LPR_VAL, 1); break;                                                \
+        case 2: GRIM_TMD_LAUNCH(LPR_VAL, 2); break;                                                \
+        case 4: GRIM_TMD_LAUNCH(LPR_VAL, 4); break;                                                \
+        default: GRIM_TMD_LAUNCH(LPR_VAL, 8); break;                                               \
+    }
+
 hipError_t tmoe_down(hipStream_t st, const TmoeArgs& a) {
     if (a.M <= 0) return hipSuccess;
     if (a.K > kTmMaxK) return hipErrorInvalidValue;
     const int lpr = lanes_for(a.I / 32);
     const int per_block = (kWave / lpr) * 2;
     const dim3 grid(unsigned(int64_t(a.M) * ((a.H + per_block - 1) / per_block)));
-    GRIM_TM_SWITCH(tmoe_down_kernel, lpr, grid);
+    const int need = (a.K + kTmThreads / kWave - 1) / (kTmThreads / kWave);
+    const int kw = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
+    switch (lpr) {
+        case 1: GRIM_TMD_KW(1); break;
+        case 2: GRIM_TMD_KW(2); break;
+        case 4: GRIM_TMD_KW(4); break;
+        case 8: GRIM_TMD_KW(8); break;
+        case 16: GRIM_TMD_KW(16); break;
+        case 32: GRIM_TMD_KW(32); break;
+        default: GRIM_TMD_KW(64); break;
+    }
     return hipGetLastError();
 }
 
