@@ -361,9 +361,39 @@ __global__ __launch_bounds__(256) void rowdot_sigmoid(const float* __restrict__ 
     if (lane == 0) gate[t] = det_sigmoid(a);
 }
 
+// The same with 4 columns per lane per step (float4 of x, four bf16 of w)
+// and the row's loads unrolled 8 deep, so a wave has a whole 2048-wide row
+// in flight instead of one dependent 4-byte load per step.  H % 4 == 0,
+// x rows 16-byte and w 8-byte aligned.
+__global__ __launch_bounds__(256) void rowdot_sigmoid4(const float* __restrict__ x,
+                                                       const uint16_t* __restrict__ w,
+                                                       float* __restrict__ gate, int T, int H) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int t = blockIdx.x * 4 + threadIdx.x / kWave;
+    if (t >= T) return;
+    const float* xr = x + int64_t(t) * H;
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll 8
+    for (int c = lane * 4; c < H; c += kWave * 4) {
+        const float4 v = *reinterpret_cast<const float4*>(xr + c);
+        const uint2 u = *reinterpret_cast<const uint2*>(w + c);
+        a0 = __builtin_fmaf(bits_f(u.x << 16), v.x, a0);
+        a1 = __builtin_fmaf(bits_f(u.x & 0xFFFF0000u), v.y, a1);
+        a2 = __builtin_fmaf(bits_f(u.y << 16), v.z, a2);
+        a3 = __builtin_fmaf(bits_f(u.y & 0xFFFF0000u), v.w, a3);
+    }
+    float a = (a0 + a1) + (a2 + a3);
+    a = group_sum<kWave>(a);
+    if (lane == 0) gate[t] = det_sigmoid(a);
+}
+
 hipError_t rowdot_sigmoid_launch(hipStream_t st, const float* x, const uint16_t* w, float* gate,
                                  int T, int H) {
-    hipLaunchKernelGGL(rowdot_sigmoid, dim3((T + 3) / 4), dim3(256), 0, st, x, w, gate, T, H);
+    if (H % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+        (reinterpret_cast<uintptr_t>(w) & 7) == 0)
+        hipLaunchKernelGGL(rowdot_sigmoid4, dim3((T + 3) / 4), dim3(256), 0, st, x, w, gate, T, H);
+    else
+        hipLaunchKernelGGL(rowdot_sigmoid, dim3((T + 3) / 4), dim3(256), 0, st, x, w, gate, T, H);
     return hipGetLastError();
 }
 
