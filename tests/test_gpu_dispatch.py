@@ -92,7 +92,8 @@ def test_unpermute_bit_exact(gpu, T, K, H):
 
 @pytest.mark.parametrize("T,K,H,shared,outs", [(1, 8, 2048, True, "both"), (33, 10, 2048, True, "f32"),
                                                (5, 4, 2880, False, "bf"), (3, 8, 7168, True, "both"),
-                                               (2, 2, 9000, True, "both"), (7, 3, 12, False, "both")])
+                                               (2, 2, 9000, True, "both"), (7, 3, 12, False, "both"),
+                                               (3, 16, 1024, True, "both"), (4, 1, 256, False, "f32")])
 def test_rmsnorm_moe_residual(gpu, T, K, H, shared, outs):
     """launch_rmsnorm_moe_residual_batched (src/prefill.cpp:1004-1045): the residual
     update is bit-exact (same fma order); the normalised output differs only by the

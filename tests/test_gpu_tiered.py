@@ -22,7 +22,8 @@ def _close(got, want, tol=1e-5):
 
 
 @pytest.mark.parametrize("H,I,K,E,M,host_every", [(2048, 768, 8, 16, 1, 3), (2048, 768, 8, 16, 4, 0),
-                                                  (256, 128, 3, 6, 5, 2), (3072, 640, 4, 8, 2, 4)])
+                                                  (256, 128, 3, 6, 5, 2), (3072, 640, 4, 8, 2, 4),
+                                                  (256, 128, 17, 24, 2, 5), (512, 256, 1, 4, 3, 0)])
 def test_tmoe_parity(gpu, H, I, K, E, M, host_every):
     print(f"tmoe H={H} I={I} K={K} E={E} M={M} host_every={host_every}", flush=True)
     lay = O.tmoe_layout(H, I)
