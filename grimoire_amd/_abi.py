@@ -130,6 +130,7 @@ SIGNATURES = {
     "grimoire_moe_router_logits": (I32, [P, P, P, P, I32, I32, I32]),
     "grimoire_moe_router_topk": (I32, [P, P, I32, I32, P, P, I32]),
     "grimoire_moe_router_topk_batched": (I32, [P, P, I32, I32, I32, P, P, I32]),
+    "grimoire_moe_router_topk_bf16_batched": (I32, [P, P, I32, I32, I32, P, P, I32]),
     "grimoire_moe_router_topk_sigmoid": (I32, [P, P, P, I32, I32, I32, P, P, I32, F32]),
     "grimoire_moe_router_topk_group": (I32, [P, P, P, I32, I32, I32, I32, I32, P, P, I32, F32]),
     "grimoire_moe_gate_up": (I32, [P, LP, P, P, P]),

@@ -320,6 +320,19 @@ int grimoire_moe_router_topk_batched(void* stream, const float* logits, int toke
     return topk_common(stream, a);
 }
 
+int grimoire_moe_router_topk_bf16_batched(void* stream, const uint16_t* logits, int tokens,
+                                          int n_experts, int top_k, int32_t* out_expert,
+                                          float* out_weight, int normalize) {
+    if (tokens <= 0) return GRIM_OK;
+    if (!logits || !out_expert || !out_weight) return fail(GRIM_ERR_ARG, "null pointer");
+    if (n_experts <= 0 || n_experts > 512)
+        return fail(GRIM_ERR_SHAPE, "n_experts=%d (1..512)", n_experts);
+    if (top_k <= 0 || top_k > 16 || top_k > n_experts)
+        return fail(GRIM_ERR_SHAPE, "top_k=%d (1..16)", top_k);
+    return status(topk_bf16_launch(S(stream), logits, tokens, n_experts, top_k, normalize,
+                                   out_expert, out_weight));
+}
+
 int grimoire_moe_router_topk_sigmoid(void* stream, const float* logits, const uint16_t* bias_bf16,
                                      int tokens, int n_experts, int top_k, int32_t* out_expert,
                                      float* out_weight, int normalize, float scaling) {

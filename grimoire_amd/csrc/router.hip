@@ -23,6 +23,30 @@ __global__ __launch_bounds__(kTopkWaves * kWave) void topk_kernel(
               topk_group, out_e + int64_t(t) * K, out_w + int64_t(t) * K, gsel[wv], gscore[wv]);
 }
 
+// launch_router_topk_bf16_batched (src/ops.cpp:1425-1480): the batched
+// softmax top-k (mode 1) on bf16 logits
+__global__ __launch_bounds__(kTopkWaves * kWave) void topk_bf16_kernel(
+    const uint16_t* __restrict__ logits, int T, int E, int K, int normalize,
+    int32_t* __restrict__ out_e, float* __restrict__ out_w) {
+    __shared__ float gsel[kTopkWaves][512];
+    __shared__ float gscore[kTopkWaves][64];
+    const int wv = threadIdx.x / kWave;
+    const int t = blockIdx.x * kTopkWaves + wv;
+    if (t >= T) return;   // whole wave exits together
+    float lv[kMaxV];
+    topk_load(logits + int64_t(t) * E, E, lv);
+    topk_wave_regs(lv, E, K, 1, normalize, 1.0f, nullptr, nullptr, 0, 0,
+                   out_e + int64_t(t) * K, out_w + int64_t(t) * K, gsel[wv], gscore[wv]);
+}
+
+hipError_t topk_bf16_launch(hipStream_t st, const uint16_t* logits, int T, int E, int K,
+                            int normalize, int32_t* out_e, float* out_w) {
+    dim3 grid((T + kTopkWaves - 1) / kTopkWaves);
+    hipLaunchKernelGGL(topk_bf16_kernel, grid, dim3(kTopkWaves * kWave), 0, st, logits, T, E, K,
+                       normalize, out_e, out_w);
+    return hipGetLastError();
+}
+
 hipError_t topk_launch(hipStream_t st, const TopkArgs& a) {
     dim3 grid((a.T + kTopkWaves - 1) / kTopkWaves);
     hipLaunchKernelGGL(topk_kernel, grid, dim3(kTopkWaves * kWave), 0, st, a.logits, a.T, a.E,

@@ -19,6 +19,8 @@ struct TopkArgs {
 };
 
 hipError_t topk_launch(hipStream_t st, const TopkArgs& a);
+hipError_t topk_bf16_launch(hipStream_t st, const uint16_t* logits, int T, int E, int K,
+                            int normalize, int32_t* out_e, float* out_w);
 hipError_t router_logits_launch(hipStream_t st, const float* W, const float* x,
                                 const float* bias, float* logits, int T, int E, int H);
 hipError_t rowdot_sigmoid_launch(hipStream_t st, const float* x, const uint16_t* w, float* gate,

@@ -147,6 +147,18 @@ __device__ __forceinline__ void topk_load(const float* __restrict__ row, int E, 
     }
 }
 
+// bf16 logits, widened exactly to fp32 (launch_router_topk_bf16_batched)
+__device__ __forceinline__ void topk_load(const uint16_t* __restrict__ row, int E,
+                                          float (&lv)[kMaxV]) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int V = (E + kWave - 1) / kWave;
+#pragma unroll
+    for (int j = 0; j < kMaxV; ++j) {
+        const int e = lane * V + j;
+        lv[j] = bf16_to_f32(row[(j < V && e < E) ? e : 0]);
+    }
+}
+
 // Top-k of one token by one wave from logits held as topk_load leaves
 // them.  mode 0: softmax (decode semantics); 1: softmax batched semantics
 // (normalize == 0 -> raw logits); 2: sigmoid + bf16 bias; 3: group-limited

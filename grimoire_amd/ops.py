@@ -60,6 +60,16 @@ def launch_router_topk_batched(logits, tokens, n_experts, top_k, out_expert, out
                                                  int(normalize)), "router_topk_batched")
 
 
+def launch_router_topk_bf16_batched(logits_bf16, tokens, n_experts, top_k, out_expert,
+                                    out_weight, normalize=True, stream=None):
+    """launch_router_topk_bf16_batched (src/ops.cpp:1425): logits as bf16 bits."""
+    _dev(logits_bf16)
+    check(lib().grimoire_moe_router_topk_bf16_batched(_stream(stream), _p(logits_bf16), tokens,
+                                                      n_experts, top_k, _p(out_expert),
+                                                      _p(out_weight), int(normalize)),
+          "router_topk_bf16_batched")
+
+
 def launch_router_topk_k2(logits, bias_bf16, tokens, n_experts, top_k, out_expert, out_weight,
                           normalize=True, scaling=1.0, stream=None):
     """launch_router_topk_k2 (src/ops.cpp:2059): sigmoid + selection-only bias."""

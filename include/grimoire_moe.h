@@ -137,6 +137,13 @@ int grimoire_moe_router_topk_batched(void* stream, const float* logits, int toke
                                      int n_experts, int top_k, int32_t* out_expert,
                                      float* out_weight, int normalize);
 
+/* The batched top-k on bf16 logits [T][E] (widened exactly to fp32; same
+ * picks, ties and weights as grimoire_moe_router_topk_batched).  Replaces
+ * launch_router_topk_bf16_batched (src/ops.cpp:1425). */
+int grimoire_moe_router_topk_bf16_batched(void* stream, const uint16_t* logits, int tokens,
+                                          int n_experts, int top_k, int32_t* out_expert,
+                                          float* out_weight, int normalize);
+
 /* Sigmoid scoring with a selection-only bf16 bias (may be NULL): rank on
  * sigmoid(l) + bias[e], weight = unbiased sigmoid(l), divided by the sum of
  * the picks when `normalize`, then multiplied by `scaling`.

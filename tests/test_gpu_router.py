@@ -56,6 +56,22 @@ def test_topk_softmax_bit_exact(gpu, T, E, K, normalize):
     assert torch.equal(ow.cpu(), ww), (ow.cpu() - ww).abs().max()
 
 
+@pytest.mark.parametrize("T,E,K", [(1, 128, 8), (40, 512, 10), (9, 300, 7)])
+@pytest.mark.parametrize("normalize", [True, False])
+def test_topk_bf16_batched_bit_exact(gpu, T, E, K, normalize):
+    """launch_router_topk_bf16_batched (src/ops.cpp:1425): the batched
+    semantics on bf16 logits (bf16 rounding adds many exact ties)."""
+    print(f"topk bf16 T={T} E={E} K={K} norm={normalize}", flush=True)
+    lb = _ties(T, E, E * K + 1).bfloat16()
+    oe = torch.empty(T, K, dtype=torch.int32, device=gpu)
+    ow = torch.empty(T, K, dtype=torch.float32, device=gpu)
+    ops.launch_router_topk_bf16_batched(lb.view(torch.int16).to(gpu), T, E, K, oe, ow, normalize)
+    torch.cuda.synchronize()
+    we, ww = O.topk_softmax(lb.float().contiguous(), K, normalize, batched=True)
+    assert torch.equal(oe.cpu(), we)
+    assert torch.equal(ow.cpu(), ww)
+
+
 @pytest.mark.parametrize("T,E,K,scaling", [(1, 128, 8, 1.0), (16, 100, 8, 2.5), (32, 512, 16, 1.0)])
 def test_topk_sigmoid_bit_exact(gpu, T, E, K, scaling):
     print(f"topk sigmoid T={T} E={E} K={K}", flush=True)
