@@ -147,6 +147,11 @@ SIGNATURES = {
     "grimoire_moe_unpermute": (I32, [P, P, P, P, P, I32, I32, I32]),
     "grimoire_moe_unpermute_bf16": (I32, [P, P, P, P, P, I32, I32, I32]),
     "grimoire_moe_combine": (I32, [P, P, P, P, P, P, P, I32, I32, I32]),
+    "grimoire_moe_unpermute_range": (I32, [P, P, P, P, P, I32, I32, I32, I32, I32, I32]),
+    "grimoire_moe_permute_rows_bf16": (I32, [P, P, P, P, I32, I32]),
+    "grimoire_moe_swiglu_bf16": (I32, [P, P, P, I32, I32]),
+    "grimoire_moe_scale_by_sigmoid": (I32, [P, P, P, I32]),
+    "grimoire_moe_scale_by_sigmoid_batched": (I32, [P, P, P, I32, I32]),
     "grimoire_moe_rmsnorm_residual": (I32, [P, P, P, P, P, P, P, F32, P, P, I32, I32, I32,
                                             F32]),
     "grimoire_rmsnorm_residual": (I32, [P, P, P, P, P, F32, P, P, I32, I32, F32]),

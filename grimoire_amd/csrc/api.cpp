@@ -18,6 +18,7 @@
 #include "gemm.hpp"
 #include "gemm_i8.hpp"
 #include "gemv.hpp"
+#include "elementwise.hpp"
 #include "ingest.hpp"
 #include "tiered.hpp"
 #include "router.hpp"
@@ -750,6 +751,50 @@ int grimoire_tmoe_place(void* stream, const uint8_t** eptr, int e, uint8_t* dst_
         if (c != hipSuccess) return status(c);
     }
     return status(tmoe_store(st, eptr, e, dst_block));
+}
+
+int grimoire_moe_unpermute_range(void* stream, const float* src, const int32_t* inverse,
+                                 const float* route_weight, float* dst, int tokens, int top_k,
+                                 int hidden, int p0, int p1, int accumulate) {
+    if (p0 < 0 || p1 < p0) return fail(GRIM_ERR_ARG, "route range [%d, %d)", p0, p1);
+    CombineArgs a{src, 0, inverse, route_weight, nullptr, 0, nullptr, dst, tokens, top_k, hidden};
+    a.p0 = p0;
+    a.p1 = p1;
+    a.accumulate = accumulate ? 1 : 0;
+    return combine_common(stream, a);
+}
+
+int grimoire_moe_permute_rows_bf16(void* stream, const float* src, const int32_t* perm_token,
+                                   uint16_t* dst, int rows, int width) {
+    if (rows <= 0) return GRIM_OK;
+    if (!src || !perm_token || !dst) return fail(GRIM_ERR_ARG, "null pointer");
+    if (width <= 0) return fail(GRIM_ERR_SHAPE, "width=%d", width);
+    if ((width & 3) == 0 && ((reinterpret_cast<uintptr_t>(src) & 15) ||
+                             (reinterpret_cast<uintptr_t>(dst) & 7)))
+        return fail(GRIM_ERR_ARG, "src 16-byte / dst 8-byte alignment");
+    return status(permute_rows_bf16_launch(S(stream), src, perm_token, dst, rows, width));
+}
+
+int grimoire_moe_swiglu_bf16(void* stream, const uint16_t* gu, uint16_t* out, int tokens,
+                             int inter) {
+    if (tokens <= 0) return GRIM_OK;
+    if (!gu || !out) return fail(GRIM_ERR_ARG, "null pointer");
+    if (inter <= 0) return fail(GRIM_ERR_SHAPE, "inter=%d", inter);
+    return status(swiglu_bf16_launch(S(stream), gu, out, tokens, inter));
+}
+
+int grimoire_moe_scale_by_sigmoid(void* stream, float* x, const float* g, int n) {
+    if (n <= 0) return GRIM_OK;
+    if (!x || !g) return fail(GRIM_ERR_ARG, "null pointer");
+    return status(scale_by_sigmoid_launch(S(stream), x, g, n, 0));
+}
+
+int grimoire_moe_scale_by_sigmoid_batched(void* stream, float* x, const float* gate, int tokens,
+                                          int hidden) {
+    if (tokens <= 0) return GRIM_OK;
+    if (!x || !gate) return fail(GRIM_ERR_ARG, "null pointer");
+    if (hidden <= 0) return fail(GRIM_ERR_SHAPE, "hidden=%d", hidden);
+    return status(scale_by_sigmoid_launch(S(stream), x, gate, int64_t(tokens) * hidden, hidden));
 }
 
 int grimoire_moe_quant_limbs(void* stream, const float* src, int rows, int n, int8_t* dst,

@@ -239,14 +239,16 @@ template <bool SRC_BF16, int KT>
 __global__ __launch_bounds__(kDispThreads) void combine_kernel(
     const void* __restrict__ src, const int32_t* __restrict__ inverse,
     const float* __restrict__ rw, const void* __restrict__ shared_src, int shared_bf16,
-    const float* __restrict__ gate, float* __restrict__ dst, int H, int K) {
+    const float* __restrict__ gate, float* __restrict__ dst, int H, int K, int p0, int p1,
+    int accumulate) {
     const int t = blockIdx.x;
     int p[KT];
     float w[KT];
 #pragma unroll
     for (int s = 0; s < KT; ++s) {
         const int sc = s < K ? s : K - 1;
-        p[s] = s < K ? inverse[int64_t(t) * K + sc] : -1;
+        const int q = s < K ? inverse[int64_t(t) * K + sc] : -1;
+        p[s] = (q >= p0 && q < p1) ? q - p0 : -1;   // a route of another range: skipped
         w[s] = rw[int64_t(t) * K + sc];
     }
     const float g = gate ? gate[t] : 1.0f;
@@ -264,6 +266,10 @@ __global__ __launch_bounds__(kDispThreads) void combine_kernel(
             a1[s] = combine_load<SRC_BF16>(src, row, H, d1);
         }
         float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+        if (accumulate) {
+            v0 = *reinterpret_cast<const float4*>(dst + int64_t(t) * H + d0);
+            v1 = *reinterpret_cast<const float4*>(dst + int64_t(t) * H + d1);
+        }
 #pragma unroll
         for (int s = 0; s < KT; ++s) {
             const bool on = p[s] >= 0;
@@ -296,7 +302,7 @@ static void combine_k(hipStream_t st, const CombineArgs& a) {
 #define GRIM_COMBINE(KT)                                                                          \
     hipLaunchKernelGGL((combine_kernel<SRC_BF16, KT>), dim3(a.T), dim3(kDispThreads), 0, st,      \
                        a.src, a.inverse, a.rw, a.shared_src, a.shared_bf16, a.gate, a.dst, a.H,   \
-                       a.K)
+                       a.K, a.p0, a.p1, a.accumulate)
     switch (a.K) {
         case 1: GRIM_COMBINE(1); break;
         case 2: GRIM_COMBINE(2); break;

@@ -32,6 +32,8 @@ struct CombineArgs {
     const float* gate;      // [T] or null
     float* dst;             // [T][H]
     int T, K, H;
+    int p0 = 0, p1 = 0x7FFFFFFF;  // routes with inverse in [p0, p1) read src row p - p0
+    int accumulate = 0;           // dst += instead of dst =
 };
 
 // Fused combine + residual + RMSNorm (src/prefill.cpp:1004-1045); K == 0 is

@@ -171,6 +171,43 @@ def launch_rmsnorm_residual_batched(h, r0, r1, weight, out, tokens, hidden, eps,
                                           hidden, float(eps)), "rmsnorm_residual")
 
 
+def launch_moe_unpermute_range(src, inverse, route_weight, dst, tokens, top_k, hidden, p0, p1,
+                               accumulate=False, stream=None):
+    """launch_moe_unpermute_range (src/prefill.cpp:2674)."""
+    _dev(src)
+    check(lib().grimoire_moe_unpermute_range(_stream(stream), _p(src), _p(inverse),
+                                             _p(route_weight), _p(dst), tokens, top_k, hidden, p0,
+                                             p1, int(accumulate)), "unpermute_range")
+
+
+def launch_permute_rows_bf16(src, perm_token, dst, rows, width, stream=None):
+    """launch_permute_rows_bf16 (src/prefill.cpp:2644)."""
+    _dev(src)
+    check(lib().grimoire_moe_permute_rows_bf16(_stream(stream), _p(src), _p(perm_token), _p(dst),
+                                               rows, width), "permute_rows_bf16")
+
+
+def launch_swiglu_bf16(gu, out, tokens, inter, stream=None):
+    """launch_swiglu_bf16 (src/prefill.cpp:2541)."""
+    _dev(gu)
+    check(lib().grimoire_moe_swiglu_bf16(_stream(stream), _p(gu), _p(out), tokens, inter),
+          "swiglu_bf16")
+
+
+def launch_scale_by_sigmoid_batched(x, gate, tokens, hidden, stream=None):
+    """launch_scale_by_sigmoid_batched (src/prefill.cpp:2610)."""
+    _dev(x)
+    check(lib().grimoire_moe_scale_by_sigmoid_batched(_stream(stream), _p(x), _p(gate), tokens,
+                                                      hidden), "scale_by_sigmoid_batched")
+
+
+def launch_scale_by_sigmoid(x, g, n, stream=None):
+    """launch_scale_by_sigmoid (src/ops.cpp:1491)."""
+    _dev(x)
+    check(lib().grimoire_moe_scale_by_sigmoid(_stream(stream), _p(x), _p(g), n),
+          "scale_by_sigmoid")
+
+
 def grouped_gemm(w: Weight, N, swiglu, A, out, offsets, counts, num_experts, total_rows,
                  a_pair=False, out_bf16=False, stream=None):
     """launch_moe_mxfp4_grouped (src/gemm_fast.cpp:2343) for int8/mxfp4/bf16."""

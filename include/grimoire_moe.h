@@ -257,6 +257,31 @@ int grimoire_moe_unpermute_bf16(void* stream, const uint16_t* src, const int32_t
                                 const float* route_weight, float* dst, int tokens,
                                 int top_k, int hidden);
 
+/* One route range of a grouped expert pass: a route whose dispatch row p
+ * lies in [p0, p1) reads src row p - p0; dst = the fma chain over slots in
+ * slot order, starting from 0, or from dst when accumulate != 0.  Replaces
+ * launch_moe_unpermute_range (src/prefill.cpp:2674-2688). */
+int grimoire_moe_unpermute_range(void* stream, const float* src, const int32_t* inverse,
+                                 const float* route_weight, float* dst, int tokens, int top_k,
+                                 int hidden, int p0, int p1, int accumulate);
+
+/* dst[r] = bf16(src[perm_token[r]]) (round to nearest even) over `width`
+ * columns.  Replaces launch_permute_rows_bf16 (src/prefill.cpp:2644). */
+int grimoire_moe_permute_rows_bf16(void* stream, const float* src, const int32_t* perm_token,
+                                   uint16_t* dst, int rows, int width);
+
+/* out[t][d] = bf16(silu(g) * u), g = gu[t][d], u = gu[t][inter + d], all
+ * bf16.  Replaces launch_swiglu_bf16 (src/prefill.cpp:2541). */
+int grimoire_moe_swiglu_bf16(void* stream, const uint16_t* gu, uint16_t* out, int tokens,
+                             int inter);
+
+/* x[i] *= sigmoid(g[0]) over n elements (launch_scale_by_sigmoid,
+ * src/ops.cpp:1491); the batched form scales row t by sigmoid(gate[t])
+ * (launch_scale_by_sigmoid_batched, src/prefill.cpp:2610). */
+int grimoire_moe_scale_by_sigmoid(void* stream, float* x, const float* g, int n);
+int grimoire_moe_scale_by_sigmoid_batched(void* stream, float* x, const float* gate, int tokens,
+                                          int hidden);
+
 /* Combine with the gated shared expert: dst[t] = unpermute(...)[t] +
  * gate[t] * shared_src[t] (gate NULL = 1).  Replaces the unpermute plus the
  * shared-expert add of src/grimoire.cpp:23118 and :23247-23283. */

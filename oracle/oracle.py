@@ -326,3 +326,38 @@ class Heat:
                 break
             out.append((hot[i][1], hot[i][2], cold[i][1], cold[i][2]))
         return out
+
+
+# --- small launchers around the path (numpy restatements) -------------------
+
+def permute_rows_bf16(src, perm, width):
+    """launch_permute_rows_bf16 (src/prefill.cpp:2644-2652): bf16 bits (int16)."""
+    return src[perm.long()].contiguous().bfloat16().view(torch.int16)
+
+
+def unpermute_range(src, inverse, rw, dst0, T, K, H, p0, p1, accumulate):
+    """launch_moe_unpermute_range (src/prefill.cpp:2674-2688), fp32 fma chain
+    in slot order (numpy float32; fma emulated in float64 then rounded, exact
+    for a single fma)."""
+    s = src.numpy().astype(np.float32)
+    inv = inverse.numpy().reshape(T, K)
+    w = rw.numpy().reshape(T, K).astype(np.float32)
+    v = dst0.numpy().astype(np.float32).copy() if accumulate else np.zeros((T, H), np.float32)
+    for t in range(T):
+        for k in range(K):
+            p = int(inv[t, k])
+            if p0 <= p < p1:
+                v[t] = (np.float64(w[t, k]) * s[p - p0].astype(np.float64) + v[t].astype(np.float64)).astype(np.float32)
+    return torch.from_numpy(v)
+
+
+def swiglu_bf16(gu_bits, T, inter):
+    """launch_swiglu_bf16 (src/prefill.cpp:2541-2558) in float64, then bf16."""
+    gu = gu_bits.view(torch.bfloat16).double().reshape(T, 2 * inter)
+    g, u = gu[:, :inter], gu[:, inter:]
+    return (g / (1 + torch.exp(-g)) * u)
+
+
+def scale_by_sigmoid_batched(x, gate):
+    """launch_scale_by_sigmoid_batched (src/prefill.cpp:2610-2622) in float64."""
+    return x.double() * (1.0 / (1.0 + torch.exp(-gate.double())))[:, None]

@@ -148,3 +148,70 @@ def test_rmsnorm_residual(gpu, T, H, addends):
     err = (out.cpu() - want).abs().max().item()
     assert err <= 1e-5 * want.abs().max().item(), err
     assert (obf.cpu().int() - want_bf.int()).abs().max().item() <= 1
+
+
+
+@pytest.mark.parametrize("T,K,H", [(33, 10, 2048), (5, 4, 2880)])
+def test_unpermute_range_bit_exact(gpu, T, K, H):
+    """launch_moe_unpermute_range (src/prefill.cpp:2674): two ranges, the
+    second accumulating, against the oracle's fma chain; the full range equals
+    the plain unpermute bit for bit."""
+    print(f"unpermute_range T={T} K={K} H={H}", flush=True)
+    R = T * K
+    g = torch.Generator().manual_seed(T)
+    src = torch.randn(R, H, generator=g)
+    inv = torch.randperm(R, generator=g).int()
+    inv[::7] = -1
+    rw = torch.rand(R, generator=g)
+    cut = R // 3
+    dst = torch.empty(T, H, device=gpu)
+    ops.launch_moe_unpermute_range(src[:cut].to(gpu), inv.to(gpu), rw.to(gpu), dst, T, K, H, 0, cut)
+    ops.launch_moe_unpermute_range(src[cut:].to(gpu), inv.to(gpu), rw.to(gpu), dst, T, K, H, cut, R,
+                                   accumulate=True)
+    torch.cuda.synchronize()
+    want = O.unpermute_range(src[:cut], inv, rw, torch.zeros(T, H), T, K, H, 0, cut, False)
+    want = O.unpermute_range(src[cut:], inv, rw, want, T, K, H, cut, R, True)
+    assert torch.equal(dst.cpu(), want)
+    full = torch.empty(T, H, device=gpu)
+    ops.launch_moe_unpermute_range(src.to(gpu), inv.to(gpu), rw.to(gpu), full, T, K, H, 0, R)
+    torch.cuda.synchronize()
+    assert torch.equal(full.cpu(), O.unpermute(src, inv, rw, T, K, H))
+
+
+@pytest.mark.parametrize("rows,width", [(300, 2048), (7, 130)])
+def test_permute_rows_bf16_exact(gpu, rows, width):
+    print(f"permute_rows rows={rows} width={width}", flush=True)
+    g = torch.Generator().manual_seed(rows)
+    src = torch.randn(64, width, generator=g)
+    perm = torch.randint(0, 64, (rows,), dtype=torch.int32, generator=g)
+    dst = torch.empty(rows, width, dtype=torch.int16, device=gpu)
+    ops.launch_permute_rows_bf16(src.to(gpu), perm.to(gpu), dst, rows, width)
+    torch.cuda.synchronize()
+    assert torch.equal(dst.cpu(), O.permute_rows_bf16(src, perm, width))
+
+
+def test_swiglu_and_scale_by_sigmoid(gpu):
+    """launch_swiglu_bf16 within one bf16 ulp of float64 (plus 1e-6 of the
+    largest for cancellation); scale_by_sigmoid{,_batched} within 2e-7
+    relative."""
+    print("swiglu_bf16 / scale_by_sigmoid", flush=True)
+    g = torch.Generator().manual_seed(5)
+    T, I, H = 17, 768, 1000
+    gu = (torch.randn(T, 2 * I, generator=g) * 3).bfloat16().view(torch.int16)
+    out = torch.empty(T, I, dtype=torch.int16, device=gpu)
+    ops.launch_swiglu_bf16(gu.to(gpu), out, T, I)
+    x = torch.randn(T, H, generator=g)
+    gate = torch.randn(T, generator=g) * 4
+    xd = x.to(gpu)
+    ops.launch_scale_by_sigmoid_batched(xd, gate.to(gpu), T, H)
+    x1 = torch.randn(H, generator=g)
+    x1d = x1.to(gpu)
+    ops.launch_scale_by_sigmoid(x1d, gate[:1].to(gpu), H)
+    torch.cuda.synchronize()
+    want = O.swiglu_bf16(gu, T, I)
+    got = out.cpu().view(torch.bfloat16).double()
+    assert ((got - want).abs() <= want.abs() * 2.0 ** -8 + 1e-6 * want.abs().max()).all()
+    wx = O.scale_by_sigmoid_batched(x, gate)
+    assert ((xd.cpu().double() - wx).abs() <= 2e-7 * wx.abs() + 1e-30).all()
+    w1 = x1.double() / (1 + torch.exp(-gate[0].double()))
+    assert ((x1d.cpu().double() - w1).abs() <= 2e-7 * w1.abs() + 1e-30).all()

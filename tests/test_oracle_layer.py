@@ -254,6 +254,34 @@ def test_rmsnorm_residual_pinned():
     assert torch.equal(hn3, h + r1)
 
 
+def test_small_launchers_pinned():
+    """unpermute_range over the full route range is the pinned unpermute bit
+    for bit, an empty range with accumulate leaves dst, and a range reads
+    src rows shifted by p0 (brute force); permute_rows is torch's bf16."""
+    g = torch.Generator().manual_seed(21)
+    T, K, H = 4, 3, 8
+    R = T * K
+    src = torch.randn(R, H, generator=g)
+    inv = torch.randperm(R, generator=g).int()
+    inv[2] = -1
+    rw = torch.rand(R, generator=g)
+    full = O.unpermute_range(src, inv, rw, torch.zeros(T, H), T, K, H, 0, R, False)
+    assert torch.equal(full, O.unpermute(src, inv, rw, T, K, H))
+    d0 = torch.randn(T, H, generator=g)
+    assert torch.equal(O.unpermute_range(src, inv, rw, d0, T, K, H, 5, 5, True), d0)
+    part = O.unpermute_range(src[4:9], inv, rw, torch.zeros(T, H), T, K, H, 4, 9, False)
+    for t in range(T):
+        want = torch.zeros(H)
+        for k in range(K):
+            p = int(inv[t * K + k])
+            if 4 <= p < 9:
+                want = want + rw[t * K + k] * src[p]
+        assert (part[t] - want).abs().max() < 1e-6
+    perm = torch.tensor([3, 0, 0, 2], dtype=torch.int32)
+    x = torch.randn(4, 6, generator=g)
+    assert torch.equal(O.permute_rows_bf16(x, perm, 6), x[perm.long()].bfloat16().view(torch.int16))
+
+
 # -------------------------------------------------------------- expert ffn
 
 def _small_layer(fmt, E=8, H=256, I=128, K=3, shared=False, seed=0):
