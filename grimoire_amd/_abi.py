@@ -177,6 +177,9 @@ SIGNATURES = {
     "grimoire_moe_quant_limbs": (I32, [P, P, I32, I32, P, P]),
     "grimoire_moe_grouped_gemm_i8": (I32, [P, QWP, I32, I32, P, P, P, P, P, I32, I32]),
     "grimoire_xe2_grouped_mxfp4_bf16": (None, [P, P, P, P, P, I32, I32, P, P, I32, P]),
+    "grimoire_xe2_grouped_mxfp4_bf16_full": (None, [P, P, P, P, P, I32, I32, P, P, I32, P]),
+    "grimoire_xe2_grouped_mxfp4_bf16_m8": (None, [P, P, P, P, P, I32, I32, P, P, I32, P]),
+    "grimoire_xe2_grouped_mxfp4_bf16_m16": (None, [P, P, P, P, P, I32, I32, P, P, I32, P]),
     "grimoire_xe2_grouped_w4a16": (None, [P, P, P, P, P, I32, I32, P, P, I32, I32, P]),
     "grimoire_xe2_fused_moe_gate_up_mxfp4_silu_bf16": (None, [P, P, P, P, P, I32, I32, P, I32, P]),
     "grimoire_moe_forward_workspace_bytes": (SZ, [LP, I32]),

@@ -902,6 +902,30 @@ void grimoire_xe2_grouped_mxfp4_bf16(void* stream, const void* a, const unsigned
     bridge_common(stream, w, n, 0, 0, a, d, rows_per_expert, num_experts);
 }
 
+void grimoire_xe2_grouped_mxfp4_bf16_full(void* stream, const void* a, const unsigned char* b,
+                                          const unsigned char* scales, void* d, int n, int k,
+                                          const int* rows_per_expert, const int* expert_ids,
+                                          int num_experts, int* atomic_buffer) {
+    grimoire_xe2_grouped_mxfp4_bf16(stream, a, b, scales, d, n, k, rows_per_expert, expert_ids,
+                                    num_experts, atomic_buffer);
+}
+
+void grimoire_xe2_grouped_mxfp4_bf16_m8(void* stream, const void* a, const unsigned char* b,
+                                        const unsigned char* scales, void* d, int n, int k,
+                                        const int* rows_per_expert, const int* expert_ids,
+                                        int num_experts, int* atomic_buffer) {
+    grimoire_xe2_grouped_mxfp4_bf16(stream, a, b, scales, d, n, k, rows_per_expert, expert_ids,
+                                    num_experts, atomic_buffer);
+}
+
+void grimoire_xe2_grouped_mxfp4_bf16_m16(void* stream, const void* a, const unsigned char* b,
+                                         const unsigned char* scales, void* d, int n, int k,
+                                         const int* rows_per_expert, const int* expert_ids,
+                                         int num_experts, int* atomic_buffer) {
+    grimoire_xe2_grouped_mxfp4_bf16(stream, a, b, scales, d, n, k, rows_per_expert, expert_ids,
+                                    num_experts, atomic_buffer);
+}
+
 void grimoire_xe2_grouped_w4a16(void* stream, const void* activations_bf16,
                                 const unsigned char* weights_int4, const void* scales_bf16,
                                 void* outputs_bf16, int n, int k, const int* rows_per_expert,

@@ -527,6 +527,24 @@ void grimoire_xe2_grouped_mxfp4_bf16(void* stream, const void* a, const unsigned
                                      const int* rows_per_expert, const int* expert_ids,
                                      int num_experts, int* atomic_buffer);
 
+/* The reference's tile-policy variants of the same product
+ * (src/xe2_grouped_bridge.cpp:149 full-tile, :163 8-row, :171 16-row
+ * tiles), bound by name at src/grimoire.cpp:20638-20642.  Same arguments
+ * and results; this library picks its tiles itself, so all three run the
+ * kernel above. */
+void grimoire_xe2_grouped_mxfp4_bf16_full(void* stream, const void* a, const unsigned char* b,
+                                          const unsigned char* scales, void* d, int n, int k,
+                                          const int* rows_per_expert, const int* expert_ids,
+                                          int num_experts, int* atomic_buffer);
+void grimoire_xe2_grouped_mxfp4_bf16_m8(void* stream, const void* a, const unsigned char* b,
+                                        const unsigned char* scales, void* d, int n, int k,
+                                        const int* rows_per_expert, const int* expert_ids,
+                                        int num_experts, int* atomic_buffer);
+void grimoire_xe2_grouped_mxfp4_bf16_m16(void* stream, const void* a, const unsigned char* b,
+                                         const unsigned char* scales, void* d, int n, int k,
+                                         const int* rows_per_expert, const int* expert_ids,
+                                         int num_experts, int* atomic_buffer);
+
 /* Signed-s4 weights [E][n][k/2] with bf16 group scales [E][n][k/group].
  * Declared, never defined, in the reference (src/xe2_grouped_bridge.hpp:22). */
 void grimoire_xe2_grouped_w4a16(void* stream, const void* activations_bf16,

@@ -131,3 +131,24 @@ def test_fused_gate_up_bridge(gpu):
                                               k, rows.to(gpu), E)
     torch.cuda.synchronize()
     _bf16_close(d.cpu().float(), want, "fused gate_up bridge")
+
+
+def test_grouped_mxfp4_bridge_variants(gpu):
+    """The _full / _m8 / _m16 symbols (src/xe2_grouped_bridge.cpp:149-177)
+    give the base bridge's result bit for bit."""
+    from grimoire_amd import _abi
+    E, n, k = 3, 256, 512
+    rows = _rows(E, 7)
+    R = int(rows.sum())
+    w = make_mxfp4(E * n, k, seed=13)
+    a = torch.randn(R, k, generator=torch.Generator().manual_seed(8)).bfloat16().to(gpu)
+    pw, ps, rd = w.payload.to(gpu), w.scales.to(gpu), rows.to(gpu)
+    base = torch.empty(R, n, dtype=torch.bfloat16, device=gpu)
+    ops.xe2_grouped_mxfp4_bf16(a, pw, ps, base, n, k, rd, E)
+    for v in ("full", "m8", "m16"):
+        d = torch.full((R, n), float("nan"), dtype=torch.bfloat16, device=gpu)
+        getattr(_abi.lib(), f"grimoire_xe2_grouped_mxfp4_bf16_{v}")(
+            None, a.data_ptr(), pw.data_ptr(), ps.data_ptr(), d.data_ptr(), n, k, rd.data_ptr(),
+            None, E, None)
+        torch.cuda.synchronize()
+        assert torch.equal(d.view(torch.int16), base.view(torch.int16)), v
