@@ -13,11 +13,15 @@
         2.5, MXFP4.
 
 Router weights fp32 N(0, 0.02); activations bf16 N(0, 1) held as fp32.
-Expert popularity skew is a router bias b_e = -s * log(pi(e) + 1), pi a
-seeded permutation of the experts.
+Expert popularity skew (C3, C4) is a router logit bias b_e = z(pi(e)), pi a
+seeded permutation of the experts and z fitted so that the share of routes
+the expert of popularity rank r receives follows Zipf(s): route probability
+per token q_r = min(1, lam * (r + 1)^-s) with sum_r q_r = K (an expert
+cannot take a token twice, so the head saturates at every token).
 """
 from __future__ import annotations
 
+import functools
 import math
 from dataclasses import dataclass
 from typing import Optional
@@ -87,6 +91,40 @@ def make_layer(cfg: Config, device="cpu", seed=0) -> MoeLayer:
     return MoeLayer(cfg.H, cfg.I, cfg.E, cfg.K, gu, dn, router.contiguous(), sgu, sdn, sgw, True)
 
 
+def zipf_route_prob(E: int, K: int, s: float) -> torch.Tensor:
+    """Target route probability per token of the expert at each popularity
+    rank: q_r = min(1, lam * (r + 1)^-s), lam set so that sum q = K."""
+    p = (torch.arange(E, dtype=torch.float64) + 1.0) ** -s
+    lo, hi = 0.0, float(K) / float(p[-1])
+    for _ in range(200):
+        lam = 0.5 * (lo + hi)
+        if float(torch.clamp(lam * p, max=1.0).sum()) > K:
+            hi = lam
+        else:
+            lo = lam
+    return torch.clamp(lo * p, max=1.0)
+
+
+@functools.lru_cache(maxsize=None)
+def zipf_rank_bias(E: int, K: int, s: float, H: int, samples: int = 16384,
+                   iters: int = 160) -> torch.Tensor:
+    """Logit bias per popularity rank that makes top-K routing over router
+    logits N(0, (0.02 * sqrt(H))^2) (router N(0, 0.02) times x N(0, 1))
+    follow zipf_route_prob.  Fitted on a fixed seeded sample of logits by
+    damped updates of log(target / observed); deterministic."""
+    q = zipf_route_prob(E, K, s).float()
+    g = torch.Generator().manual_seed(0x5EED + E * 131 + K)
+    l = torch.randn((samples, E), generator=g) * (0.02 * math.sqrt(H))
+    b = torch.zeros(E)
+    eps = 0.5 / samples
+    for _ in range(iters):
+        idx = torch.topk(l + b, K, dim=1).indices
+        f = torch.bincount(idx.flatten(), minlength=E).float() / samples
+        b += 0.3 * (torch.log(q + eps) - torch.log(f + eps)).clamp(-1.0, 1.0)
+        b -= b.max()
+    return b
+
+
 def make_route_bias(cfg: Config, device="cpu", seed=0) -> Optional[torch.Tensor]:
     g = torch.Generator(device="cpu")
     g.manual_seed(seed * 1000 + 7)
@@ -94,8 +132,8 @@ def make_route_bias(cfg: Config, device="cpu", seed=0) -> Optional[torch.Tensor]
         if cfg.zipf <= 0:
             return None
         pi = torch.randperm(cfg.E, generator=g)
-        b = -cfg.zipf * torch.log(pi.double() + 1.0)
-        return b.float().to(device)
+        b = zipf_rank_bias(cfg.E, cfg.K, cfg.zipf, cfg.H)[pi]
+        return b.float().contiguous().to(device)
     if cfg.bias_std > 0:
         b = torch.randn((cfg.E,), generator=g) * cfg.bias_std
         if cfg.route == _abi.ROUTE_SIGMOID:
