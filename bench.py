@@ -189,20 +189,20 @@ def prefill_bench(dev, stream, reps=5):
         hq = torch.empty(R, 2 * cfg.I, dtype=torch.int8, device=dev)
         hs = torch.empty(R, device=dev)
         yp = torch.empty(R, cfg.H, device=dev)
-        ops.grouped_gemm_i8(L.gate_up, 2 * cfg.I, True, xq, xs, h, offsets, counts, cfg.E, R,
+        ops.grouped_gemm_i8(L.gate_up, 2 * cfg.I, True, xq, xs, h, offsets, counts, cfg.E, te, tmb,
                             stream=stream)
         ops.quant_limbs(h, hq, hs, stream=stream)
-        ops.grouped_gemm_i8(L.down, cfg.H, False, hq, hs, yp, offsets, counts, cfg.E, R,
+        ops.grouped_gemm_i8(L.down, cfg.H, False, hq, hs, yp, offsets, counts, cfg.E, te, tmb,
                             stream=stream)
         torch.cuda.synchronize()
         with Timer(stream) as tg:
             for _ in range(reps):
                 ops.grouped_gemm_i8(L.gate_up, 2 * cfg.I, True, xq, xs, h, offsets, counts, cfg.E,
-                                    R, stream=stream)
+                                    te, tmb, stream=stream)
         gu_ms = tg.ms() / reps
         with Timer(stream) as td:
             for _ in range(reps):
-                ops.grouped_gemm_i8(L.down, cfg.H, False, hq, hs, yp, offsets, counts, cfg.E, R,
+                ops.grouped_gemm_i8(L.down, cfg.H, False, hq, hs, yp, offsets, counts, cfg.E, te, tmb,
                                     stream=stream)
         dn_ms = td.ms() / reps
         cnt = counts.cpu()

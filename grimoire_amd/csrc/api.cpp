@@ -171,94 +171,14 @@ int down_common(void* stream, const grim_moe_layer* L, const grim_quant_weight* 
     return status(decode_launch(S(stream), L->down.fmt, a));
 }
 
-// Library-held scratch for the bridges, whose signatures carry none.
-struct BridgeScratch {
-    int device = -1;
-    void* p = nullptr;
-    size_t bytes = 0;
-};
-std::mutex g_scratch_mu;
-std::vector<BridgeScratch> g_scratch;
-
-void* bridge_scratch(size_t bytes) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-    std::lock_guard<std::mutex> lk(g_scratch_mu);
-    for (auto& s : g_scratch)
-        if (s.device == dev) {
-            if (s.bytes >= bytes) return s.p;
-            if (hipFree(s.p) != hipSuccess) return nullptr;
-            s.p = nullptr;
-            if (hipMalloc(&s.p, bytes) != hipSuccess) { s.bytes = 0; return nullptr; }
-            s.bytes = bytes;
-            return s.p;
-        }
-    BridgeScratch s;
-    s.device = dev;
-    if (hipMalloc(&s.p, bytes) != hipSuccess) return nullptr;
-    s.bytes = bytes;
-    g_scratch.push_back(s);
-    return s.p;
-}
-
-// rows per expert -> counts, exclusive offsets and the (expert, m-block)
-// tile table, by one 1024-thread block: each thread sums a contiguous run
-// of experts, a block scan gives every run its row and tile offsets, then
-// each thread writes its run.
-__global__ __launch_bounds__(1024) void tiles_from_counts(const int* __restrict__ rows, int ne, int mc,
-                                                          int32_t* __restrict__ counts,
-                                                          int32_t* __restrict__ offsets,
-                                                          int32_t* __restrict__ tile_e,
-                                                          int32_t* __restrict__ tile_mb, int tmax,
-                                                          int32_t* __restrict__ n_tiles) {
-    __shared__ int s_rows[1024], s_tiles[1024];
-    const int tid = threadIdx.x;
-    const int per = (ne + 1023) / 1024;
-    const int e0 = tid * per, e1 = min(e0 + per, ne);
-    int rsum = 0, tsum = 0;
-    for (int e = e0; e < e1; ++e) {
-        const int c = rows[e] > 0 ? rows[e] : 0;
-        rsum += c;
-        tsum += (c + mc - 1) / mc;
-    }
-    s_rows[tid] = rsum;
-    s_tiles[tid] = tsum;
-    __syncthreads();
-    for (int d = 1; d < 1024; d <<= 1) {   // inclusive scan
-        const int r = tid >= d ? s_rows[tid - d] : 0, t = tid >= d ? s_tiles[tid - d] : 0;
-        __syncthreads();
-        s_rows[tid] += r;
-        s_tiles[tid] += t;
-        __syncthreads();
-    }
-    int off = s_rows[tid] - rsum, nt = s_tiles[tid] - tsum;
-    for (int e = e0; e < e1; ++e) {
-        const int c = rows[e] > 0 ? rows[e] : 0;
-        counts[e] = c;
-        offsets[e] = off;
-        off += c;
-        for (int mb = 0; mb * mc < c; ++mb, ++nt)
-            if (nt < tmax) { tile_e[nt] = e; tile_mb[nt] = mb; }
-    }
-    if (tid == 1023) *n_tiles = s_tiles[1023] < tmax ? s_tiles[1023] : tmax;
-}
-
-constexpr int kBridgeTileCap = 1 << 16;
-
-// Shared body of the three bridges: counts -> tile table, then one grouped
-// GEMM over [ne][n (x2 for swiglu)][k] packed experts.
+// Shared body of the three bridges: one grouped GEMM over [ne][n (x2 for
+// swiglu)][k] packed experts in rows mode (each work-group forms the
+// expert offsets and tile order from rows_per_expert in LDS), so a bridge
+// call allocates nothing and shares nothing with other calls.
 int bridge_common(void* stream, const grim_quant_weight& w, int N, int I, int swiglu,
                   const void* a, void* d, const int* rows, int ne) {
-    const size_t need = size_t(4 * ne + 2 * kBridgeTileCap + 4) * sizeof(int32_t);
-    int32_t* sc = static_cast<int32_t*>(bridge_scratch(need));
-    if (!sc) return fail(GRIM_ERR_WORKSPACE, "bridge scratch allocation failed");
-    int32_t* counts = sc;
-    int32_t* offsets = sc + ne;
-    int32_t* tile_e = sc + 2 * ne;
-    int32_t* tile_mb = tile_e + kBridgeTileCap;
-    int32_t* n_tiles = tile_mb + kBridgeTileCap;
-    hipLaunchKernelGGL(tiles_from_counts, dim3(1), dim3(1024), 0, S(stream), rows, ne, kGemmBM,
-                       counts, offsets, tile_e, tile_mb, kBridgeTileCap, n_tiles);
+    if (ne > kGemmRowsMaxExperts)
+        return fail(GRIM_ERR_SHAPE, "bridge: num_experts %d > %d", ne, kGemmRowsMaxExperts);
     GemmArgs g{};
     g.w = view(w);
     g.N = N;
@@ -269,12 +189,9 @@ int bridge_common(void* stream, const grim_quant_weight& w, int N, int I, int sw
     g.out_bf16 = 1;
     g.A = static_cast<const uint16_t*>(a);
     g.out = d;
-    g.offsets = offsets;
-    g.counts = counts;
-    g.tile_e = tile_e;
-    g.tile_mb = tile_mb;
-    g.tmax = kBridgeTileCap;
-    g.n_tiles_dev = n_tiles;
+    g.rows = rows;
+    g.ne = ne;
+    g.tmax = 0;
     g.T_sh = 0;
     return status(gemm_launch(S(stream), w.fmt, g));
 }
@@ -807,27 +724,18 @@ int grimoire_moe_quant_limbs(void* stream, const float* src, int rows, int n, in
 
 int grimoire_moe_grouped_gemm_i8(void* stream, const grim_quant_weight* w, int N, int swiglu,
                                  const int8_t* A, const float* a_scale, float* out,
-                                 const int32_t* offsets, const int32_t* counts, int num_experts,
-                                 int total_rows) {
-    if (!w || !A || !a_scale || !out || !offsets || !counts) return fail(GRIM_ERR_ARG, "null pointer");
+                                 const int32_t* offsets, const int32_t* counts,
+                                 const int32_t* tile_e, const int32_t* tile_mb, int tmax,
+                                 int num_experts) {
+    if (!w || !A || !a_scale || !out || !offsets || !counts || !tile_e || !tile_mb)
+        return fail(GRIM_ERR_ARG, "null pointer");
     if (w->fmt != GRIM_FMT_INT8) return fail(GRIM_ERR_FORMAT, "INT8 weights only");
     int r = check_weight(w, "grouped weight", int64_t(num_experts) * N, w->K);
     if (r) return r;
     if (swiglu && N % 2) return fail(GRIM_ERR_SHAPE, "swiglu needs even N");
     if (!gemm_i8_shape_ok(N, w->K, swiglu ? N / 2 : 0, swiglu))
         return fail(GRIM_ERR_SHAPE, "K=%d: a multiple of 64 in [192, 8192]", w->K);
-    if (total_rows <= 0) return GRIM_OK;
-    const int tmax = num_experts + (total_rows + kGemmBM - 1) / kGemmBM;
-    const size_t need = size_t(2 * tmax + 4) * sizeof(int32_t);
-    int32_t* sc = static_cast<int32_t*>(bridge_scratch(need + size_t(2 * num_experts) * 4));
-    if (!sc) return fail(GRIM_ERR_WORKSPACE, "scratch allocation failed");
-    int32_t* tile_e = sc;
-    int32_t* tile_mb = sc + tmax;
-    int32_t* n_tiles = sc + 2 * tmax;
-    int32_t* cnt2 = n_tiles + 4;
-    int32_t* off2 = cnt2 + num_experts;
-    hipLaunchKernelGGL(tiles_from_counts, dim3(1), dim3(1024), 0, S(stream), counts, num_experts,
-                       kGemmBM, cnt2, off2, tile_e, tile_mb, tmax, n_tiles);
+    if (tmax <= 0) return GRIM_OK;
     GemmI8Args g{};
     g.w = w->payload;
     g.ws = static_cast<const float*>(w->scales);
@@ -844,7 +752,7 @@ int grimoire_moe_grouped_gemm_i8(void* stream, const grim_quant_weight* w, int N
     g.tile_e = tile_e;
     g.tile_mb = tile_mb;
     g.tmax = tmax;
-    g.n_tiles_dev = n_tiles;
+    g.n_tiles_dev = nullptr;   // the table is -1 padded to tmax
     return status(gemm_i8_launch(S(stream), g));
 }
 
@@ -860,18 +768,8 @@ int grimoire_moe_grouped_gemm(void* stream, const grim_quant_weight* w, int N, i
     if (w->K % 64) return fail(GRIM_ERR_SHAPE, "K=%d not a multiple of 64", w->K);
     if (swiglu && (N % 2 || a_pair)) return fail(GRIM_ERR_SHAPE, "swiglu needs even N, bf16 A");
     if (total_rows <= 0) return GRIM_OK;
-    // counts/offsets live on the device: build the tile table there
-    const int tmax = num_experts + (total_rows + kGemmBM - 1) / kGemmBM;
-    const size_t need = size_t(2 * tmax + 4) * sizeof(int32_t);
-    int32_t* sc = static_cast<int32_t*>(bridge_scratch(need + size_t(2 * num_experts) * 4));
-    if (!sc) return fail(GRIM_ERR_WORKSPACE, "scratch allocation failed");
-    int32_t* tile_e = sc;
-    int32_t* tile_mb = sc + tmax;
-    int32_t* n_tiles = sc + 2 * tmax;
-    int32_t* cnt2 = n_tiles + 4;
-    int32_t* off2 = cnt2 + num_experts;
-    hipLaunchKernelGGL(tiles_from_counts, dim3(1), dim3(1024), 0, S(stream), counts, num_experts,
-                       kGemmBM, cnt2, off2, tile_e, tile_mb, tmax, n_tiles);
+    if (num_experts > kGemmRowsMaxExperts)
+        return fail(GRIM_ERR_SHAPE, "num_experts %d > %d", num_experts, kGemmRowsMaxExperts);
     GemmArgs g{};
     g.w = view(*w);
     g.N = N;
@@ -882,12 +780,9 @@ int grimoire_moe_grouped_gemm(void* stream, const grim_quant_weight* w, int N, i
     g.out_bf16 = swiglu ? 0 : out_bf16;   // SwiGLU: h as bf16 pairs
     g.A = A;
     g.out = out;
-    g.offsets = offsets;
-    g.counts = counts;
-    g.tile_e = tile_e;
-    g.tile_mb = tile_mb;
-    g.tmax = tmax;
-    g.n_tiles_dev = n_tiles;
+    g.offsets = offsets;   // rows mode on the device counts
+    g.rows = counts;
+    g.ne = num_experts;
     return status(gemm_launch(S(stream), w->fmt, g));
 }
 
@@ -895,10 +790,19 @@ void grimoire_xe2_grouped_mxfp4_bf16(void* stream, const void* a, const unsigned
                                      const unsigned char* scales, void* d, int n, int k,
                                      const int* rows_per_expert, const int* expert_ids,
                                      int num_experts, int* atomic_buffer) {
-    (void)expert_ids;
-    (void)atomic_buffer;
+    (void)expert_ids;      // rows are grouped in expert order, as the reference
+    (void)atomic_buffer;   // no work counter: each work-group forms the tile order
+    if (!a || !b || !scales || !d || !rows_per_expert) {
+        fail(GRIM_ERR_ARG, "xe2 mxfp4: null pointer");
+        return;
+    }
+    if (n <= 0 || k <= 0 || num_experts <= 0 || k % 64) {
+        fail(GRIM_ERR_SHAPE, "xe2 mxfp4: n=%d k=%d num_experts=%d (k a multiple of 64)", n, k,
+             num_experts);
+        return;
+    }
     grim_quant_weight w{GRIM_FMT_MXFP4, num_experts * n, k, k / 32, k / 2, b, scales, nullptr};
-    if (check_weight(&w, "xe2 mxfp4", int64_t(num_experts) * n, k) || k % 64) return;
+    if (check_weight(&w, "xe2 mxfp4", int64_t(num_experts) * n, k)) return;
     bridge_common(stream, w, n, 0, 0, a, d, rows_per_expert, num_experts);
 }
 
@@ -932,7 +836,7 @@ void grimoire_xe2_grouped_w4a16(void* stream, const void* activations_bf16,
                                 const int* expert_ids, int num_experts, int group_size,
                                 int* atomic_buffer) {
     (void)expert_ids;      // rows are grouped in expert order, as the reference
-    (void)atomic_buffer;   // no work counter: the tile table is built on the device
+    (void)atomic_buffer;   // no work counter: each work-group forms the tile order
     if (!activations_bf16 || !weights_int4 || !scales_bf16 || !outputs_bf16 || !rows_per_expert) {
         fail(GRIM_ERR_ARG, "xe2 w4a16: null pointer");
         return;
@@ -952,13 +856,18 @@ void grimoire_xe2_fused_moe_gate_up_mxfp4_silu_bf16(void* stream, const void* ac
                                                     const unsigned char* scales, void* outputs,
                                                     int n, int k, const int* rows_per_expert,
                                                     int num_experts, int32_t* atomic_buffer) {
-    (void)atomic_buffer;   // no work counter: the tile table is built on the device
-    grim_quant_weight w{GRIM_FMT_MXFP4, num_experts * 2 * n, k, k / 32, k / 2, weights, scales, nullptr};
-    if (check_weight(&w, "xe2 fused gate_up", int64_t(num_experts) * 2 * n, k) || k % 64 || n % 8) return;
-    if (!activations || !outputs || !rows_per_expert) {
+    (void)atomic_buffer;   // no work counter: each work-group forms the tile order
+    if (!activations || !weights || !scales || !outputs || !rows_per_expert) {
         fail(GRIM_ERR_ARG, "xe2 fused gate_up: null pointer");
         return;
     }
+    if (n <= 0 || k <= 0 || num_experts <= 0 || k % 64 || n % 8) {
+        fail(GRIM_ERR_SHAPE, "xe2 fused gate_up: n=%d k=%d num_experts=%d (k %% 64, n %% 8)", n, k,
+             num_experts);
+        return;
+    }
+    grim_quant_weight w{GRIM_FMT_MXFP4, num_experts * 2 * n, k, k / 32, k / 2, weights, scales, nullptr};
+    if (check_weight(&w, "xe2 fused gate_up", int64_t(num_experts) * 2 * n, k)) return;
     bridge_common(stream, w, 2 * n, n, 1, activations, outputs, rows_per_expert, num_experts);
 }
 

@@ -136,13 +136,66 @@ __device__ __forceinline__ float col_scale(const GemmSrc& w, int64_t row) {
 }
 
 // One (m-tile, column-tile) of the grouped product.
+// Rows mode: tp[e] = m-tiles of the experts before e, rp[e] = their rows
+// (tp[ne], rp[ne] the totals), from rows_per_expert (negative = 0).
+__device__ __forceinline__ int rows_tables(const int* __restrict__ rows, int ne, int* tp, int* rp) {
+    constexpr int PER = kGemmRowsMaxExperts / kGemmThreads;
+    __shared__ int st[kGemmThreads], sr[kGemmThreads];
+    const int tid = threadIdx.x;
+    int c[PER], ts = 0, rs = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int e = tid * PER + j;
+        const int v = e < ne ? rows[e] : 0;
+        c[j] = v > 0 ? v : 0;
+        ts += (c[j] + BM - 1) / BM;
+        rs += c[j];
+    }
+    st[tid] = ts;
+    sr[tid] = rs;
+    __syncthreads();
+    for (int d = 1; d < kGemmThreads; d <<= 1) {   // inclusive scan
+        const int a = tid >= d ? st[tid - d] : 0, b = tid >= d ? sr[tid - d] : 0;
+        __syncthreads();
+        st[tid] += a;
+        sr[tid] += b;
+        __syncthreads();
+    }
+    int t0 = st[tid] - ts, r0 = sr[tid] - rs;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int e = tid * PER + j;
+        if (e <= ne) { tp[e] = t0; rp[e] = r0; }
+        t0 += (c[j] + BM - 1) / BM;
+        r0 += c[j];
+    }
+    const int total = st[kGemmThreads - 1];
+    if (tid == kGemmThreads - 1) { tp[ne] = total; rp[ne] = sr[kGemmThreads - 1]; }
+    __syncthreads();
+    return total;
+}
+
 template <int F, bool SWIGLU, bool APAIR, bool OUT_BF16>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, const GemmSrc& w, bool routed, int ty,
-                                          int nt, uint16_t (*As)[APAIR ? 2 : 1][BM * LDK]) {
+                                          int nt, uint16_t (*As)[APAIR ? 2 : 1][BM * LDK],
+                                          const int* tp, const int* rp) {
     // ---- which rows / weights
     int rows_valid;
     int64_t arow0, wrow0;
-    if (routed) {
+    if (routed && g.rows) {
+        // the expert whose m-tiles hold tile ty: last e with tp[e] <= ty
+        int lo = 0, hi = g.ne - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (tp[mid] <= ty) lo = mid; else hi = mid - 1;
+        }
+        const int e = __builtin_amdgcn_readfirstlane(lo);
+        const int mb = ty - tp[e];
+        rows_valid = min(BM, (rp[e + 1] - rp[e]) - mb * BM);
+        const int off = g.offsets ? __builtin_amdgcn_readfirstlane(g.offsets[e]) : rp[e];
+        arow0 = int64_t(off) + int64_t(mb) * BM;
+        wrow0 = int64_t(e) * g.N;
+    } else if (routed) {
         // table values are the same for the whole work-group: keep them in
         // scalar registers (buffer descriptors built from them must be)
         const int e = __builtin_amdgcn_readfirstlane(g.tile_e[ty]);
@@ -502,8 +555,11 @@ __global__ __launch_bounds__(kGemmThreads, GRIM_GEMM_OCC) void grouped_gemm_kern
     const GemmSrc w{routed ? g.w.payload : g.w_sh.payload, routed ? g.w.scales : g.w_sh.scales,
                     routed ? g.w.row_bytes : g.w_sh.row_bytes, routed ? g.w.row_scales : g.w_sh.row_scales,
                     routed ? g.A : g.A_sh, routed ? g.out : g.out_sh};
+    __shared__ int tp[kGemmRowsMaxExperts + 1], rp[kGemmRowsMaxExperts + 1];
     int total;
-    if (routed) {
+    if (routed && g.rows) {
+        total = rows_tables(g.rows, g.ne, tp, rp);
+    } else if (routed) {
         total = g.n_tiles_dev ? __builtin_amdgcn_readfirstlane(*g.n_tiles_dev) : g.tmax;
         total = total < g.tmax ? total : g.tmax;
     } else {
@@ -513,7 +569,8 @@ __global__ __launch_bounds__(kGemmThreads, GRIM_GEMM_OCC) void grouped_gemm_kern
     const int lo = int(int64_t(total) * xcd / kXcds), hi = int(int64_t(total) * (xcd + 1) / kXcds);
     const int items = (hi - lo) * n_col_tiles;
     for (int i = blockIdx.x / kXcds; i < items; i += per_xcd) {
-        gemm_tile<F, SWIGLU, APAIR, OUT_BF16>(g, w, routed, lo + i / n_col_tiles, i % n_col_tiles, As);
+        gemm_tile<F, SWIGLU, APAIR, OUT_BF16>(g, w, routed, lo + i / n_col_tiles, i % n_col_tiles, As,
+                                              tp, rp);
         __syncthreads();
     }
 }
@@ -533,7 +590,7 @@ static hipError_t launch_kernel(hipStream_t st, const GemmArgs& g, int ntiles) {
         grid = (per_cu > 0 ? per_cu : 1) * cus;
         grid = (grid + kXcds - 1) / kXcds * kXcds;
     }
-    if (g.tmax > 0)
+    if (g.tmax > 0 || g.rows)
         hipLaunchKernelGGL((grouped_gemm_kernel<F, SWIGLU, APAIR, OUT_BF16>), dim3(grid),
                            dim3(kGemmThreads), 0, st, g, ntiles, 0);
     if (g.T_sh > 0) {
@@ -549,7 +606,7 @@ template <int F>
 static hipError_t launch_fmt(hipStream_t st, const GemmArgs& g) {
     const int ntiles = g.swiglu ? (g.I + BN / 2 - 1) / (BN / 2) : (g.N + BN - 1) / BN;
     const int my_max = g.tmax + (g.T_sh > 0 ? (g.T_sh + BM - 1) / BM : 0);
-    if (my_max <= 0 || ntiles <= 0) return hipSuccess;
+    if ((my_max <= 0 && !g.rows) || ntiles <= 0) return hipSuccess;
     if (g.swiglu)
         return g.out_bf16 ? launch_kernel<F, true, false, true>(st, g, ntiles)
                           : launch_kernel<F, true, false, false>(st, g, ntiles);

@@ -21,7 +21,14 @@ struct GemmArgs {
     int tmax;                   // capacity of the tile table
     const int32_t* n_tiles_dev; // live routed tile count (device) or null = tmax
     int T_sh;                   // shared-expert rows (0 = none)
+    // rows mode: rows_per_expert[ne] in place of counts and the tile table;
+    // every work-group forms the tile order (and, without offsets, the
+    // offsets) in LDS, so the caller supplies no scratch
+    const int* rows;
+    int ne;
 };
+
+constexpr int kGemmRowsMaxExperts = 1024;
 
 constexpr int kGemmBM = 128;
 // Bridge-only weight format of the grouped GEMM: signed 4-bit codes

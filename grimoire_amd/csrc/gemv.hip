@@ -58,8 +58,19 @@ void decode_plan(int fmt, DecodeArgs& a, int roles) {
     if (a.xf) {
         // wave-centric gate_up: 4 waves x RU rows (RU 4 for one chunk iteration, else 2)
         const int nci = (a.H / 32 + kWave - 1) / kWave;
-        const int rb = kGemvWaves * (nci == 1 ? 4 : 2);
-        a.gu_rb = (a.I + rb - 1) / rb;
+        int ru = nci == 1 ? 4 : 2;
+        if (nci == 1) {
+            // the row count per wave that levels the work over the 256 CUs:
+            // fewest (work-groups per CU) x (rows per work-group)
+            auto cost = [&](int r) {
+                const int64_t ng = int64_t(a.M) * KS * ((a.I + kGemvWaves * r - 1) / (kGemvWaves * r));
+                return ((ng + 255) / 256) * r;
+            };
+            for (int r : {6, 8})
+                if (cost(r) < cost(ru)) ru = r;
+        }
+        a.gu_ru = ru;
+        a.gu_rb = (a.I + kGemvWaves * ru - 1) / (kGemvWaves * ru);
     }
     a.dn_rb = down_rows_per_block(a.lpr_dn, KS);
     a.dn_wave = 0;

@@ -43,6 +43,7 @@ struct DecodeArgs {
     uint32_t* xf;
     int xf_words;
     int dn_wave;              // wave-centric down (one wave per slot)
+    int gu_ru;                // wave-centric gate_up: row pairs per wave
 };
 
 // Words per token of the formatted h (n = KS * I elements):

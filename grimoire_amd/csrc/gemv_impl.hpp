@@ -865,7 +865,11 @@ inline hipError_t launch_t(hipStream_t st, const DecodeArgs& a) {
         if (a.NG && a.xf) {
             // wave-centric gate_up: NCI chunk iterations of RU rows (4 for one iteration, else 2)
             const int nci = (a.H / 32 + kWave - 1) / kWave;
-            if (nci == 1)
+            if (nci == 1 && a.gu_ru == 6)
+                hipLaunchKernelGGL((moe_gate_up_wave_kernel<F, 6, 1, SH>), dim3(a.NG), dim3(kGemvThreads), 0, st, a);
+            else if (nci == 1 && a.gu_ru == 8)
+                hipLaunchKernelGGL((moe_gate_up_wave_kernel<F, 8, 1, SH>), dim3(a.NG), dim3(kGemvThreads), 0, st, a);
+            else if (nci == 1)
                 hipLaunchKernelGGL((moe_gate_up_wave_kernel<F, 4, 1, SH>), dim3(a.NG), dim3(kGemvThreads), 0, st, a);
             else if (nci == 2)
                 hipLaunchKernelGGL((moe_gate_up_wave_kernel<F, 2, 2, SH>), dim3(a.NG), dim3(kGemvThreads), 0, st, a);

@@ -226,13 +226,36 @@ def quant_limbs(src, dst, scale, stream=None):
           "quant_limbs")
 
 
+def tile_table(counts, mc: int = 128, tmax: int = None):
+    """The (expert, m-block) tile table of the dispatch (src/grimoire.cpp:
+    20743 layout: tile_e / tile_mb, -1 padded to tmax) from per-expert row
+    counts, formed on the host."""
+    c = [max(0, int(v)) for v in torch.as_tensor(counts).cpu().tolist()]
+    te, tm = [], []
+    for e, n in enumerate(c):
+        for mb in range((n + mc - 1) // mc):
+            te.append(e)
+            tm.append(mb)
+    if tmax is None:
+        tmax = max(1, len(te))
+    te += [-1] * (tmax - len(te))
+    tm += [0] * (tmax - len(tm))
+    dev = torch.as_tensor(counts).device
+    return (torch.tensor(te[:tmax], dtype=torch.int32, device=dev),
+            torch.tensor(tm[:tmax], dtype=torch.int32, device=dev))
+
+
 def grouped_gemm_i8(w: Weight, N, swiglu, A, a_scale, out, offsets, counts, num_experts,
-                    total_rows, stream=None):
-    """INT8 experts on the int8 MFMA (limb rows from quant_limbs), fp32 out."""
+                    tile_e=None, tile_mb=None, stream=None):
+    """INT8 experts on the int8 MFMA (limb rows from quant_limbs), fp32 out,
+    walked through the tile table (tile_table(counts) when not given)."""
     _dev(A)
+    if tile_e is None:
+        tile_e, tile_mb = tile_table(counts)
     check(lib().grimoire_moe_grouped_gemm_i8(_stream(stream), w.struct(), N, int(swiglu), _p(A),
                                              _p(a_scale), _p(out), _p(offsets), _p(counts),
-                                             num_experts, total_rows), "grouped_gemm_i8")
+                                             _p(tile_e), _p(tile_mb), int(tile_e.numel()),
+                                             num_experts), "grouped_gemm_i8")
 
 
 # ------------------------------------------------------------------- layer

@@ -484,7 +484,9 @@ int grimoire_heat_propose(const grim_heat* s, const uint8_t* resident, const uin
  *                 (a_pair != 0), out is bf16 [R][N] (out_bf16 != 0) or
  *                 fp32 [R][N].
  * Replaces launch_moe_mxfp4_grouped (src/gemm_fast.cpp:2343-2365) and, with
- * the tile table, gemm_mxfp4_fused_grouped (src/gemm_fast.cpp:1603). */
+ * the tile table, gemm_mxfp4_fused_grouped (src/gemm_fast.cpp:1603).  The
+ * work-groups form the tile order from counts themselves (num_experts <=
+ * 1024); nothing is allocated. */
 int grimoire_moe_grouped_gemm(void* stream, const grim_quant_weight* w, int N, int swiglu,
                               const uint16_t* A, int a_pair, void* out, int out_bf16,
                               const int32_t* offsets, const int32_t* counts,
@@ -500,23 +502,31 @@ int grimoire_moe_quant_limbs(void* stream, const float* src, int rows, int n, in
                              float* scale);
 
 /* Grouped GEMM for INT8 weights (w->fmt GRIM_FMT_INT8, fp32 per-row scales)
- * on limb rows A [R][2K] with scales a_scale [R], grouped by expert as in
- * grimoire_moe_grouped_gemm; out fp32: swiglu != 0 -> h [R][N/2] =
+ * on limb rows A [R][2K] with scales a_scale [R], grouped by expert
+ * (offsets / counts [num_experts]) and walked through the caller's
+ * (expert, 128-row m-block) tile table tile_e / tile_mb [tmax], -1 padded
+ * (as the dispatch writes it); out fp32: swiglu != 0 -> h [R][N/2] =
  * silu(A_r . gate_e) * (A_r . up_e), else [R][N].  The computation of
- * launch_moe_mxfp4_grouped (src/gemm_fast.cpp:2343-2365) for the INT8
- * experts that the reference runs one expert at a time
- * (src/grimoire.cpp:23214-23229). */
+ * launch_moe_mxfp4_grouped (src/gemm_fast.cpp:2343-2365, which takes the
+ * same tile table) for the INT8 experts that the reference runs one expert
+ * at a time (src/grimoire.cpp:23214-23229).  Allocates nothing. */
 int grimoire_moe_grouped_gemm_i8(void* stream, const grim_quant_weight* w, int N, int swiglu,
                                  const int8_t* A, const float* a_scale, float* out,
-                                 const int32_t* offsets, const int32_t* counts, int num_experts,
-                                 int total_rows);
+                                 const int32_t* offsets, const int32_t* counts,
+                                 const int32_t* tile_e, const int32_t* tile_mb, int tmax,
+                                 int num_experts);
 
 /* ------------------------------------------------------------------------
  * Bridges (the vLLM-XPU grouped GEMMs the reference dlopens).  Same
  * argument lists apart from the queue.  rows_per_expert [ne] gives the
  * contiguous row blocks of `a`; expert_ids may be NULL (expert i = block
  * i).  atomic_buffer is accepted and ignored (no persistent tile counter is
- * needed here).
+ * needed here).  A bridge call allocates nothing and keeps no state between
+ * calls: every work-group of its one launch forms the expert offsets and
+ * the tile order from rows_per_expert itself (num_experts <= 1024), so
+ * calls on different streams may run concurrently.  Errors (null pointers,
+ * k not a multiple of 64, ...) launch nothing and leave the message in
+ * grimoire_moe_last_error().
  * ---------------------------------------------------------------------- */
 
 /* d[r][n] = a[r] . dequant(b_e)[n], b u8 [E][n][k/2] MXFP4, scales e8m0

@@ -146,3 +146,32 @@ def test_tiered_rejections():
     h = lib.grimoire_heat_create(2, 8, None)
     assert lib.grimoire_heat_propose(h, None, None, None, 0) == _abi.ERR_ARG
     lib.grimoire_heat_destroy(h)
+
+
+def test_bridge_rejections():
+    """Bridge argument errors are caught on the host (nothing launched) and
+    reported through grimoire_moe_last_error()."""
+    lib = _abi.lib()
+    P = 1 << 12
+    rows = (C.c_int32 * 2)(3, 4)
+    r = C.cast(rows, C.c_void_p)
+
+    def last():
+        return lib.grimoire_moe_last_error().decode()
+
+    lib.grimoire_xe2_grouped_mxfp4_bf16(None, P, P, P, P, 128, 96, r, None, 2, None)
+    assert "multiple of 64" in last()                    # k % 64
+    lib.grimoire_xe2_grouped_mxfp4_bf16(None, P, P, P, P, 128, 128, None, None, 2, None)
+    assert "null pointer" in last()                      # rows_per_expert
+    lib.grimoire_xe2_grouped_mxfp4_bf16(None, None, P, P, P, 128, 128, r, None, 2, None)
+    assert "null pointer" in last()                      # a
+    lib.grimoire_xe2_grouped_mxfp4_bf16_m8(None, P, P, P, None, 128, 128, r, None, 2, None)
+    assert "null pointer" in last()                      # d, through a variant
+    lib.grimoire_xe2_grouped_mxfp4_bf16(None, P, P, P, P, 128, 128, r, None, 2000, None)
+    assert "num_experts" in last()                       # beyond the in-LDS tile order
+    lib.grimoire_xe2_fused_moe_gate_up_mxfp4_silu_bf16(None, P, P, P, P, 100, 128, r, 2, None)
+    assert "n %% 8" in last() or "n % 8" in last()
+    lib.grimoire_xe2_fused_moe_gate_up_mxfp4_silu_bf16(None, P, None, P, P, 128, 128, r, 2, None)
+    assert "null pointer" in last()
+    lib.grimoire_xe2_grouped_w4a16(None, P, P, P, P, 128, 128, r, None, 2, 96, None)
+    assert "group" in last()

@@ -152,3 +152,35 @@ def test_grouped_mxfp4_bridge_variants(gpu):
             None, E, None)
         torch.cuda.synchronize()
         assert torch.equal(d.view(torch.int16), base.view(torch.int16)), v
+
+
+def test_bridges_on_two_streams(gpu):
+    """Bridge calls in flight on two streams at once (the reference runs the
+    shared expert on an auxiliary queue, src/grimoire.cpp:22750-22765) with
+    different expert layouts: each result matches its own reference, so
+    no call's tile order leaks into the other's."""
+    E1, n1, k1 = 7, 256, 512
+    E2, n2, k2 = 3, 192, 1024
+    rows1, rows2 = _rows(E1, 21, hi=300), _rows(E2, 22, hi=90)
+    R1, R2 = int(rows1.sum()), int(rows2.sum())
+    w1 = make_mxfp4(E1 * n1, k1, seed=31)
+    w2 = make_mxfp4(E2 * 2 * n2, k2, seed=32)
+    a1 = torch.randn(R1, k1, generator=torch.Generator().manual_seed(33)).bfloat16()
+    a2 = torch.randn(R2, k2, generator=torch.Generator().manual_seed(34)).bfloat16()
+    want1 = _dense(a1.float(), dequant(w1), rows1, n1)
+    gu = _dense(a2.float(), dequant(w2), rows2, 2 * n2)
+    want2 = gu[:, :n2] / (1.0 + torch.exp(-gu[:, :n2])) * gu[:, n2:]
+    g1 = [t.to(gpu) for t in (a1, w1.payload, w1.scales, rows1)]
+    g2 = [t.to(gpu) for t in (a2, w2.payload, w2.scales, rows2)]
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs1 = [torch.full((R1, n1), float("nan"), dtype=torch.bfloat16, device=gpu) for _ in range(6)]
+    outs2 = [torch.full((R2, n2), float("nan"), dtype=torch.bfloat16, device=gpu) for _ in range(6)]
+    torch.cuda.synchronize()
+    for d1, d2 in zip(outs1, outs2):
+        ops.xe2_grouped_mxfp4_bf16(g1[0], g1[1], g1[2], d1, n1, k1, g1[3], E1, stream=s1)
+        ops.xe2_fused_moe_gate_up_mxfp4_silu_bf16(g2[0], g2[1], g2[2], d2, n2, k2, g2[3], E2,
+                                                  stream=s2)
+    torch.cuda.synchronize()
+    for i, (d1, d2) in enumerate(zip(outs1, outs2)):
+        _bf16_close(d1.cpu().float(), want1, f"stream 1 call {i}")
+        _bf16_close(d2.cpu().float(), want2, f"stream 2 call {i}")

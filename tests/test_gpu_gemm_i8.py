@@ -85,7 +85,7 @@ def test_gemm_i8_exact_on_exact_limbs(gpu):
     q, s = _limbs(gpu, A)
     assert (s.cpu() == 1.0).all()
     out = torch.full((R, N), float("nan"), device=gpu)
-    ops.grouped_gemm_i8(w.to(gpu), N, False, q, s, out, offsets.to(gpu), counts.to(gpu), E, R)
+    ops.grouped_gemm_i8(w.to(gpu), N, False, q, s, out, offsets.to(gpu), counts.to(gpu), E)
     torch.cuda.synchronize()
     want = _dense(A, dequant(w), counts, offsets, N)
     assert rel_l2(out.cpu(), want) < 1e-6
@@ -102,7 +102,7 @@ def test_gemm_i8_plain_ragged(gpu, N, K):
     A = torch.randn(R, K).bfloat16().float()
     q, s = _limbs(gpu, A)
     out = torch.full((R, N), float("nan"), device=gpu)
-    ops.grouped_gemm_i8(w.to(gpu), N, False, q, s, out, offsets.to(gpu), counts.to(gpu), E, R)
+    ops.grouped_gemm_i8(w.to(gpu), N, False, q, s, out, offsets.to(gpu), counts.to(gpu), E)
     torch.cuda.synchronize()
     want = _dense(A, dequant(w), counts, offsets, N)
     assert not torch.isnan(out).any()
@@ -120,7 +120,7 @@ def test_gemm_i8_swiglu_then_down(gpu):
     A = torch.randn(R, H).bfloat16().float()
     q, s = _limbs(gpu, A)
     h = torch.full((R, I), float("nan"), device=gpu)
-    ops.grouped_gemm_i8(wgu.to(gpu), 2 * I, True, q, s, h, offsets.to(gpu), counts.to(gpu), E, R)
+    ops.grouped_gemm_i8(wgu.to(gpu), 2 * I, True, q, s, h, offsets.to(gpu), counts.to(gpu), E)
     torch.cuda.synchronize()
     gu = _dense(A, dequant(wgu), counts, offsets, 2 * I)
     g, u = gu[:, :I], gu[:, I:]
@@ -128,7 +128,7 @@ def test_gemm_i8_swiglu_then_down(gpu):
     assert rel_l2(h.cpu(), h_want) < 2e-4
     hq, hs = _limbs(gpu, h)
     y = torch.full((R, H), float("nan"), device=gpu)
-    ops.grouped_gemm_i8(wdn.to(gpu), H, False, hq, hs, y, offsets.to(gpu), counts.to(gpu), E, R)
+    ops.grouped_gemm_i8(wdn.to(gpu), H, False, hq, hs, y, offsets.to(gpu), counts.to(gpu), E)
     torch.cuda.synchronize()
     y_want = _dense(h_want.float(), dequant(wdn), counts, offsets, H)
     assert rel_l2(y.cpu(), y_want) < 5e-4
