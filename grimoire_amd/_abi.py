@@ -184,6 +184,8 @@ SIGNATURES = {
     "grimoire_xe2_fused_moe_gate_up_mxfp4_silu_bf16": (None, [P, P, P, P, P, I32, I32, P, I32, P]),
     "grimoire_moe_forward_workspace_bytes": (SZ, [LP, I32]),
     "grimoire_moe_forward": (I32, [P, LP, RPP, P, P, P, I32, P, P, I32, P, SZ]),
+    "grimoire_moe_forward_noalloc_max_bytes": (SZ, []),
+    "grimoire_moe_forward_noalloc": (I32, [P, LP, RPP, P, P, P, I32, P, P, I32]),
     "grimoire_moe_decode_stage": (I32, [P, LP, RPP, P, P, P, I32, I32, P, SZ]),
 }
 

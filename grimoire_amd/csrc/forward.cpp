@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
+#include <mutex>
 
 #include "../../include/grimoire_moe.h"
 #include "common.hpp"
@@ -250,6 +251,67 @@ extern "C" int grimoire_moe_forward(void* stream, const grim_moe_layer* L,
                                     size_t workspace_bytes) {
     return forward_impl(stream, L, rp, shared_gate_w, x, y, tokens, out_expert, out_weight, regime,
                         workspace, workspace_bytes, kRoleRouter | kRoleGateUp | kRoleDown);
+}
+
+// ---- the allocation-free variant
+//
+// Its workspace is one file-scope device array per GPU (the module's copy
+// on each device), addressed through the pointer hipGetSymbolAddress gives
+// for that device: the array's name is a host-side stand-in and is never
+// passed to a kernel.  Every call on a GPU shares that GPU's array and
+// finds the previous call's contents in it; the forward writes every word
+// it reads, so nothing is cleared.  Calls that overlap on one GPU race.
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// The current device's address of `scratch`, looked up on the first call
+// on that device (with it current) and kept.
+int scratch_ptr(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return int(e);
+    if (dev < 0 || dev >= kMaxDevices) return GRIM_ERR_ARG;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return e != hipSuccess ? int(e) : GRIM_ERR_WORKSPACE;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return GRIM_OK;
+}
+}  // namespace
+
+extern "C" size_t grimoire_moe_forward_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int grimoire_moe_forward_noalloc(void* stream, const grim_moe_layer* L,
+                                            const grim_route_params* rp,
+                                            const uint16_t* shared_gate_w, const float* x, float* y,
+                                            int tokens, int32_t* out_expert, float* out_weight,
+                                            int regime) {
+    if (!L || !x || !y) return ferr(GRIM_ERR_ARG, "null layer/x/y");
+    if (tokens <= 0) return GRIM_OK;
+    Plan p{};
+    const size_t need = carve(L, tokens, use_gemv(L, tokens, regime), nullptr, p);
+    if (need > kNoAllocScratchBytes) {
+        static thread_local char msg[160];
+        std::snprintf(msg, sizeof msg,
+                      "forward_noalloc: this call needs %zu bytes of workspace, above the %zu-byte "
+                      "scratch limit (use grimoire_moe_forward with a workspace)",
+                      need, kNoAllocScratchBytes);
+        return ferr(GRIM_ERR_WORKSPACE, msg);
+    }
+    void* ws = nullptr;
+    const int r = scratch_ptr(&ws);
+    if (r) return ferr(r, "forward_noalloc: no device address for the scratch array");
+    return forward_impl(stream, L, rp, shared_gate_w, x, y, tokens, out_expert, out_weight, regime,
+                        ws, kNoAllocScratchBytes, kRoleRouter | kRoleGateUp | kRoleDown);
 }
 
 extern "C" int grimoire_moe_decode_stage(void* stream, const grim_moe_layer* L,

@@ -609,6 +609,22 @@ int grimoire_moe_forward(void* stream, const grim_moe_layer* L, const grim_route
                          int32_t* out_expert, float* out_weight, int regime, void* workspace,
                          size_t workspace_bytes);
 
+/* grimoire_moe_forward without a workspace argument and without any
+ * allocation: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No reference counterpart.  The workspace is a fixed device
+ * array of grimoire_moe_forward_noalloc_max_bytes() (8 MiB) per GPU inside
+ * the library; a call whose workspace (grimoire_moe_forward_workspace_bytes
+ * for its regime) exceeds it returns GRIM_ERR_WORKSPACE and launches
+ * nothing (single-token and small-batch decode fit; large prefills do not).
+ * All calls on one GPU share that array: calls that overlap on one GPU
+ * (other streams, other threads) race and must be serialised by the
+ * caller. */
+size_t grimoire_moe_forward_noalloc_max_bytes(void);
+int grimoire_moe_forward_noalloc(void* stream, const grim_moe_layer* L, const grim_route_params* rp,
+                                 const uint16_t* shared_gate_w, const float* x, float* y,
+                                 int tokens, int32_t* out_expert, float* out_weight, int regime);
+
 /* One stage of the decode path of grimoire_moe_forward (regime 1, tokens
  * <= 8): stage 1 = router logits (and the formatted activations), 2 =
  * top-k + gate_up + SwiGLU, 4 = down + combine, each reading what the
