@@ -132,13 +132,14 @@ def _heat_sequence(seed, L, E):
     return seq
 
 
-@pytest.mark.parametrize("seed", [0, 1, 2])
-def test_heat_oracle_and_library(seed):
+@pytest.mark.parametrize("seed,L,E,moves", [(0, 3, 12, 5), (1, 3, 12, 5), (2, 3, 12, 5),
+                                            (3, 6, 40, 32), (4, 2, 100, 64)])
+def test_heat_oracle_and_library(seed, L, E, moves):
     """Python restatement == reference ExpertHeat (when built) == library,
     heats exactly and proposals exactly, on random credit sequences with
-    over-cap calls and out-of-range ids."""
-    L, E = 3, 12
-    cap, moves = 64.0, 5
+    over-cap calls and out-of-range ids (budgets below and above the
+    candidate counts, many equal heats)."""
+    cap = 64.0
     py = O.Heat(L, E, credit_cap=cap, moves=moves)
     p = _abi.HeatParams(0.95, 1.25, 1.5, cap, moves)
     lib_h = tiered.Heat(L, E, p)
