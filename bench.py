@@ -14,10 +14,16 @@ x and y.  Inputs are resident in HBM before timing starts.
 The JSON line also carries:
   roofline      gate_up decode kernel (the dominant one), timed with HIP
                 events on its stream, against 8 TB/s;
-  cpu_baseline  the reference's own CPU oracle (src/moe_ref.cpp, built into
-                oracle/_ref) on a bounded sample of the same layers;
-  prefill       C4 (T=4096, E=512, top-10, int8, shared expert): layer time
-                and grouped-GEMM TFLOPS against the bf16 MFMA peak;
+  cpu_baseline  the CPU path on all host threads (this build's C restatement
+                of src/moe_ref.cpp, OpenMP over tokens) on a bounded sample
+                of the same layer, with the host's core count; beside it
+                the reference's own moe_ref.cpp (oracle/_ref), one thread;
+  prefill       C4 (T=4096, E=512, top-10 Zipf(1.2), int8, shared expert):
+                layer time and grouped-GEMM TFLOPS against the bf16 MFMA
+                peak;
+  c3, c5        C3 (T=8 MXFP4 decode, Zipf(1.1)) and C5 (T=32 verify, 6 GB
+                of MXFP4 experts, group-limited routing): layer time, GB/s
+                and the HBM fraction;
   edges         the fused combine + residual + RMSNorm and the residual
                 RMSNorm (C4 shapes) against 8 TB/s, and the GPTQ ingestion
                 of one C2 layer's experts, and the tiered NVFP4 experts.
@@ -336,42 +342,155 @@ def _tiered_bench(dev, stream, timed):
     return out
 
 
-def cpu_baseline(d, budget_s=15.0):
-    """The reference's src/moe_ref.cpp (oracle/_ref) on the same layers."""
+def _host_info():
+    info = {"os_cpu_count": os.cpu_count()}
+    try:
+        info["affinity_cpus"] = len(os.sched_getaffinity(0))
+    except Exception:  # pragma: no cover
+        pass
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                info["model"] = line.split(":", 1)[1].strip()
+                break
+    except Exception:  # pragma: no cover
+        pass
+    return info
+
+
+def _omp_threads():
+    n = os.environ.get("OMP_NUM_THREADS")
+    if n and n.isdigit():
+        return int(n)
+    try:
+        return len(os.sched_getaffinity(0))
+    except Exception:  # pragma: no cover
+        return os.cpu_count() or 1
+
+
+def cpu_baseline(d, budget_s=12.0):
+    """The CPU path on the host cores: this build's C restatement of
+    src/moe_ref.cpp (oracle/moe_oracle.c, OpenMP over tokens) on all the
+    threads OpenMP is given, one C2 token per thread (the layer's own
+    routing), as whole-host GB/s of the decode metric; beside it the
+    reference's own moe_ref.cpp (oracle/_ref), single thread."""
     try:
         from oracle import oracle as O
     except Exception as e:  # pragma: no cover
         return {"error": f"oracle unavailable: {e}"}
-    r = O.ref()
-    kind = "reference"
-    if r is None:
-        kind = "port"
     cfg = d["cfg"]
     x = d["x"].cpu()
-    done, nbytes, dt, reps = 0, 0.0, 0.0, 20
-    t_wall = time.perf_counter()
-    for L, oe, ow in zip(d["layers"], d["oes"], d["ows"]):
-        Lc = L.to("cpu")                     # host copy of the layer: not timed
-        s = Lc.struct()
-        y = torch.empty(1, cfg.H)
-        e, w = oe.cpu().contiguous(), ow.cpu().contiguous()
+    L0 = d["layers"][0]
+    Lc = L0.to("cpu")                         # host copy of the layer: not timed
+    s = Lc.struct()
+    e1, w1 = d["oes"][0].cpu().contiguous(), d["ows"][0].cpu().contiguous()
+    one_bytes = (len(set(e1.flatten().tolist())) * L0.expert_bytes() + cfg.E * cfg.H * 4
+                 + 2 * cfg.H * 4)
+    nt = _omp_threads()
+    xs = x.repeat(nt, 1).contiguous()
+    es, ws = e1.repeat(nt, 1).contiguous(), w1.repeat(nt, 1).contiguous()
+    ys = torch.empty(nt, cfg.H)
+    O.orc().orc_moe_forward(O.byref(s), O._p(es), O._p(ws), None, O._p(xs), O._p(ys), nt)
+    calls, dt = 0, 0.0
+    while dt < budget_s and calls < 200:
         t0 = time.perf_counter()
-        for _ in range(reps):
-            if r is not None:
-                r.ref_moe_forward(O.byref(s), O._p(e), O._p(w), O._p(x), O._p(y), 1)
-            else:
-                O.orc().orc_moe_forward(O.byref(s), O._p(e), O._p(w), None, O._p(x), O._p(y), 1)
+        O.orc().orc_moe_forward(O.byref(s), O._p(es), O._p(ws), None, O._p(xs), O._p(ys), nt)
         dt += time.perf_counter() - t0
-        done += 1
-        nbytes += reps * (len(set(e.flatten().tolist())) * L.expert_bytes() + cfg.E * cfg.H * 4
-                          + 2 * cfg.H * 4)
-        if dt > budget_s or time.perf_counter() - t_wall > 3 * budget_s:
-            break
-    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": f"{done} of the {LAYERS} C2 layers x {reps} calls each, one token per "
-                      f"call, single thread ({dt:.1f} s of reference time; the host copy of "
-                      f"each layer is not timed)",
-            "us_per_layer": round(dt / (done * reps) * 1e6, 1)}
+        calls += 1
+    out = {"value": round(nt * calls * one_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": nt,
+           "kind": "port",
+           "sample": f"layer 0 of the C2 step, {nt} copies of its token (one per OpenMP "
+                     f"thread), {calls} calls ({dt:.1f} s); value = tokens x the one-token "
+                     f"layer's algorithmic bytes / time",
+           "us_per_token_layer": round(dt / (calls * nt) * 1e6, 1),
+           "host": _host_info()}
+    r = O.ref()
+    if r is not None:
+        y = torch.empty(1, cfg.H)
+        done, dt1 = 0, 0.0
+        while dt1 < budget_s / 2 and done < 100:
+            t0 = time.perf_counter()
+            r.ref_moe_forward(O.byref(s), O._p(e1), O._p(w1), O._p(x), O._p(y), 1)
+            dt1 += time.perf_counter() - t0
+            done += 1
+        out["reference_single_thread"] = {
+            "value": round(done * one_bytes / dt1 / 1e9, 4), "unit": "GB/s", "cores": 1,
+            "kind": "reference", "us_per_layer": round(dt1 / done * 1e6, 1),
+            "sample": f"src/moe_ref.cpp built into oracle/_ref, layer 0, {done} calls"}
+    return out
+
+
+def _touched_bytes(L, oe):
+    return len(set(oe.flatten().tolist())) * L.expert_bytes() + L.shared_bytes()
+
+
+def c3_bench(dev, stream, n_layers=4, reps=10):
+    """C3 (T=8 users, H=2880, E=128, top-4 softmax with Zipf(1.1)
+    popularity, I=2880, MXFP4): the decode forward of n_layers distinct
+    layers in one graph (their touched experts exceed the 256 MB MALL)."""
+    cfg = configs.CONFIGS["c3"]
+    layers = [configs.make_layer(cfg, dev, seed=300 + i) for i in range(n_layers)]
+    bias = configs.make_route_bias(cfg, dev, seed=3)
+    x = configs.make_x(cfg, dev, seed=3)
+    fwds = [ops.MoeForward(L, cfg.T, configs.route_params(cfg, bias), regime=1) for L in layers]
+    ys = [torch.empty(cfg.T, cfg.H, device=dev) for _ in layers]
+    oes = [torch.empty(cfg.T, cfg.K, dtype=torch.int32, device=dev) for _ in layers]
+    ows = [torch.empty(cfg.T, cfg.K, dtype=torch.float32, device=dev) for _ in layers]
+
+    def step():
+        for f, y, oe, ow in zip(fwds, ys, oes, ows):
+            f(x, y, oe, ow, stream=stream)
+
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.synchronize()
+    g = _graph(step, stream)
+    _replay(g, stream, 3)
+    torch.cuda.synchronize()
+    with Timer(stream) as t:
+        _replay(g, stream, reps)
+    us = t.ms() * 1e3 / (reps * n_layers)
+    nbytes = sum(_touched_bytes(L, oe.cpu()) for L, oe in zip(layers, oes)) / n_layers
+    nbytes += cfg.E * cfg.H * 4 + 2 * cfg.T * cfg.H * 4
+    touched = sum(len(set(oe.cpu().flatten().tolist())) for oe in oes) / n_layers
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"workload": "c3: T=8 H=2880 E=128 top-4 softmax (Zipf 1.1) I=2880 MXFP4, "
+                        f"{n_layers} distinct layers in one graph",
+            "us_per_layer": round(us, 2), "experts_touched": touched,
+            "bytes_per_layer": int(nbytes), "gbs": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "tflops": round(6.0 * cfg.T * cfg.K * cfg.H * cfg.I / (us * 1e-6) / 1e12, 3)}
+
+
+def c5_bench(dev, stream, reps=5):
+    """C5 (T=32, H=7168, 256 routed + 1 shared expert, I=2048, MXFP4,
+    group-limited sigmoid top-8, scaling 2.5): the whole layer forward
+    (grouped-GEMM regime: bf16 MFMA on MXFP4 weights decoded in registers)."""
+    cfg = configs.CONFIGS["c5"]
+    L = configs.make_layer(cfg, dev, seed=500)
+    bias = configs.make_route_bias(cfg, dev, seed=5)
+    x = configs.make_x(cfg, dev, seed=5)
+    fwd = ops.MoeForward(L, cfg.T, configs.route_params(cfg, bias), regime=0)
+    y = torch.empty(cfg.T, cfg.H, device=dev)
+    oe = torch.empty(cfg.T, cfg.K, dtype=torch.int32, device=dev)
+    ow = torch.empty(cfg.T, cfg.K, dtype=torch.float32, device=dev)
+    with torch.cuda.stream(stream):
+        fwd(x, y, oe, ow, stream=stream)
+        torch.cuda.synchronize()
+        with Timer(stream) as t:
+            for _ in range(reps):
+                fwd(x, y, oe, ow, stream=stream)
+    us = t.ms() * 1e3 / reps
+    nbytes = _touched_bytes(L, oe.cpu()) + cfg.E * cfg.H * 4 + 2 * cfg.T * cfg.H * 4
+    flops = 6.0 * cfg.T * (cfg.K + 1) * cfg.H * cfg.I
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"workload": "c5: T=32 H=7168 E=256+1 shared, group-limited sigmoid top-8 "
+                        "(8 groups, top-4 groups, bias, scaling 2.5) I=2048 MXFP4",
+            "us_per_layer": round(us, 1), "experts_touched": len(set(oe.cpu().flatten().tolist())),
+            "bytes_per_layer": int(nbytes), "gbs": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "tflops": round(flops / (us * 1e-6) / 1e12, 2),
+            "bound": "hbm (intensity ~6.6 FLOP/B, far below the ~315 FLOP/B bf16 ridge)"}
 
 
 def main():
@@ -416,8 +535,9 @@ def main():
         "hbm_frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "grim::moe_gate_up_wave_kernel<64, 4, 1, false> (decode stage 2: top-k + "
-                      "gate_up + SwiGLU, GPTQ int4 fp16 scales), 48 layers in one graph",
+            "kernel": "grim::moe_gate_up_wave_kernel<64, 6, 1, false> (decode stage 2: top-k + "
+                      "gate_up + SwiGLU, GPTQ int4 fp16 scales; 6 row pairs per wave), 48 layers "
+                      "in one graph",
             "achieved": round(d["gu_bytes"] / (d["gu_us"] * 1e-6) / 1e9, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -437,6 +557,9 @@ def main():
         log("prefill bench (C4)...")
         out["prefill"] = prefill_bench(dev, stream)
     if not a.no_prefill:
+        log("C3 (T=8 MXFP4 decode) and C5 (T=32 verify, 6 GB of experts)...")
+        out["c3"] = c3_bench(dev, stream)
+        out["c5"] = c5_bench(dev, stream)
         log("edges (fused norms, ingestion)...")
         out["edges"] = edges_bench(dev, stream)
     if not a.no_cpu:

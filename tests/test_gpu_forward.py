@@ -111,3 +111,39 @@ def test_forward_c4_full_size_sampled(gpu):
     Lg2, y2, oe2, ow2, _ = _run(configs.Workload(cfg, Lg, wl.x, wl.route_bias), gpu, regime=1, T=64)
     assert torch.equal(oe2, oe[:64])
     assert_close(y[:64], y2, what="c4 gemm vs gemv regime")
+
+
+def _slice_experts(w, ids, rows_per_expert):
+    """A Weight holding only experts `ids` (rows_per_expert rows each), on the CPU."""
+    from grimoire_amd.weights import Weight
+    rp = rows_per_expert
+    pay = torch.cat([w.payload[e * rp:(e + 1) * rp] for e in ids]).cpu()
+    sc = torch.cat([w.scales[e * rp:(e + 1) * rp] for e in ids]).cpu()
+    return Weight(w.fmt, len(ids) * rp, w.K, pay, sc, None, w.row_scales)
+
+
+def test_forward_c5_full_size_sampled(gpu):
+    """C5 at full size (T=32, H=7168, 256 routed experts + shared, I=2048,
+    MXFP4, group-limited sigmoid top-8 with bias, scaling 2.5; ~6 GB of
+    experts): routing of all 32 tokens bit-exact against the oracle on the
+    same logits; outputs of a seeded sample of tokens against the oracle,
+    which reads only the experts those tokens use (copied to the host)."""
+    from grimoire_amd.weights import MoeLayer
+    print("forward c5 full size", flush=True)
+    cfg = configs.CONFIGS["c5"]
+    Lg = configs.make_layer(cfg, gpu, seed=6)
+    x = configs.make_x(cfg, "cpu", seed=6)
+    bias = configs.make_route_bias(cfg, "cpu", seed=6)
+    wl = configs.Workload(cfg, Lg, x, bias)
+    _, y, oe, ow, logits = _run(wl, gpu, regime=0)
+    _check_routing(wl, logits, oe, ow)
+    idx = torch.randperm(cfg.T, generator=torch.Generator().manual_seed(1))[:4]
+    ids = sorted(set(oe[idx].flatten().tolist()))
+    remap = {e: j for j, e in enumerate(ids)}
+    oe_s = torch.tensor([[remap[int(e)] for e in row] for row in oe[idx]], dtype=torch.int32)
+    small = MoeLayer(cfg.H, cfg.I, len(ids), cfg.K,
+                     _slice_experts(Lg.gate_up, ids, 2 * cfg.I), _slice_experts(Lg.down, ids, cfg.H),
+                     Lg.router[:len(ids)].cpu().contiguous(),
+                     Lg.shared_gate_up.to("cpu"), Lg.shared_down.to("cpu"), None, True)
+    yo = O.moe_forward(small.struct(), oe_s, ow[idx].contiguous(), None, x[idx].contiguous())
+    assert_close(y[idx], yo, what="c5 sampled tokens")
