@@ -424,7 +424,7 @@ def _touched_bytes(L, oe):
     return len(set(oe.flatten().tolist())) * L.expert_bytes() + L.shared_bytes()
 
 
-def c3_bench(dev, stream, n_layers=4, reps=10):
+def c3_bench(dev, stream, n_layers=4, reps=10, regime=1):
     """C3 (T=8 users, H=2880, E=128, top-4 softmax with Zipf(1.1)
     popularity, I=2880, MXFP4): the decode forward of n_layers distinct
     layers in one graph (their touched experts exceed the 256 MB MALL)."""
@@ -432,7 +432,7 @@ def c3_bench(dev, stream, n_layers=4, reps=10):
     layers = [configs.make_layer(cfg, dev, seed=300 + i) for i in range(n_layers)]
     bias = configs.make_route_bias(cfg, dev, seed=3)
     x = configs.make_x(cfg, dev, seed=3)
-    fwds = [ops.MoeForward(L, cfg.T, configs.route_params(cfg, bias), regime=1) for L in layers]
+    fwds = [ops.MoeForward(L, cfg.T, configs.route_params(cfg, bias), regime=regime) for L in layers]
     ys = [torch.empty(cfg.T, cfg.H, device=dev) for _ in layers]
     oes = [torch.empty(cfg.T, cfg.K, dtype=torch.int32, device=dev) for _ in layers]
     ows = [torch.empty(cfg.T, cfg.K, dtype=torch.float32, device=dev) for _ in layers]
@@ -559,6 +559,7 @@ def main():
     if not a.no_prefill:
         log("C3 (T=8 MXFP4 decode) and C5 (T=32 verify, 6 GB of experts)...")
         out["c3"] = c3_bench(dev, stream)
+        out["c3_grouped"] = c3_bench(dev, stream, regime=4)
         out["c5"] = c5_bench(dev, stream)
         log("edges (fused norms, ingestion)...")
         out["edges"] = edges_bench(dev, stream)

@@ -24,10 +24,12 @@ __device__ __forceinline__ uint32_t f_bits(float f) { return __float_as_uint(f);
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return bits_f(uint32_t(b) << 16); }
 
 // round to nearest even; NaN stays NaN (include/b70/formats.hpp:88-97)
+// (selects, not branches: it runs per element in the staging loops)
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
     const uint32_t u = f_bits(f);
-    if (((u >> 23) & 0xFFu) == 0xFFu) return uint16_t((u >> 16) | ((u & 0x7FFFFFu) ? 0x40u : 0u));
-    return uint16_t((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+    const uint32_t special = (u >> 16) | ((u & 0x7FFFFFu) ? 0x40u : 0u);   // inf / NaN (quieted)
+    const uint32_t rounded = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;     // nearest even
+    return uint16_t(((u >> 23) & 0xFFu) == 0xFFu ? special : rounded);
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
@@ -37,10 +39,12 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
 }
 
 // e8m0 -> fp32 (include/b70/formats.hpp:105-109)
+// (selects, not branches: it sits in the inner loops)
 __device__ __forceinline__ float e8m0_to_f32(uint8_t x) {
-    if (x == 0xFF) return bits_f(0x7FC00000u);
-    if (x == 0x00) return bits_f(0x00400000u);
-    return bits_f(uint32_t(x) << 23);
+    uint32_t b = uint32_t(x) << 23;
+    b = x == 0x00 ? 0x00400000u : b;
+    b = x == 0xFF ? 0x7FC00000u : b;
+    return bits_f(b);
 }
 
 // exp(x): Cody-Waite reduction to |r| <= ln2/2, degree-7 Taylor polynomial

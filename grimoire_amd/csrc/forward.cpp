@@ -20,6 +20,7 @@
 #include "dispatch.hpp"
 #include "gemm.hpp"
 #include "gemm_i8.hpp"
+#include "gemv_grouped.hpp"
 #include "gemv.hpp"
 #include "router.hpp"
 
@@ -48,7 +49,7 @@ constexpr int kDecodeMaxTokens = 8;
 
 bool use_gemv(const grim_moe_layer* L, int T, int regime) {
     if (regime == 1 || regime == 3) return true;
-    if (regime == 2) return false;
+    if (regime == 2 || regime == 4) return false;
     return int64_t(T) * L->cfg.top_k <= 64;
 }
 
@@ -70,7 +71,27 @@ struct Plan {
     // INT8 weights: activation limbs for the int8 MFMA
     int8_t *xq, *xrowq, *hq, *hshq;
     float *sx, *sxrow, *sh, *shsh, *h32, *h32sh;
+    // expert-grouped GEMV (gemv_grouped.hip): its own tile table (MT-row
+    // blocks), the route -> token map and fp32 h rows
+    int32_t *gv_te, *gv_tm, *gv_perm;
+    int gv_tmax;
+    float *gv_h, *gv_hsh;
+    uint32_t *gv_xf, *gv_hf, *gv_hfsh;   // formatted activation rows
 };
+
+// The expert-grouped GEMV covers these shapes and formats.
+bool gv_ok(const grim_moe_layer* L) {
+    const int f = L->gate_up.fmt;
+    const int H = L->cfg.hidden, I = L->cfg.inter;
+    // payload rows packed (K / 2 bytes): a sub-block's rows are one span
+    auto packed = [](const grim_quant_weight& w, int K) {
+        // INT4 scale groups of >= 32 elements: at most K / 16 scale bytes per row
+        return w.row_bytes == int64_t(K / 2) && int64_t(w.row_scales) * 32 <= K;
+    };
+    return f == L->down.fmt && gv_shape_ok(f, H, I) && packed(L->gate_up, H) && packed(L->down, I) &&
+           (!L->has_shared || (L->shared_gate_up.fmt == f && L->shared_down.fmt == f &&
+                               packed(L->shared_gate_up, H) && packed(L->shared_down, I)));
+}
 
 size_t carve(const grim_moe_layer* L, int T, bool gemv, char* base, Plan& p) {
     const auto& c = L->cfg;
@@ -101,6 +122,17 @@ size_t carve(const grim_moe_layer* L, int T, bool gemv, char* base, Plan& p) {
         p.hp_sh = sh ? cv.take<uint16_t>(size_t(T) * 2 * I) : nullptr;
         p.yperm = cv.take<float>(R * H);
         p.ysh = sh ? cv.take<float>(size_t(T) * H) : nullptr;
+        if (gv_ok(L)) {
+            p.gv_tmax = int(E + (R + kGvMT - 1) / kGvMT);
+            p.gv_te = cv.take<int32_t>(p.gv_tmax + 4);
+            p.gv_tm = cv.take<int32_t>(p.gv_tmax);
+            p.gv_perm = cv.take<int32_t>(R);
+            p.gv_h = cv.take<float>(R * I);
+            p.gv_hsh = sh ? cv.take<float>(size_t(T) * I) : nullptr;
+            p.gv_xf = cv.take<uint32_t>(size_t(T) * gv_act_bytes(H) / 4);
+            p.gv_hf = cv.take<uint32_t>(R * gv_act_bytes(I) / 4);
+            p.gv_hfsh = sh ? cv.take<uint32_t>(size_t(T) * gv_act_bytes(I) / 4) : nullptr;
+        }
         if (L->gate_up.fmt == GRIM_FMT_INT8 && L->down.fmt == GRIM_FMT_INT8) {
             p.xq = cv.take<int8_t>(R * 2 * H);
             p.sx = cv.take<float>(R);
@@ -231,6 +263,73 @@ static int forward_gemm_i8(hipStream_t st, const grim_moe_layer* L, const Plan& 
     d.out = p.yperm;
     d.out_sh = p.ysh;
     e = gemm_i8_launch(st, d);
+    if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    CombineArgs cb{p.yperm, 0, p.inverse, p.rwt, p.ysh, 0, (sh && shared_gate_w) ? p.gate : nullptr,
+                   y, tokens, K, H};
+    e = combine_launch(st, cb);
+    if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    return GRIM_OK;
+}
+
+// Expert-grouped GEMV regime (few rows per expert): routes -> counts,
+// offsets and an (expert, MT-row block) table -> [shared gate] -> gate_up
+// + SwiGLU per group (fp32 h per route) -> down per group (fp32 rows per
+// route) -> combine (slot-order fma chain + gate * shared).
+static int forward_gv(hipStream_t st, const grim_moe_layer* L, const Plan& p, const float* x,
+                      float* y, int tokens, const uint16_t* shared_gate_w) {
+    const auto& c = L->cfg;
+    const int E = c.num_experts, K = c.top_k, H = c.hidden, I = c.inter;
+    const bool sh = L->has_shared;
+    int r = grimoire_moe_route_grouped(st, x, p.rex, nullptr, nullptr, p.counts, p.offsets,
+                                       p.inverse, p.gv_te, p.gv_tm, p.gv_tmax, tokens, H, E, kGvMT,
+                                       K, p.gv_perm, p.disp_ws,
+                                       dispatch_workspace_bytes(tokens, K, E));
+    if (r) return r;
+    if (sh && shared_gate_w) {
+        hipError_t e = rowdot_sigmoid_launch(st, x, shared_gate_w, p.gate, tokens, H);
+        if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    }
+    {
+        hipError_t e = gv_format_launch(st, L->gate_up.fmt, x, tokens, p.gv_xf, nullptr, 0, nullptr, H);
+        if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    }
+    GvArgs g{};
+    g.w = make_view(L->gate_up);
+    g.af = p.gv_xf;
+    g.af_sh = p.gv_xf;
+    g.w_sh = sh ? make_view(L->shared_gate_up) : g.w;
+    g.N = I;
+    g.K = H;
+    g.x = x;
+    g.perm_token = p.gv_perm;
+    g.h = p.gv_h;
+    g.h_sh = p.gv_hsh;
+    g.counts = p.counts;
+    g.offsets = p.offsets;
+    g.tile_e = p.gv_te;
+    g.tile_mb = p.gv_tm;
+    g.n_live = dispatch_live_tiles(p.disp_ws, tokens, K, E);
+    g.T_sh = sh ? tokens : 0;
+#ifdef GRIM_TIMING
+    g.ts = g_timing;
+#endif
+    hipError_t e = gv_launch(st, L->gate_up.fmt, g, true);
+    if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    e = gv_format_launch(st, L->down.fmt, p.gv_h, tokens * K, p.gv_hf, p.gv_hsh, sh ? tokens : 0, p.gv_hfsh, I);
+    if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    GvArgs d = g;
+    d.af = p.gv_hf;
+    d.af_sh = p.gv_hfsh;
+    d.w = make_view(L->down);
+    d.w_sh = sh ? make_view(L->shared_down) : d.w;
+    d.N = H;
+    d.K = I;
+    d.y = p.yperm;
+    d.y_sh = p.ysh;
+#ifdef GRIM_TIMING
+    d.ts = g_timing ? g_timing + 4096 * 16 : nullptr;
+#endif
+    e = gv_launch(st, L->down.fmt, d, false);
     if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
     CombineArgs cb{p.yperm, 0, p.inverse, p.rwt, p.ysh, 0, (sh && shared_gate_w) ? p.gate : nullptr,
                    y, tokens, K, H};
@@ -447,6 +546,12 @@ static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_
         return grimoire_moe_down_batched(stream, L, p.rex, p.rwt, p.h, y, tokens);
     }
 
+    // few rows per expert (on average at most 2): stream each expert once
+    // per group of rows instead of once per 128-row MFMA tile
+    if (p.gv_te && (regime == 4 || (regime == 0 && int64_t(tokens) * K <= 2 * int64_t(E))))
+        return forward_gv(st, L, p, x, y, tokens, shared_gate_w);
+    if (regime == 4) return ferr(GRIM_ERR_FORMAT, "regime 4: int4 / mxfp4 experts, hidden and inter % 32");
+
     // ---- GEMM regime
     const int fu = L->gate_up.fmt, fd = L->down.fmt;
     if (!gemm_format_ok(fu) || !gemm_format_ok(fd))
@@ -456,6 +561,7 @@ static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_
                     (!sh || (L->shared_gate_up.fmt == fu && L->shared_down.fmt == fd)) &&
                     gemm_i8_shape_ok(2 * I, H, I, 1) && gemm_i8_shape_ok(H, I, 0, 0) && I <= 4096;
     if (i8) return forward_gemm_i8(st, L, p, x, y, tokens, shared_gate_w);
+
     r = grimoire_moe_route_grouped(stream, x, p.rex, p.xperm, p.xrow, p.counts, p.offsets,
                                    p.inverse, p.tile_e, p.tile_mb, p.tmax, tokens, H, E, kGemmBM, K,
                                    nullptr, p.disp_ws, dispatch_workspace_bytes(tokens, K, E));

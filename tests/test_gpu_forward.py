@@ -147,3 +147,37 @@ def test_forward_c5_full_size_sampled(gpu):
                      Lg.shared_gate_up.to("cpu"), Lg.shared_down.to("cpu"), None, True)
     yo = O.moe_forward(small.struct(), oe_s, ow[idx].contiguous(), None, x[idx].contiguous())
     assert_close(y[idx], yo, what="c5 sampled tokens")
+
+
+@pytest.mark.parametrize("name,kw", [
+    ("c3", {}),                                           # MXFP4, Zipf routing, T=8
+    ("c5", dict(T=32, H=1024, E=64, I=256)),              # group-limited, shared expert
+    ("c1", {}),                                           # GPTQ int4, T=16
+    ("c2", dict(T=24)),                                   # GPTQ int4, more rows than experts' groups
+])
+def test_forward_grouped_gemv(gpu, name, kw):
+    """The expert-grouped GEMV regime (4): each expert's weights streamed
+    once per group of up to 4 of its rows.  Routing bit-exact, outputs
+    within the layer tolerance, on MXFP4 and GPTQ int4 experts."""
+    print(f"forward grouped gemv {name} {kw}", flush=True)
+    cfg = configs.scaled(configs.CONFIGS[name], **kw) if kw else configs.CONFIGS[name]
+    wl = configs.make_workload(cfg, "cpu", seed=9)
+    Lg, y, oe, ow, logits = _run(wl, gpu, regime=4)
+    _check_routing(wl, logits, oe, ow)
+    yo = _oracle_y(wl.layer, wl.x, oe, ow, wl.layer.shared_gate_w)
+    assert_close(y, yo, what=f"grouped gemv {name}")
+
+
+def test_forward_grouped_gemv_fp32_activations(gpu):
+    """Activations that are not bf16 values: the lo halves take the second
+    pass of the grouped GEMV kernels (gate_up and down)."""
+    print("forward grouped gemv fp32 x", flush=True)
+    cfg = configs.scaled(configs.CONFIGS["c5"], T=12, H=512, E=32, I=256)
+    wl = configs.make_workload(cfg, "cpu", seed=10)
+    x = torch.randn(cfg.T, cfg.H, generator=torch.Generator().manual_seed(3))
+    assert (x != x.bfloat16().float()).any()
+    wl = configs.Workload(cfg, wl.layer, x.contiguous(), wl.route_bias)
+    Lg, y, oe, ow, logits = _run(wl, gpu, regime=4)
+    _check_routing(wl, logits, oe, ow)
+    yo = _oracle_y(wl.layer, wl.x, oe, ow, None)
+    assert_close(y, yo, what="grouped gemv fp32 x")
