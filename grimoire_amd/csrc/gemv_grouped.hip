@@ -301,7 +301,8 @@ template <int F, int CI, bool GU> struct GvShape {
     static constexpr int NSS = (KMAX / (kInt4 ? 16 : 32) + 3 + 255) / 256;
     static constexpr int NSZ = kInt4 ? (KMAX / 32 + 3 + 255) / 256 : 0;
     static constexpr int NT = RW * (CI + NSS + NSZ);        // loads per wave and stage
-    static constexpr int ST = 1 + (63 / NT < 4 ? 63 / NT : 4);   // ring stages: up to 4 ahead
+    static constexpr int SA = CI >= 3 ? 2 : 4;             // stages ahead, at most (long rows: more waves)
+    static constexpr int ST = 1 + (63 / NT < SA ? 63 / NT : SA);
     static_assert((ST - 1) * NT <= 63, "vmcnt holds 63");
     static_assert(kGvMT % MT == 0, "parts of a group");
 };
