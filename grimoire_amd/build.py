@@ -21,7 +21,7 @@ OBJ = PKG / "_build"
 
 SOURCES = ["router.hip", "gemv.hip", "gemv_f0.hip", "gemv_f3.hip", "gemv_f4.hip", "gemv_f6.hip",
            "gemv_f64.hip", "dispatch.hip", "gemm.hip", "gemm_i8.hip", "ingest.hip",
-           "tiered.hip", "elementwise.hip", "gemv_grouped.hip", "api.cpp", "forward.cpp", "heat.cpp"]
+           "tiered.hip", "elementwise.hip", "gemv_grouped.hip", "gemv_mx.hip", "api.cpp", "forward.cpp", "heat.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

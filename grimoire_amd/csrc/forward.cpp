@@ -21,6 +21,7 @@
 #include "gemm.hpp"
 #include "gemm_i8.hpp"
 #include "gemv_grouped.hpp"
+#include "gemv_mx.hpp"
 #include "gemv.hpp"
 #include "router.hpp"
 
@@ -49,7 +50,7 @@ constexpr int kDecodeMaxTokens = 8;
 
 bool use_gemv(const grim_moe_layer* L, int T, int regime) {
     if (regime == 1 || regime == 3) return true;
-    if (regime == 2 || regime == 4) return false;
+    if (regime == 2 || regime == 4 || regime == 5) return false;
     return int64_t(T) * L->cfg.top_k <= 64;
 }
 
@@ -276,7 +277,7 @@ static int forward_gemm_i8(hipStream_t st, const grim_moe_layer* L, const Plan& 
 // + SwiGLU per group (fp32 h per route) -> down per group (fp32 rows per
 // route) -> combine (slot-order fma chain + gate * shared).
 static int forward_gv(hipStream_t st, const grim_moe_layer* L, const Plan& p, const float* x,
-                      float* y, int tokens, const uint16_t* shared_gate_w) {
+                      float* y, int tokens, const uint16_t* shared_gate_w, bool mx) {
     const auto& c = L->cfg;
     const int E = c.num_experts, K = c.top_k, H = c.hidden, I = c.inter;
     const bool sh = L->has_shared;
@@ -290,7 +291,11 @@ static int forward_gv(hipStream_t st, const grim_moe_layer* L, const Plan& p, co
         if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
     }
     {
-        hipError_t e = gv_format_launch(st, L->gate_up.fmt, x, tokens, p.gv_xf, nullptr, 0, nullptr, H);
+        // (the limb format of the matrix-core kernel is smaller than the
+        // vector-ALU format the buffers are sized for)
+        hipError_t e = mx ? gvm_format_launch(st, x, tokens, reinterpret_cast<uint8_t*>(p.gv_xf), nullptr, 0,
+                                              nullptr, H)
+                          : gv_format_launch(st, L->gate_up.fmt, x, tokens, p.gv_xf, nullptr, 0, nullptr, H);
         if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
     }
     GvArgs g{};
@@ -313,9 +318,11 @@ static int forward_gv(hipStream_t st, const grim_moe_layer* L, const Plan& p, co
 #ifdef GRIM_TIMING
     g.ts = g_timing;
 #endif
-    hipError_t e = gv_launch(st, L->gate_up.fmt, g, true);
+    hipError_t e = mx ? gvm_launch(st, g, true) : gv_launch(st, L->gate_up.fmt, g, true);
     if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
-    e = gv_format_launch(st, L->down.fmt, p.gv_h, tokens * K, p.gv_hf, p.gv_hsh, sh ? tokens : 0, p.gv_hfsh, I);
+    e = mx ? gvm_format_launch(st, p.gv_h, tokens * K, reinterpret_cast<uint8_t*>(p.gv_hf), p.gv_hsh,
+                               sh ? tokens : 0, reinterpret_cast<uint8_t*>(p.gv_hfsh), I)
+           : gv_format_launch(st, L->down.fmt, p.gv_h, tokens * K, p.gv_hf, p.gv_hsh, sh ? tokens : 0, p.gv_hfsh, I);
     if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
     GvArgs d = g;
     d.af = p.gv_hf;
@@ -329,7 +336,7 @@ static int forward_gv(hipStream_t st, const grim_moe_layer* L, const Plan& p, co
 #ifdef GRIM_TIMING
     d.ts = g_timing ? g_timing + 4096 * 16 : nullptr;
 #endif
-    e = gv_launch(st, L->down.fmt, d, false);
+    e = mx ? gvm_launch(st, d, false) : gv_launch(st, L->down.fmt, d, false);
     if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
     CombineArgs cb{p.yperm, 0, p.inverse, p.rwt, p.ysh, 0, (sh && shared_gate_w) ? p.gate : nullptr,
                    y, tokens, K, H};
@@ -548,9 +555,12 @@ static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_
 
     // few rows per expert (on average at most 2): stream each expert once
     // per group of rows instead of once per 128-row MFMA tile
-    if (p.gv_te && (regime == 4 || (regime == 0 && int64_t(tokens) * K <= 2 * int64_t(E))))
-        return forward_gv(st, L, p, x, y, tokens, shared_gate_w);
-    if (regime == 4) return ferr(GRIM_ERR_FORMAT, "regime 4: int4 / mxfp4 experts, hidden and inter % 32");
+    if (p.gv_te && (regime == 4 || regime == 5 || (regime == 0 && int64_t(tokens) * K <= 2 * int64_t(E)))) {
+        const bool mx = regime != 5 && L->gate_up.fmt == GRIM_FMT_MXFP4 && gvm_shape_ok(H, I);
+        return forward_gv(st, L, p, x, y, tokens, shared_gate_w, mx);
+    }
+    if (regime == 4 || regime == 5)
+        return ferr(GRIM_ERR_FORMAT, "regimes 4, 5: int4 / mxfp4 experts, hidden and inter % 32");
 
     // ---- GEMM regime
     const int fu = L->gate_up.fmt, fd = L->down.fmt;

@@ -1,0 +1,337 @@
+// gemv_mx.hip -- the expert-grouped GEMV for MXFP4 experts on the scaled
+// fp4 x fp8 matrix core (v_mfma_scale_f32_16x16x128_f8f6f4).
+//
+// Same work as gemv_grouped.hip (each touched expert's weights streamed once
+// per group of up to kGvMT of its rows), with the arithmetic moved off the
+// vector ALU: the e2m1 weight codes and their e8m0 block scales go to the
+// matrix core exactly as stored, and the activations are split into three
+// e4m3 limbs under one e8m0 scale per 32-element block,
+//     x = 2^s (hi + mid + lo),   s = floor(log2 max|block|) - 7,
+// each limb the round-to-nearest e4m3 of what the previous ones left: the
+// three cover 12 significant bits of every value within 2^9 of its block's
+// largest one (bf16 values, 8 bits, exactly).  One MFMA per limb
+// accumulates 16 weight rows x 16 activation rows x 128 K in fp32; the
+// group's <= 4 rows use 4 of the 16 columns and the others are never
+// stored.  The vector ALU is left with the SwiGLU and the stores.
+//
+// Operand layout of the instruction with A = e2m1 and B = e4m3 (measured
+// with one-hot operands): lane l of A holds row l % 16 and the 32-element
+// K block g = l / 16 of the 128 (16 bytes, element p at nibble p, low
+// nibble first: a weight row's stored bytes), with that block's scale; lane
+// l of B holds column l % 16 and, in its 32 bytes, elements [16 (g & 1),
+// +16) of blocks (g >> 1) and (g >> 1) + 2, with the scale of block g; D
+// holds column l % 16, rows 4 (l / 16) + [0, 4).
+//
+// Each wave owns 128 weight rows of an item (gate_up: 64 gate and the
+// matching 64 up rows) and walks the K steps of 128: per step its rows'
+// 8 KiB of codes and 512 bytes of scales, and the group's limb rows at the
+// step, stream through its own LDS ring by buffer_load ... lds (two steps
+// ahead; code slots XOR-swizzled so that the 16-row operand reads are free
+// of bank conflicts), and 8 row blocks x 3 limbs of MFMAs accumulate.  Like
+// gemv_grouped.hip: one work-group per CU, no barrier, every wave waits on
+// its own vmcnt only.
+#include "gemv_mx.hpp"
+
+#include "gemv_impl.hpp"
+
+namespace grim {
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* gvm_lds_ptr_t;
+
+constexpr int kGvmWaves = 3;
+constexpr int kGvmRows = 64;                    // weight rows per wave and item
+constexpr int kGvmKS = 256;                     // K per ring stage (two MFMA steps)
+constexpr int kGvmStages = 4;                   // ring stages per wave
+constexpr int kGvmLimbs = 3;
+// stage: codes 64 rows x 128 B, their scales 64 x 8 B, the group's limb rows
+// 4 x 3 x 256 B, their scales 4 x 8 B
+constexpr int kGvmOS = kGvmRows * kGvmKS / 2;                       // 8192
+constexpr int kGvmOA = kGvmOS + kGvmRows * kGvmKS / 32;             // 8704
+constexpr int kGvmOAS = kGvmOA + 4 * kGvmLimbs * kGvmKS;            // 11776
+constexpr int kGvmStage = kGvmOAS + 256;                            // 12032
+
+__device__ __forceinline__ uint32_t gvm_lds_addr(const void* p) {
+    return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t*)(p)));
+}
+
+// Activation row in the limb format: limb L's K bytes at L * K, then one
+// e8m0 scale per 32-element block at 3 K; rounded to 16 bytes.
+__host__ __device__ inline int gvm_row_bytes(int K) { return (3 * K + K / 32 + 15) & ~15; }
+
+size_t gvm_act_bytes(int K) { return size_t(gvm_row_bytes(K)); }
+
+// One thread per 32-element block.
+__global__ __launch_bounds__(256) void gvm_format_kernel(const float* src0, int rows0, uint8_t* dst0,
+                                                         const float* src1, int rows1, uint8_t* dst1, int K) {
+    const int nb = K / 32;
+    const int64_t gi = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t n0 = int64_t(rows0) * nb;
+    if (gi >= n0 + int64_t(rows1) * nb) return;
+    const bool second = gi >= n0;
+    const int64_t li = second ? gi - n0 : gi;
+    const int row = int(li / nb), b = int(li % nb);
+    const float4* s4 = reinterpret_cast<const float4*>((second ? src1 : src0) + int64_t(row) * K + b * 32);
+    uint8_t* dst = (second ? dst1 : dst0) + int64_t(row) * gvm_row_bytes(K);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 q = s4[i];
+        v[4 * i] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) mx = fmaxf(mx, fabsf(v[i]));
+    // the largest value lands in [128, 256): e4m3 holds up to 448
+    const int ex = mx > 0.0f ? int((f_bits(mx) >> 23) & 0xFF) - 127 : -127;
+    const int s = max(-127, min(127, ex - 7));
+    const float inv = bits_f(uint32_t(127 - s) << 23);   // 2^-s (s >= -127: 2^127 at most)
+    uint32_t w[3][8];
+#pragma unroll
+    for (int i = 0; i < 32; i += 4) {
+        float r[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r[j] = v[i + j] * inv;
+#pragma unroll
+        for (int L = 0; L < kGvmLimbs; ++L) {
+            int p = __builtin_amdgcn_cvt_pk_fp8_f32(r[0], r[1], 0, false);
+            p = __builtin_amdgcn_cvt_pk_fp8_f32(r[2], r[3], p, true);
+            w[L][i / 4] = uint32_t(p);
+            r[0] -= __builtin_amdgcn_cvt_f32_fp8(p, 0);
+            r[1] -= __builtin_amdgcn_cvt_f32_fp8(p, 1);
+            r[2] -= __builtin_amdgcn_cvt_f32_fp8(p, 2);
+            r[3] -= __builtin_amdgcn_cvt_f32_fp8(p, 3);
+        }
+    }
+#pragma unroll
+    for (int L = 0; L < kGvmLimbs; ++L) {
+        uint4* d4 = reinterpret_cast<uint4*>(dst + int64_t(L) * K + b * 32);
+        d4[0] = make_uint4(w[L][0], w[L][1], w[L][2], w[L][3]);
+        d4[1] = make_uint4(w[L][4], w[L][5], w[L][6], w[L][7]);
+    }
+    dst[3 * K + b] = uint8_t(s + 127);
+}
+
+hipError_t gvm_format_launch(hipStream_t st, const float* src0, int rows0, uint8_t* dst0, const float* src1,
+                             int rows1, uint8_t* dst1, int K) {
+    const int64_t n = int64_t(rows0 + rows1) * (K / 32);
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(gvm_format_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, src0, rows0, dst0, src1,
+                       rows1, dst1, K);
+    return hipGetLastError();
+}
+
+// One persistent kernel for both products (GU: gate_up + SwiGLU, rows are
+// (gate, up) pairs, out h; else down, out y).  Items: (group, chunk of
+// kGvmWaves x 32 pairs / 64 rows); work-group b walks b, b + gridDim.x, ...
+// A wave's ring stage s (K [256 s, +256)) holds its 64 rows' codes (one
+// 128-byte line per row), their scales, and the group's limb rows at those
+// K with their block scales: everything a stage's MFMAs read comes with the
+// stage, so one vmcnt wait per stage covers it.
+template <bool GU>
+__global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
+    constexpr int NT = 14;                                   // DMA instructions per stage
+    constexpr int ST = kGvmStages;
+    constexpr int WAIT = NT * (ST - 1);
+    static_assert(WAIT <= 63, "vmcnt holds 63");
+    extern __shared__ __attribute__((aligned(1024))) uint8_t gvm_ring[];
+    const int N = a.N, Kd = a.K, S = Kd / kGvmKS;
+    const int lrow = Kd / 2, srb = Kd / 32;                  // code / scale bytes per weight row
+    const int AB = gvm_row_bytes(Kd);
+    constexpr int PW = GU ? kGvmRows / 2 : kGvmRows;         // rows (pairs) per wave
+    constexpr int NRB = kGvmRows / 16;                       // 16-row blocks per wave
+    const int per_item = kGvmWaves * PW;
+    const int rows_per_expert = GU ? 2 * N : N;
+    const int n_chunks = (N + per_item - 1) / per_item;
+    const int n_live = __builtin_amdgcn_readfirstlane(*a.n_live);
+    const int groups = n_live + (a.T_sh + kGvMT - 1) / kGvMT;
+    const int n_items = groups * n_chunks;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+    uint8_t* ring = gvm_ring + wave * (ST * kGvmStage);
+    const uint32_t ring_base = gvm_lds_addr(ring);
+    const int col = lane & 15, grp = lane >> 4;              // B / D column, lane group
+
+    for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+        const int g = item / n_chunks, chunk = item % n_chunks;
+        struct {
+            int64_t wrow0;
+            int r0, mc;
+            bool sh;
+        } it{0, 0, 0, false};
+        if (g < n_live) {
+            const int e = __builtin_amdgcn_readfirstlane(a.tile_e[g]);
+            if (e < 0) continue;   // uniform
+            const int mb = __builtin_amdgcn_readfirstlane(a.tile_mb[g]);
+            it.r0 = __builtin_amdgcn_readfirstlane(a.offsets[e]) + mb * kGvMT;
+            it.mc = min(kGvMT, __builtin_amdgcn_readfirstlane(a.counts[e]) - mb * kGvMT);
+            it.wrow0 = int64_t(e) * rows_per_expert;
+        } else {
+            it.r0 = (g - n_live) * kGvMT;
+            it.mc = min(kGvMT, a.T_sh - it.r0);
+            it.sh = true;
+        }
+        if (it.mc <= 0) continue;   // uniform
+        const WView& w = it.sh ? a.w_sh : a.w;
+        const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(w.payload + it.wrow0 * lrow), 0, rows_per_expert * lrow, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(static_cast<const uint8_t*>(w.scales) + it.wrow0 * srb), 0,
+            rows_per_expert * srb, 0x00020000);
+        const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint32_t*>(it.sh ? a.af_sh : a.af), 0, 0x7FFFFFFF, 0x00020000);
+        const int i0 = chunk * per_item + wave * PW;         // this wave's first row (pair)
+        // weight row of the wave's row r (GU: r < 32 gate, else up); rows
+        // past N repeat the last (loaded, never stored)
+        auto wrow = [&](int r) {
+            if constexpr (GU) return (r >= PW ? N : 0) + min(i0 + (r & (PW - 1)), N - 1);
+            else return min(i0 + r, N - 1);
+        };
+        // activation row of group row m (rows past mc repeat row 0: never stored)
+        auto arow = [&](int m) {
+            const int rr = it.r0 + (m < it.mc ? m : 0);
+            return GU ? (it.sh ? rr : a.perm_token[rr]) : rr;
+        };
+        // Per-lane DMA offsets.  Codes: instruction j covers rows 8 j + lane / 8,
+        // slot lane % 8 holding 16-byte piece (lane % 8) ^ ((row >> 1) & 7).
+        // Scales: instruction jj covers rows 32 jj + lane / 2, 4 bytes each.
+        // Activations: piece p = 64 ja + lane of [row m][limb L][16 x 16 B]
+        // (192 pieces), then the 4 rows' 8 block scales (lane = 2 m + half).
+        int pofs[8], sofs[2], aofs[3];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int r = 8 * j + (lane >> 3);
+            pofs[j] = wrow(r) * lrow + (((lane & 7) ^ ((r >> 1) & 7)) << 4);
+        }
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) sofs[jj] = wrow(32 * jj + (lane >> 1)) * srb + (lane & 1) * 4;
+#pragma unroll
+        for (int ja = 0; ja < 3; ++ja) {
+            const int pc = 64 * ja + lane;
+            aofs[ja] = arow(pc / 48) * AB + ((pc / 16) % 3) * Kd + (pc % 16) * 16;
+        }
+        const int asofs = arow((lane >> 1) & 3) * AB + 3 * Kd + (lane & 1) * 4;
+        auto issue = [&](int s) {   // stage s (clamped: a repeat of the last is never read)
+            const int sc = min(s, S - 1);
+            uint8_t* st = ring + (s % ST) * kGvmStage;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (gvm_lds_ptr_t)(st + j * 1024), 16, pofs[j], sc * 128, 0,
+                                                         2);
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (gvm_lds_ptr_t)(st + kGvmOS + jj * 256), 4, sofs[jj],
+                                                         sc * 8, 0, 0);
+#pragma unroll
+            for (int ja = 0; ja < 3; ++ja)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (gvm_lds_ptr_t)(st + kGvmOA + ja * 1024), 16, aofs[ja],
+                                                         sc * 256, 0, 0);
+            if (lane < 8)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (gvm_lds_ptr_t)(st + kGvmOAS), 4, asofs, sc * 8, 0, 0);
+        };
+
+        f32x4 acc[NRB];
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < ST - 1; ++u) issue(u);
+        const int mcol = col < it.mc ? col : 0;
+        // B operand of MFMA step t of a stage: limb L's bytes at
+        // [m][L][256]: K 128 t + 32 (g >> 1) + 16 (g & 1), and + 64
+        const uint32_t boff = uint32_t(mcol * kGvmLimbs * kGvmKS + 32 * (grp >> 1) + 16 * (grp & 1));
+
+#pragma unroll 1
+        for (int s = 0; s < S; ++s) {
+            // stage s + ST - 1 in, then stage s complete: NT (ST - 1) younger loads
+            issue(s + ST - 1);
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAIT) : "memory");
+            const uint32_t stb = ring_base + uint32_t(s % ST) * kGvmStage;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                u32x4 bq[kGvmLimbs][2];
+                uint32_t sb, sa[NRB];
+                u32x4 aq[NRB];
+#pragma unroll
+                for (int L = 0; L < kGvmLimbs; ++L) {
+                    const uint32_t pb = stb + kGvmOA + boff + L * kGvmKS + t * 128;
+                    asm volatile("ds_read_b128 %0, %1" : "=v"(bq[L][0]) : "v"(pb));
+                    asm volatile("ds_read_b128 %0, %1" : "=v"(bq[L][1]) : "v"(pb + 64));
+                }
+                asm volatile("ds_read_u8 %0, %1" : "=v"(sb) : "v"(stb + kGvmOAS + mcol * 8 + 4 * t + grp));
+#pragma unroll
+                for (int rb = 0; rb < NRB; ++rb) {
+                    const int r = 16 * rb + col;
+                    const int pc = 4 * t + grp;                      // 16-byte piece of the row's 128
+                    asm volatile("ds_read_b128 %0, %1"
+                                 : "=v"(aq[rb]) : "v"(stb + r * 128 + ((pc ^ ((r >> 1) & 7)) << 4)));
+                    asm volatile("ds_read_u8 %0, %1" : "=v"(sa[rb]) : "v"(stb + kGvmOS + r * 8 + pc));
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+                for (int L = 0; L < kGvmLimbs; ++L) asm volatile("" : "+v"(bq[L][0]), "+v"(bq[L][1]));
+                asm volatile("" : "+v"(sb));
+#pragma unroll
+                for (int rb = 0; rb < NRB; ++rb) asm volatile("" : "+v"(aq[rb]), "+v"(sa[rb]));
+                // limbs outer: consecutive MFMAs update different accumulators
+#pragma unroll
+                for (int L = 0; L < kGvmLimbs; ++L) {
+                    const i32x8 B{int(bq[L][0].x), int(bq[L][0].y), int(bq[L][0].z), int(bq[L][0].w),
+                                  int(bq[L][1].x), int(bq[L][1].y), int(bq[L][1].z), int(bq[L][1].w)};
+#pragma unroll
+                    for (int rb = 0; rb < NRB; ++rb) {
+                        const i32x8 A{int(aq[rb].x), int(aq[rb].y), int(aq[rb].z), int(aq[rb].w), 0, 0, 0, 0};
+                        acc[rb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, acc[rb], 4, 0, 0,
+                                                                                  int(sa[rb]), 0, int(sb));
+                    }
+                }
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the clamped repeats, before the ring is reused
+
+        // D: column col = group row, weight rows 4 grp + [0, 4) of each block
+        if (col < it.mc) {
+            const int64_t orow = int64_t(it.r0 + col) * N;
+            if constexpr (GU) {
+                float* h = it.sh ? a.h_sh : a.h;
+#pragma unroll
+                for (int rb = 0; rb < NRB / 2; ++rb) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int i = i0 + 16 * rb + 4 * grp + q;
+                        if (i < N) h[orow + i] = fast_silu(acc[rb][q]) * acc[NRB / 2 + rb][q];
+                    }
+                }
+            } else {
+                float* y = it.sh ? a.y_sh : a.y;
+#pragma unroll
+                for (int rb = 0; rb < NRB; ++rb) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int i = i0 + 16 * rb + 4 * grp + q;
+                        if (i < N) y[orow + i] = acc[rb][q];
+                    }
+                }
+            }
+        }
+    }
+}
+
+bool gvm_shape_ok(int H, int I) { return H % kGvmKS == 0 && I % kGvmKS == 0; }
+
+hipError_t gvm_launch(hipStream_t st, const GvArgs& a, bool gate_up) {
+    if (a.K % kGvmKS) return hipErrorInvalidValue;
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return hipErrorInvalidConfiguration;
+    }
+    const size_t lds = size_t(kGvmWaves) * kGvmStages * kGvmStage;
+    if (gate_up) hipLaunchKernelGGL(gvm_kernel<true>, dim3(cus), dim3(kGvmWaves * kWave), lds, st, a);
+    else hipLaunchKernelGGL(gvm_kernel<false>, dim3(cus), dim3(kGvmWaves * kWave), lds, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace grim

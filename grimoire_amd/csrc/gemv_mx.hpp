@@ -1,0 +1,19 @@
+// gemv_mx.hpp -- host interface of the MXFP4 expert-grouped GEMV on the
+// scaled fp4 x fp8 matrix core (gemv_mx.hip).
+#pragma once
+
+#include "gemv_grouped.hpp"
+
+namespace grim {
+
+// MXFP4 experts whose reduction lengths are multiples of 128 (one MFMA K step).
+bool gvm_shape_ok(int H, int I);
+// Bytes of one activation row of K elements in the limb format.
+size_t gvm_act_bytes(int K);
+// Format rows0 rows of src0 into dst0 and rows1 rows of src1 into dst1.
+hipError_t gvm_format_launch(hipStream_t st, const float* src0, int rows0, uint8_t* dst0, const float* src1,
+                             int rows1, uint8_t* dst1, int K);
+// The product: GvArgs with af / af_sh pointing at limb-format rows.
+hipError_t gvm_launch(hipStream_t st, const GvArgs& g, bool gate_up);
+
+}  // namespace grim

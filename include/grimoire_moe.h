@@ -601,9 +601,13 @@ size_t grimoire_moe_forward_workspace_bytes(const grim_moe_layer* L, int tokens)
 /* y fp32 [T][H] = MoE(x fp32 [T][H]).  shared_gate_w bf16 [H] (may be NULL:
  * shared expert weight 1, as src/moe_ref.cpp:100-104).  Routing is written
  * to out_expert/out_weight [T][K] when not NULL.  regime: 0 = choose
- * (slot GEMV for T*K <= 64, grouped MFMA GEMM otherwise), 1 = GEMV,
- * 2 = grouped GEMM, 3 = GEMV with one launch per stage (no on-device
- * hand-off between gate_up and down). */
+ * (slot GEMV for T*K <= 64; else the expert-grouped GEMV for T*K <= 2E
+ * on INT4 / MXFP4 experts; else the grouped MFMA GEMM), 1 = GEMV,
+ * 2 = grouped GEMM, 3 = GEMV with one launch per stage, 4 = expert-grouped
+ * GEMV (MXFP4 with hidden and inter multiples of 256: on the scaled fp4
+ * matrix core; otherwise on the vector ALU), 5 = expert-grouped GEMV on
+ * the vector ALU.  No reference counterpart for 3-5 (regimes of this
+ * build; the reference picks its kernels per batch size the same way). */
 int grimoire_moe_forward(void* stream, const grim_moe_layer* L, const grim_route_params* rp,
                          const uint16_t* shared_gate_w, const float* x, float* y, int tokens,
                          int32_t* out_expert, float* out_weight, int regime, void* workspace,

@@ -149,35 +149,41 @@ def test_forward_c5_full_size_sampled(gpu):
     assert_close(y[idx], yo, what="c5 sampled tokens")
 
 
+@pytest.mark.parametrize("regime", [4, 5])
 @pytest.mark.parametrize("name,kw", [
-    ("c3", {}),                                           # MXFP4, Zipf routing, T=8
+    ("c3", {}),                                           # MXFP4, Zipf routing, T=8 (K % 128 != 0)
     ("c5", dict(T=32, H=1024, E=64, I=256)),              # group-limited, shared expert
+    ("c5", dict(T=16, H=1280, E=32, I=768)),              # MXFP4, K % 256 == 0, ragged item tail
     ("c1", {}),                                           # GPTQ int4, T=16
     ("c2", dict(T=24)),                                   # GPTQ int4, more rows than experts' groups
 ])
-def test_forward_grouped_gemv(gpu, name, kw):
-    """The expert-grouped GEMV regime (4): each expert's weights streamed
-    once per group of up to 4 of its rows.  Routing bit-exact, outputs
-    within the layer tolerance, on MXFP4 and GPTQ int4 experts."""
-    print(f"forward grouped gemv {name} {kw}", flush=True)
+def test_forward_grouped_gemv(gpu, name, kw, regime):
+    """The expert-grouped GEMV regimes: each expert's weights streamed once
+    per group of up to 4 of its rows -- 4: MXFP4 experts with K % 256 == 0
+    on the scaled fp4 x fp8 matrix core (activations as three e4m3 limbs),
+    others on the vector ALU; 5: the vector ALU always.  Routing bit-exact,
+    outputs within the layer tolerance, on MXFP4 and GPTQ int4 experts."""
+    print(f"forward grouped gemv {name} {kw} regime {regime}", flush=True)
     cfg = configs.scaled(configs.CONFIGS[name], **kw) if kw else configs.CONFIGS[name]
     wl = configs.make_workload(cfg, "cpu", seed=9)
-    Lg, y, oe, ow, logits = _run(wl, gpu, regime=4)
+    Lg, y, oe, ow, logits = _run(wl, gpu, regime=regime)
     _check_routing(wl, logits, oe, ow)
     yo = _oracle_y(wl.layer, wl.x, oe, ow, wl.layer.shared_gate_w)
     assert_close(y, yo, what=f"grouped gemv {name}")
 
 
-def test_forward_grouped_gemv_fp32_activations(gpu):
-    """Activations that are not bf16 values: the lo halves take the second
-    pass of the grouped GEMV kernels (gate_up and down)."""
-    print("forward grouped gemv fp32 x", flush=True)
+@pytest.mark.parametrize("regime", [4, 5])
+def test_forward_grouped_gemv_fp32_activations(gpu, regime):
+    """Activations that are not bf16 values: on the vector ALU the lo halves
+    take gate_up's second path; on the matrix core the three limbs carry
+    them (12 significant bits)."""
+    print(f"forward grouped gemv fp32 x regime {regime}", flush=True)
     cfg = configs.scaled(configs.CONFIGS["c5"], T=12, H=512, E=32, I=256)
     wl = configs.make_workload(cfg, "cpu", seed=10)
     x = torch.randn(cfg.T, cfg.H, generator=torch.Generator().manual_seed(3))
     assert (x != x.bfloat16().float()).any()
     wl = configs.Workload(cfg, wl.layer, x.contiguous(), wl.route_bias)
-    Lg, y, oe, ow, logits = _run(wl, gpu, regime=4)
+    Lg, y, oe, ow, logits = _run(wl, gpu, regime=regime)
     _check_routing(wl, logits, oe, ow)
     yo = _oracle_y(wl.layer, wl.x, oe, ow, None)
     assert_close(y, yo, what="grouped gemv fp32 x")
