@@ -40,10 +40,10 @@ typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void* gvm_lds_ptr_t;
 
-constexpr int kGvmWaves = 3;
+constexpr int kGvmWaves = 4;
 constexpr int kGvmRows = 64;                    // weight rows per wave and item
 constexpr int kGvmKS = 256;                     // K per ring stage (two MFMA steps)
-constexpr int kGvmStages = 4;                   // ring stages per wave
+constexpr int kGvmStages = 3;                   // ring stages per wave
 constexpr int kGvmLimbs = 3;
 // stage: codes 64 rows x 128 B, their scales 64 x 8 B, the group's limb rows
 // 4 x 3 x 256 B, their scales 4 x 8 B
@@ -51,6 +51,10 @@ constexpr int kGvmOS = kGvmRows * kGvmKS / 2;                       // 8192
 constexpr int kGvmOA = kGvmOS + kGvmRows * kGvmKS / 32;             // 8704
 constexpr int kGvmOAS = kGvmOA + 4 * kGvmLimbs * kGvmKS;            // 11776
 constexpr int kGvmStage = kGvmOAS + 256;                            // 12032
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gvm_rsrc(const void* p, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
 
 __device__ __forceinline__ uint32_t gvm_lds_addr(const void* p) {
     return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t*)(p)));
@@ -122,6 +126,31 @@ hipError_t gvm_format_launch(hipStream_t st, const float* src0, int rows0, uint8
     return hipGetLastError();
 }
 
+// Stage s of an item into the ring stage at st: exactly 14 instructions,
+// each with lane 0 active.  Codes: instruction j covers the wave's rows
+// 8 j + lane / 8, slot lane % 8 holding 16-byte piece (lane % 8) ^
+// ((row >> 1) & 7).  Scales: instruction jj covers rows 32 jj + lane / 2,
+// 4 bytes each.  Activations: piece p = 64 ja + lane of [row m][limb L]
+// [16 x 16 B] (192 pieces; rows past mc are not loaded: their columns are
+// never stored), then the 4 rows' 8 block scales (lane = 2 m + half).
+__device__ __forceinline__ void gvm_issue(uint8_t* st, __amdgpu_buffer_rsrc_t rp, __amdgpu_buffer_rsrc_t rs,
+                                          __amdgpu_buffer_rsrc_t ra, const int (&pofs)[8], const int (&sofs)[2],
+                                          const int (&aofs)[3], int asofs, int mc, int lane, int s) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (gvm_lds_ptr_t)(st + j * 1024), 16, pofs[j], s * 128, 0, 2);
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (gvm_lds_ptr_t)(st + kGvmOS + jj * 256), 4, sofs[jj], s * 8, 0,
+                                                 0);
+#pragma unroll
+    for (int ja = 0; ja < 3; ++ja)
+        if ((64 * ja + lane) / 48 < mc)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (gvm_lds_ptr_t)(st + kGvmOA + ja * 1024), 16, aofs[ja],
+                                                     s * 256, 0, 0);
+    if (lane < 8) __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (gvm_lds_ptr_t)(st + kGvmOAS), 4, asofs, s * 8, 0, 0);
+}
+
 // One persistent kernel for both products (GU: gate_up + SwiGLU, rows are
 // (gate, up) pairs, out h; else down, out y).  Items: (group, chunk of
 // kGvmWaves x 32 pairs / 64 rows); work-group b walks b, b + gridDim.x, ...
@@ -153,100 +182,125 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
     const uint32_t ring_base = gvm_lds_addr(ring);
     const int col = lane & 15, grp = lane >> 4;              // B / D column, lane group
 
-    for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-        const int g = item / n_chunks, chunk = item % n_chunks;
-        struct {
-            int64_t wrow0;
-            int r0, mc;
-            bool sh;
-        } it{0, 0, 0, false};
-        if (g < n_live) {
-            const int e = __builtin_amdgcn_readfirstlane(a.tile_e[g]);
-            if (e < 0) continue;   // uniform
-            const int mb = __builtin_amdgcn_readfirstlane(a.tile_mb[g]);
-            it.r0 = __builtin_amdgcn_readfirstlane(a.offsets[e]) + mb * kGvMT;
-            it.mc = min(kGvMT, __builtin_amdgcn_readfirstlane(a.counts[e]) - mb * kGvMT);
-            it.wrow0 = int64_t(e) * rows_per_expert;
-        } else {
-            it.r0 = (g - n_live) * kGvMT;
-            it.mc = min(kGvMT, a.T_sh - it.r0);
-            it.sh = true;
+    // One item's addressing: its weight and activation descriptors and the
+    // per-lane DMA offsets (see issue below), its rows and outputs.
+    struct Desc {
+        const uint8_t* pb;     // the expert's codes, scales; the activation rows
+        const uint8_t* sbp;
+        const uint32_t* ab;
+        int pofs[8], sofs[2], aofs[3], asofs;
+        int r0, mc, i0;
+        bool sh;
+    };
+    // The item with index >= item0 that has rows, in this work-group's
+    // order (mc = 0: none left).
+    auto make = [&](int item0, int& item) {
+        Desc d;
+        d.mc = 0;
+        for (item = item0; item < n_items; item += gridDim.x) {
+            const int g = item / n_chunks, chunk = item % n_chunks;
+            int64_t wrow0 = 0;
+            if (g < n_live) {
+                const int e = __builtin_amdgcn_readfirstlane(a.tile_e[g]);
+                if (e < 0) continue;   // uniform
+                const int mb = __builtin_amdgcn_readfirstlane(a.tile_mb[g]);
+                d.r0 = __builtin_amdgcn_readfirstlane(a.offsets[e]) + mb * kGvMT;
+                d.mc = min(kGvMT, __builtin_amdgcn_readfirstlane(a.counts[e]) - mb * kGvMT);
+                wrow0 = int64_t(e) * rows_per_expert;
+                d.sh = false;
+            } else {
+                d.r0 = (g - n_live) * kGvMT;
+                d.mc = min(kGvMT, a.T_sh - d.r0);
+                d.sh = true;
+            }
+            if (d.mc <= 0) continue;   // uniform
+            const WView& w = d.sh ? a.w_sh : a.w;
+            d.pb = w.payload + wrow0 * lrow;
+            d.sbp = static_cast<const uint8_t*>(w.scales) + wrow0 * srb;
+            d.ab = d.sh ? a.af_sh : a.af;
+            d.i0 = chunk * per_item + wave * PW;             // this wave's first row (pair)
+            // weight row of the wave's row r (GU: r < 32 gate, else up); rows
+            // past N repeat the last (loaded, never stored)
+            auto wrow = [&](int r) {
+                if constexpr (GU) return (r >= PW ? N : 0) + min(d.i0 + (r & (PW - 1)), N - 1);
+                else return min(d.i0 + r, N - 1);
+            };
+            // activation row of group row m (rows past mc: row 0, never used)
+            auto arow = [&](int m) {
+                const int rr = d.r0 + (m < d.mc ? m : 0);
+                return GU ? (d.sh ? rr : a.perm_token[rr]) : rr;
+            };
+            // Codes: instruction j covers rows 8 j + lane / 8, slot lane % 8
+            // holding 16-byte piece (lane % 8) ^ ((row >> 1) & 7).  Scales:
+            // instruction jj covers rows 32 jj + lane / 2, 4 bytes each.
+            // Activations: piece p = 64 ja + lane of [row m][limb L][16 x 16 B]
+            // (192 pieces), then the 4 rows' 8 block scales (lane = 2 m + half).
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int r = 8 * j + (lane >> 3);
+                d.pofs[j] = wrow(r) * lrow + (((lane & 7) ^ ((r >> 1) & 7)) << 4);
+            }
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) d.sofs[jj] = wrow(32 * jj + (lane >> 1)) * srb + (lane & 1) * 4;
+#pragma unroll
+            for (int ja = 0; ja < 3; ++ja) {
+                const int pc = 64 * ja + lane;
+                d.aofs[ja] = arow(pc / 48) * AB + ((pc / 16) % 3) * Kd + (pc % 16) * 16;
+            }
+            d.asofs = arow((lane >> 1) & 3) * AB + 3 * Kd + (lane & 1) * 4;
+            break;
         }
-        if (it.mc <= 0) continue;   // uniform
-        const WView& w = it.sh ? a.w_sh : a.w;
-        const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t*>(w.payload + it.wrow0 * lrow), 0, rows_per_expert * lrow, 0x00020000);
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t*>(static_cast<const uint8_t*>(w.scales) + it.wrow0 * srb), 0,
-            rows_per_expert * srb, 0x00020000);
-        const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint32_t*>(it.sh ? a.af_sh : a.af), 0, 0x7FFFFFFF, 0x00020000);
-        const int i0 = chunk * per_item + wave * PW;         // this wave's first row (pair)
-        // weight row of the wave's row r (GU: r < 32 gate, else up); rows
-        // past N repeat the last (loaded, never stored)
-        auto wrow = [&](int r) {
-            if constexpr (GU) return (r >= PW ? N : 0) + min(i0 + (r & (PW - 1)), N - 1);
-            else return min(i0 + r, N - 1);
-        };
-        // activation row of group row m (rows past mc repeat row 0: never stored)
-        auto arow = [&](int m) {
-            const int rr = it.r0 + (m < it.mc ? m : 0);
-            return GU ? (it.sh ? rr : a.perm_token[rr]) : rr;
-        };
-        // Per-lane DMA offsets.  Codes: instruction j covers rows 8 j + lane / 8,
-        // slot lane % 8 holding 16-byte piece (lane % 8) ^ ((row >> 1) & 7).
-        // Scales: instruction jj covers rows 32 jj + lane / 2, 4 bytes each.
-        // Activations: piece p = 64 ja + lane of [row m][limb L][16 x 16 B]
-        // (192 pieces), then the 4 rows' 8 block scales (lane = 2 m + half).
-        int pofs[8], sofs[2], aofs[3];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int r = 8 * j + (lane >> 3);
-            pofs[j] = wrow(r) * lrow + (((lane & 7) ^ ((r >> 1) & 7)) << 4);
-        }
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) sofs[jj] = wrow(32 * jj + (lane >> 1)) * srb + (lane & 1) * 4;
-#pragma unroll
-        for (int ja = 0; ja < 3; ++ja) {
-            const int pc = 64 * ja + lane;
-            aofs[ja] = arow(pc / 48) * AB + ((pc / 16) % 3) * Kd + (pc % 16) * 16;
-        }
-        const int asofs = arow((lane >> 1) & 3) * AB + 3 * Kd + (lane & 1) * 4;
-        auto issue = [&](int s) {   // stage s (clamped: a repeat of the last is never read)
-            const int sc = min(s, S - 1);
-            uint8_t* st = ring + (s % ST) * kGvmStage;
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (gvm_lds_ptr_t)(st + j * 1024), 16, pofs[j], sc * 128, 0,
-                                                         2);
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (gvm_lds_ptr_t)(st + kGvmOS + jj * 256), 4, sofs[jj],
-                                                         sc * 8, 0, 0);
-#pragma unroll
-            for (int ja = 0; ja < 3; ++ja)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (gvm_lds_ptr_t)(st + kGvmOA + ja * 1024), 16, aofs[ja],
-                                                         sc * 256, 0, 0);
-            if (lane < 8)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (gvm_lds_ptr_t)(st + kGvmOAS), 4, asofs, sc * 8, 0, 0);
-        };
+        return d;
+    };
+    // buffer descriptors of the current and the next item (codes, scales,
+    // activation rows)
+    __amdgpu_buffer_rsrc_t cp, cs, ca, np, ns, na;
+    Desc cur, nxt;
+    // Stage s of the current item (the next one when nx) into ring slot
+    // q % ST (gvm_issue)
+    auto issue = [&](bool nx, int s, int q) {
+        if (nx) gvm_issue(ring + (q % ST) * kGvmStage, np, ns, na, nxt.pofs, nxt.sofs, nxt.aofs, nxt.asofs, nxt.mc, lane, s);
+        else gvm_issue(ring + (q % ST) * kGvmStage, cp, cs, ca, cur.pofs, cur.sofs, cur.aofs, cur.asofs, cur.mc, lane, s);
+    };
 
+    // One continuous stream of stages over this wave's items: the last
+    // ST - 1 iterations of an item issue the next item's first stages (or,
+    // past the last item, repeats of the current one's last stage, never
+    // read), so an item starts with its data in flight.
+    // (the descriptors are built here, not in the lambdas: a buffer
+    // descriptor formed inside a lambda keeps the host pass from emitting
+    // the kernel)
+    int item_c = 0, item_n = 0;
+    cur = make(blockIdx.x, item_c);
+    if (cur.mc <= 0) return;
+    nxt = make(item_c + gridDim.x, item_n);
+    cp = gvm_rsrc(cur.pb, rows_per_expert * lrow);
+    cs = gvm_rsrc(cur.sbp, rows_per_expert * srb);
+    ca = gvm_rsrc(cur.ab, 0x7FFFFFFF);
+    np = gvm_rsrc(nxt.pb, rows_per_expert * lrow);
+    ns = gvm_rsrc(nxt.sbp, rows_per_expert * srb);
+    na = gvm_rsrc(nxt.ab, 0x7FFFFFFF);
+    int q = 0;                                               // stages consumed by this wave
+#pragma unroll
+    for (int u = 0; u < ST - 1; ++u) issue(false, min(u, S - 1), u);
+    while (true) {
         f32x4 acc[NRB];
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int u = 0; u < ST - 1; ++u) issue(u);
-        const int mcol = col < it.mc ? col : 0;
+        const int mcol = col < cur.mc ? col : 0;
         // B operand of MFMA step t of a stage: limb L's bytes at
         // [m][L][256]: K 128 t + 32 (g >> 1) + 16 (g & 1), and + 64
         const uint32_t boff = uint32_t(mcol * kGvmLimbs * kGvmKS + 32 * (grp >> 1) + 16 * (grp & 1));
 
 #pragma unroll 1
-        for (int s = 0; s < S; ++s) {
+        for (int s = 0; s < S; ++s, ++q) {
             // stage s + ST - 1 in, then stage s complete: NT (ST - 1) younger loads
-            issue(s + ST - 1);
+            const int ahead = s + ST - 1;
+            if (ahead < S) issue(false, ahead, q + ST - 1);
+            else if (nxt.mc > 0) issue(true, ahead - S, q + ST - 1);
+            else issue(false, S - 1, q + ST - 1);
             asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAIT) : "memory");
-            const uint32_t stb = ring_base + uint32_t(s % ST) * kGvmStage;
+            const uint32_t stb = ring_base + uint32_t(q % ST) * kGvmStage;
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 u32x4 bq[kGvmLimbs][2];
@@ -287,40 +341,54 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
                 }
             }
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the clamped repeats, before the ring is reused
 
         // D: column col = group row, weight rows 4 grp + [0, 4) of each block
-        if (col < it.mc) {
-            const int64_t orow = int64_t(it.r0 + col) * N;
+        if (col < cur.mc) {
+            const int64_t orow = int64_t(cur.r0 + col) * N;
             if constexpr (GU) {
-                float* h = it.sh ? a.h_sh : a.h;
+                float* h = cur.sh ? a.h_sh : a.h;
 #pragma unroll
                 for (int rb = 0; rb < NRB / 2; ++rb) {
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int i = i0 + 16 * rb + 4 * grp + q;
-                        if (i < N) h[orow + i] = fast_silu(acc[rb][q]) * acc[NRB / 2 + rb][q];
+                    for (int qq = 0; qq < 4; ++qq) {
+                        const int i = cur.i0 + 16 * rb + 4 * grp + qq;
+                        if (i < N) h[orow + i] = fast_silu(acc[rb][qq]) * acc[NRB / 2 + rb][qq];
                     }
                 }
             } else {
-                float* y = it.sh ? a.y_sh : a.y;
+                float* y = cur.sh ? a.y_sh : a.y;
 #pragma unroll
                 for (int rb = 0; rb < NRB; ++rb) {
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int i = i0 + 16 * rb + 4 * grp + q;
-                        if (i < N) y[orow + i] = acc[rb][q];
+                    for (int qq = 0; qq < 4; ++qq) {
+                        const int i = cur.i0 + 16 * rb + 4 * grp + qq;
+                        if (i < N) y[orow + i] = acc[rb][qq];
                     }
                 }
             }
         }
+        if (nxt.mc <= 0) break;
+        cur = nxt;
+        cp = np;
+        cs = ns;
+        ca = na;
+        nxt = make(item_n + gridDim.x, item_n);
+        np = gvm_rsrc(nxt.pb, rows_per_expert * lrow);
+        ns = gvm_rsrc(nxt.sbp, rows_per_expert * srb);
+        na = gvm_rsrc(nxt.ab, 0x7FFFFFFF);
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the repeats past the last item
 }
 
-bool gvm_shape_ok(int H, int I) { return H % kGvmKS == 0 && I % kGvmKS == 0; }
+// K a multiple of 256 with at least ST - 1 stages per item (the stream's
+// look-ahead reaches at most into the next item).
+bool gvm_shape_ok(int H, int I) {
+    const int kmin = (kGvmStages - 1) * kGvmKS;
+    return H % kGvmKS == 0 && I % kGvmKS == 0 && H >= kmin && I >= kmin;
+}
 
 hipError_t gvm_launch(hipStream_t st, const GvArgs& a, bool gate_up) {
-    if (a.K % kGvmKS) return hipErrorInvalidValue;
+    if (a.K % kGvmKS || a.K < (kGvmStages - 1) * kGvmKS) return hipErrorInvalidValue;
     static int cus = 0;
     if (cus == 0) {
         int dev = 0;

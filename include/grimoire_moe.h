@@ -604,7 +604,7 @@ size_t grimoire_moe_forward_workspace_bytes(const grim_moe_layer* L, int tokens)
  * (slot GEMV for T*K <= 64; else the expert-grouped GEMV for T*K <= 2E
  * on INT4 / MXFP4 experts; else the grouped MFMA GEMM), 1 = GEMV,
  * 2 = grouped GEMM, 3 = GEMV with one launch per stage, 4 = expert-grouped
- * GEMV (MXFP4 with hidden and inter multiples of 256: on the scaled fp4
+ * GEMV (MXFP4, hidden and inter multiples of 256, >= 512: on the scaled fp4
  * matrix core; otherwise on the vector ALU), 5 = expert-grouped GEMV on
  * the vector ALU.  No reference counterpart for 3-5 (regimes of this
  * build; the reference picks its kernels per batch size the same way). */

@@ -153,6 +153,7 @@ def test_forward_c5_full_size_sampled(gpu):
 @pytest.mark.parametrize("name,kw", [
     ("c3", {}),                                           # MXFP4, Zipf routing, T=8 (K % 128 != 0)
     ("c5", dict(T=32, H=1024, E=64, I=256)),              # group-limited, shared expert
+    ("c5", dict(T=32, H=1024, E=64, I=512)),              # the same, matrix core: two stages per down item
     ("c5", dict(T=16, H=1280, E=32, I=768)),              # MXFP4, K % 256 == 0, ragged item tail
     ("c1", {}),                                           # GPTQ int4, T=16
     ("c2", dict(T=24)),                                   # GPTQ int4, more rows than experts' groups
