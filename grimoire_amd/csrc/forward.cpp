@@ -12,6 +12,7 @@
 //     (slot-order fma chain + gate * shared)
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <mutex>
 
@@ -48,10 +49,21 @@ struct Carve {
 // The decode path with device-side routing covers up to this many tokens.
 constexpr int kDecodeMaxTokens = 8;
 
+bool gv_ok(const grim_moe_layer* L);
+
+// MXFP4 experts that the matrix-core grouped GEMV takes: from 16 routes
+// per call on, one stream per expert group beats the per-route decode
+// kernels (C3: 8 tokens x top-4, 204 -> ~120 us measured).
+bool prefer_grouped_mx(const grim_moe_layer* L, int T) {
+    const int64_t R = int64_t(T) * L->cfg.top_k;
+    return L->gate_up.fmt == GRIM_FMT_MXFP4 && R >= 16 && R <= 2 * int64_t(L->cfg.num_experts) &&
+           gvm_shape_ok(L->cfg.hidden, L->cfg.inter) && gv_ok(L);
+}
+
 bool use_gemv(const grim_moe_layer* L, int T, int regime) {
     if (regime == 1 || regime == 3) return true;
     if (regime == 2 || regime == 4 || regime == 5) return false;
-    return int64_t(T) * L->cfg.top_k <= 64;
+    return int64_t(T) * L->cfg.top_k <= 64 && !prefer_grouped_mx(L, T);
 }
 
 struct Plan {
@@ -130,9 +142,12 @@ size_t carve(const grim_moe_layer* L, int T, bool gemv, char* base, Plan& p) {
             p.gv_perm = cv.take<int32_t>(R);
             p.gv_h = cv.take<float>(R * I);
             p.gv_hsh = sh ? cv.take<float>(size_t(T) * I) : nullptr;
-            p.gv_xf = cv.take<uint32_t>(size_t(T) * gv_act_bytes(H) / 4);
-            p.gv_hf = cv.take<uint32_t>(R * gv_act_bytes(I) / 4);
-            p.gv_hfsh = sh ? cv.take<uint32_t>(size_t(T) * gv_act_bytes(I) / 4) : nullptr;
+            // formatted activation rows: either kernel's format fits
+            const size_t ax = std::max(gv_act_bytes(H), gvm_act_bytes(H)) / 4;
+            const size_t ai = std::max(gv_act_bytes(I), gvm_act_bytes(I)) / 4;
+            p.gv_xf = cv.take<uint32_t>(size_t(T) * ax);
+            p.gv_hf = cv.take<uint32_t>(R * ai);
+            p.gv_hfsh = sh ? cv.take<uint32_t>(size_t(T) * ai) : nullptr;
         }
         if (L->gate_up.fmt == GRIM_FMT_INT8 && L->down.fmt == GRIM_FMT_INT8) {
             p.xq = cv.take<int8_t>(R * 2 * H);

@@ -48,9 +48,10 @@ constexpr int kGvmLimbs = 3;
 // stage: codes 64 rows x 128 B, their scales 64 x 8 B, the group's limb rows
 // 4 x 3 x 256 B, their scales 4 x 8 B
 constexpr int kGvmOS = kGvmRows * kGvmKS / 2;                       // 8192
-constexpr int kGvmOA = kGvmOS + kGvmRows * kGvmKS / 32;             // 8704
-constexpr int kGvmOAS = kGvmOA + 4 * kGvmLimbs * kGvmKS;            // 11776
-constexpr int kGvmStage = kGvmOAS + 256;                            // 12032
+// (each row's 8 scale bytes come in the 12 from their 4-byte-aligned start)
+constexpr int kGvmOA = kGvmOS + kGvmRows * 12;                      // 8960
+constexpr int kGvmOAS = kGvmOA + 4 * kGvmLimbs * kGvmKS;            // 12032
+constexpr int kGvmStage = kGvmOAS + 256;                            // 12288
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t gvm_rsrc(const void* p, int bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
@@ -60,16 +61,24 @@ __device__ __forceinline__ uint32_t gvm_lds_addr(const void* p) {
     return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t*)(p)));
 }
 
-// Activation row in the limb format: limb L's K bytes at L * K, then one
-// e8m0 scale per 32-element block at 3 K; rounded to 16 bytes.
-__host__ __device__ inline int gvm_row_bytes(int K) { return (3 * K + K / 32 + 15) & ~15; }
+// K padded to whole stages.
+__host__ __device__ inline int gvm_kpad(int K) { return (K + kGvmKS - 1) / kGvmKS * kGvmKS; }
+
+// Activation row in the limb format, K padded to Kp = gvm_kpad(K) with
+// zeros: limb L's Kp bytes at L * Kp, then one e8m0 scale per 32-element
+// block at 3 Kp; rounded to 16 bytes.
+__host__ __device__ inline int gvm_row_bytes(int K) {
+    const int kp = gvm_kpad(K);
+    return (3 * kp + kp / 32 + 15) & ~15;
+}
 
 size_t gvm_act_bytes(int K) { return size_t(gvm_row_bytes(K)); }
 
-// One thread per 32-element block.
+// One thread per 32-element block of the padded row (blocks past K: zero
+// limbs under scale 1).
 __global__ __launch_bounds__(256) void gvm_format_kernel(const float* src0, int rows0, uint8_t* dst0,
                                                          const float* src1, int rows1, uint8_t* dst1, int K) {
-    const int nb = K / 32;
+    const int kp = gvm_kpad(K), nb = kp / 32;
     const int64_t gi = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     const int64_t n0 = int64_t(rows0) * nb;
     if (gi >= n0 + int64_t(rows1) * nb) return;
@@ -79,9 +88,10 @@ __global__ __launch_bounds__(256) void gvm_format_kernel(const float* src0, int 
     const float4* s4 = reinterpret_cast<const float4*>((second ? src1 : src0) + int64_t(row) * K + b * 32);
     uint8_t* dst = (second ? dst1 : dst0) + int64_t(row) * gvm_row_bytes(K);
     float v[32];
+    const bool in = b * 32 < K;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const float4 q = s4[i];
+        const float4 q = in ? s4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
         v[4 * i] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
     }
     float mx = 0.0f;
@@ -110,37 +120,39 @@ __global__ __launch_bounds__(256) void gvm_format_kernel(const float* src0, int 
     }
 #pragma unroll
     for (int L = 0; L < kGvmLimbs; ++L) {
-        uint4* d4 = reinterpret_cast<uint4*>(dst + int64_t(L) * K + b * 32);
+        uint4* d4 = reinterpret_cast<uint4*>(dst + int64_t(L) * kp + b * 32);
         d4[0] = make_uint4(w[L][0], w[L][1], w[L][2], w[L][3]);
         d4[1] = make_uint4(w[L][4], w[L][5], w[L][6], w[L][7]);
     }
-    dst[3 * K + b] = uint8_t(s + 127);
+    dst[3 * kp + b] = uint8_t(s + 127);
 }
 
 hipError_t gvm_format_launch(hipStream_t st, const float* src0, int rows0, uint8_t* dst0, const float* src1,
                              int rows1, uint8_t* dst1, int K) {
-    const int64_t n = int64_t(rows0 + rows1) * (K / 32);
+    const int64_t n = int64_t(rows0 + rows1) * (gvm_kpad(K) / 32);
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(gvm_format_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, src0, rows0, dst0, src1,
                        rows1, dst1, K);
     return hipGetLastError();
 }
 
-// Stage s of an item into the ring stage at st: exactly 14 instructions,
+// Stage s of an item into the ring stage at st: exactly 15 instructions,
 // each with lane 0 active.  Codes: instruction j covers the wave's rows
 // 8 j + lane / 8, slot lane % 8 holding 16-byte piece (lane % 8) ^
-// ((row >> 1) & 7).  Scales: instruction jj covers rows 32 jj + lane / 2,
-// 4 bytes each.  Activations: piece p = 64 ja + lane of [row m][limb L]
+// ((row >> 1) & 7).  Scales: the 12 bytes of each row from the 4-byte-
+// aligned start of its 8 (row r's at 12 r; lane 64 jj + i is dword i % 3
+// of row (64 jj + i) / 3).  Activations: piece p = 64 ja + lane of [row m][limb L]
 // [16 x 16 B] (192 pieces; rows past mc are not loaded: their columns are
 // never stored), then the 4 rows' 8 block scales (lane = 2 m + half).
 __device__ __forceinline__ void gvm_issue(uint8_t* st, __amdgpu_buffer_rsrc_t rp, __amdgpu_buffer_rsrc_t rs,
-                                          __amdgpu_buffer_rsrc_t ra, const int (&pofs)[8], const int (&sofs)[2],
+                                          __amdgpu_buffer_rsrc_t ra, const int (&pofs)[8], const int (&sofs)[3],
                                           const int (&aofs)[3], int asofs, int mc, int lane, int s) {
+    constexpr int NS = 3;
 #pragma unroll
     for (int j = 0; j < 8; ++j)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (gvm_lds_ptr_t)(st + j * 1024), 16, pofs[j], s * 128, 0, 2);
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj)
+    for (int jj = 0; jj < NS; ++jj)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (gvm_lds_ptr_t)(st + kGvmOS + jj * 256), 4, sofs[jj], s * 8, 0,
                                                  0);
 #pragma unroll
@@ -160,12 +172,12 @@ __device__ __forceinline__ void gvm_issue(uint8_t* st, __amdgpu_buffer_rsrc_t rp
 // stage, so one vmcnt wait per stage covers it.
 template <bool GU>
 __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
-    constexpr int NT = 14;                                   // DMA instructions per stage
+    constexpr int NT = 15;                                   // DMA instructions per stage
     constexpr int ST = kGvmStages;
     constexpr int WAIT = NT * (ST - 1);
     static_assert(WAIT <= 63, "vmcnt holds 63");
     extern __shared__ __attribute__((aligned(1024))) uint8_t gvm_ring[];
-    const int N = a.N, Kd = a.K, S = Kd / kGvmKS;
+    const int N = a.N, Kd = a.K, Kp = gvm_kpad(Kd), S = Kp / kGvmKS;
     const int lrow = Kd / 2, srb = Kd / 32;                  // code / scale bytes per weight row
     const int AB = gvm_row_bytes(Kd);
     constexpr int PW = GU ? kGvmRows / 2 : kGvmRows;         // rows (pairs) per wave
@@ -188,7 +200,7 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
         const uint8_t* pb;     // the expert's codes, scales; the activation rows
         const uint8_t* sbp;
         const uint32_t* ab;
-        int pofs[8], sofs[2], aofs[3], asofs;
+        int pofs[8], sofs[3], aofs[3], asofs;
         int r0, mc, i0;
         bool sh;
     };
@@ -241,13 +253,16 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
                 d.pofs[j] = wrow(r) * lrow + (((lane & 7) ^ ((r >> 1) & 7)) << 4);
             }
 #pragma unroll
-            for (int jj = 0; jj < 2; ++jj) d.sofs[jj] = wrow(32 * jj + (lane >> 1)) * srb + (lane & 1) * 4;
+            for (int jj = 0; jj < 3; ++jj) {
+                const int gi = 64 * jj + lane;                   // row gi / 3, dword gi % 3
+                d.sofs[jj] = ((wrow(gi / 3) * srb) & ~3) + (gi % 3) * 4;
+            }
 #pragma unroll
             for (int ja = 0; ja < 3; ++ja) {
                 const int pc = 64 * ja + lane;
-                d.aofs[ja] = arow(pc / 48) * AB + ((pc / 16) % 3) * Kd + (pc % 16) * 16;
+                d.aofs[ja] = arow(pc / 48) * AB + ((pc / 16) % 3) * Kp + (pc % 16) * 16;
             }
-            d.asofs = arow((lane >> 1) & 3) * AB + 3 * Kd + (lane & 1) * 4;
+            d.asofs = arow((lane >> 1) & 3) * AB + 3 * Kp + (lane & 1) * 4;
             break;
         }
         return d;
@@ -288,6 +303,14 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
         const int mcol = col < cur.mc ? col : 0;
+        // byte offset of each of this lane's rows' scales from its 4-byte-aligned start
+        int soff[NRB];
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) {
+            const int r = 16 * rb + col;
+            const int wr = GU ? (r >= PW ? N : 0) + min(cur.i0 + (r & (PW - 1)), N - 1) : min(cur.i0 + r, N - 1);
+            soff[rb] = wr * srb;
+        }
         // B operand of MFMA step t of a stage: limb L's bytes at
         // [m][L][256]: K 128 t + 32 (g >> 1) + 16 (g & 1), and + 64
         const uint32_t boff = uint32_t(mcol * kGvmLimbs * kGvmKS + 32 * (grp >> 1) + 16 * (grp & 1));
@@ -319,7 +342,8 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
                     const int pc = 4 * t + grp;                      // 16-byte piece of the row's 128
                     asm volatile("ds_read_b128 %0, %1"
                                  : "=v"(aq[rb]) : "v"(stb + r * 128 + ((pc ^ ((r >> 1) & 7)) << 4)));
-                    asm volatile("ds_read_u8 %0, %1" : "=v"(sa[rb]) : "v"(stb + kGvmOS + r * 8 + pc));
+                    asm volatile("ds_read_u8 %0, %1"
+                                 : "=v"(sa[rb]) : "v"(stb + kGvmOS + r * 12 + (soff[rb] & 3) + pc));
                 }
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
@@ -327,6 +351,19 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
                 asm volatile("" : "+v"(sb));
 #pragma unroll
                 for (int rb = 0; rb < NRB; ++rb) asm volatile("" : "+v"(aq[rb]), "+v"(sa[rb]));
+                if (Kp != Kd && s == S - 1) {
+                    // blocks past K (the codes of the next row, or zero past
+                    // the buffer; the activations there are zero): zero
+                    // codes under scale 1, so that no scale byte read there
+                    // can turn the zero products into NaN
+                    if ((8 * s + 4 * t + grp) * 32 >= Kd) {
+#pragma unroll
+                        for (int rb = 0; rb < NRB; ++rb) {
+                            aq[rb] = u32x4{0u, 0u, 0u, 0u};
+                            sa[rb] = 127u;
+                        }
+                    }
+                }
                 // limbs outer: consecutive MFMAs update different accumulators
 #pragma unroll
                 for (int L = 0; L < kGvmLimbs; ++L) {
@@ -380,15 +417,16 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the repeats past the last item
 }
 
-// K a multiple of 256 with at least ST - 1 stages per item (the stream's
-// look-ahead reaches at most into the next item).
+// K a multiple of 64 (2-byte aligned scale rows) with at least ST - 1
+// stages per item (the stream's look-ahead reaches at most into the next
+// item).
 bool gvm_shape_ok(int H, int I) {
     const int kmin = (kGvmStages - 1) * kGvmKS;
-    return H % kGvmKS == 0 && I % kGvmKS == 0 && H >= kmin && I >= kmin;
+    return H % 64 == 0 && I % 64 == 0 && gvm_kpad(H) >= kmin && gvm_kpad(I) >= kmin;
 }
 
 hipError_t gvm_launch(hipStream_t st, const GvArgs& a, bool gate_up) {
-    if (a.K % kGvmKS || a.K < (kGvmStages - 1) * kGvmKS) return hipErrorInvalidValue;
+    if (a.K % 64 || gvm_kpad(a.K) < (kGvmStages - 1) * kGvmKS) return hipErrorInvalidValue;
     static int cus = 0;
     if (cus == 0) {
         int dev = 0;
