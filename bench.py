@@ -506,6 +506,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 64 MiB device copy 5 times (HBM counter calibration)")
+    ap.add_argument("--only", choices=("c3", "c4", "c5", "edges"),
+                    help="run only this workload's section and print it alone (for profiling runs)")
     ap.add_argument("--decode-regime", type=int, default=1, choices=(1, 3),
                     help="1: router logits, gate_up (with the top-k), down; "
                          "3: router logits, top-k, gate_up, down as four launches")
@@ -517,6 +519,17 @@ def main():
     dev = torch.device("cuda:0")
     _abi.lib()
     stream = torch.cuda.Stream()
+    if a.copy_probe:
+        src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+    if a.only:
+        run = {"c3": lambda: c3_bench(dev, stream), "c4": lambda: prefill_bench(dev, stream),
+               "c5": lambda: c5_bench(dev, stream), "edges": lambda: edges_bench(dev, stream)}[a.only]
+        print(json.dumps({"only": a.only, a.only: run()}), flush=True)
+        return
     log("decode bench (C2, 48 layers)...")
     d = decode_bench(a.steps, a.warmup, dev, stream, a.decode_regime)
     out = {
@@ -551,12 +564,6 @@ def main():
             "bytes_per_launch": int(d["gu_bytes"]),
         },
     }
-    if a.copy_probe:
-        src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
     if not a.no_prefill:
         log("prefill bench (C4)...")
         out["prefill"] = prefill_bench(dev, stream)
