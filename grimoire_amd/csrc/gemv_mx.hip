@@ -22,14 +22,17 @@
 // +16) of blocks (g >> 1) and (g >> 1) + 2, with the scale of block g; D
 // holds column l % 16, rows 4 (l / 16) + [0, 4).
 //
-// Each wave owns 128 weight rows of an item (gate_up: 64 gate and the
-// matching 64 up rows) and walks the K steps of 128: per step its rows'
-// 8 KiB of codes and 512 bytes of scales, and the group's limb rows at the
-// step, stream through its own LDS ring by buffer_load ... lds (two steps
-// ahead; code slots XOR-swizzled so that the 16-row operand reads are free
-// of bank conflicts), and 8 row blocks x 3 limbs of MFMAs accumulate.  Like
-// gemv_grouped.hip: one work-group per CU, no barrier, every wave waits on
-// its own vmcnt only.
+// Each wave owns 64 weight rows of an item (gate_up: 32 gate and the
+// matching 32 up rows) and walks K in stages of 256 (two MFMA steps): per
+// stage its rows' 8 KiB of codes and their scale bytes, and the group's
+// limb rows at the stage with their scales, stream through its own
+// three-stage LDS ring by buffer_load ... lds (code slots XOR-swizzled so
+// that the 16-row operand reads are free of bank conflicts), and 4 row
+// blocks x 3 limbs of MFMAs per step accumulate.  K is padded to whole
+// stages: the activation limbs past K are zero and the weight tail is
+// masked.  One continuous stage stream runs across a wave's items, so an
+// item starts with its data in flight.  Like gemv_grouped.hip: one
+// work-group per CU, no barrier, every wave waits on its own vmcnt only.
 #include "gemv_mx.hpp"
 
 #include "gemv_impl.hpp"

@@ -601,11 +601,13 @@ size_t grimoire_moe_forward_workspace_bytes(const grim_moe_layer* L, int tokens)
 /* y fp32 [T][H] = MoE(x fp32 [T][H]).  shared_gate_w bf16 [H] (may be NULL:
  * shared expert weight 1, as src/moe_ref.cpp:100-104).  Routing is written
  * to out_expert/out_weight [T][K] when not NULL.  regime: 0 = choose
- * (slot GEMV for T*K <= 64; else the expert-grouped GEMV for T*K <= 2E
- * on INT4 / MXFP4 experts; else the grouped MFMA GEMM), 1 = GEMV,
+ * (the expert-grouped GEMV on the matrix core for MXFP4 batches of
+ * 16 <= T*K <= 2E whose shapes it takes; else slot GEMV for T*K <= 64;
+ * else the expert-grouped GEMV for T*K <= 2E on INT4 / MXFP4 experts;
+ * else the grouped MFMA GEMM), 1 = GEMV,
  * 2 = grouped GEMM, 3 = GEMV with one launch per stage, 4 = expert-grouped
- * GEMV (MXFP4, hidden and inter multiples of 256, >= 512: on the scaled fp4
- * matrix core; otherwise on the vector ALU), 5 = expert-grouped GEMV on
+ * GEMV (MXFP4 with hidden and inter multiples of 64 above 256: on the
+ * scaled fp4 matrix core, K padded to 256; otherwise on the vector ALU), 5 = expert-grouped GEMV on
  * the vector ALU.  No reference counterpart for 3-5 (regimes of this
  * build; the reference picks its kernels per batch size the same way). */
 int grimoire_moe_forward(void* stream, const grim_moe_layer* L, const grim_route_params* rp,
