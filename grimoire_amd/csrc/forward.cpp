@@ -253,6 +253,11 @@ static int forward_gemm_i8(hipStream_t st, const grim_moe_layer* L, const Plan& 
     g.tmax = p.tmax;
     g.n_tiles_dev = dispatch_live_tiles(p.disp_ws, tokens, K, E);
     g.T_sh = sh ? tokens : 0;
+    // experts with few rows on 32-row tiles (tile lists formed in the kernels)
+    if (E <= kI8MaxListExperts) {
+        g.split = kI8DefaultSplit;
+        g.num_experts = E;
+    }
     e = gemm_i8_launch(st, g);
     if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
     // h limbs (rows beyond the routed count are never read)

@@ -85,6 +85,64 @@ __device__ __forceinline__ int sload_i32(const int32_t* p) {
     return v;
 }
 
+__device__ __forceinline__ int lds_i32(int addr) {
+    int v;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+    return v;
+}
+
+// Rows mode: the tile list of a kernel from the per-expert row counts.
+// Expert e takes ceil(count / BM) tiles when lo < count <= hi; tp[e] is
+// the inclusive prefix of those tile counts (tile ty belongs to the first
+// e with tp[e] > ty).  All threads of the work-group call it, before any
+// LDS-DMA is in flight; tmp holds 2 KiB.  Returns the list's length.
+template <int BM, int NT>
+__device__ int i8_list_scan(const int32_t* __restrict__ counts, int E, int lo, int hi, int32_t* tp,
+                            int32_t* tmp) {
+    constexpr int PER = kI8MaxListExperts / NT;   // experts per thread
+    const int t = threadIdx.x;
+    int v[PER], sum = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int e = PER * t + j;
+        const int c = e < E ? counts[e] : 0;
+        v[j] = (c > lo && c <= hi) ? (c + BM - 1) / BM : 0;
+        sum += v[j];
+    }
+    tmp[t] = sum;
+    __syncthreads();
+    for (int off = 1; off < NT; off <<= 1) {
+        const int a = t >= off ? tmp[t - off] : 0;
+        __syncthreads();
+        tmp[t] += a;
+        __syncthreads();
+    }
+    int run = tmp[t] - sum;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        run += v[j];
+        if (PER * t + j < E) tp[PER * t + j] = run;
+    }
+    const int total = tmp[NT - 1];
+    __syncthreads();
+    return total;
+}
+
+// The expert of list tile ty (wave-uniform, ty < the list's length) and
+// the end of its tiles, tend = tp[e]: two ballots over 16-expert blocks.
+__device__ __forceinline__ int i8_list_find(int tp_addr, int E, int ty, int& tend) {
+    const int ln = lane_id();
+    const int i0 = min(E - 1, 16 * ln + 15);
+    const uint64_t b0 = __ballot(lds_i32(tp_addr + 4 * i0) > ty);
+    const int f = __builtin_amdgcn_readfirstlane(int(__builtin_ctzll(b0)));
+    const int i1 = min(E - 1, 16 * f + (ln & 15));
+    const int v1 = lds_i32(tp_addr + 4 * i1);
+    const uint64_t b1 = __ballot(v1 > ty) & 0xFFFFull;
+    const int j = __builtin_amdgcn_readfirstlane(int(__builtin_ctzll(b1)));
+    tend = __builtin_amdgcn_readlane(v1, j);
+    return 16 * f + j;
+}
+
 struct I8Src {
     const uint8_t* w;
     const float* ws;
@@ -105,28 +163,41 @@ struct I8Item {
     int sh;                // 1: a shared-expert item (its own A rows, weights, output)
 };
 
-template <bool SWIGLU>
-__device__ __forceinline__ I8Item i8_item(const GemmI8Args& g, int n_routed, int ty, int nt) {
+// Item (list tile ty, column tile nt) of a kernel with BM x BN tiles.  The
+// routed tiles come from the dispatch's table, or in rows mode (tp_addr >=
+// 0) from the kernel's own list; tiles past n_routed are the shared
+// expert's.
+template <bool SWIGLU, int BM, int BN>
+__device__ __forceinline__ I8Item i8_item(const GemmI8Args& g, int n_routed, int ty, int nt,
+                                          int tp_addr) {
     int rows_valid;
     int64_t arow0, wrow0;
     ty = __builtin_amdgcn_readfirstlane(ty);
     const bool routed = ty < n_routed;
     if (!routed) ty -= n_routed;
-    if (routed) {
+    if (routed && tp_addr >= 0) {
+        int tend;
+        const int e = i8_list_find(tp_addr, g.num_experts, ty, tend);
+        const int c = sload_i32(g.counts + e);
+        const int mb = ty - (tend - (c + BM - 1) / BM);
+        rows_valid = min(BM, c - mb * BM);
+        arow0 = int64_t(sload_i32(g.offsets + e)) + int64_t(mb) * BM;
+        wrow0 = int64_t(e) * g.N;
+    } else if (routed) {
         const int e = sload_i32(g.tile_e + ty);
         const int ec = e < 0 ? 0 : e;
         const int mb = sload_i32(g.tile_mb + ty);
-        rows_valid = e < 0 ? 0 : min(QBM, sload_i32(g.counts + ec) - mb * QBM);
-        arow0 = int64_t(sload_i32(g.offsets + ec)) + int64_t(mb) * QBM;
+        rows_valid = e < 0 ? 0 : min(BM, sload_i32(g.counts + ec) - mb * BM);
+        arow0 = int64_t(sload_i32(g.offsets + ec)) + int64_t(mb) * BM;
         wrow0 = int64_t(ec) * g.N;
     } else {
-        rows_valid = min(QBM, g.T_sh - ty * QBM);
-        arow0 = int64_t(ty) * QBM;
+        rows_valid = min(BM, g.T_sh - ty * BM);
+        arow0 = int64_t(ty) * BM;
         wrow0 = 0;
     }
     I8Item it;
     it.sh = routed ? 0 : 1;
-    it.col0 = nt * (SWIGLU ? QBN / 2 : QBN);
+    it.col0 = nt * (SWIGLU ? BN / 2 : BN);
     it.rows = max(0, __builtin_amdgcn_readfirstlane(rows_valid));
     it.arow0 = int64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(arow0)))) |
                (int64_t(__builtin_amdgcn_readfirstlane(int(arow0 >> 32))) << 32);
@@ -170,6 +241,7 @@ __global__ __launch_bounds__(kQThreads) void grouped_gemm_i8_kernel(GemmI8Args g
     // per item parity: row scales [128] at 0, column scales at 1024 (plain:
     // [256]; SwiGLU: gate [128] then up [128])
     __shared__ __attribute__((aligned(16))) float meta[2][512];
+    __shared__ int32_t tp[kI8MaxListExperts];
     // parts: 1 = routed m-tiles, 2 = the shared expert's, 3 = both in one
     // list (routed first; the host fuses them only when the two weight sets
     // share a row length, which the per-lane weight offsets assume)
@@ -177,10 +249,15 @@ __global__ __launch_bounds__(kQThreads) void grouped_gemm_i8_kernel(GemmI8Args g
     const I8Src src_s{g.w_sh, g.ws_sh, g.row_bytes_sh, g.A_sh, g.sa_sh, g.out_sh};
     const int64_t wrb = parts == 2 ? g.row_bytes_sh : g.row_bytes;
     int n_routed = 0;
-    if (parts & 1) {
+    const bool rows_mode = g.split > 0;
+    if ((parts & 1) && rows_mode) {
+        n_routed = i8_list_scan<QBM, kQThreads>(g.counts, g.num_experts, g.list_lo, 0x7FFFFFFF, tp,
+                                     reinterpret_cast<int32_t*>(&smem[0][0]));
+    } else if (parts & 1) {
         n_routed = g.n_tiles_dev ? __builtin_amdgcn_readfirstlane(*g.n_tiles_dev) : g.tmax;
         n_routed = n_routed < g.tmax ? n_routed : g.tmax;
     }
+    const int tp_addr = rows_mode ? int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int32_t*)(&tp[0]))) : -1;
     const int total = n_routed + ((parts & 2) ? (g.T_sh + QBM - 1) / QBM : 0);
     // work-group b runs on XCD b % 8: each XCD walks a contiguous range of
     // the m-tile list, column tiles fastest, so an expert's weights and an
@@ -283,7 +360,7 @@ __global__ __launch_bounds__(kQThreads) void grouped_gemm_i8_kernel(GemmI8Args g
     };
 
     const int nk = K / QBK;   // >= 3
-    I8Item cur = i8_item<SWIGLU>(g, n_routed, tile_of(i), col_of(i));
+    I8Item cur = i8_item<SWIGLU, QBM, QBN>(g, n_routed, tile_of(i), col_of(i), tp_addr);
     I8Item none;
     none.arow0 = 0; none.wrow = 0; none.rows = 0; none.col0 = 0; none.sh = 0;
     request_meta(cur, 0);
@@ -300,7 +377,7 @@ __global__ __launch_bounds__(kQThreads) void grouped_gemm_i8_kernel(GemmI8Args g
     for (; i < items; i += per_xcd) {
         GRIM_I8_OFFSETS();
         const bool more = i + per_xcd < items;
-        const I8Item nxt = more ? i8_item<SWIGLU>(g, n_routed, tile_of(i + per_xcd), col_of(i + per_xcd))
+        const I8Item nxt = more ? i8_item<SWIGLU, QBM, QBN>(g, n_routed, tile_of(i + per_xcd), col_of(i + per_xcd), tp_addr)
                                 : none;
 #pragma unroll
         for (int l = 0; l < 2; ++l)
@@ -464,6 +541,273 @@ __global__ __launch_bounds__(kQThreads) void grouped_gemm_i8_kernel(GemmI8Args g
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// ------------------------------------------------------- narrow tiles
+//
+// Experts with few rows (the long tail of a skewed routing: most of C4's
+// 512 experts hold fewer than 32 of its 40960 rows) on the 128-row tiles
+// above cost a whole tile's A feed and MFMAs for a handful of rows, and
+// their weights -- read once, from memory -- are the real work.  This
+// kernel runs them in 32-row x 256-column tiles whose ring stages span
+// 128 K: each weight row's 128 bytes of a stage are one whole memory line,
+// and every DMA instruction moves whole lines (B: 8 rows x 128 bytes; A: 4
+// limb rows x 256 bytes), which streams weights markedly faster than the
+// half-line segments of 64-K stages.  Four waves, three stages of 40 KiB
+// (two in flight while one is multiplied); wave w owns tile columns
+// [64 w, +64) (SwiGLU: h columns [32 w, +32), gate and up) for all 32
+// rows.  Same wait accounting and continuous stage stream across items as
+// the 128-row kernel.
+constexpr int NBM = 32, NBN = 256, NBK = 128;
+constexpr int kNThreads = 256;
+constexpr int kNStages = 3;
+constexpr int kNA = NBM * 2 * NBK;                 // 8 KiB of limbs
+constexpr int kNStageBytes = kNA + NBN * NBK;      // + 32 KiB of codes
+
+bool gemm_i8_narrow_ok(int K) { return K % NBK == 0 && K >= (kNStages - 1) * NBK; }
+
+template <bool SWIGLU>
+__global__ __launch_bounds__(kNThreads) void grouped_gemm_i8_narrow_kernel(GemmI8Args g, int n_col_tiles) {
+    constexpr int NJA = 2, NJB = 8;          // A / B instructions per wave per stage
+    constexpr int OPS = NJA + NJB;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kNStages][kNStageBytes];
+    // per item parity: row scales [32] at 0 (the DMA pads to 256), column
+    // scales at 256 (plain: [256]; SwiGLU: gate [128] then up [128])
+    __shared__ __attribute__((aligned(16))) float meta[2][512];
+    __shared__ int32_t tp[kI8MaxListExperts];
+    const int total = i8_list_scan<NBM, kNThreads>(g.counts, g.num_experts, 0, g.split, tp,
+                                                   reinterpret_cast<int32_t*>(&smem[0][0]));
+    const int tp_addr = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int32_t*)(&tp[0])));
+    const int xcd = blockIdx.x % kQXcds, per_xcd = gridDim.x / kQXcds;
+    const int lo = int(int64_t(total) * xcd / kQXcds), hi = int(int64_t(total) * (xcd + 1) / kQXcds);
+    const int items = (hi - lo) * n_col_tiles;
+    int i = blockIdx.x / kQXcds;
+    if (i >= items) return;
+
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+    const int K = g.K;
+    const int a_row_bytes = 2 * K;
+    const int64_t wrb = g.row_bytes;
+
+    // Stage layout (K [128 s, +128)):
+    //   A 8 KiB: limb row r's 256 bytes (two 64-K blocks of hi then lo
+    //     codes: chunk c = 8 block + 4 limb + K%64/16) at r * 256, chunk c
+    //     at slot c ^ (r & 15);
+    //   B 32 KiB: tile column n's 128 bytes (chunk c = K/16) at 8192 +
+    //     n * 128, chunk c at slot c ^ ((n >> 1) & 7).
+    // A fragment read (32 rows, one chunk) and a B fragment read (32
+    // columns, one chunk) each hit 16 distinct 16-byte slots per 16 lanes.
+    int a_off[NJA], b_off[NJB], fa_off[2][2][2], fb_off[2][2][2];
+#define GRIM_N8_OFFSETS()                                                                         \
+    do {                                                                                          \
+        const int ln = lane_id();                                                                 \
+        _Pragma("unroll") for (int j = 0; j < NJA; ++j) {                                         \
+            const int r = 4 * (NJA * wave + j) + (ln >> 4), sl = ln & 15;                         \
+            a_off[j] = r * a_row_bytes + ((sl ^ (r & 15)) << 4);                                  \
+        }                                                                                         \
+        _Pragma("unroll") for (int j = 0; j < NJB; ++j) {                                         \
+            const int col = 8 * (NJB * wave + j) + (ln >> 3), sl = ln & 7;                        \
+            const int nsub = col >> 5, x = col & 31;                                              \
+            const int row = SWIGLU ? ((nsub & 1) ? g.I : 0) + (nsub >> 1) * 32 + x : col;         \
+            b_off[j] = row * int(wrb) + ((sl ^ ((col >> 1) & 7)) << 4);                           \
+        }                                                                                         \
+        _Pragma("unroll") for (int kk = 0; kk < 2; ++kk)                                          \
+            _Pragma("unroll") for (int ks = 0; ks < 2; ++ks) {                                    \
+                const int ch = 2 * ks + (ln >> 5);                                                \
+                const int r = ln & 31;                                                            \
+                _Pragma("unroll") for (int l = 0; l < 2; ++l)                                     \
+                    fa_off[kk][ks][l] = r * 256 + (((8 * kk + 4 * l + ch) ^ (r & 15)) << 4);      \
+                _Pragma("unroll") for (int ni = 0; ni < 2; ++ni) {                                \
+                    const int n = (2 * wave + ni) * 32 + (ln & 31);                               \
+                    fb_off[kk][ks][ni] = kNA + n * 128 + (((4 * kk + ch) ^ ((n >> 1) & 7)) << 4); \
+                }                                                                                 \
+            }                                                                                     \
+    } while (0)
+    GRIM_N8_OFFSETS();
+
+    auto tile_of = [&](int ii) { return lo + ii / n_col_tiles; };
+    auto col_of = [&](int ii) { return ii % n_col_tiles; };
+    const int n_slab = SWIGLU ? 2 * g.I : g.N;
+    const int ldo = SWIGLU ? g.I : g.N;
+    auto rsrc_a = [&](const I8Item& it) {
+        return i8_rsrc(g.A + it.arow0 * a_row_bytes, it.rows * a_row_bytes);
+    };
+    auto rsrc_b = [&](const I8Item& it) {
+        return i8_rsrc(g.w + it.wrow * wrb, it.rows > 0 ? int((n_slab - it.col0) * wrb) : 0);
+    };
+    // scale requests: wave 0 the 32 row scales, wave 1 the 256 column
+    // scales (SwiGLU: lanes 0..31 gate, 32..63 up)
+    auto request_meta = [&](const I8Item& it, int par) {
+        const int ln = lane_id();
+        if (wave == 0) {
+            dma16<0>(i8_rsrc(g.sa + it.arow0, it.rows * 4), reinterpret_cast<uint8_t*>(&meta[par][0]),
+                     ln * 16, 0);
+        } else if (wave == 1) {
+            const int m_off = (SWIGLU && ln >= 32) ? g.I * 4 + (ln - 32) * 16 : ln * 16;
+            dma16<0>(i8_rsrc(g.ws + it.wrow, it.rows > 0 ? (n_slab - it.col0) * 4 : 0),
+                     reinterpret_cast<uint8_t*>(&meta[par][256]), m_off, 0);
+        }
+    };
+    auto request = [&](const I8Item& it, int stage, int t) {
+        uint8_t* st = smem[stage];
+        const __amdgpu_buffer_rsrc_t ra = rsrc_a(it), rb = rsrc_b(it);
+#pragma unroll
+        for (int j = 0; j < NJA; ++j) dma16<0>(ra, st + (NJA * wave + j) * 1024, a_off[j], t * 256);
+#pragma unroll
+        for (int j = 0; j < NJB; ++j) dma16<2>(rb, st + kNA + (NJB * wave + j) * 1024, b_off[j], t * NBK);
+    };
+
+    const int nk = K / NBK;   // >= kNStages - 1
+    I8Item cur = i8_item<SWIGLU, NBM, NBN>(g, total, tile_of(i), col_of(i), tp_addr);
+    I8Item none;
+    none.arow0 = 0; none.wrow = 0; none.rows = 0; none.col0 = 0; none.sh = 0;
+    request_meta(cur, 0);
+#pragma unroll
+    for (int p = 0; p < kNStages - 1; ++p) request(cur, p, p);
+
+    const int smem_base = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)(&smem[0][0])));
+    const int meta_base = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) float*)(&meta[0][0])));
+    int gs = 0, par = 0;       // gs: ring slot of the item's stage 0
+    bool first = true;
+    i32x16 acc[2][2];
+    i32x4 fb[2][2], fa[2][2];
+    for (; i < items; i += per_xcd) {
+        GRIM_N8_OFFSETS();
+        const bool more = i + per_xcd < items;
+        const I8Item nxt = more ? i8_item<SWIGLU, NBM, NBN>(g, total, tile_of(i + per_xcd), col_of(i + per_xcd), tp_addr)
+                                : none;
+#pragma unroll
+        for (int l = 0; l < 2; ++l)
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[l][ni][v] = 0;
+        // the wait before stage t: the next stage's loads (YT) are younger,
+        // and right after an epilogue (t < 2) also its stores (ES per lane)
+        constexpr int YT = OPS;
+        constexpr int ES = (SWIGLU ? 1 : 2) * 16;
+        constexpr int YE = YT + ES < 63 ? YT + ES : 63;
+#define GRIM_N8_WAIT(after_epi)                                                                   \
+        asm volatile("s_cmp_eq_u32 %0, 0\n\t"                                                    \
+                     "s_cbranch_scc1 .Lgrim_n16_%=\n\t"                                           \
+                     "s_waitcnt vmcnt(%2)\n\t"                                                   \
+                     "s_branch .Lgrim_ndone_%=\n"                                                 \
+                     ".Lgrim_n16_%=:\n\t"                                                        \
+                     "s_waitcnt vmcnt(%1)\n"                                                      \
+                     ".Lgrim_ndone_%=:\n\t"                                                      \
+                     "s_waitcnt lgkmcnt(0)\n\t"                                                  \
+                     "s_barrier" ::"s"(__builtin_amdgcn_readfirstlane(after_epi)), "n"(YT), "n"(YE) \
+                     : "memory", "scc")
+#define GRIM_N8_DSR(dst, addr)                                                                    \
+        asm volatile("ds_read_b128 %0, %1" : "=v"(dst) : "v"(addr))
+#define GRIM_N8_LGKM(n, ks_)                                                                      \
+        asm volatile("s_waitcnt lgkmcnt(" #n ")"                                                   \
+                     : "+v"(fb[ks_][0]), "+v"(fb[ks_][1]), "+v"(fa[ks_][0]), "+v"(fa[ks_][1]))
+#define GRIM_N8_MMA(ks_)                                                                          \
+        _Pragma("unroll") for (int ni = 0; ni < 2; ++ni)                                          \
+            _Pragma("unroll") for (int l = 0; l < 2; ++l)                                         \
+                acc[l][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks_][l], fb[ks_][ni], acc[l][ni], 0, 0, 0)
+#define GRIM_N8_READS(kk_)                                                                        \
+        _Pragma("unroll") for (int ks = 0; ks < 2; ++ks) {                                        \
+            GRIM_N8_DSR(fb[ks][0], sb + fb_off[kk_][ks][0]);                                      \
+            GRIM_N8_DSR(fb[ks][1], sb + fb_off[kk_][ks][1]);                                      \
+            GRIM_N8_DSR(fa[ks][0], sb + fa_off[kk_][ks][0]);                                      \
+            GRIM_N8_DSR(fa[ks][1], sb + fa_off[kk_][ks][1]);                                      \
+        }
+#define GRIM_N8_DMA(q)                                                                            \
+        do {                                                                                      \
+            if ((q) < NJA) dma16<0>(qa, nx + (NJA * wave + (q)) * 1024, a_off[(q) % NJA], tu * 256); \
+            else dma16<2>(qb, nx + kNA + (NJB * wave + (q) - NJA) * 1024, b_off[((q) - NJA) % NJB], tu * NBK); \
+        } while (0)
+#define GRIM_N8_ITER(t_, META)                                                                    \
+        do {                                                                                      \
+            const int t = (t_);                                                                   \
+            GRIM_N8_WAIT((t < kNStages - 1 && !first) ? 1 : 0);                                   \
+            const int slot = (gs + t) % kNStages;                                                 \
+            const int sb = slot * kNStageBytes + smem_base;                                       \
+            GRIM_N8_READS(0);                                                                     \
+            if (META) request_meta(nxt, par ^ 1);                                                 \
+            /* stream stage t + 2: this item's, or the next item's 0, 1 */                        \
+            const int u = t + kNStages - 1;                                                       \
+            const bool own = u < nk;                                                              \
+            const __amdgpu_buffer_rsrc_t qa = rsrc_a(own ? cur : nxt);                            \
+            const __amdgpu_buffer_rsrc_t qb = rsrc_b(own ? cur : nxt);                            \
+            const int tu = own ? u : u - nk;                                                      \
+            uint8_t* nx = smem[(gs + u) % kNStages];                                              \
+            GRIM_N8_LGKM(4, 0); GRIM_N8_MMA(0); GRIM_N8_DMA(0); GRIM_N8_DMA(1);                   \
+            GRIM_N8_LGKM(0, 1); GRIM_N8_MMA(1); GRIM_N8_DMA(2); GRIM_N8_DMA(3); GRIM_N8_DMA(4);   \
+            GRIM_N8_READS(1);                                                                     \
+            GRIM_N8_DMA(5); GRIM_N8_DMA(6);                                                       \
+            GRIM_N8_LGKM(4, 0); GRIM_N8_MMA(0); GRIM_N8_DMA(7); GRIM_N8_DMA(8);                   \
+            GRIM_N8_LGKM(0, 1); GRIM_N8_MMA(1); GRIM_N8_DMA(9);                                   \
+        } while (0)
+        GRIM_N8_ITER(0, true);
+        for (int t1 = 1; t1 < nk; ++t1) GRIM_N8_ITER(t1, false);
+#undef GRIM_N8_ITER
+#undef GRIM_N8_WAIT
+#undef GRIM_N8_DSR
+#undef GRIM_N8_LGKM
+#undef GRIM_N8_MMA
+#undef GRIM_N8_READS
+#undef GRIM_N8_DMA
+
+        // ---- epilogue.  acc[l][ni][v] is row 8 (v/4) + 4 (lane/32) + v%4,
+        // column 32 (2 w + ni) + lane%32 of the tile.
+        const __amdgpu_buffer_rsrc_t ro = i8_rsrc(g.out + cur.arow0 * ldo, cur.rows * ldo * 4);
+        const int mb = meta_base + par * 2048;
+        const int ln = lane_id();
+        const int hrow = 4 * (ln >> 5);
+        f32x4v s4[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) s4[q] = lds_f32x4(mb + (8 * q + hrow) * 4);
+        if constexpr (SWIGLU) {
+            const int hcl = wave * 32 + (ln & 31);
+            float sg = lds_f32(mb + 1024 + hcl * 4), su = lds_f32(mb + 1024 + (128 + hcl) * 4);
+            int base = cur.col0 + hcl < g.I ? (hrow * g.I + cur.col0 + hcl) * 4 : 0x40000000;
+            asm volatile("" : "+v"(base));
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(s4[0]), "+v"(s4[1]), "+v"(s4[2]), "+v"(s4[3]), "+v"(sg), "+v"(su));
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int v = 4 * q + j;
+                    const float gv = s4[q][j] * sg * __builtin_fmaf(float(acc[1][0][v]), kLoScale, float(acc[0][0][v]));
+                    const float uv = s4[q][j] * su * __builtin_fmaf(float(acc[1][1][v]), kLoScale, float(acc[0][1][v]));
+                    const int off = base + (8 * q + j) * g.I * 4;
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, fast_silu(gv) * uv), ro, off, 0, 0);
+                }
+        } else {
+            float sc[2];
+            int base[2];
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) {
+                const int cl = wave * 64 + ni * 32 + (ln & 31);
+                sc[ni] = lds_f32(mb + 1024 + cl * 4);
+                base[ni] = cur.col0 + cl < g.N ? (hrow * g.N + cur.col0 + cl) * 4 : 0x40000000;
+            }
+            asm volatile("" : "+v"(base[0]), "+v"(base[1]));
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(s4[0]), "+v"(s4[1]), "+v"(s4[2]), "+v"(s4[3]), "+v"(sc[0]), "+v"(sc[1]));
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int v = 4 * q + j;
+                        const float y = s4[q][j] * sc[ni] * __builtin_fmaf(float(acc[1][ni][v]), kLoScale, float(acc[0][ni][v]));
+                        const int off = base[ni] + (8 * q + j) * g.N * 4;
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ro, off, 0, 0);
+                    }
+        }
+        gs = (gs + nk) % kNStages;
+        par ^= 1;
+        cur = nxt;
+        first = false;
+    }
+#undef GRIM_N8_OFFSETS
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 // ------------------------------------------------------------ quantisers
 
 // Row max, limbs, scale: one wave per row of n <= 4096 elements (8 per lane
@@ -589,34 +933,50 @@ __global__ __launch_bounds__(256) void quant_permute_kernel(const float* __restr
 
 // ----------------------------------------------------------------- host
 
+template <typename Kern>
+static int i8_grid(Kern k, int threads = kQThreads) {
+    int per_cu = 0, dev = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, threads, 0) != hipSuccess ||
+        hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    const int grid = (per_cu > 0 ? per_cu : 1) * cus;
+    return (grid + kQXcds - 1) / kQXcds * kQXcds;
+}
+
 template <bool SWIGLU>
 static hipError_t launch_i8(hipStream_t st, const GemmI8Args& g, int ntiles) {
-    static int grid = 0;
+    static int grid = 0, grid_n = 0;
     if (grid == 0) {
-        int per_cu = 0, dev = 0, cus = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, grouped_gemm_i8_kernel<SWIGLU>,
-                                                         kQThreads, 0) != hipSuccess ||
-            hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        grid = i8_grid(grouped_gemm_i8_kernel<SWIGLU>);
+        grid_n = i8_grid(grouped_gemm_i8_narrow_kernel<SWIGLU>, kNThreads);
+        if (grid == 0 || grid_n == 0) {
+            grid = 0;
             return hipErrorInvalidConfiguration;
-        grid = (per_cu > 0 ? per_cu : 1) * cus;
-        grid = (grid + kQXcds - 1) / kQXcds * kQXcds;
+        }
     }
-    const bool fuse = g.tmax > 0 && g.T_sh > 0 && g.row_bytes == g.row_bytes_sh;
+    const bool rows_mode = g.split > 0;
+    const bool routed = rows_mode || g.tmax > 0;
+    const bool fuse = routed && g.T_sh > 0 && g.row_bytes == g.row_bytes_sh;
     if (fuse) {
         // the shared expert's m-tiles follow the routed ones in one launch
         hipLaunchKernelGGL(grouped_gemm_i8_kernel<SWIGLU>, dim3(grid), dim3(kQThreads), 0, st, g,
                            ntiles, 3);
-        return hipGetLastError();
+    } else {
+        if (routed)
+            hipLaunchKernelGGL(grouped_gemm_i8_kernel<SWIGLU>, dim3(grid), dim3(kQThreads), 0, st, g,
+                               ntiles, 1);
+        if (g.T_sh > 0) {
+            const int items = (g.T_sh + QBM - 1) / QBM * ntiles;
+            const int gs = min(grid, (items + kQXcds - 1) / kQXcds * kQXcds);
+            hipLaunchKernelGGL(grouped_gemm_i8_kernel<SWIGLU>, dim3(gs), dim3(kQThreads), 0, st, g,
+                               ntiles, 2);
+        }
     }
-    if (g.tmax > 0)
-        hipLaunchKernelGGL(grouped_gemm_i8_kernel<SWIGLU>, dim3(grid), dim3(kQThreads), 0, st, g,
-                           ntiles, 1);
-    if (g.T_sh > 0) {
-        const int items = (g.T_sh + QBM - 1) / QBM * ntiles;
-        const int gs = min(grid, (items + kQXcds - 1) / kQXcds * kQXcds);
-        hipLaunchKernelGGL(grouped_gemm_i8_kernel<SWIGLU>, dim3(gs), dim3(kQThreads), 0, st, g,
-                           ntiles, 2);
+    if (rows_mode && g.list_lo > 0) {
+        const int nct = SWIGLU ? (g.I + NBN / 2 - 1) / (NBN / 2) : (g.N + NBN - 1) / NBN;
+        hipLaunchKernelGGL(grouped_gemm_i8_narrow_kernel<SWIGLU>, dim3(grid_n), dim3(kNThreads), 0,
+                           st, g, nct);
     }
     return hipGetLastError();
 }
@@ -629,6 +989,17 @@ bool gemm_i8_shape_ok(int N, int K, int I, int swiglu) {
 
 hipError_t gemm_i8_launch(hipStream_t st, const GemmI8Args& g) {
     if (!gemm_i8_shape_ok(g.N, g.K, g.I, g.swiglu)) return hipErrorInvalidValue;
+    if (g.split > 0 && (g.num_experts <= 0 || g.num_experts > kI8MaxListExperts))
+        return hipErrorInvalidValue;
+    if (g.split > 0) {
+        // rows mode: the 128-row kernel takes the experts above list_lo rows,
+        // the narrow one the rest (all on the 128-row kernel when K does not
+        // fit the narrow kernel's 128-K stages)
+        GemmI8Args r = g;
+        r.list_lo = gemm_i8_narrow_ok(g.K) ? g.split : 0;
+        const int nt = r.swiglu ? (r.I + QBN / 2 - 1) / (QBN / 2) : (r.N + QBN - 1) / QBN;
+        return r.swiglu ? launch_i8<true>(st, r, nt) : launch_i8<false>(st, r, nt);
+    }
     const int ntiles = g.swiglu ? (g.I + QBN / 2 - 1) / (QBN / 2) : (g.N + QBN - 1) / QBN;
     if (ntiles <= 0) return hipSuccess;
     return g.swiglu ? launch_i8<true>(st, g, ntiles) : launch_i8<false>(st, g, ntiles);

@@ -29,7 +29,18 @@ struct GemmI8Args {
     int tmax;
     const int32_t* n_tiles_dev; // live routed tile count (device) or null = tmax
     int T_sh;                   // shared-expert rows (0 = none)
+    // split > 0: rows mode -- the table is not read; each kernel forms its
+    // tile list from counts (num_experts <= 1024): experts of more than
+    // split rows in 128-row tiles, the others in 32-row tiles on the
+    // narrow kernel.  0: the tile table, all on 128-row tiles.
+    int split;
+    int num_experts;
+    int list_lo;                // set by the launcher: the 128-row list takes counts > list_lo
 };
+
+constexpr int kI8MaxListExperts = 1024;
+// rows mode: experts of at most this many rows run on 32-row tiles
+constexpr int kI8DefaultSplit = 64;
 
 bool gemm_i8_shape_ok(int N, int K, int I, int swiglu);
 hipError_t gemm_i8_launch(hipStream_t st, const GemmI8Args& g);

@@ -245,6 +245,17 @@ def tile_table(counts, mc: int = 128, tmax: int = None):
             torch.tensor(tm[:tmax], dtype=torch.int32, device=dev))
 
 
+def grouped_gemm_i8_rows(w: Weight, N, swiglu, A, a_scale, out, offsets, counts, num_experts,
+                         split=0, stream=None):
+    """grouped_gemm_i8 with the library's own tile lists formed from counts:
+    experts of more than `split` rows (0: the default) on 128-row tiles,
+    the others on 32-row tiles."""
+    _dev(A)
+    check(lib().grimoire_moe_grouped_gemm_i8_rows(_stream(stream), w.struct(), N, int(swiglu), _p(A),
+                                                  _p(a_scale), _p(out), _p(offsets), _p(counts),
+                                                  num_experts, int(split)), "grouped_gemm_i8_rows")
+
+
 def grouped_gemm_i8(w: Weight, N, swiglu, A, a_scale, out, offsets, counts, num_experts,
                     tile_e=None, tile_mb=None, stream=None):
     """INT8 experts on the int8 MFMA (limb rows from quant_limbs), fp32 out,

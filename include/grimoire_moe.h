@@ -516,6 +516,19 @@ int grimoire_moe_grouped_gemm_i8(void* stream, const grim_quant_weight* w, int N
                                  const int32_t* tile_e, const int32_t* tile_mb, int tmax,
                                  int num_experts);
 
+/* grimoire_moe_grouped_gemm_i8 without a tile table: the library forms its
+ * own tile lists from counts (num_experts <= 1024) -- experts of more than
+ * `split` rows (<= 0: the library's default, 64) in 128-row tiles, the
+ * others in 32-row tiles, so that the long tail of a skewed routing does
+ * not pay for empty tile rows.  Same products, bit for bit, as the tiled
+ * call.  No reference counterpart (the reference's INT8 experts run one
+ * expert at a time, src/grimoire.cpp:23214-23229); the forward's INT8
+ * prefill uses it.  Allocates nothing. */
+int grimoire_moe_grouped_gemm_i8_rows(void* stream, const grim_quant_weight* w, int N, int swiglu,
+                                      const int8_t* A, const float* a_scale, float* out,
+                                      const int32_t* offsets, const int32_t* counts, int num_experts,
+                                      int split);
+
 /* ------------------------------------------------------------------------
  * Bridges (the vLLM-XPU grouped GEMMs the reference dlopens).  Same
  * argument lists apart from the queue.  rows_per_expert [ne] gives the

@@ -63,6 +63,10 @@ def test_shape_rejections():
     assert lib.grimoire_moe_router_topk(None, 1, 64, 17, 1, 1, 1) == _abi.ERR_SHAPE
     assert lib.grimoire_moe_router_topk_group(None, 1, None, 1, 256, 8, 7, 4, 1, 1, 1, 1.0) == _abi.ERR_SHAPE
     assert lib.grimoire_moe_router_topk_group(None, 1, None, 1, 256, 40, 8, 1, 1, 1, 1, 1.0) == _abi.ERR_SHAPE
+    # the INT8 GEMM's own tile lists cover at most 1024 experts
+    w = _abi.QuantWeight()
+    w.fmt = _abi.FMT_INT8
+    assert lib.grimoire_moe_grouped_gemm_i8_rows(None, w, 64, 0, 1, 1, 1, 1, 1, 1025, 0) == _abi.ERR_SHAPE
 
 
 def test_null_and_workspace_rejections():

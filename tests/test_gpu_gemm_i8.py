@@ -132,3 +132,48 @@ def test_gemm_i8_swiglu_then_down(gpu):
     torch.cuda.synchronize()
     y_want = _dense(h_want.float(), dequant(wdn), counts, offsets, H)
     assert rel_l2(y.cpu(), y_want) < 5e-4
+
+
+def _rows_case(E, seed):
+    """row counts around both tile sizes (0, 1, 31, 32, 33, 64, 65, 128,
+    129, ...) over E experts, most of them empty when E is large"""
+    g = torch.Generator().manual_seed(seed)
+    edge = torch.tensor([0, 1, 31, 32, 33, 63, 64, 65, 127, 128, 129, 200, 3, 17])
+    c = torch.zeros(E, dtype=torch.int32)
+    pick = torch.randperm(E, generator=g)[: min(E, 3 * len(edge))]
+    c[pick] = edge.repeat(3)[: len(pick)].int()
+    return c
+
+
+@pytest.mark.parametrize("E,split,K", [(14, 64, 512), (37, 1, 512), (37, 32, 256), (37, 100000, 512),
+                                       (1000, 64, 640), (1024, 200, 512), (37, 64, 320)])
+@pytest.mark.parametrize("swiglu", [False, True])
+def test_gemm_i8_rows_mode_matches_tiles(gpu, E, split, K, swiglu):
+    """The library's own tile lists (32-row tiles for experts of <= split
+    rows, 128-row tiles above) give the tiled call's products bit for bit,
+    and the fp64 products within the limb error.  K = 320 is not a whole
+    number of the narrow tiles' 128-K stages: all experts then take the
+    128-row tiles."""
+    print(f"gemm i8 rows mode E={E} split={split} K={K} swiglu={swiglu}", flush=True)
+    I = 320
+    N = 2 * I if swiglu else 576
+    w = make_int8(E * N, K, seed=E + split)
+    counts = _rows_case(E, E + 7)
+    offsets = (torch.cumsum(counts, 0) - counts).int()
+    R = int(counts.sum())
+    A = torch.randn(R, K).bfloat16().float()
+    q, s = _limbs(gpu, A)
+    cols = I if swiglu else N
+    ref = torch.full((R, cols), float("nan"), device=gpu)
+    out = torch.full((R, cols), float("nan"), device=gpu)
+    wg = w.to(gpu)
+    ops.grouped_gemm_i8(wg, N, swiglu, q, s, ref, offsets.to(gpu), counts.to(gpu), E)
+    ops.grouped_gemm_i8_rows(wg, N, swiglu, q, s, out, offsets.to(gpu), counts.to(gpu), E, split=split)
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any()
+    assert torch.equal(out.cpu(), ref.cpu())
+    want = _dense(A, dequant(w), counts, offsets, N)
+    if swiglu:
+        g_, u_ = want[:, :I], want[:, I:]
+        want = g_ / (1 + torch.exp(-g_)) * u_
+    assert rel_l2(out.cpu(), want) < 2e-4
