@@ -195,21 +195,27 @@ def prefill_bench(dev, stream, reps=5):
         hq = torch.empty(R, 2 * cfg.I, dtype=torch.int8, device=dev)
         hs = torch.empty(R, device=dev)
         yp = torch.empty(R, cfg.H, device=dev)
-        ops.grouped_gemm_i8(L.gate_up, 2 * cfg.I, True, xq, xs, h, offsets, counts, cfg.E, te, tmb,
-                            stream=stream)
+        # the forward's own call: tile lists formed from the row counts
+        # (experts of few rows on 32-row tiles)
+        def gate_up():
+            ops.grouped_gemm_i8_rows(L.gate_up, 2 * cfg.I, True, xq, xs, h, offsets, counts, cfg.E,
+                                     stream=stream)
+
+        def down():
+            ops.grouped_gemm_i8_rows(L.down, cfg.H, False, hq, hs, yp, offsets, counts, cfg.E,
+                                     stream=stream)
+
+        gate_up()
         ops.quant_limbs(h, hq, hs, stream=stream)
-        ops.grouped_gemm_i8(L.down, cfg.H, False, hq, hs, yp, offsets, counts, cfg.E, te, tmb,
-                            stream=stream)
+        down()
         torch.cuda.synchronize()
         with Timer(stream) as tg:
             for _ in range(reps):
-                ops.grouped_gemm_i8(L.gate_up, 2 * cfg.I, True, xq, xs, h, offsets, counts, cfg.E,
-                                    te, tmb, stream=stream)
+                gate_up()
         gu_ms = tg.ms() / reps
         with Timer(stream) as td:
             for _ in range(reps):
-                ops.grouped_gemm_i8(L.down, cfg.H, False, hq, hs, yp, offsets, counts, cfg.E, te, tmb,
-                                    stream=stream)
+                down()
         dn_ms = td.ms() / reps
         cnt = counts.cpu()
     touched = int((cnt > 0).sum())

@@ -230,43 +230,37 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t i8_rsrc(const void* p, int byt
 // at the texture unit, 16 cycles each, and hold the MFMAs back).  Past the
 // last item the stream requests tiles from an empty buffer (num_records 0:
 // no memory traffic), which keeps every iteration alike.
+// The body of the 128-row kernel for one work-group: it takes the items
+// slot, slot + per_xcd, ... of its XCD's range; n_routed routed tiles (from
+// the table, or from the list at tp_addr >= 0) then, for parts & 2, the
+// shared expert's.  smem / meta: the kernel's LDS.  Returns where the
+// work-group's sequence continues past the last item (its first index in
+// a list that follows).
 template <bool SWIGLU>
-__global__ __launch_bounds__(kQThreads) void grouped_gemm_i8_kernel(GemmI8Args g, int n_col_tiles,
-                                                                   int parts) {
+__device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, int parts,
+                                           int n_routed, int tp_addr, int slot, int per_xcd,
+                                           uint8_t (*smem)[kQStageBytes], float (*meta)[512]) {
     // 8 waves, two per SIMD: wave w owns tile columns [64 (w % 4), +64) for
     // rows [64 (w / 4), +64)
     constexpr int MIW = 2;                   // 32-row MFMA tiles per wave
     constexpr int NJ = 2;                    // DMA instructions per wave per K tile, for A and for B
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[kQStages][kQStageBytes];
-    // per item parity: row scales [128] at 0, column scales at 1024 (plain:
-    // [256]; SwiGLU: gate [128] then up [128])
-    __shared__ __attribute__((aligned(16))) float meta[2][512];
-    __shared__ int32_t tp[kI8MaxListExperts];
+    // meta, per item parity: row scales [128] at 0, column scales at 1024
+    // (plain: [256]; SwiGLU: gate [128] then up [128]).
     // parts: 1 = routed m-tiles, 2 = the shared expert's, 3 = both in one
     // list (routed first; the host fuses them only when the two weight sets
     // share a row length, which the per-lane weight offsets assume)
     const I8Src src_r{g.w, g.ws, g.row_bytes, g.A, g.sa, g.out};
     const I8Src src_s{g.w_sh, g.ws_sh, g.row_bytes_sh, g.A_sh, g.sa_sh, g.out_sh};
     const int64_t wrb = parts == 2 ? g.row_bytes_sh : g.row_bytes;
-    int n_routed = 0;
-    const bool rows_mode = g.split > 0;
-    if ((parts & 1) && rows_mode) {
-        n_routed = i8_list_scan<QBM, kQThreads>(g.counts, g.num_experts, g.list_lo, 0x7FFFFFFF, tp,
-                                     reinterpret_cast<int32_t*>(&smem[0][0]));
-    } else if (parts & 1) {
-        n_routed = g.n_tiles_dev ? __builtin_amdgcn_readfirstlane(*g.n_tiles_dev) : g.tmax;
-        n_routed = n_routed < g.tmax ? n_routed : g.tmax;
-    }
-    const int tp_addr = rows_mode ? int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int32_t*)(&tp[0]))) : -1;
     const int total = n_routed + ((parts & 2) ? (g.T_sh + QBM - 1) / QBM : 0);
     // work-group b runs on XCD b % 8: each XCD walks a contiguous range of
     // the m-tile list, column tiles fastest, so an expert's weights and an
     // A row block stay under one L2
-    const int xcd = blockIdx.x % kQXcds, per_xcd = gridDim.x / kQXcds;
+    const int xcd = blockIdx.x % kQXcds;
     const int lo = int(int64_t(total) * xcd / kQXcds), hi = int(int64_t(total) * (xcd + 1) / kQXcds);
     const int items = (hi - lo) * n_col_tiles;
-    int i = blockIdx.x / kQXcds;
-    if (i >= items) return;
+    int i = slot;
+    if (i >= items) return i - items;
 
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
     const int wn = wave & 3, wm = wave >> 2;
@@ -539,6 +533,23 @@ __global__ __launch_bounds__(kQThreads) void grouped_gemm_i8_kernel(GemmI8Args g
 #undef GRIM_I8_OFFSETS
     // drain: the last iterations requested tiles from the empty buffer
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return i - items;
+}
+
+// Table mode: the dispatch's tile table (parts & 1) and / or the shared
+// expert's tiles (parts & 2) over the whole grid.
+template <bool SWIGLU>
+__global__ __launch_bounds__(kQThreads) void grouped_gemm_i8_kernel(GemmI8Args g, int n_col_tiles,
+                                                                   int parts) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kQStages][kQStageBytes];
+    __shared__ __attribute__((aligned(16))) float meta[2][512];
+    int n_routed = 0;
+    if (parts & 1) {
+        n_routed = g.n_tiles_dev ? __builtin_amdgcn_readfirstlane(*g.n_tiles_dev) : g.tmax;
+        n_routed = n_routed < g.tmax ? n_routed : g.tmax;
+    }
+    i8_big_run<SWIGLU>(g, n_col_tiles, parts, n_routed, -1, blockIdx.x / kQXcds, gridDim.x / kQXcds,
+                       smem, meta);
 }
 
 // ------------------------------------------------------- narrow tiles
@@ -564,22 +575,21 @@ constexpr int kNStageBytes = kNA + NBN * NBK;      // + 32 KiB of codes
 
 bool gemm_i8_narrow_ok(int K) { return K % NBK == 0 && K >= (kNStages - 1) * NBK; }
 
+// The body of the narrow kernel for one work-group (its first kNThreads
+// threads): slot / per_xcd as for i8_big_run, total tiles in the list at
+// tp_addr.  smem / meta: the kernel's LDS.
 template <bool SWIGLU>
-__global__ __launch_bounds__(kNThreads) void grouped_gemm_i8_narrow_kernel(GemmI8Args g, int n_col_tiles) {
+__device__ __forceinline__ void i8_narrow_run(const GemmI8Args& g, int n_col_tiles, int total,
+                                              int tp_addr, int slot, int per_xcd,
+                                              uint8_t (*smem)[kNStageBytes], float (*meta)[512]) {
     constexpr int NJA = 2, NJB = 8;          // A / B instructions per wave per stage
     constexpr int OPS = NJA + NJB;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[kNStages][kNStageBytes];
-    // per item parity: row scales [32] at 0 (the DMA pads to 256), column
-    // scales at 256 (plain: [256]; SwiGLU: gate [128] then up [128])
-    __shared__ __attribute__((aligned(16))) float meta[2][512];
-    __shared__ int32_t tp[kI8MaxListExperts];
-    const int total = i8_list_scan<NBM, kNThreads>(g.counts, g.num_experts, 0, g.split, tp,
-                                                   reinterpret_cast<int32_t*>(&smem[0][0]));
-    const int tp_addr = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int32_t*)(&tp[0])));
-    const int xcd = blockIdx.x % kQXcds, per_xcd = gridDim.x / kQXcds;
+    // meta, per item parity: row scales [32] at 0 (the DMA pads to 256),
+    // column scales at 256 (plain: [256]; SwiGLU: gate [128] then up [128])
+    const int xcd = blockIdx.x % kQXcds;
     const int lo = int(int64_t(total) * xcd / kQXcds), hi = int(int64_t(total) * (xcd + 1) / kQXcds);
     const int items = (hi - lo) * n_col_tiles;
-    int i = blockIdx.x / kQXcds;
+    int i = slot;
     if (i >= items) return;
 
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
@@ -808,6 +818,37 @@ __global__ __launch_bounds__(kNThreads) void grouped_gemm_i8_narrow_kernel(GemmI
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// Rows mode, one launch: every work-group forms both tile lists (experts
+// above list_lo rows in 128-row tiles, then the shared expert's for parts &
+// 2; experts of 1..split rows in 32-row tiles when list_lo > 0) and walks
+// its share of the 128-row items, then -- continuing the same round robin
+// over its XCD's work-groups -- its share of the narrow ones, on its first
+// four waves (the others end there; a barrier waits for the surviving
+// waves only).  One launch instead of two: no second ramp-up, and the
+// first list's tail overlaps the second list's start.
+template <bool SWIGLU>
+__global__ __launch_bounds__(kQThreads) void grouped_gemm_i8_rows_kernel(GemmI8Args g, int nct_big,
+                                                                        int nct_nar, int parts) {
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[kQStages * kQStageBytes];
+    __shared__ __attribute__((aligned(16))) float meta[2][512];
+    __shared__ int32_t tpb[kI8MaxListExperts], tpn[kI8MaxListExperts];
+    static_assert(kNStages * kNStageBytes <= kQStages * kQStageBytes, "narrow ring fits");
+    int32_t* tmp = reinterpret_cast<int32_t*>(ring);
+    const int E = g.num_experts;
+    const int nb = (parts & 1) ? i8_list_scan<QBM, kQThreads>(g.counts, E, g.list_lo, 0x7FFFFFFF, tpb, tmp) : 0;
+    const int nn = ((parts & 1) && g.list_lo > 0) ? i8_list_scan<NBM, kQThreads>(g.counts, E, 0, g.split, tpn, tmp) : 0;
+    const int S = gridDim.x / kQXcds;            // work-group slots per XCD
+    const int tpa_b = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int32_t*)(&tpb[0])));
+    const int next = i8_big_run<SWIGLU>(g, nct_big, parts, nb, tpa_b, blockIdx.x / kQXcds, S,
+                                        reinterpret_cast<uint8_t (*)[kQStageBytes]>(ring), meta);
+    if (nn == 0) return;
+    __syncthreads();                             // every wave is past the 128-row ring
+    if (threadIdx.x >= kNThreads) return;
+    const int tpa_n = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int32_t*)(&tpn[0])));
+    i8_narrow_run<SWIGLU>(g, nct_nar, nn, tpa_n, next, S,
+                          reinterpret_cast<uint8_t (*)[kNStageBytes]>(ring), meta);
+}
+
 // ------------------------------------------------------------ quantisers
 
 // Row max, limbs, scale: one wave per row of n <= 4096 elements (8 per lane
@@ -946,11 +987,11 @@ static int i8_grid(Kern k, int threads = kQThreads) {
 
 template <bool SWIGLU>
 static hipError_t launch_i8(hipStream_t st, const GemmI8Args& g, int ntiles) {
-    static int grid = 0, grid_n = 0;
+    static int grid = 0, grid_r = 0;
     if (grid == 0) {
         grid = i8_grid(grouped_gemm_i8_kernel<SWIGLU>);
-        grid_n = i8_grid(grouped_gemm_i8_narrow_kernel<SWIGLU>, kNThreads);
-        if (grid == 0 || grid_n == 0) {
+        grid_r = i8_grid(grouped_gemm_i8_rows_kernel<SWIGLU>);
+        if (grid == 0 || grid_r == 0) {
             grid = 0;
             return hipErrorInvalidConfiguration;
         }
@@ -958,25 +999,23 @@ static hipError_t launch_i8(hipStream_t st, const GemmI8Args& g, int ntiles) {
     const bool rows_mode = g.split > 0;
     const bool routed = rows_mode || g.tmax > 0;
     const bool fuse = routed && g.T_sh > 0 && g.row_bytes == g.row_bytes_sh;
-    if (fuse) {
+    if (rows_mode) {
+        const int nct = SWIGLU ? (g.I + NBN / 2 - 1) / (NBN / 2) : (g.N + NBN - 1) / NBN;
+        hipLaunchKernelGGL(grouped_gemm_i8_rows_kernel<SWIGLU>, dim3(grid_r), dim3(kQThreads), 0, st, g,
+                           ntiles, nct, fuse ? 3 : 1);
+    } else if (fuse) {
         // the shared expert's m-tiles follow the routed ones in one launch
         hipLaunchKernelGGL(grouped_gemm_i8_kernel<SWIGLU>, dim3(grid), dim3(kQThreads), 0, st, g,
                            ntiles, 3);
-    } else {
-        if (routed)
-            hipLaunchKernelGGL(grouped_gemm_i8_kernel<SWIGLU>, dim3(grid), dim3(kQThreads), 0, st, g,
-                               ntiles, 1);
-        if (g.T_sh > 0) {
-            const int items = (g.T_sh + QBM - 1) / QBM * ntiles;
-            const int gs = min(grid, (items + kQXcds - 1) / kQXcds * kQXcds);
-            hipLaunchKernelGGL(grouped_gemm_i8_kernel<SWIGLU>, dim3(gs), dim3(kQThreads), 0, st, g,
-                               ntiles, 2);
-        }
+    } else if (routed) {
+        hipLaunchKernelGGL(grouped_gemm_i8_kernel<SWIGLU>, dim3(grid), dim3(kQThreads), 0, st, g,
+                           ntiles, 1);
     }
-    if (rows_mode && g.list_lo > 0) {
-        const int nct = SWIGLU ? (g.I + NBN / 2 - 1) / (NBN / 2) : (g.N + NBN - 1) / NBN;
-        hipLaunchKernelGGL(grouped_gemm_i8_narrow_kernel<SWIGLU>, dim3(grid_n), dim3(kNThreads), 0,
-                           st, g, nct);
+    if (g.T_sh > 0 && !fuse) {
+        const int items = (g.T_sh + QBM - 1) / QBM * ntiles;
+        const int gs = min(grid, (items + kQXcds - 1) / kQXcds * kQXcds);
+        hipLaunchKernelGGL(grouped_gemm_i8_kernel<SWIGLU>, dim3(gs), dim3(kQThreads), 0, st, g,
+                           ntiles, 2);
     }
     return hipGetLastError();
 }
