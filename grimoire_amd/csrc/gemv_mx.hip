@@ -55,9 +55,21 @@ constexpr int kGvmOS = kGvmRows * kGvmKS / 2;                       // 8192
 constexpr int kGvmOA = kGvmOS + kGvmRows * 12;                      // 8960
 constexpr int kGvmOAS = kGvmOA + 4 * kGvmLimbs * kGvmKS;            // 12032
 constexpr int kGvmStage = kGvmOAS + 256;                            // 12288
+// a buffer offset past every activation descriptor's range
+constexpr int kGvmNoLoad = int(0x80000000u);
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t gvm_rsrc(const void* p, int bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
+
+// Scalar load of one int from a wave-uniform address.  It waits on
+// lgkmcnt, not vmcnt: the item descriptors read between stages do not wait
+// for the DMA ring in flight (a compiler-visible vector load there would
+// bring an s_waitcnt vmcnt(0) that drains it).
+__device__ __forceinline__ int gvm_sload(const int32_t* p) {
+    int v;
+    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+    return v;
 }
 
 __device__ __forceinline__ uint32_t gvm_lds_addr(const void* p) {
@@ -140,7 +152,10 @@ hipError_t gvm_format_launch(hipStream_t st, const float* src0, int rows0, uint8
 }
 
 // Stage s of an item into the ring stage at st: exactly 15 instructions,
-// each with lane 0 active.  Codes: instruction j covers the wave's rows
+// every lane active (the stage loop's vmcnt wait counts 15 per stage: a
+// lane-masked load whose lanes are all off would be branched around and
+// not counted).  Lanes with nothing to load read past the buffer
+// (kGvmNoLoad): zeros, into LDS that no MFMA of theirs reads.  Codes: instruction j covers the wave's rows
 // 8 j + lane / 8, slot lane % 8 holding 16-byte piece (lane % 8) ^
 // ((row >> 1) & 7).  Scales: the 12 bytes of each row from the 4-byte-
 // aligned start of its 8 (row r's at 12 r; lane 64 jj + i is dword i % 3
@@ -159,11 +174,12 @@ __device__ __forceinline__ void gvm_issue(uint8_t* st, __amdgpu_buffer_rsrc_t rp
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (gvm_lds_ptr_t)(st + kGvmOS + jj * 256), 4, sofs[jj], s * 8, 0,
                                                  0);
 #pragma unroll
-    for (int ja = 0; ja < 3; ++ja)
-        if ((64 * ja + lane) / 48 < mc)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (gvm_lds_ptr_t)(st + kGvmOA + ja * 1024), 16, aofs[ja],
-                                                     s * 256, 0, 0);
-    if (lane < 8) __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (gvm_lds_ptr_t)(st + kGvmOAS), 4, asofs, s * 8, 0, 0);
+    for (int ja = 0; ja < 3; ++ja) {
+        const int vo = (64 * ja + lane) / 48 < mc ? aofs[ja] : kGvmNoLoad;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (gvm_lds_ptr_t)(st + kGvmOA + ja * 1024), 16, vo, s * 256, 0, 0);
+    }
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (gvm_lds_ptr_t)(st + kGvmOAS), 4, lane < 8 ? asofs : kGvmNoLoad,
+                                             s * 8, 0, 0);
 }
 
 // One persistent kernel for both products (GU: gate_up + SwiGLU, rows are
@@ -216,11 +232,11 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
             const int g = item / n_chunks, chunk = item % n_chunks;
             int64_t wrow0 = 0;
             if (g < n_live) {
-                const int e = __builtin_amdgcn_readfirstlane(a.tile_e[g]);
+                const int e = gvm_sload(a.tile_e + g);
                 if (e < 0) continue;   // uniform
-                const int mb = __builtin_amdgcn_readfirstlane(a.tile_mb[g]);
-                d.r0 = __builtin_amdgcn_readfirstlane(a.offsets[e]) + mb * kGvMT;
-                d.mc = min(kGvMT, __builtin_amdgcn_readfirstlane(a.counts[e]) - mb * kGvMT);
+                const int mb = gvm_sload(a.tile_mb + g);
+                d.r0 = gvm_sload(a.offsets + e) + mb * kGvMT;
+                d.mc = min(kGvMT, gvm_sload(a.counts + e) - mb * kGvMT);
                 wrow0 = int64_t(e) * rows_per_expert;
                 d.sh = false;
             } else {
@@ -241,9 +257,26 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
                 else return min(d.i0 + r, N - 1);
             };
             // activation row of group row m (rows past mc: row 0, never used)
-            auto arow = [&](int m) {
+            // (four named values selected per lane: an indexed array here
+            // goes to scratch memory, whose loads wait like the ring's)
+            static_assert(kGvMT == 4, "four group rows");
+            auto trow = [&](int m) {
                 const int rr = d.r0 + (m < d.mc ? m : 0);
-                return GU ? (d.sh ? rr : a.perm_token[rr]) : rr;
+                return (GU && !d.sh) ? gvm_sload(a.perm_token + rr) : rr;
+            };
+            const int ar0 = trow(0), ar1 = trow(1), ar2 = trow(2), ar3 = trow(3);
+            auto arow = [&](int m) {
+                // per-lane select in the vector ALU (the optimiser turns a
+                // plain select chain back into an indexed table)
+                int v = ar0;
+                asm volatile("v_cmp_eq_u32_e32 vcc, 1, %1\n\t"
+                             "v_cndmask_b32_e32 %0, %0, %2, vcc\n\t"
+                             "v_cmp_eq_u32_e32 vcc, 2, %1\n\t"
+                             "v_cndmask_b32_e32 %0, %0, %3, vcc\n\t"
+                             "v_cmp_eq_u32_e32 vcc, 3, %1\n\t"
+                             "v_cndmask_b32_e32 %0, %0, %4, vcc"
+                             : "+v"(v) : "v"(m), "v"(ar1), "v"(ar2), "v"(ar3) : "vcc");
+                return v;
             };
             // Codes: instruction j covers rows 8 j + lane / 8, slot lane % 8
             // holding 16-byte piece (lane % 8) ^ ((row >> 1) & 7).  Scales:
