@@ -297,20 +297,29 @@ static int forward_gemm_i8(hipStream_t st, const grim_moe_layer* L, const Plan& 
 // + SwiGLU per group (fp32 h per route) -> down per group (fp32 rows per
 // route) -> combine (slot-order fma chain + gate * shared).
 static int forward_gv(hipStream_t st, const grim_moe_layer* L, const Plan& p, const float* x,
-                      float* y, int tokens, const uint16_t* shared_gate_w, bool mx) {
+                      float* y, int tokens, const uint16_t* shared_gate_w, bool mx, const TopkArgs* route) {
     const auto& c = L->cfg;
     const int E = c.num_experts, K = c.top_k, H = c.hidden, I = c.inter;
     const bool sh = L->has_shared;
-    int r = grimoire_moe_route_grouped(st, x, p.rex, nullptr, nullptr, p.counts, p.offsets,
-                                       p.inverse, p.gv_te, p.gv_tm, p.gv_tmax, tokens, H, E, kGvMT,
-                                       K, p.gv_perm, p.disp_ws,
-                                       dispatch_workspace_bytes(tokens, K, E));
-    if (r) return r;
+    if (route) {
+        // top-k, dispatch and the x limbs in one launch (small batches)
+        GvmRouteArgs ra{p.counts, p.offsets, p.gv_te, p.gv_tm, p.gv_tmax,
+                        dispatch_live_tiles(p.disp_ws, tokens, K, E), p.inverse, p.gv_perm, x,
+                        reinterpret_cast<uint8_t*>(p.gv_xf), H};
+        hipError_t e = gvm_route_launch(st, *route, ra);
+        if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    } else {
+        int r = grimoire_moe_route_grouped(st, x, p.rex, nullptr, nullptr, p.counts, p.offsets,
+                                           p.inverse, p.gv_te, p.gv_tm, p.gv_tmax, tokens, H, E, kGvMT,
+                                           K, p.gv_perm, p.disp_ws,
+                                           dispatch_workspace_bytes(tokens, K, E));
+        if (r) return r;
+    }
     if (sh && shared_gate_w) {
         hipError_t e = rowdot_sigmoid_launch(st, x, shared_gate_w, p.gate, tokens, H);
         if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
     }
-    {
+    if (!route) {
         // (the limb format of the matrix-core kernel is smaller than the
         // vector-ALU format the buffers are sized for)
         hipError_t e = mx ? gvm_format_launch(st, x, tokens, reinterpret_cast<uint8_t*>(p.gv_xf), nullptr, 0,
@@ -556,10 +565,17 @@ static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_
         if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
     }
     int r = GRIM_OK;
+    const TopkArgs tka{p.logits, tokens, E, K, topk_mode, c.norm_topk, scaling, b16, b32,
+                       rp ? rp->n_group : 0, rp ? rp->topk_group : 0, p.rex, p.rwt};
+    // few rows per expert (on average at most 2): stream each expert once
+    // per group of rows instead of once per 128-row MFMA tile
+    const bool gv = !gemv && p.gv_te &&
+                    (regime == 4 || regime == 5 || (regime == 0 && int64_t(tokens) * K <= 2 * int64_t(E)));
+    const bool gv_mx = gv && regime != 5 && L->gate_up.fmt == GRIM_FMT_MXFP4 && gvm_shape_ok(H, I);
+    if (gv_mx && int64_t(tokens) * K <= kGvmRouteMax)
+        return forward_gv(st, L, p, x, y, tokens, shared_gate_w, true, &tka);
     {
-        TopkArgs a{p.logits, tokens, E, K, topk_mode, c.norm_topk, scaling, b16, b32,
-                   rp ? rp->n_group : 0, rp ? rp->topk_group : 0, p.rex, p.rwt};
-        hipError_t e = topk_launch(st, a);
+        hipError_t e = topk_launch(st, tka);
         if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
     }
 
@@ -573,12 +589,7 @@ static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_
         return grimoire_moe_down_batched(stream, L, p.rex, p.rwt, p.h, y, tokens);
     }
 
-    // few rows per expert (on average at most 2): stream each expert once
-    // per group of rows instead of once per 128-row MFMA tile
-    if (p.gv_te && (regime == 4 || regime == 5 || (regime == 0 && int64_t(tokens) * K <= 2 * int64_t(E)))) {
-        const bool mx = regime != 5 && L->gate_up.fmt == GRIM_FMT_MXFP4 && gvm_shape_ok(H, I);
-        return forward_gv(st, L, p, x, y, tokens, shared_gate_w, mx);
-    }
+    if (gv) return forward_gv(st, L, p, x, y, tokens, shared_gate_w, gv_mx, nullptr);
     if (regime == 4 || regime == 5)
         return ferr(GRIM_ERR_FORMAT, "regimes 4, 5: int4 / mxfp4 experts, hidden and inter % 32");
 

@@ -725,7 +725,7 @@ __device__ __forceinline__ void i8_narrow_run(const GemmI8Args& g, int n_col_til
 #define GRIM_N8_DMA(q)                                                                            \
         do {                                                                                      \
             if ((q) < NJA) dma16<0>(qa, nx + (NJA * wave + (q)) * 1024, a_off[(q) % NJA], tu * 256); \
-            else dma16<2>(qb, nx + kNA + (NJB * wave + (q) - NJA) * 1024, b_off[((q) - NJA) % NJB], tu * NBK); \
+            else dma16<2>(qb, nx + kNA + (NJB * wave + (q) - NJA) * 1024, b_off[((q) + NJB - NJA) % NJB], tu * NBK); \
         } while (0)
 #define GRIM_N8_ITER(t_, META)                                                                    \
         do {                                                                                      \

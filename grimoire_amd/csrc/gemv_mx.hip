@@ -36,6 +36,7 @@
 #include "gemv_mx.hpp"
 
 #include "gemv_impl.hpp"
+#include "topk.hpp"
 
 namespace grim {
 
@@ -89,19 +90,11 @@ __host__ __device__ inline int gvm_row_bytes(int K) {
 
 size_t gvm_act_bytes(int K) { return size_t(gvm_row_bytes(K)); }
 
-// One thread per 32-element block of the padded row (blocks past K: zero
-// limbs under scale 1).
-__global__ __launch_bounds__(256) void gvm_format_kernel(const float* src0, int rows0, uint8_t* dst0,
-                                                         const float* src1, int rows1, uint8_t* dst1, int K) {
-    const int kp = gvm_kpad(K), nb = kp / 32;
-    const int64_t gi = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t n0 = int64_t(rows0) * nb;
-    if (gi >= n0 + int64_t(rows1) * nb) return;
-    const bool second = gi >= n0;
-    const int64_t li = second ? gi - n0 : gi;
-    const int row = int(li / nb), b = int(li % nb);
-    const float4* s4 = reinterpret_cast<const float4*>((second ? src1 : src0) + int64_t(row) * K + b * 32);
-    uint8_t* dst = (second ? dst1 : dst0) + int64_t(row) * gvm_row_bytes(K);
+// Block b (32 elements) of one row: src the row (K floats), dst its limb
+// row (gvm_row_bytes(K)); blocks past K give zero limbs under scale 1.
+__device__ __forceinline__ void gvm_format_block(const float* __restrict__ src, uint8_t* __restrict__ dst, int K,
+                                                 int kp, int b) {
+    const float4* s4 = reinterpret_cast<const float4*>(src + b * 32);
     float v[32];
     const bool in = b * 32 < K;
 #pragma unroll
@@ -142,12 +135,111 @@ __global__ __launch_bounds__(256) void gvm_format_kernel(const float* src0, int 
     dst[3 * kp + b] = uint8_t(s + 127);
 }
 
+// One thread per 32-element block of the padded row.
+__global__ __launch_bounds__(256) void gvm_format_kernel(const float* src0, int rows0, uint8_t* dst0,
+                                                         const float* src1, int rows1, uint8_t* dst1, int K) {
+    const int kp = gvm_kpad(K), nb = kp / 32;
+    const int64_t gi = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t n0 = int64_t(rows0) * nb;
+    if (gi >= n0 + int64_t(rows1) * nb) return;
+    const bool second = gi >= n0;
+    const int64_t li = second ? gi - n0 : gi;
+    const int row = int(li / nb), b = int(li % nb);
+    gvm_format_block((second ? src1 : src0) + int64_t(row) * K, (second ? dst1 : dst0) + int64_t(row) * gvm_row_bytes(K),
+                     K, kp, b);
+}
+
 hipError_t gvm_format_launch(hipStream_t st, const float* src0, int rows0, uint8_t* dst0, const float* src1,
                              int rows1, uint8_t* dst1, int K) {
     const int64_t n = int64_t(rows0 + rows1) * (gvm_kpad(K) / 32);
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(gvm_format_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, src0, rows0, dst0, src1,
                        rows1, dst1, K);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------- small-batch routing
+//
+// Everything between the router logits and the grouped GEMV for a batch of
+// at most kGvmRouteMax routes, in one work-group instead of six launches
+// (top-k, the dispatch's count / column scan / scan / rank, the activation
+// formatting): each wave runs topk_wave for its tokens (the batched top-k's
+// code, so the same picks and weights), the expert counts come from LDS
+// atomics (counts only: order-free), one scan forms the offsets and the
+// (expert, group of kGvMT rows) table, and each route's row is its
+// expert's offset plus the number of earlier routes of that expert -- the
+// dispatch's stable order (src/grimoire.cpp:23162-23170).  The x rows are
+// formatted as limbs by the same code as gvm_format_kernel.
+constexpr int kGvmRouteThreads = 1024;
+constexpr int kGvmRouteWaves = kGvmRouteThreads / kWave;
+
+__global__ __launch_bounds__(kGvmRouteThreads) void gvm_route_kernel(TopkArgs tk, GvmRouteArgs ra) {
+    __shared__ float gsel[kGvmRouteWaves][512];
+    __shared__ float gscore[kGvmRouteWaves][64];
+    __shared__ int32_t ids[kGvmRouteMax];
+    __shared__ int32_t cnt[kGvmRouteThreads], sc[kGvmRouteThreads], sg[kGvmRouteThreads];
+    const int tid = threadIdx.x, wave = tid / kWave;
+    const int T = tk.T, E = tk.E, K = tk.K, R = T * K;
+    for (int e = tid; e < kGvmRouteThreads; e += kGvmRouteThreads) cnt[e] = 0;
+    for (int t = wave; t < T; t += kGvmRouteWaves)
+        topk_wave(tk.logits + int64_t(t) * E, E, K, tk.mode, tk.normalize, tk.scaling, tk.bias16, tk.bias32,
+                  tk.n_group, tk.topk_group, ids + t * K, tk.out_w + int64_t(t) * K, gsel[wave], gscore[wave]);
+    __syncthreads();
+    const int my_id = tid < R ? ids[tid] : -1;
+    if (my_id >= 0 && my_id < E) atomicAdd(&cnt[my_id], 1);
+    __syncthreads();
+    // inclusive scans of the counts and of the groups per expert
+    const int c = tid < E ? cnt[tid] : 0;
+    const int ng = (c + kGvMT - 1) / kGvMT;
+    sc[tid] = c;
+    sg[tid] = ng;
+    __syncthreads();
+    for (int off = 1; off < kGvmRouteThreads; off <<= 1) {
+        const int a = tid >= off ? sc[tid - off] : 0, b = tid >= off ? sg[tid - off] : 0;
+        __syncthreads();
+        sc[tid] += a;
+        sg[tid] += b;
+        __syncthreads();
+    }
+    const int off_e = sc[tid] - c, g0 = sg[tid] - ng, groups = sg[kGvmRouteThreads - 1];
+    if (tid < E) {
+        ra.counts[tid] = c;
+        ra.offsets[tid] = off_e;
+        for (int i = 0; i < ng; ++i)
+            if (g0 + i < ra.tmax) {
+                ra.tile_e[g0 + i] = tid;
+                ra.tile_mb[g0 + i] = i;
+            }
+    }
+    for (int g = groups + tid; g < ra.tmax; g += kGvmRouteThreads) {
+        ra.tile_e[g] = -1;
+        ra.tile_mb[g] = 0;
+    }
+    if (tid == 0) *ra.n_live = groups < ra.tmax ? groups : ra.tmax;
+    __syncthreads();
+    cnt[tid] = off_e;   // the offsets, for the ranks
+    __syncthreads();
+    if (tid < R) {
+        int dest = -1;
+        if (my_id >= 0 && my_id < E) {
+            int rank = 0;
+            for (int j = 0; j < tid; ++j) rank += ids[j] == my_id ? 1 : 0;
+            dest = cnt[my_id] + rank;
+            ra.perm_token[dest] = tid / K;
+        }
+        ra.inverse[tid] = dest;
+        tk.out_e[tid] = my_id;
+    }
+    // the x rows in the limb format
+    const int kp = gvm_kpad(ra.H), nb = kp / 32;
+    const int ab = gvm_row_bytes(ra.H);
+    for (int i = tid; i < T * nb; i += kGvmRouteThreads)
+        gvm_format_block(ra.x + int64_t(i / nb) * ra.H, ra.af + int64_t(i / nb) * ab, ra.H, kp, i % nb);
+}
+
+hipError_t gvm_route_launch(hipStream_t st, const TopkArgs& tk, const GvmRouteArgs& ra) {
+    if (int64_t(tk.T) * tk.K > kGvmRouteMax || tk.E > 512 || tk.E <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gvm_route_kernel, dim3(1), dim3(kGvmRouteThreads), 0, st, tk, ra);
     return hipGetLastError();
 }
 

@@ -3,6 +3,7 @@
 #pragma once
 
 #include "gemv_grouped.hpp"
+#include "router.hpp"
 
 namespace grim {
 
@@ -13,6 +14,21 @@ size_t gvm_act_bytes(int K);
 // Format rows0 rows of src0 into dst0 and rows1 rows of src1 into dst1.
 hipError_t gvm_format_launch(hipStream_t st, const float* src0, int rows0, uint8_t* dst0, const float* src1,
                              int rows1, uint8_t* dst1, int K);
+// Routing for a batch of at most kGvmRouteMax routes in one launch: the
+// top-k of tk (picks into tk.out_e, weights into tk.out_w), expert counts,
+// offsets, the (expert, kGvMT-row group) table, each route's row (inverse)
+// and token (perm_token by row), and the x rows [T][H] in the limb format.
+constexpr int kGvmRouteMax = 1024;
+struct GvmRouteArgs {
+    int32_t *counts, *offsets, *tile_e, *tile_mb;
+    int tmax;
+    int32_t* n_live;
+    int32_t *inverse, *perm_token;
+    const float* x;
+    uint8_t* af;
+    int H;
+};
+hipError_t gvm_route_launch(hipStream_t st, const TopkArgs& tk, const GvmRouteArgs& ra);
 // The product: GvArgs with af / af_sh pointing at limb-format rows.
 hipError_t gvm_launch(hipStream_t st, const GvArgs& g, bool gate_up);
 

@@ -175,13 +175,18 @@ __device__ __forceinline__ void topk_wave_regs(const float (&lv)[kMaxV], int E, 
     const int lane = threadIdx.x & (kWave - 1);
     const int V = (E + kWave - 1) / kWave;
 
+    const int gsz = mode == 3 ? E / n_group : 0;
+    const int lpg = gsz / V;   // lanes per group when groups are whole lanes
+    const bool lane_groups = mode == 3 && gsz % V == 0 && lpg >= 1 && lpg <= kWave && (lpg & (lpg - 1)) == 0;
     uint32_t key[kMaxV];
-    float wsrc[kMaxV];
+    float wsrc[kMaxV], selv[kMaxV];
+    auto sel_of = [&](int j) { return selv[j]; };
 #pragma unroll
     for (int j = 0; j < kMaxV; ++j) {
         const int e = lane * V + j;
         key[j] = 0;
         wsrc[j] = 0.0f;
+        selv[j] = 0.0f;
         if (j < V && e < E) {
             const float l = lv[j];
             float sel;
@@ -196,11 +201,47 @@ __device__ __forceinline__ void topk_wave_regs(const float (&lv)[kMaxV], int E, 
                 wsrc[j] = sc;
             }
             key[j] = score_key(sel);
-            if (mode == 3) gsel_w[e] = sel;
+            selv[j] = sel;
+            if (mode == 3 && !lane_groups) gsel_w[e] = sel;
         }
     }
 
-    if (mode == 3) {
+    if (lane_groups) {
+        // groups of lpg whole lanes: each lane's two largest biased scores,
+        // merged across its group by butterflies (the two largest of a
+        // multiset), group score = largest + second largest (the largest
+        // alone for one-expert groups); group g is kept when fewer than
+        // topk_group groups beat it (higher score, or equal and lower
+        // index) -- the same groups and the same sums as the serial pass
+        // below, with no LDS and no serial loop over a group
+        float m1 = -__builtin_inff(), m2 = -__builtin_inff();
+#pragma unroll
+        for (int j = 0; j < kMaxV; ++j) {
+            const int e = lane * V + j;
+            if (j < V && e < E) {
+                const float v = sel_of(j);
+                if (v > m1) { m2 = m1; m1 = v; }
+                else if (v > m2) m2 = v;
+            }
+        }
+        for (int o = 1; o < lpg; o <<= 1) {
+            const float b1 = __shfl_xor(m1, o, kWave), b2 = __shfl_xor(m2, o, kWave);
+            const float lo1 = fminf(m1, b1), hi2 = fmaxf(m2, b2);
+            m1 = fmaxf(m1, b1);
+            m2 = fmaxf(lo1, hi2);
+        }
+        const float score = gsz > 1 ? m1 + m2 : m1;
+        const int gi = lane / lpg;
+        int rank = 0;
+        for (int g = 0; g < n_group; ++g) {
+            const float o = lane_f(score, g * lpg);
+            rank += (o > score || (o == score && g < gi)) ? 1 : 0;
+        }
+        if (rank >= topk_group) {
+#pragma unroll
+            for (int j = 0; j < kMaxV; ++j) key[j] = 0;
+        }
+    } else if (mode == 3) {
         // group score: sum of the two largest biased scores of each group
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();

@@ -86,8 +86,12 @@ def test_topk_sigmoid_bit_exact(gpu, T, E, K, scaling):
     assert torch.equal(ow.cpu(), ww)
 
 
+# groups of whole lanes (1, 2, 4, 8 or 64 lanes per group: the butterfly
+# path) and groups that split lanes (96 experts in 8 groups, 160 in 5: the
+# serial path)
 @pytest.mark.parametrize("T,E,K,ng,kg", [(32, 256, 8, 8, 4), (5, 64, 6, 8, 3), (4, 512, 8, 16, 4),
-                                         (3, 64, 4, 1, 1)])
+                                         (3, 64, 4, 1, 1), (6, 128, 6, 32, 4), (5, 256, 8, 64, 4),
+                                         (6, 96, 4, 8, 3), (4, 160, 6, 5, 2)])
 def test_topk_group_bit_exact(gpu, T, E, K, ng, kg):
     print(f"topk group T={T} E={E} K={K} groups {kg}/{ng}", flush=True)
     l = _ties(T, E, 17 + E, scale=1.0)
