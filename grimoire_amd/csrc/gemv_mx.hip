@@ -256,11 +256,16 @@ hipError_t gvm_route_launch(hipStream_t st, const TopkArgs& tk, const GvmRouteAr
 // never stored), then the 4 rows' 8 block scales (lane = 2 m + half).
 __device__ __forceinline__ void gvm_issue(uint8_t* st, __amdgpu_buffer_rsrc_t rp, __amdgpu_buffer_rsrc_t rs,
                                           __amdgpu_buffer_rsrc_t ra, const int (&pofs)[8], const int (&sofs)[3],
-                                          const int (&aofs)[3], int asofs, int mc, int lane, int s) {
+                                          const int (&aofs)[3], int asofs, int mc, int lane, int s, bool nt) {
     constexpr int NS = 3;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (gvm_lds_ptr_t)(st + j * 1024), 16, pofs[j], s * 128, 0, 2);
+    for (int j = 0; j < 8; ++j) {
+        // non-temporal when a row's 128 bytes of a stage are whole memory
+        // lines; rows that straddle lines (K/2 % 128 != 0) keep them cached,
+        // for the next stage reads the rest of each line
+        if (nt) __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (gvm_lds_ptr_t)(st + j * 1024), 16, pofs[j], s * 128, 0, 2);
+        else __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (gvm_lds_ptr_t)(st + j * 1024), 16, pofs[j], s * 128, 0, 0);
+    }
 #pragma unroll
     for (int jj = 0; jj < NS; ++jj)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (gvm_lds_ptr_t)(st + kGvmOS + jj * 256), 4, sofs[jj], s * 8, 0,
@@ -291,6 +296,7 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
     const int N = a.N, Kd = a.K, Kp = gvm_kpad(Kd), S = Kp / kGvmKS;
     const int lrow = Kd / 2, srb = Kd / 32;                  // code / scale bytes per weight row
     const int AB = gvm_row_bytes(Kd);
+    const bool nt = lrow % 128 == 0;
     constexpr int PW = GU ? kGvmRows / 2 : kGvmRows;         // rows (pairs) per wave
     constexpr int NRB = kGvmRows / 16;                       // 16-row blocks per wave
     const int per_item = kGvmWaves * PW;
@@ -402,8 +408,8 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
     // Stage s of the current item (the next one when nx) into ring slot
     // q % ST (gvm_issue)
     auto issue = [&](bool nx, int s, int q) {
-        if (nx) gvm_issue(ring + (q % ST) * kGvmStage, np, ns, na, nxt.pofs, nxt.sofs, nxt.aofs, nxt.asofs, nxt.mc, lane, s);
-        else gvm_issue(ring + (q % ST) * kGvmStage, cp, cs, ca, cur.pofs, cur.sofs, cur.aofs, cur.asofs, cur.mc, lane, s);
+        if (nx) gvm_issue(ring + (q % ST) * kGvmStage, np, ns, na, nxt.pofs, nxt.sofs, nxt.aofs, nxt.asofs, nxt.mc, lane, s, nt);
+        else gvm_issue(ring + (q % ST) * kGvmStage, cp, cs, ca, cur.pofs, cur.sofs, cur.aofs, cur.asofs, cur.mc, lane, s, nt);
     };
 
     // One continuous stream of stages over this wave's items: the last
