@@ -46,6 +46,9 @@ constexpr float kLoScale = 1.0f / 254.0f;
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 
+// AUX: the buffer load's cache policy bits (0 everywhere here: the weight
+// tiles are read again -- the other half of a line by the next K tile, the
+// same lines by an expert's next m-tile -- so they stay cacheable)
 template <int AUX>
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, int voff, int soff) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, soff, 0, AUX);
@@ -350,7 +353,7 @@ __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, 
         for (int j = 0; j < NJ; ++j) dma16<0>(ra, st + (NJ * wave + j) * 1024, a_off[j], t * 128);
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
-            dma16<2>(rb, st + 16384 + (NJ * wave + j) * 1024, b_off[j], t * QBK);
+            dma16<0>(rb, st + 16384 + (NJ * wave + j) * 1024, b_off[j], t * QBK);
     };
 
     const int nk = K / QBK;   // >= 3
@@ -420,7 +423,7 @@ __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, 
 #define GRIM_I8_DMA(q)                                                                            \
         do {                                                                                      \
             if ((q) < NJ) dma16<0>(qa, nx + (NJ * wave + (q)) * 1024, a_off[(q) % NJ], tu * 128); \
-            else dma16<2>(qb, nx + 16384 + (NJ * wave + (q) - NJ) * 1024, b_off[(q) % NJ], tu * QBK); \
+            else dma16<0>(qb, nx + 16384 + (NJ * wave + (q) - NJ) * 1024, b_off[(q) % NJ], tu * QBK); \
         } while (0)
 #define GRIM_I8_ITER(t_, META)                                                                    \
         do {                                                                                      \
@@ -662,7 +665,7 @@ __device__ __forceinline__ void i8_narrow_run(const GemmI8Args& g, int n_col_til
 #pragma unroll
         for (int j = 0; j < NJA; ++j) dma16<0>(ra, st + (NJA * wave + j) * 1024, a_off[j], t * 256);
 #pragma unroll
-        for (int j = 0; j < NJB; ++j) dma16<2>(rb, st + kNA + (NJB * wave + j) * 1024, b_off[j], t * NBK);
+        for (int j = 0; j < NJB; ++j) dma16<0>(rb, st + kNA + (NJB * wave + j) * 1024, b_off[j], t * NBK);
     };
 
     const int nk = K / NBK;   // >= kNStages - 1
@@ -725,7 +728,7 @@ __device__ __forceinline__ void i8_narrow_run(const GemmI8Args& g, int n_col_til
 #define GRIM_N8_DMA(q)                                                                            \
         do {                                                                                      \
             if ((q) < NJA) dma16<0>(qa, nx + (NJA * wave + (q)) * 1024, a_off[(q) % NJA], tu * 256); \
-            else dma16<2>(qb, nx + kNA + (NJB * wave + (q) - NJA) * 1024, b_off[((q) + NJB - NJA) % NJB], tu * NBK); \
+            else dma16<0>(qb, nx + kNA + (NJB * wave + (q) - NJA) * 1024, b_off[((q) + NJB - NJA) % NJB], tu * NBK); \
         } while (0)
 #define GRIM_N8_ITER(t_, META)                                                                    \
         do {                                                                                      \
