@@ -917,6 +917,52 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float* __restrict
     if (lane == 0) scale[r] = sc;
 }
 
+// Rows of n <= 512 (h of C4-like layers): one wave per kQuantRowsPerWave
+// rows, each lane holding its 8 elements of every row in registers, all
+// loads issued before the first reduction; the same arithmetic as
+// quant_rows_kernel (limbs8), so the same limbs and scales.
+constexpr int kQuantRowsPerWave = 4;
+
+__global__ __launch_bounds__(256) void quant_rows_short_kernel(const float* __restrict__ src, int rows,
+                                                               int n, int8_t* __restrict__ dst,
+                                                               float* __restrict__ scale) {
+    const int lane = threadIdx.x & 63;
+    const int r0 = (blockIdx.x * 4 + int(threadIdx.x) / 64) * kQuantRowsPerWave;
+    if (r0 >= rows) return;
+    const int c = lane * 8;
+    const bool in = c < n;
+    float v[kQuantRowsPerWave][8];
+#pragma unroll
+    for (int q = 0; q < kQuantRowsPerWave; ++q) {
+        const int r = r0 + q < rows ? r0 + q : r0;
+        const float* s = src + int64_t(r) * n + (in ? c : 0);
+        const float4 a = *reinterpret_cast<const float4*>(s);
+        const float4 b = *reinterpret_cast<const float4*>(s + 4);
+        v[q][0] = a.x; v[q][1] = a.y; v[q][2] = a.z; v[q][3] = a.w;
+        v[q][4] = b.x; v[q][5] = b.y; v[q][6] = b.z; v[q][7] = b.w;
+    }
+#pragma unroll
+    for (int q = 0; q < kQuantRowsPerWave; ++q) {
+        const int r = r0 + q;
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[q][i]));
+        m = wave_max_f(in ? m : 0.0f);
+        const float sc = m > 0.0f ? m / 127.0f : 1.0f;
+        const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+        uint32_t h0, h1, l0, l1;
+        limbs8(v[q], inv, h0, h1, l0, l1);
+        if (r < rows) {
+            if (in) {
+                int8_t* blk = dst + int64_t(r) * 2 * n + limb_block(c);
+                *reinterpret_cast<uint2*>(blk) = make_uint2(h0, h1);
+                *reinterpret_cast<uint2*>(blk + 64) = make_uint2(l0, l1);
+            }
+            if (lane == 0) scale[r] = sc;
+        }
+    }
+}
+
 // The activations of every token as limbs, written to each of its K
 // permuted rows (inverse) and to its own row (xrow, the shared expert's
 // input) when given.  One work-group of 256 threads per token, n <= 8192.
@@ -1051,6 +1097,12 @@ hipError_t quant_rows_launch(hipStream_t st, const float* src, int rows, int n, 
                              float* scale) {
     if (rows <= 0) return hipSuccess;
     if (n % 64 || n > 4096) return hipErrorInvalidValue;
+    if (n <= 512) {
+        const int per_block = 4 * kQuantRowsPerWave;
+        hipLaunchKernelGGL(quant_rows_short_kernel, dim3((rows + per_block - 1) / per_block), dim3(256), 0, st,
+                           src, rows, n, dst, scale);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(quant_rows_kernel, dim3((rows + kQuantRowsPerBlock - 1) / kQuantRowsPerBlock),
                        dim3(256), 0, st, src, rows, n, dst, scale);
     return hipGetLastError();
