@@ -231,7 +231,10 @@ __device__ __forceinline__ float4 combine_load(const void* src, int64_t row, int
         return make_float4(bits_f(u.x << 16), bits_f(u.x & 0xFFFF0000u), bits_f(u.y << 16),
                            bits_f(u.y & 0xFFFF0000u));
     } else {
-        return *reinterpret_cast<const float4*>(static_cast<const float*>(src) + row * H + d);
+        // the expert rows are read once: non-temporal
+        typedef float f4nt __attribute__((ext_vector_type(4)));
+        const f4nt v = __builtin_nontemporal_load(reinterpret_cast<const f4nt*>(static_cast<const float*>(src) + row * H + d));
+        return make_float4(v.x, v.y, v.z, v.w);
     }
 }
 
