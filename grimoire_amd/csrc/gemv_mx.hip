@@ -254,9 +254,11 @@ hipError_t gvm_route_launch(hipStream_t st, const TopkArgs& tk, const GvmRouteAr
 // of row (64 jj + i) / 3).  Activations: piece p = 64 ja + lane of [row m][limb L]
 // [16 x 16 B] (192 pieces; rows past mc are not loaded: their columns are
 // never stored), then the 4 rows' 8 block scales (lane = 2 m + half).
-__device__ __forceinline__ void gvm_issue(uint8_t* st, __amdgpu_buffer_rsrc_t rp, __amdgpu_buffer_rsrc_t rs,
-                                          __amdgpu_buffer_rsrc_t ra, const int (&pofs)[8], const int (&sofs)[3],
-                                          const int (&aofs)[3], int asofs, int mc, int lane, int s, bool nt) {
+template <bool S16>
+__device__ __forceinline__ void gvm_issue(uint8_t* st, uint8_t* sup, __amdgpu_buffer_rsrc_t rp,
+                                          __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t ra, const int (&pofs)[8],
+                                          const int (&sofs)[3], const int (&aofs)[3], int asofs, int mc, int lane,
+                                          int s, bool nt) {
     constexpr int NS = 3;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -266,10 +268,19 @@ __device__ __forceinline__ void gvm_issue(uint8_t* st, __amdgpu_buffer_rsrc_t rp
         if (nt) __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (gvm_lds_ptr_t)(st + j * 1024), 16, pofs[j], s * 128, 0, 2);
         else __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (gvm_lds_ptr_t)(st + j * 1024), 16, pofs[j], s * 128, 0, 0);
     }
+    if constexpr (S16) {
+        // even stages: the next two stages' scales of the wave's 64 rows,
+        // 16 bytes a lane (row = lane), into the super-stage buffer sup;
+        // odd stages: the same instruction past the buffer, into a dummy
+        // area (one load per stage either way)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (gvm_lds_ptr_t)sup, 16, (s & 1) ? kGvmNoLoad : sofs[0],
+                                                 (s >> 1) * 16, 0, 0);
+    } else {
 #pragma unroll
-    for (int jj = 0; jj < NS; ++jj)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (gvm_lds_ptr_t)(st + kGvmOS + jj * 256), 4, sofs[jj], s * 8, 0,
-                                                 0);
+        for (int jj = 0; jj < NS; ++jj)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (gvm_lds_ptr_t)(st + kGvmOS + jj * 256), 4, sofs[jj], s * 8,
+                                                     0, 0);
+    }
 #pragma unroll
     for (int ja = 0; ja < 3; ++ja) {
         const int vo = (64 * ja + lane) / 48 < mc ? aofs[ja] : kGvmNoLoad;
@@ -286,9 +297,13 @@ __device__ __forceinline__ void gvm_issue(uint8_t* st, __amdgpu_buffer_rsrc_t rp
 // 128-byte line per row), their scales, and the group's limb rows at those
 // K with their block scales: everything a stage's MFMAs read comes with the
 // stage, so one vmcnt wait per stage covers it.
-template <bool GU>
+// S16: scale rows 16-byte aligned (K % 512 == 0): a row's scales for two
+// stages come as one 16-byte lane of one instruction every other stage
+// (instead of three 4-byte-lane instructions per stage, each reaching 64
+// rows' lines), into a double-buffered per-wave super-stage area.
+template <bool GU, bool S16>
 __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
-    constexpr int NT = 15;                                   // DMA instructions per stage
+    constexpr int NT = S16 ? 13 : 15;                        // DMA instructions per stage
     constexpr int ST = kGvmStages;
     constexpr int WAIT = NT * (ST - 1);
     static_assert(WAIT <= 63, "vmcnt holds 63");
@@ -308,6 +323,9 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     uint8_t* ring = gvm_ring + wave * (ST * kGvmStage);
+    // per wave: two 1 KiB super-stage scale buffers and a 1 KiB dummy area
+    uint8_t* supw = gvm_ring + kGvmWaves * ST * kGvmStage + wave * 3 * 1024;
+    const uint32_t sup_base = gvm_lds_addr(supw);
     const uint32_t ring_base = gvm_lds_addr(ring);
     const int col = lane & 15, grp = lane >> 4;              // B / D column, lane group
 
@@ -386,10 +404,15 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
                 const int r = 8 * j + (lane >> 3);
                 d.pofs[j] = wrow(r) * lrow + (((lane & 7) ^ ((r >> 1) & 7)) << 4);
             }
+            if constexpr (S16) {
+                d.sofs[0] = wrow(lane) * srb;                    // row lane's scales
+                d.sofs[1] = d.sofs[2] = 0;
+            } else {
 #pragma unroll
-            for (int jj = 0; jj < 3; ++jj) {
-                const int gi = 64 * jj + lane;                   // row gi / 3, dword gi % 3
-                d.sofs[jj] = ((wrow(gi / 3) * srb) & ~3) + (gi % 3) * 4;
+                for (int jj = 0; jj < 3; ++jj) {
+                    const int gi = 64 * jj + lane;               // row gi / 3, dword gi % 3
+                    d.sofs[jj] = ((wrow(gi / 3) * srb) & ~3) + (gi % 3) * 4;
+                }
             }
 #pragma unroll
             for (int ja = 0; ja < 3; ++ja) {
@@ -407,9 +430,16 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
     Desc cur, nxt;
     // Stage s of the current item (the next one when nx) into ring slot
     // q % ST (gvm_issue)
+    // (S16: global stage q's super-stage buffer is (q / 2) % 2; items hold
+    // an even number of stages, so q and s have the same parity)
     auto issue = [&](bool nx, int s, int q) {
-        if (nx) gvm_issue(ring + (q % ST) * kGvmStage, np, ns, na, nxt.pofs, nxt.sofs, nxt.aofs, nxt.asofs, nxt.mc, lane, s, nt);
-        else gvm_issue(ring + (q % ST) * kGvmStage, cp, cs, ca, cur.pofs, cur.sofs, cur.aofs, cur.asofs, cur.mc, lane, s, nt);
+        uint8_t* sup = supw + ((q & 1) ? 2048 : ((q >> 1) & 1) * 1024);
+        if (nx)
+            gvm_issue<S16>(ring + (q % ST) * kGvmStage, sup, np, ns, na, nxt.pofs, nxt.sofs, nxt.aofs, nxt.asofs,
+                           nxt.mc, lane, s, nt);
+        else
+            gvm_issue<S16>(ring + (q % ST) * kGvmStage, sup, cp, cs, ca, cur.pofs, cur.sofs, cur.aofs, cur.asofs,
+                           cur.mc, lane, s, nt);
     };
 
     // One continuous stream of stages over this wave's items: the last
@@ -476,8 +506,9 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
                     const int pc = 4 * t + grp;                      // 16-byte piece of the row's 128
                     asm volatile("ds_read_b128 %0, %1"
                                  : "=v"(aq[rb]) : "v"(stb + r * 128 + ((pc ^ ((r >> 1) & 7)) << 4)));
-                    asm volatile("ds_read_u8 %0, %1"
-                                 : "=v"(sa[rb]) : "v"(stb + kGvmOS + r * 12 + (soff[rb] & 3) + pc));
+                    const uint32_t sadr = S16 ? sup_base + uint32_t(((q >> 1) & 1) * 1024 + r * 16 + (s & 1) * 8 + pc)
+                                              : stb + uint32_t(kGvmOS + r * 12 + (soff[rb] & 3) + pc);
+                    asm volatile("ds_read_u8 %0, %1" : "=v"(sa[rb]) : "v"(sadr));
                 }
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
@@ -568,9 +599,15 @@ hipError_t gvm_launch(hipStream_t st, const GvArgs& a, bool gate_up) {
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             return hipErrorInvalidConfiguration;
     }
-    const size_t lds = size_t(kGvmWaves) * kGvmStages * kGvmStage;
-    if (gate_up) hipLaunchKernelGGL(gvm_kernel<true>, dim3(cus), dim3(kGvmWaves * kWave), lds, st, a);
-    else hipLaunchKernelGGL(gvm_kernel<false>, dim3(cus), dim3(kGvmWaves * kWave), lds, st, a);
+    const size_t lds = size_t(kGvmWaves) * kGvmStages * kGvmStage + kGvmWaves * 3 * 1024;
+    const dim3 grid(cus), blk(kGvmWaves * kWave);
+    if (a.K % 512 == 0) {
+        if (gate_up) hipLaunchKernelGGL((gvm_kernel<true, true>), grid, blk, lds, st, a);
+        else hipLaunchKernelGGL((gvm_kernel<false, true>), grid, blk, lds, st, a);
+    } else {
+        if (gate_up) hipLaunchKernelGGL((gvm_kernel<true, false>), grid, blk, lds, st, a);
+        else hipLaunchKernelGGL((gvm_kernel<false, false>), grid, blk, lds, st, a);
+    }
     return hipGetLastError();
 }
 
