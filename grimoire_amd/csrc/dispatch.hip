@@ -223,7 +223,7 @@ hipError_t dispatch_launch(hipStream_t st, const DispatchArgs& a) {
 // slot tables stay in registers and all KT row loads are issued before the
 // first use.  A skipped slot (p < 0, or s >= K) reads row 0 and is masked
 // after the load, not branched around.
-template <bool SRC_BF16>
+template <bool SRC_BF16, bool NT = false>
 __device__ __forceinline__ float4 combine_load(const void* src, int64_t row, int H, int d) {
     if constexpr (SRC_BF16) {
         const uint2 u =
@@ -231,14 +231,18 @@ __device__ __forceinline__ float4 combine_load(const void* src, int64_t row, int
         return make_float4(bits_f(u.x << 16), bits_f(u.x & 0xFFFF0000u), bits_f(u.y << 16),
                            bits_f(u.y & 0xFFFF0000u));
     } else {
-        // the expert rows are read once: non-temporal
-        typedef float f4nt __attribute__((ext_vector_type(4)));
-        const f4nt v = __builtin_nontemporal_load(reinterpret_cast<const f4nt*>(static_cast<const float*>(src) + row * H + d));
-        return make_float4(v.x, v.y, v.z, v.w);
+        const float* p = static_cast<const float*>(src) + row * H + d;
+        if constexpr (NT) {
+            typedef float f4nt __attribute__((ext_vector_type(4)));
+            const f4nt v = __builtin_nontemporal_load(reinterpret_cast<const f4nt*>(p));
+            return make_float4(v.x, v.y, v.z, v.w);
+        } else {
+            return *reinterpret_cast<const float4*>(p);
+        }
     }
 }
 
-template <bool SRC_BF16, int KT>
+template <bool SRC_BF16, int KT, bool NT>
 __global__ __launch_bounds__(kDispThreads) void combine_kernel(
     const void* __restrict__ src, const int32_t* __restrict__ inverse,
     const float* __restrict__ rw, const void* __restrict__ shared_src, int shared_bf16,
@@ -265,8 +269,8 @@ __global__ __launch_bounds__(kDispThreads) void combine_kernel(
 #pragma unroll
         for (int s = 0; s < KT; ++s) {
             const int64_t row = p[s] < 0 ? 0 : p[s];
-            a0[s] = combine_load<SRC_BF16>(src, row, H, d0);
-            a1[s] = combine_load<SRC_BF16>(src, row, H, d1);
+            a0[s] = combine_load<SRC_BF16, NT>(src, row, H, d0);
+            a1[s] = combine_load<SRC_BF16, NT>(src, row, H, d1);
         }
         float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
         if (accumulate) {
@@ -300,10 +304,15 @@ __global__ __launch_bounds__(kDispThreads) void combine_kernel(
     }
 }
 
-template <bool SRC_BF16>
+// Expert rows larger than the last-level cache (256 MiB) stream through
+// with non-temporal loads; smaller ones (a few tokens' rows, just written by
+// the down projection) are still cached and load normally.
+constexpr int64_t kCombineStreamBytes = int64_t(256) << 20;
+
+template <bool SRC_BF16, bool NT>
 static void combine_k(hipStream_t st, const CombineArgs& a) {
 #define GRIM_COMBINE(KT)                                                                          \
-    hipLaunchKernelGGL((combine_kernel<SRC_BF16, KT>), dim3(a.T), dim3(kDispThreads), 0, st,      \
+    hipLaunchKernelGGL((combine_kernel<SRC_BF16, KT, NT>), dim3(a.T), dim3(kDispThreads), 0, st,  \
                        a.src, a.inverse, a.rw, a.shared_src, a.shared_bf16, a.gate, a.dst, a.H,   \
                        a.K, a.p0, a.p1, a.accumulate)
     switch (a.K) {
@@ -321,8 +330,9 @@ static void combine_k(hipStream_t st, const CombineArgs& a) {
 hipError_t combine_launch(hipStream_t st, const CombineArgs& a) {
     if (a.T <= 0) return hipSuccess;
     if (a.K <= 0 || a.K > 16) return hipErrorInvalidValue;
-    if (a.src_bf16) combine_k<true>(st, a);
-    else combine_k<false>(st, a);
+    const bool nt = int64_t(a.T) * a.K * a.H * (a.src_bf16 ? 2 : 4) > kCombineStreamBytes;
+    if (a.src_bf16) nt ? combine_k<true, true>(st, a) : combine_k<true, false>(st, a);
+    else nt ? combine_k<false, true>(st, a) : combine_k<false, false>(st, a);
     return hipGetLastError();
 }
 

@@ -36,7 +36,6 @@
 #include "gemv_mx.hpp"
 
 #include "gemv_impl.hpp"
-#include "topk.hpp"
 
 namespace grim {
 
@@ -160,30 +159,36 @@ hipError_t gvm_format_launch(hipStream_t st, const float* src0, int rows0, uint8
 
 // ------------------------------------------------- small-batch routing
 //
-// Everything between the router logits and the grouped GEMV for a batch of
-// at most kGvmRouteMax routes, in one work-group instead of six launches
-// (top-k, the dispatch's count / column scan / scan / rank, the activation
-// formatting): each wave runs topk_wave for its tokens (the batched top-k's
-// code, so the same picks and weights), the expert counts come from LDS
-// atomics (counts only: order-free), one scan forms the offsets and the
-// (expert, group of kGvMT rows) table, and each route's row is its
-// expert's offset plus the number of earlier routes of that expert -- the
-// dispatch's stable order (src/grimoire.cpp:23162-23170).  The x rows are
-// formatted as limbs by the same code as gvm_format_kernel.
+// Everything between the top-k and the grouped GEMV for a batch of at most
+// kGvmRouteMax routes in one launch instead of five (the dispatch's count /
+// column scan / scan / rank and the activation formatting).  Work-group 0:
+// the expert counts come from LDS atomics (counts only: order-free), one
+// scan forms the offsets and the (expert, group of kGvMT rows) table, and
+// each route's row is its expert's offset plus the number of earlier
+// routes of that expert -- the dispatch's stable order
+// (src/grimoire.cpp:23162-23170).  (The top-k itself stays a launch of its
+// own: in one work-group the tokens' top-k would share one CU.)  The x rows are
+// formatted as limbs by the same code as gvm_format_kernel, one block of
+// 32 elements per thread of the launch's other work-groups.
 constexpr int kGvmRouteThreads = 1024;
-constexpr int kGvmRouteWaves = kGvmRouteThreads / kWave;
 
 __global__ __launch_bounds__(kGvmRouteThreads) void gvm_route_kernel(TopkArgs tk, GvmRouteArgs ra) {
-    __shared__ float gsel[kGvmRouteWaves][512];
-    __shared__ float gscore[kGvmRouteWaves][64];
-    __shared__ int32_t ids[kGvmRouteMax];
+    if (blockIdx.x > 0) {
+        // work-groups 1..: the x rows in the limb format, in parallel with
+        // the routing in work-group 0
+        const int kp = gvm_kpad(ra.H), nb = kp / 32;
+        const int ab = gvm_row_bytes(ra.H);
+        const int i = (int(blockIdx.x) - 1) * kGvmRouteThreads + int(threadIdx.x);
+        if (i < tk.T * nb)
+            gvm_format_block(ra.x + int64_t(i / nb) * ra.H, ra.af + int64_t(i / nb) * ab, ra.H, kp, i % nb);
+        return;
+    }
+    __shared__ __attribute__((aligned(16))) int32_t ids[kGvmRouteMax];
     __shared__ int32_t cnt[kGvmRouteThreads], sc[kGvmRouteThreads], sg[kGvmRouteThreads];
-    const int tid = threadIdx.x, wave = tid / kWave;
+    const int tid = threadIdx.x;
     const int T = tk.T, E = tk.E, K = tk.K, R = T * K;
-    for (int e = tid; e < kGvmRouteThreads; e += kGvmRouteThreads) cnt[e] = 0;
-    for (int t = wave; t < T; t += kGvmRouteWaves)
-        topk_wave(tk.logits + int64_t(t) * E, E, K, tk.mode, tk.normalize, tk.scaling, tk.bias16, tk.bias32,
-                  tk.n_group, tk.topk_group, ids + t * K, tk.out_w + int64_t(t) * K, gsel[wave], gscore[wave]);
+    cnt[tid] = 0;
+    if (tid < R) ids[tid] = tk.out_e[tid];
     __syncthreads();
     const int my_id = tid < R ? ids[tid] : -1;
     if (my_id >= 0 && my_id < E) atomicAdd(&cnt[my_id], 1);
@@ -222,24 +227,33 @@ __global__ __launch_bounds__(kGvmRouteThreads) void gvm_route_kernel(TopkArgs tk
     if (tid < R) {
         int dest = -1;
         if (my_id >= 0 && my_id < E) {
+            // earlier routes of the same expert: four ids per 16-byte read,
+            // four reads in flight (the same count as a route-by-route loop)
             int rank = 0;
-            for (int j = 0; j < tid; ++j) rank += ids[j] == my_id ? 1 : 0;
+            const int4* ids4 = reinterpret_cast<const int4*>(ids);
+            const int n4 = (tid + 3) / 4;
+#pragma unroll 4
+            for (int j = 0; j < n4; ++j) {
+                const int4 v = ids4[j];
+                rank += (v.x == my_id && 4 * j < tid) ? 1 : 0;
+                rank += (v.y == my_id && 4 * j + 1 < tid) ? 1 : 0;
+                rank += (v.z == my_id && 4 * j + 2 < tid) ? 1 : 0;
+                rank += (v.w == my_id && 4 * j + 3 < tid) ? 1 : 0;
+            }
             dest = cnt[my_id] + rank;
             ra.perm_token[dest] = tid / K;
         }
         ra.inverse[tid] = dest;
-        tk.out_e[tid] = my_id;
     }
-    // the x rows in the limb format
-    const int kp = gvm_kpad(ra.H), nb = kp / 32;
-    const int ab = gvm_row_bytes(ra.H);
-    for (int i = tid; i < T * nb; i += kGvmRouteThreads)
-        gvm_format_block(ra.x + int64_t(i / nb) * ra.H, ra.af + int64_t(i / nb) * ab, ra.H, kp, i % nb);
 }
 
 hipError_t gvm_route_launch(hipStream_t st, const TopkArgs& tk, const GvmRouteArgs& ra) {
+    hipError_t e = topk_launch(st, tk);
+    if (e != hipSuccess) return e;
     if (int64_t(tk.T) * tk.K > kGvmRouteMax || tk.E > 512 || tk.E <= 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gvm_route_kernel, dim3(1), dim3(kGvmRouteThreads), 0, st, tk, ra);
+    const int64_t blocks = int64_t(tk.T) * (gvm_kpad(ra.H) / 32);
+    const int fmt_groups = int((blocks + kGvmRouteThreads - 1) / kGvmRouteThreads);
+    hipLaunchKernelGGL(gvm_route_kernel, dim3(1 + fmt_groups), dim3(kGvmRouteThreads), 0, st, tk, ra);
     return hipGetLastError();
 }
 

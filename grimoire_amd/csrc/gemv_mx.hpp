@@ -14,10 +14,11 @@ size_t gvm_act_bytes(int K);
 // Format rows0 rows of src0 into dst0 and rows1 rows of src1 into dst1.
 hipError_t gvm_format_launch(hipStream_t st, const float* src0, int rows0, uint8_t* dst0, const float* src1,
                              int rows1, uint8_t* dst1, int K);
-// Routing for a batch of at most kGvmRouteMax routes in one launch: the
-// top-k of tk (picks into tk.out_e, weights into tk.out_w), expert counts,
-// offsets, the (expert, kGvMT-row group) table, each route's row (inverse)
-// and token (perm_token by row), and the x rows [T][H] in the limb format.
+// Routing for a batch of at most kGvmRouteMax routes in two launches: the
+// top-k of tk (picks into tk.out_e, weights into tk.out_w), then expert
+// counts, offsets, the (expert, kGvMT-row group) table, each route's row
+// (inverse) and token (perm_token by row), and the x rows [T][H] in the
+// limb format.
 constexpr int kGvmRouteMax = 1024;
 struct GvmRouteArgs {
     int32_t *counts, *offsets, *tile_e, *tile_mb;
