@@ -25,6 +25,14 @@
 // first tiles and its scales in LDS before the current one's epilogue,
 // which stores straight from the accumulators.  Persistent XCD-aware grid
 // over (m-tile, column tile) items, rows from the dispatch's tile table.
+//
+// Rows mode (the forward's): no tile table; every work-group lists the
+// tiles itself from the per-expert row counts.  Experts above `split` rows
+// take the 128-row tiles; the rest (the tail of a skewed routing, where a
+// 128-row tile would be mostly empty rows and the expert's weights read
+// once from memory are the real work) take 32-row x 256-column tiles whose
+// stages span 128 K, so every weight DMA lane moves a whole 128-byte line.
+// One launch walks the 128-row items, then the narrow ones.
 #include "common.hpp"
 #include "gemm.hpp"
 #include "gemm_i8.hpp"

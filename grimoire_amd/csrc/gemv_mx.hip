@@ -33,6 +33,13 @@
 // masked.  One continuous stage stream runs across a wave's items, so an
 // item starts with its data in flight.  Like gemv_grouped.hip: one
 // work-group per CU, no barrier, every wave waits on its own vmcnt only.
+// Scale rows that are 16-byte aligned (K % 512 == 0) come in a 16-byte lane
+// per row for two stages at a time (gvm_kernel<., true>); weight rows that
+// straddle memory lines are loaded without the non-temporal hint.
+//
+// Also here: the formatting of activation rows into limbs, and for small
+// batches the dispatch (counts, offsets, group table, stable ranks) in one
+// launch beside that formatting (gvm_route_kernel).
 #include "gemv_mx.hpp"
 
 #include "gemv_impl.hpp"
