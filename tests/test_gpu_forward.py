@@ -189,3 +189,44 @@ def test_forward_grouped_gemv_fp32_activations(gpu, regime):
     _check_routing(wl, logits, oe, ow)
     yo = _oracle_y(wl.layer, wl.x, oe, ow, None)
     assert_close(y, yo, what="grouped gemv fp32 x")
+
+
+@pytest.mark.parametrize("name,kw,regime", [
+    ("c3", {}, 0),                                        # matrix-core grouped GEMV, merged dispatch
+    ("c5", dict(T=32, H=1024, E=64, I=512), 0),           # the same, aligned scale loads, shared expert
+    ("c4", dict(T=256, H=1024, E=64, I=256), 2),          # INT8 rows mode (128- and 32-row tiles)
+])
+def test_forward_graph_replays(gpu, name, kw, regime):
+    """The forward captured once in a HIP graph and replayed on new inputs,
+    three rounds with eager work and synchronisations between replays:
+    every replay equals the eager forward on the same input, bit for bit."""
+    print(f"forward graph replays {name} {kw} regime {regime}", flush=True)
+    cfg = configs.scaled(configs.CONFIGS[name], **kw) if kw else configs.CONFIGS[name]
+    wl = configs.make_workload(cfg, "cpu", seed=21)
+    Lg = wl.layer.to(gpu)
+    bias = None if wl.route_bias is None else wl.route_bias.to(gpu)
+    fwd = ops.MoeForward(Lg, cfg.T, configs.route_params(cfg, bias), regime)
+    xs = [(wl.x * (1.0 + 0.25 * s)).to(gpu) for s in range(3)]
+    x = xs[0].clone()
+    y = torch.empty(cfg.T, cfg.H, device=gpu)
+    oe = torch.empty(cfg.T, cfg.K, dtype=torch.int32, device=gpu)
+    ow = torch.empty(cfg.T, cfg.K, dtype=torch.float32, device=gpu)
+    eager = []
+    for xi in xs:
+        x.copy_(xi)
+        fwd(x, y, oe, ow)
+        torch.cuda.synchronize()
+        eager.append((y.cpu().clone(), oe.cpu().clone()))
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        fwd(x, y, oe, ow, stream=s)
+    for rep in range(3):
+        for i, xi in enumerate(xs):
+            x.copy_(xi)
+            torch.cuda.synchronize()
+            with torch.cuda.stream(s):
+                g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(oe.cpu(), eager[i][1]), f"routes, replay {rep} input {i}"
+            assert torch.equal(y.cpu(), eager[i][0]), f"output, replay {rep} input {i}"
