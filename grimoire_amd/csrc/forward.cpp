@@ -347,12 +347,18 @@ static int forward_gv(hipStream_t st, const grim_moe_layer* L, const Plan& p, co
 #ifdef GRIM_TIMING
     g.ts = g_timing;
 #endif
+    if (mx) {
+        // the matrix-core gate_up writes h in the down's limb format itself
+        g.hf = reinterpret_cast<uint8_t*>(p.gv_hf);
+        g.hf_sh = reinterpret_cast<uint8_t*>(p.gv_hfsh);
+    }
     hipError_t e = mx ? gvm_launch(st, g, true) : gv_launch(st, L->gate_up.fmt, g, true);
     if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
-    e = mx ? gvm_format_launch(st, p.gv_h, tokens * K, reinterpret_cast<uint8_t*>(p.gv_hf), p.gv_hsh,
-                               sh ? tokens : 0, reinterpret_cast<uint8_t*>(p.gv_hfsh), I)
-           : gv_format_launch(st, L->down.fmt, p.gv_h, tokens * K, p.gv_hf, p.gv_hsh, sh ? tokens : 0, p.gv_hfsh, I);
-    if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    if (!mx) {
+        e = gv_format_launch(st, L->down.fmt, p.gv_h, tokens * K, p.gv_hf, p.gv_hsh, sh ? tokens : 0, p.gv_hfsh, I);
+        if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    }
+    g.hf = g.hf_sh = nullptr;
     GvArgs d = g;
     d.af = p.gv_hf;
     d.af_sh = p.gv_hfsh;

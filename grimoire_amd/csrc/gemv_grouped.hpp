@@ -21,6 +21,8 @@ struct GvArgs {
     const int32_t* perm_token;   // gate_up: route row -> token
     float* h;                    // gate_up out / down in: per route [R][I]
     float* h_sh;                 // shared expert [T_sh][I]
+    uint8_t* hf;                 // gate_up, matrix-core kernel: when set, h is written in the
+    uint8_t* hf_sh;              // down's limb format (rows of gvm_row_bytes(I)) instead of fp32
     float* y;                    // down out: per route [R][H]
     float* y_sh;                 // shared expert [T_sh][H]
     const int32_t* counts;       // [E]

@@ -96,8 +96,36 @@ __host__ __device__ inline int gvm_row_bytes(int K) {
 
 size_t gvm_act_bytes(int K) { return size_t(gvm_row_bytes(K)); }
 
+// Block scale exponent s (e8m0 byte s + 127) of a 32-element block whose
+// largest magnitude is mx, and inv = 2^-s: the largest value lands in
+// [128, 256), inside e4m3's range of 448.
+__device__ __forceinline__ int gvm_block_scale(float mx, float& inv) {
+    const int ex = mx > 0.0f ? int((f_bits(mx) >> 23) & 0xFF) - 127 : -127;
+    const int s = max(-127, min(127, ex - 7));
+    inv = bits_f(uint32_t(127 - s) << 23);   // 2^-s (s >= -127: 2^127 at most)
+    return s;
+}
+
+// Four consecutive values times inv as three e4m3 limbs (each the
+// remainder of the ones before), one packed word per limb.
+__device__ __forceinline__ void gvm_limbs4(const float* v, float inv, uint32_t (&q)[kGvmLimbs]) {
+    float r[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = v[j] * inv;
+#pragma unroll
+    for (int L = 0; L < kGvmLimbs; ++L) {
+        int p = __builtin_amdgcn_cvt_pk_fp8_f32(r[0], r[1], 0, false);
+        p = __builtin_amdgcn_cvt_pk_fp8_f32(r[2], r[3], p, true);
+        q[L] = uint32_t(p);
+        r[0] -= __builtin_amdgcn_cvt_f32_fp8(p, 0);
+        r[1] -= __builtin_amdgcn_cvt_f32_fp8(p, 1);
+        r[2] -= __builtin_amdgcn_cvt_f32_fp8(p, 2);
+        r[3] -= __builtin_amdgcn_cvt_f32_fp8(p, 3);
+    }
+}
+
 // Block b (32 elements) of one row: src the row (K floats), dst its limb
-// row (gvm_row_bytes(K)); blocks past K give zero limbs under scale 1.
+// row (gvm_row_bytes(K)); blocks past K give zero limbs (scale byte 0).
 __device__ __forceinline__ void gvm_format_block(const float* __restrict__ src, uint8_t* __restrict__ dst, int K,
                                                  int kp, int b) {
     const float4* s4 = reinterpret_cast<const float4*>(src + b * 32);
@@ -111,26 +139,15 @@ __device__ __forceinline__ void gvm_format_block(const float* __restrict__ src, 
     float mx = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; ++i) mx = fmaxf(mx, fabsf(v[i]));
-    // the largest value lands in [128, 256): e4m3 holds up to 448
-    const int ex = mx > 0.0f ? int((f_bits(mx) >> 23) & 0xFF) - 127 : -127;
-    const int s = max(-127, min(127, ex - 7));
-    const float inv = bits_f(uint32_t(127 - s) << 23);   // 2^-s (s >= -127: 2^127 at most)
+    float inv;
+    const int s = gvm_block_scale(mx, inv);
     uint32_t w[3][8];
 #pragma unroll
     for (int i = 0; i < 32; i += 4) {
-        float r[4];
+        uint32_t q[kGvmLimbs];
+        gvm_limbs4(v + i, inv, q);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) r[j] = v[i + j] * inv;
-#pragma unroll
-        for (int L = 0; L < kGvmLimbs; ++L) {
-            int p = __builtin_amdgcn_cvt_pk_fp8_f32(r[0], r[1], 0, false);
-            p = __builtin_amdgcn_cvt_pk_fp8_f32(r[2], r[3], p, true);
-            w[L][i / 4] = uint32_t(p);
-            r[0] -= __builtin_amdgcn_cvt_f32_fp8(p, 0);
-            r[1] -= __builtin_amdgcn_cvt_f32_fp8(p, 1);
-            r[2] -= __builtin_amdgcn_cvt_f32_fp8(p, 2);
-            r[3] -= __builtin_amdgcn_cvt_f32_fp8(p, 3);
-        }
+        for (int L = 0; L < kGvmLimbs; ++L) w[L][i / 4] = q[L];
     }
 #pragma unroll
     for (int L = 0; L < kGvmLimbs; ++L) {
@@ -566,7 +583,54 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
         }
 
         // D: column col = group row, weight rows 4 grp + [0, 4) of each block
-        if (col < cur.mc) {
+        if constexpr (GU) {
+            if (a.hf && cur.i0 < N) {
+                // h straight into the down's limb format: the wave's 32 pairs
+                // are one 32-element block b of each group row, 8 values per
+                // lane (positions 4 grp + [0, 4) and 16 + 4 grp + [0, 4)), the
+                // column's 4 lanes at lanes col + 16 grp.  Same arithmetic as
+                // gvm_format_block.  (N % 32 == 0: the block is whole.)
+                float hv[8];
+                float mx = 0.0f;
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                    for (int qq = 0; qq < 4; ++qq) {
+                        hv[4 * rb + qq] = fast_silu(acc[rb][qq]) * acc[NRB / 2 + rb][qq];
+                        mx = fmaxf(mx, fabsf(hv[4 * rb + qq]));
+                    }
+                mx = fmaxf(mx, __shfl_xor(mx, 16));
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                if (col < cur.mc) {
+                    const int hkp = gvm_kpad(N), b = cur.i0 / 32;
+                    uint8_t* dst = (cur.sh ? a.hf_sh : a.hf) + int64_t(cur.r0 + col) * gvm_row_bytes(N);
+                    float inv;
+                    const int s = gvm_block_scale(mx, inv);
+                    uint32_t q0[kGvmLimbs], q1[kGvmLimbs];
+                    gvm_limbs4(hv, inv, q0);
+                    gvm_limbs4(hv + 4, inv, q1);
+#pragma unroll
+                    for (int L = 0; L < kGvmLimbs; ++L) {
+                        uint32_t* d = reinterpret_cast<uint32_t*>(dst + int64_t(L) * hkp + b * 32) + grp;
+                        d[0] = q0[L];
+                        d[4] = q1[L];
+                    }
+                    if (grp == 0) dst[3 * hkp + b] = uint8_t(s + 127);
+                    if (cur.i0 + 32 == N) {
+                        // the last block also writes the pad blocks: zero
+                        // limbs, scale byte 0 (a zero block's)
+                        for (int pb = N / 32; pb < hkp / 32; ++pb) {
+#pragma unroll
+                            for (int L = 0; L < kGvmLimbs; ++L)
+                                *reinterpret_cast<uint2*>(dst + int64_t(L) * hkp + pb * 32 + 8 * grp) =
+                                    make_uint2(0u, 0u);
+                            if (grp == 0) dst[3 * hkp + pb] = 0;
+                        }
+                    }
+                }
+            }
+        }
+        if (col < cur.mc && !(GU && a.hf)) {
             const int64_t orow = int64_t(cur.r0 + col) * N;
             if constexpr (GU) {
                 float* h = cur.sh ? a.h_sh : a.h;
@@ -613,6 +677,7 @@ bool gvm_shape_ok(int H, int I) {
 
 hipError_t gvm_launch(hipStream_t st, const GvArgs& a, bool gate_up) {
     if (a.K % 64 || gvm_kpad(a.K) < (kGvmStages - 1) * kGvmKS) return hipErrorInvalidValue;
+    if (gate_up && a.hf && a.N % 32) return hipErrorInvalidValue;   // whole h blocks
     static int cus = 0;
     if (cus == 0) {
         int dev = 0;
