@@ -156,6 +156,7 @@ def test_forward_c5_full_size_sampled(gpu):
     ("c5", dict(T=32, H=1024, E=64, I=512)),              # the same, matrix core: two stages per down item
     ("c5", dict(T=16, H=1280, E=32, I=768)),              # MXFP4, K % 256 == 0, ragged item tail
     ("c5", dict(T=6, H=2112, E=16, I=2240)),              # matrix core, 9 stages, rows across memory lines
+    ("c5", dict(T=8, H=1536, E=16, I=1472)),              # matrix core, 6 stages, scale rows 4- / 2-byte aligned
     ("c1", {}),                                           # GPTQ int4, T=16
     ("c2", dict(T=24)),                                   # GPTQ int4, more rows than experts' groups
 ])
