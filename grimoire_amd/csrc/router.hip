@@ -72,6 +72,94 @@ __global__ __launch_bounds__(256) void router_gemv(const float* __restrict__ W,
     if (int(threadIdx.x) < nt) logits[int64_t(t0 + threadIdx.x) * E + e] = bias ? s + bias[e] : s;
 }
 
+// Small T, H <= 1024 NK: the arithmetic of router_row (thread i's chain over
+// elements 4i + 1024m in m order, DPP wave sums, the four waves added in
+// order), so the same bits, for EB experts x TT tokens per work-group: every
+// load of the work-group's rows and tokens is issued before the products
+// (addresses past H clamped to 0, their products not added), and x is read
+// E / EB times instead of E times.
+template <int NK, int EB, int TT>
+__global__ __launch_bounds__(256) void router_gemv_nk(const float* __restrict__ W,
+                                                      const float* __restrict__ x,
+                                                      const float* __restrict__ bias,
+                                                      float* __restrict__ logits, int T, int E, int H) {
+    __shared__ float red[4 * EB * TT];
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int e0 = blockIdx.x * EB, t0 = blockIdx.y * TT;
+    const int ne = min(EB, E - e0), nt = min(TT, T - t0);
+    float4 wv[NK][EB], xv[NK][TT];
+#pragma unroll
+    for (int m = 0; m < NK; ++m) {
+        const int k = int(threadIdx.x) * 4 + 1024 * m;
+        const int kk = k < H ? k : 0;
+#pragma unroll
+        for (int j = 0; j < EB; ++j)
+            wv[m][j] = *reinterpret_cast<const float4*>(W + int64_t(e0 + min(j, ne - 1)) * H + kk);
+#pragma unroll
+        for (int i = 0; i < TT; ++i)
+            xv[m][i] = *reinterpret_cast<const float4*>(x + int64_t(t0 + min(i, nt - 1)) * H + kk);
+    }
+#pragma unroll
+    for (int j = 0; j < EB; ++j) {
+#pragma unroll
+        for (int i = 0; i < TT; ++i) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int m = 0; m < NK; ++m) {
+                const int k = int(threadIdx.x) * 4 + 1024 * m;
+                float a2 = __builtin_fmaf(wv[m][j].x, xv[m][i].x, acc);
+                a2 = __builtin_fmaf(wv[m][j].y, xv[m][i].y, a2);
+                a2 = __builtin_fmaf(wv[m][j].z, xv[m][i].z, a2);
+                a2 = __builtin_fmaf(wv[m][j].w, xv[m][i].w, a2);
+                acc = k < H ? a2 : acc;
+            }
+            const float v = group_sum<kWave>(acc);
+            if (lane == 0) red[(wave * EB + j) * TT + i] = v;
+        }
+    }
+    __syncthreads();
+    const int j = int(threadIdx.x) / TT, i = int(threadIdx.x) % TT;
+    if (j < ne && i < nt) {
+        const int q = j * TT + i, st = EB * TT;
+        const float r = (red[q] + red[st + q]) + (red[2 * st + q] + red[3 * st + q]);
+        const int e = e0 + j;
+        logits[int64_t(t0 + i) * E + e] = bias ? r + bias[e] : r;
+    }
+}
+
+template <int NK, int EB, int TT>
+static void router_nk_go(hipStream_t st, const float* W, const float* x, const float* bias, float* logits, int T,
+                         int E, int H) {
+    const dim3 grid((E + EB - 1) / EB, (T + TT - 1) / TT);
+    hipLaunchKernelGGL((router_gemv_nk<NK, EB, TT>), grid, dim3(256), 0, st, W, x, bias, logits, T, E, H);
+}
+
+// EB x TT per work-group, measured (rocprof, one MI355X): 2 x 4 for rows up
+// to 5K (T=8, H=2880, E=128: 3.6 us; 2 x 8: 5.3; 1 x 8: 4.1), 4 x 4 for
+// longer ones (T=32, H=7168, E=256: 9.0 us; 1 x 4: 12.8; 2 x 4: 10.2;
+// 8 x 4: 11.7; 4 x 2: 10.2).
+template <int NK>
+static void router_nk_pick(hipStream_t st, const float* W, const float* x, const float* bias, float* logits, int T,
+                           int E, int H) {
+    if constexpr (NK <= 5) router_nk_go<NK, 2, 4>(st, W, x, bias, logits, T, E, H);
+    else router_nk_go<NK, 4, 4>(st, W, x, bias, logits, T, E, H);
+}
+
+static bool router_nk_launch(hipStream_t st, const float* W, const float* x, const float* bias, float* logits,
+                             int T, int E, int H) {
+    switch ((H + 1023) / 1024) {
+    case 1: router_nk_pick<1>(st, W, x, bias, logits, T, E, H); return true;
+    case 2: router_nk_pick<2>(st, W, x, bias, logits, T, E, H); return true;
+    case 3: router_nk_pick<3>(st, W, x, bias, logits, T, E, H); return true;
+    case 4: router_nk_pick<4>(st, W, x, bias, logits, T, E, H); return true;
+    case 5: router_nk_pick<5>(st, W, x, bias, logits, T, E, H); return true;
+    case 6: router_nk_pick<6>(st, W, x, bias, logits, T, E, H); return true;
+    case 7: router_nk_pick<7>(st, W, x, bias, logits, T, E, H); return true;
+    case 8: router_nk_pick<8>(st, W, x, bias, logits, T, E, H); return true;
+    default: return false;
+    }
+}
+
 // Large T: LDS-tiled fp32 GEMM, 64 tokens x 64 experts per block, each
 // thread a 4x4 register tile, K in steps of 16.
 __global__ __launch_bounds__(256) void router_gemm(const float* __restrict__ W,
@@ -350,7 +438,8 @@ __global__ __launch_bounds__(256) void router_bf16x3(const float* __restrict__ W
 
 hipError_t router_logits_launch(hipStream_t st, const float* W, const float* x,
                                 const float* bias, float* logits, int T, int E, int H) {
-    if (T <= 32 && H % 4 == 0) {
+    if (T <= 32 && H % 4 == 0 && router_nk_launch(st, W, x, bias, logits, T, E, H)) {
+    } else if (T <= 32 && H % 4 == 0) {
         dim3 grid(E, (T + kRouterTok - 1) / kRouterTok);
         hipLaunchKernelGGL(router_gemv, grid, dim3(256), 0, st, W, x, bias, logits, T, E, H);
     } else if (H % (kR3BK * kR3Pre) == 0) {
