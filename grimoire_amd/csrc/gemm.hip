@@ -410,20 +410,24 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, const GemmSrc& w, b
     // pairs of K tiles, then an odd last tile: no exit from the middle of
     // the unrolled pair, so the accumulators stay in one register set
     int kt = 0;
+    // MXFP4: requests past the last tile fetch the last again into a set
+    // that is never consumed (requests under a branch make the compiler wait
+    // for every load in flight at the loop head, which ends the look-ahead):
+    // 10% faster on MXFP4 (16 experts x 512 rows, N 4096, K 7168: 670 -> 600
+    // us); bf16 B tiles run 5% slower that way and keep the branches.
+    constexpr bool kAhead = F == GRIM_FMT_MXFP4;
     for (; kt + 2 <= nk; kt += 2) {
         GRIM_MMA_TILE(0, RB0);
         GRIM_FOLD(RB0, kt);
-        if (kt + 2 < nk) GRIM_LOAD_B(RB0, (kt + 2) * BK);
+        if (kAhead || kt + 2 < nk) GRIM_LOAD_B(RB0, min(kt + 2, nk - 1) * BK);
         GRIM_STORE_A(RA1, 1);
-        if (kt + 3 < nk) GRIM_LOAD_A(RA1, (kt + 3) * BK);
+        if (kAhead || kt + 3 < nk) GRIM_LOAD_A(RA1, min(kt + 3, nk - 1) * BK);
         lds_barrier();
         GRIM_MMA_TILE(1, RB1);
         GRIM_FOLD(RB1, kt + 1);
-        if (kt + 3 < nk) GRIM_LOAD_B(RB1, (kt + 3) * BK);
-        if (kt + 2 < nk) {
-            GRIM_STORE_A(RA0, 0);
-            if (kt + 4 < nk) GRIM_LOAD_A(RA0, (kt + 4) * BK);
-        }
+        if (kAhead || kt + 3 < nk) GRIM_LOAD_B(RB1, min(kt + 3, nk - 1) * BK);
+        if (kt + 2 < nk) GRIM_STORE_A(RA0, 0);
+        if (kAhead || kt + 4 < nk) GRIM_LOAD_A(RA0, min(kt + 4, nk - 1) * BK);
         lds_barrier();
     }
     if (kt < nk) {

@@ -394,10 +394,12 @@ __global__ __launch_bounds__(256) void router_bf16x3(const float* __restrict__ W
         for (int u = 0; u < kR3Pre; ++u) {
             const int kt = k0 + u, buf = kt & 1;
             // tile kt's set is free once it is in LDS: request tile kt + kR3Pre
-            if (kt + kR3Pre < nk) {
-                rt_load<64>(x, T, H, t0, (kt + kR3Pre) * kR3BK, rx[u]);
-                rt_load<64>(W, E, H, e0, (kt + kR3Pre) * kR3BK, rw[u]);
-            }
+            // (past the last tile the last again, never stored: loads under a
+            // branch would make the compiler wait for every load in flight,
+            // the ones just issued included, before each LDS store)
+            const int kn = min(kt + kR3Pre, nk - 1) * kR3BK;
+            rt_load<64>(x, T, H, t0, kn, rx[u]);
+            rt_load<64>(W, E, H, e0, kn, rw[u]);
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 // lane half h supplies K = 16 h + 8 ks .. + 7 (the same for x and W)
