@@ -345,6 +345,25 @@ def _tiered_bench(dev, stream, timed):
                      "gate_up_gbs": round(gu_bytes / (gu_ms * 1e-3) / 1e9, 1),
                      "down_us": round(dn_ms * 1e3, 1),
                      "down_gbs": round(dn_bytes / (dn_ms * 1e-3) / 1e9, 1)}
+    # the host pool on the same token with the blocks in host memory: the
+    # whole FFN (gate_up + SwiGLU + down + weighted sum) on the host cores
+    # (each call routes to the next 8 of the 128 blocks, 340 MB in all, so
+    # the blocks come from DRAM, not from the last-level cache)
+    hb = [b.cpu() for b in blocks]
+    wh, xh, yh = w[0].cpu().contiguous(), x[0].cpu().contiguous(), torch.empty(H)
+    threads = min(16, len(os.sched_getaffinity(0)))
+    cx = tiered.CpuExperts(threads)
+    sels = [[hb[(8 * c + j) % E] for j in range(K)] for c in range(E // K)]
+    for c in range(E // K):
+        cx.ffn(lay, sels[c], wh, xh, yh)
+    n, t0 = 0, time.perf_counter()
+    while n < 400 and time.perf_counter() - t0 < 2.0:
+        cx.ffn(lay, sels[n % len(sels)], wh, xh, yh)
+        n += 1
+    ffn_us = (time.perf_counter() - t0) / n * 1e6
+    out["cpu_pool"] = {"threads": threads, "ffn_us": round(ffn_us, 1),
+                       "gbs": round((gu_bytes + dn_bytes) / (ffn_us * 1e-6) / 1e9, 1),
+                       "note": "grimoire_cpu_experts_ffn, blocks in host memory (rotating over all 128), host threads"}
     return out
 
 

@@ -167,6 +167,15 @@ SIGNATURES = {
                                         P, SZ]),
     "grimoire_tmoe_expert_ffn": (I32, [P, P, C.POINTER(NvExpertLayout), F32, F32, F32, P, P, P,
                                        I32, P, SZ]),
+    "grimoire_cpu_experts_create": (P, [I32, P, I32]),
+    "grimoire_cpu_experts_destroy": (None, [P]),
+    "grimoire_cpu_experts_threads": (I32, [P]),
+    "grimoire_cpu_experts_wait_us": (C.c_double, [P]),
+    "grimoire_cpu_experts_ffn": (I32, [P, C.POINTER(NvExpertLayout), P, P, I32, P, P]),
+    "grimoire_cpu_experts_ffn_rows": (I32, [P, C.POINTER(NvExpertLayout), I32, P, P, P, P, P]),
+    "grimoire_cpu_nvfp4_dot": (F32, [P, P, P, I32]),
+    "grimoire_cpu_set_isa": (I32, [I32]),
+    "grimoire_cpu_pool_cpus": (I32, [I32, I32, P, I32]),
     "grimoire_heat_default_params": (None, [C.POINTER(HeatParams)]),
     "grimoire_heat_create": (P, [I32, I32, C.POINTER(HeatParams)]),
     "grimoire_heat_destroy": (None, [P]),

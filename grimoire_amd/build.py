@@ -22,6 +22,11 @@ OBJ = PKG / "_build"
 SOURCES = ["router.hip", "gemv.hip", "gemv_f0.hip", "gemv_f3.hip", "gemv_f4.hip", "gemv_f6.hip",
            "gemv_f64.hip", "dispatch.hip", "gemm.hip", "gemm_i8.hip", "ingest.hip",
            "tiered.hip", "elementwise.hip", "gemv_grouped.hip", "gemv_mx.hip", "api.cpp", "forward.cpp", "heat.cpp"]
+# host-only sources (x86 intrinsics, threads): the C++ compiler, not hipcc
+HOST_SOURCES = ["cpu_experts.cc"]
+CXX = os.environ.get("CXX", "g++")
+HOST_FLAGS = ["-O3", "-std=c++20", "-fPIC", "-fvisibility=hidden", "-ffp-contract=off", "-pthread",
+              "-Wall", "-I" + str(PKG.parent / "include")]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -48,14 +53,25 @@ def _compile(src: str) -> Path:
     return obj
 
 
+def _compile_host(src: str) -> Path:
+    obj = OBJ / (Path(src).stem + ".o")
+    cmd = [CXX, *HOST_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"{CXX} failed for {src}:\n{r.stderr}")
+    if r.stderr.strip():
+        print(r.stderr, file=sys.stderr)
+    return obj
+
+
 def build(verbose: bool = True) -> Path:
     """Compile every source and link the shared library; returns its path."""
     OBJ.mkdir(exist_ok=True)
     jobs = min(len(SOURCES), int(os.environ.get("MAX_JOBS", "8")))
     with cf.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+        objs = list(ex.map(_compile, SOURCES)) + list(ex.map(_compile_host, HOST_SOURCES))
     tmp = OUT.with_suffix(".so.tmp")
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-pthread", "-o", str(tmp), *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stderr)

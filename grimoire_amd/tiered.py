@@ -87,6 +87,85 @@ def expert_ffn(block, L, sg, su, sd, A, hbuf, out, scratch=None, stream=None):
                                          _p(scratch), scratch.numel()), "tmoe_expert_ffn")
 
 
+def _host(t: torch.Tensor, dtype) -> torch.Tensor:
+    if t.device.type != "cpu" or t.dtype != dtype or not t.is_contiguous():
+        raise ValueError(f"expected a contiguous host {dtype} tensor")
+    return t
+
+
+class CpuExperts:
+    """The host expert pool (include/b70/cpu_experts.hpp): NVFP4 blocks in
+    host memory computed by `threads` host threads (the caller is worker 0).
+    `cpus[t]` pins pool thread t (t >= 1)."""
+
+    def __init__(self, threads: int = 0, cpus: Optional[Sequence[int]] = None):
+        c = None if cpus is None else torch.tensor(list(cpus), dtype=torch.int32)
+        self._cpus = c
+        self._h = lib().grimoire_cpu_experts_create(threads, None if c is None else c.data_ptr(),
+                                                    0 if c is None else c.numel())
+        if not self._h:
+            raise _abi.GrimoireError("grimoire_cpu_experts_create failed")
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            lib().grimoire_cpu_experts_destroy(h)
+            self._h = None
+
+    @property
+    def threads(self) -> int:
+        return int(lib().grimoire_cpu_experts_threads(self._h))
+
+    @property
+    def wait_us(self) -> float:
+        return float(lib().grimoire_cpu_experts_wait_us(self._h))
+
+    @staticmethod
+    def _ptrs(blocks: Sequence[torch.Tensor]):
+        arr = (C.c_void_p * max(1, len(blocks)))(*[_host(b, torch.uint8).data_ptr() for b in blocks])
+        return arr
+
+    def ffn(self, L: _abi.NvExpertLayout, blocks: Sequence[torch.Tensor], w: torch.Tensor,
+            x: torch.Tensor, y: torch.Tensor) -> None:
+        """y[H] = sum_j w[j] s_d down_j(silu(s_g gate_j x) * s_u up_j x) (CpuExperts::ffn)."""
+        ptrs = self._ptrs(blocks)
+        w = _host(w, torch.float32)
+        check(lib().grimoire_cpu_experts_ffn(self._h, C.byref(L), C.cast(ptrs, C.c_void_p),
+                                             w.data_ptr(), len(blocks), _host(x, torch.float32).data_ptr(),
+                                             _host(y, torch.float32).data_ptr()), "cpu_experts_ffn")
+
+    def ffn_rows(self, L: _abi.NvExpertLayout, blocks: Sequence[torch.Tensor], w: torch.Tensor,
+                 off: torch.Tensor, x: torch.Tensor, y: torch.Tensor) -> None:
+        """ffn for each row r over blocks[off[r]:off[r+1]] (CpuExperts::ffn_rows)."""
+        ptrs = self._ptrs(blocks)
+        off = _host(off, torch.int32)
+        check(lib().grimoire_cpu_experts_ffn_rows(self._h, C.byref(L), off.numel() - 1,
+                                                  C.cast(ptrs, C.c_void_p), _host(w, torch.float32).data_ptr(),
+                                                  off.data_ptr(), _host(x, torch.float32).data_ptr(),
+                                                  _host(y, torch.float32).data_ptr()), "cpu_experts_ffn_rows")
+
+
+def cpu_nvfp4_dot(pay: torch.Tensor, scl: torch.Tensor, x: torch.Tensor) -> float:
+    """One NVFP4 row dotted with x on the host (cpu_nvfp4_dot)."""
+    return float(lib().grimoire_cpu_nvfp4_dot(_host(pay, torch.uint8).data_ptr(),
+                                              _host(scl, torch.uint8).data_ptr(),
+                                              _host(x, torch.float32).data_ptr(), x.numel()))
+
+
+def cpu_set_isa(isa: int) -> None:
+    """Host dot product path: 0 scalar, 1 AVX2, 2 AVX-512, -1 the best."""
+    check(lib().grimoire_cpu_set_isa(isa), "cpu_set_isa")
+
+
+def cpu_pool_cpus(ranks: int, rank: int) -> List[int]:
+    """Rank's contiguous share of this process's CPUs."""
+    out = torch.empty(1024, dtype=torch.int32)
+    n = lib().grimoire_cpu_pool_cpus(ranks, rank, out.data_ptr(), out.numel())
+    if n < 0:
+        raise _abi.GrimoireError("grimoire_cpu_pool_cpus failed")
+    return out[:min(n, 1024)].tolist()
+
+
 class Heat:
     """grim_heat: decayed routing counts per (layer, expert) and swap proposals."""
 

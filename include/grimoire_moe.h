@@ -444,6 +444,51 @@ int grimoire_tmoe_expert_ffn(void* stream, const uint8_t* block, const grim_nv_e
                              float sg, float su, float sd, const uint16_t* A, uint16_t* hbuf,
                              float* out, int M, void* scratch, size_t scratch_bytes);
 
+/* ------------------------------------------------------------------------
+ * Host expert pool (include/b70/cpu_experts.hpp, src/cpu_experts.cpp):
+ * NVFP4 expert blocks in host memory computed by host threads while the
+ * GPU runs the resident ones; the caller adds the two partial sums.  Plain
+ * fp32 on the exact dequantised weights; results do not depend on the
+ * thread count.  A pool is used by one calling thread at a time.
+ * ---------------------------------------------------------------------- */
+typedef struct grim_cpu_experts grim_cpu_experts;
+
+/* CpuExperts::start (cpu_experts.hpp:49-52): threads <= 0 = the hardware
+ * threads - 1; the calling thread is worker 0.  cpus[t] (t >= 1, t <
+ * ncpus) pins pool thread t; NULL = not pinned.  NULL on failure. */
+grim_cpu_experts* grimoire_cpu_experts_create(int threads, const int32_t* cpus, int ncpus);
+/* CpuExperts::stop / ~CpuExperts */
+void grimoire_cpu_experts_destroy(grim_cpu_experts* p);
+/* CpuExperts::threads, CpuExperts::wait_us (microseconds the caller spent
+ * waiting for workers after its own share, summed over calls) */
+int grimoire_cpu_experts_threads(const grim_cpu_experts* p);
+double grimoire_cpu_experts_wait_us(const grim_cpu_experts* p);
+/* CpuExperts::ffn (cpu_experts.hpp:58-61): y[H] = sum over j < n in order
+ * of (w[j] s_down_j) down_j(silu(s_gate_j gate_j x) * (s_up_j up_j x)),
+ * blocks[j] host pointers (layout grim_nv_expert_layout).  Overwrites y;
+ * n = 0 gives zeros. */
+int grimoire_cpu_experts_ffn(grim_cpu_experts* p, const grim_nv_expert_layout* L,
+                             const uint8_t* const* blocks, const float* w, int n, const float* x,
+                             float* y);
+/* CpuExperts::ffn_rows (cpu_experts.hpp:62-66): row r's experts are
+ * blocks[off[r] .. off[r + 1]) with weights w[same], input x + r H, output
+ * y + r H; each row bit-identical to grimoire_cpu_experts_ffn on it, and a
+ * block several rows route to is read once.  off[0] = 0, rows + 1 entries. */
+int grimoire_cpu_experts_ffn_rows(grim_cpu_experts* p, const grim_nv_expert_layout* L, int rows,
+                                  const uint8_t* const* blocks, const float* w, const int32_t* off,
+                                  const float* x, float* y);
+/* cpu_nvfp4_dot (cpu_experts.hpp:90): one NVFP4 row of K elements (K % 64
+ * == 0; else NaN) dotted with x. */
+float grimoire_cpu_nvfp4_dot(const uint8_t* pay, const uint8_t* scl, const float* x, int K);
+/* Instruction set of the host dot product: 0 scalar, 1 AVX2, 2 AVX-512, -1
+ * the best this CPU has (the default).  All give the same bits; for tests.
+ * GRIM_ERR_ARG if the CPU lacks it.  No reference counterpart. */
+int grimoire_cpu_set_isa(int isa);
+/* hybrid_pool_cpus (cpu_experts.hpp:93-97), for a CPU that is not hybrid:
+ * rank's contiguous share of the CPUs this process may run on, written to
+ * out (at most cap); returns how many are in the share. */
+int grimoire_cpu_pool_cpus(int ranks, int rank, int32_t* out, int cap);
+
 /* Expert heat and tier placement (include/b70/expert_heat.hpp). */
 typedef struct grim_heat_params {
     float decay;               /* per call of a layer, 0.95              */
