@@ -493,8 +493,9 @@ def c3_bench(dev, stream, n_layers=4, reps=10, regime=0):
 
 def c5_bench(dev, stream, reps=5):
     """C5 (T=32, H=7168, 256 routed + 1 shared expert, I=2048, MXFP4,
-    group-limited sigmoid top-8, scaling 2.5): the whole layer forward
-    (grouped-GEMM regime: bf16 MFMA on MXFP4 weights decoded in registers)."""
+    group-limited sigmoid top-8, scaling 2.5): the whole layer forward as
+    the forward picks it (the matrix-core expert-grouped GEMV), launched
+    eagerly (a captured graph of it replays slower: 788 vs 763 us)."""
     cfg = configs.CONFIGS["c5"]
     L = configs.make_layer(cfg, dev, seed=500)
     bias = configs.make_route_bias(cfg, dev, seed=5)
