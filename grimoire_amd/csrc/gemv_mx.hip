@@ -190,13 +190,14 @@ hipError_t gvm_format_launch(hipStream_t st, const float* src0, int rows0, uint8
 // scan forms the offsets and the (expert, group of kGvMT rows) table, and
 // each route's row is its expert's offset plus the number of earlier
 // routes of that expert -- the dispatch's stable order
-// (src/grimoire.cpp:23162-23170).  (The top-k itself stays a launch of its
-// own: in one work-group the tokens' top-k would share one CU.)  The x rows are
+// (src/grimoire.cpp:23162-23170).  Up to 16 tokens the top-k runs in
+// work-group 0 first, one wave per token; more tokens take a launch of their
+// own (all their top-k in one work-group would share one CU).  The x rows are
 // formatted as limbs by the same code as gvm_format_kernel, one block of
 // 32 elements per thread of the launch's other work-groups.
 constexpr int kGvmRouteThreads = 1024;
 
-__global__ __launch_bounds__(kGvmRouteThreads) void gvm_route_kernel(TopkArgs tk, GvmRouteArgs ra) {
+__global__ __launch_bounds__(kGvmRouteThreads) void gvm_route_kernel(TopkArgs tk, GvmRouteArgs ra, int fused_topk) {
     if (blockIdx.x > 0) {
         // work-groups 1..: the x rows in the limb format, in parallel with
         // the routing in work-group 0
@@ -211,6 +212,19 @@ __global__ __launch_bounds__(kGvmRouteThreads) void gvm_route_kernel(TopkArgs tk
     __shared__ int32_t cnt[kGvmRouteThreads], sc[kGvmRouteThreads], sg[kGvmRouteThreads];
     const int tid = threadIdx.x;
     const int T = tk.T, E = tk.E, K = tk.K, R = T * K;
+    if (fused_topk) {
+        // T <= 16: wave t selects token t's experts (topk_kernel's code,
+        // so the same bits); the picks are read back below after the
+        // barrier (one work-group: its waves share the CU's cache)
+        __shared__ float gsel[kGvmRouteThreads / kWave][512];
+        __shared__ float gscore[kGvmRouteThreads / kWave][64];
+        const int wv = tid / kWave;
+        if (wv < T)
+            topk_wave(tk.logits + int64_t(wv) * E, E, K, tk.mode, tk.normalize, tk.scaling, tk.bias16, tk.bias32,
+                      tk.n_group, tk.topk_group, tk.out_e + int64_t(wv) * K, tk.out_w + int64_t(wv) * K, gsel[wv],
+                      gscore[wv]);
+        __syncthreads();
+    }
     cnt[tid] = 0;
     if (tid < R) ids[tid] = tk.out_e[tid];
     __syncthreads();
@@ -272,12 +286,16 @@ __global__ __launch_bounds__(kGvmRouteThreads) void gvm_route_kernel(TopkArgs tk
 }
 
 hipError_t gvm_route_launch(hipStream_t st, const TopkArgs& tk, const GvmRouteArgs& ra) {
-    hipError_t e = topk_launch(st, tk);
-    if (e != hipSuccess) return e;
     if (int64_t(tk.T) * tk.K > kGvmRouteMax || tk.E > 512 || tk.E <= 0) return hipErrorInvalidValue;
+    // up to one token per wave of work-group 0: the top-k in this launch
+    const int fused = tk.T <= kGvmRouteThreads / kWave;
+    if (!fused) {
+        hipError_t e = topk_launch(st, tk);
+        if (e != hipSuccess) return e;
+    }
     const int64_t blocks = int64_t(tk.T) * (gvm_kpad(ra.H) / 32);
     const int fmt_groups = int((blocks + kGvmRouteThreads - 1) / kGvmRouteThreads);
-    hipLaunchKernelGGL(gvm_route_kernel, dim3(1 + fmt_groups), dim3(kGvmRouteThreads), 0, st, tk, ra);
+    hipLaunchKernelGGL(gvm_route_kernel, dim3(1 + fmt_groups), dim3(kGvmRouteThreads), 0, st, tk, ra, fused);
     return hipGetLastError();
 }
 
