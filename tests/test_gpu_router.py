@@ -20,10 +20,15 @@ def _ties(T, E, seed, scale=2.0):
     return l.contiguous()
 
 
-# T > 32 takes the three-limb bf16 MFMA kernel when H % 128 == 0 (33, 300),
-# the fp32 MFMA kernel when H % 32 == 0 (2080), else the tiled fp32 kernel (100)
+# T <= 32 takes the register-resident row kernel for H <= 8192 (2 or 4
+# experts x 4 tokens per work-group: ragged expert and token blocks, rows
+# not a multiple of 1024, one expert), the one-row kernel above (9000);
+# T > 32 the three-limb bf16 MFMA kernel when H % 128 == 0 (33, 300), the
+# fp32 MFMA kernel when H % 32 == 0 (2080), else the tiled fp32 kernel (100)
 @pytest.mark.parametrize("T,E,H", [(1, 128, 2048), (7, 64, 2048), (32, 256, 7168), (33, 512, 2048),
-                                   (300, 96, 512), (70, 64, 2080), (40, 32, 100)])
+                                   (300, 96, 512), (70, 64, 2080), (40, 32, 100),
+                                   (5, 37, 1028), (13, 3, 64), (32, 130, 8192), (2, 1, 4100),
+                                   (4, 9, 9000)])
 def test_router_logits(gpu, T, E, H):
     print(f"router_logits T={T} E={E} H={H}", flush=True)
     g = torch.Generator().manual_seed(T + E)
