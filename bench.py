@@ -534,9 +534,10 @@ def main():
                     help="also run a 64 MiB device copy 5 times (HBM counter calibration)")
     ap.add_argument("--only", choices=("c3", "c4", "c5", "edges"),
                     help="run only this workload's section and print it alone (for profiling runs)")
-    ap.add_argument("--decode-regime", type=int, default=1, choices=(1, 3),
+    ap.add_argument("--decode-regime", type=int, default=1, choices=(1, 3, 7),
                     help="1: router logits, gate_up (with the top-k), down; "
-                         "3: router logits, top-k, gate_up, down as four launches")
+                         "3: router logits, top-k, gate_up, down as four launches; "
+                         "7: the whole layer in one launch")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "

@@ -61,12 +61,15 @@ bool prefer_grouped_mx(const grim_moe_layer* L, int T) {
 }
 
 bool use_gemv(const grim_moe_layer* L, int T, int regime) {
-    if (regime == 1 || regime == 3) return true;
+    if (regime == 1 || regime == 3 || regime == 7) return true;
     if (regime == 2 || regime == 4 || regime == 5) return false;
     return int64_t(T) * L->cfg.top_k <= 64 && !prefer_grouped_mx(L, T);
 }
 
+static_assert(kSyncBytes == GRIM_SYNC_BYTES, "sync words of the header");
+
 struct Plan {
+    uint32_t* sync;   // fused decode: epoch-tagged words, zero before first use
     float* logits;
     int32_t* rex;
     float* rwt;
@@ -75,6 +78,7 @@ struct Plan {
     float* h;
     uint32_t* hf;   // decode: h in the staged layout
     uint32_t* xf;   // decode: x formatted for the wave-centric gate_up
+    float* hrep;    // fused decode: copies of h
     // GEMM
     void* disp_ws;
     int32_t *counts, *offsets, *inverse, *tile_e, *tile_mb;
@@ -112,6 +116,9 @@ size_t carve(const grim_moe_layer* L, int T, bool gemv, char* base, Plan& p) {
     const int64_t R = int64_t(T) * K;
     const bool sh = L->has_shared;
     Carve cv{base};
+    // every plan keeps the fused decode's sync words at the head, so no
+    // other regime's data ever lands on them
+    p.sync = cv.take<uint32_t>(kSyncBytes / 4);
     p.logits = cv.take<float>(size_t(T) * E);
     p.rex = cv.take<int32_t>(R);
     p.rwt = cv.take<float>(R);
@@ -120,6 +127,7 @@ size_t carve(const grim_moe_layer* L, int T, bool gemv, char* base, Plan& p) {
         p.h = cv.take<float>(size_t(T) * (K + (sh ? 1 : 0)) * I);
         p.hf = cv.take<uint32_t>(size_t(T) * fmt_words((K + (sh ? 1 : 0)) * I));
         p.xf = cv.take<uint32_t>(size_t(T) * xf_words(H));
+        p.hrep = T == 1 ? cv.take<float>(size_t(kSyncCopies) * fused_h_stride(K, I)) : nullptr;
     } else {
         const size_t dws = dispatch_workspace_bytes(T, K, E);
         p.disp_ws = cv.take<char>(dws);
@@ -400,8 +408,11 @@ extern "C" int grimoire_moe_forward(void* stream, const grim_moe_layer* L,
 // on each device), addressed through the pointer hipGetSymbolAddress gives
 // for that device: the array's name is a host-side stand-in and is never
 // passed to a kernel.  Every call on a GPU shares that GPU's array and
-// finds the previous call's contents in it; the forward writes every word
-// it reads, so nothing is cleared.  Calls that overlap on one GPU race.
+// finds the previous call's contents in it.  The forward writes every word
+// it reads except the fused decode's sync words at the head of the
+// workspace, which start zero (the array is zero-initialised storage) and
+// which every call leaves consistent, so nothing is cleared.  Calls that
+// overlap on one GPU race.
 constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
@@ -559,6 +570,15 @@ static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_
             }
         }
         decode_plan(L->gate_up.fmt, a, roles);
+        // one token through all three roles: the one-launch kernel
+        a.sync = p.sync;
+        a.hrep = p.hrep;
+        if (roles == (kRoleRouter | kRoleGateUp | kRoleDown) && regime == 7 &&
+            decode_plan_fused(L->gate_up.fmt, a)) {
+            hipError_t e = decode_launch(st, L->gate_up.fmt, a);
+            if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+            return GRIM_OK;
+        }
         if (decode_lds_bytes(L->gate_up.fmt, a) > 160 * 1024)
             return ferr(GRIM_ERR_SHAPE, "layer too large for the decode kernels");
         hipError_t e = decode_launch(st, L->gate_up.fmt, a);

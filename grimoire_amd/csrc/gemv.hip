@@ -85,6 +85,37 @@ void decode_plan(int fmt, DecodeArgs& a, int roles) {
     a.ND = (roles & kRoleDown) ? a.M * ((a.H + a.dn_rb - 1) / a.dn_rb) : 0;
 }
 
+bool decode_plan_fused(int fmt, DecodeArgs& a) {
+    a.fused = 0;
+    const bool wave_fmt = fmt == GRIM_FMT_INT4 || fmt == GRIM_FMT_INT4_F16 || fmt == GRIM_FMT_MXFP4;
+    if (!wave_fmt || a.M != 1 || a.shared || !a.sync || a.K > 8 || a.K < 1 || a.E > 512 ||
+        a.H % 32 || a.H > 2048 || a.I % 32 || a.I > 1024 || a.H < 32 || a.I < 32 || a.K * a.I > 8192)
+        return false;
+    // at most one 512-thread work-group per CU, so every work-group is
+    // resident while others poll for its results
+    constexpr int kMaxGrid = kSyncMaxGrid;
+    auto gu_groups = [&](int ru) { return (a.K * (a.I / ru) + 7) / 8; };
+    int ru = 0;
+    for (int r : {2, 3, 4})
+        if (a.I % r == 0 && gu_groups(r) <= kMaxGrid) { ru = r; break; }
+    if (!ru) return false;
+    const int gg = gu_groups(ru);
+    int rh = 0, G = 0;
+    for (int r : {2, 4}) {
+        const int nb = (a.H + 2 * r - 1) / (2 * r);
+        const int g = std::max(gg, nb);
+        if (g <= kMaxGrid && (!rh || g < G)) { rh = r; G = g; }
+        if (rh && nb <= gg) break;
+    }
+    if (!rh) return false;
+    if (a.E > kSyncMaxE || !a.hrep) return false;
+    a.fz_ru = ru;
+    a.fz_rh = rh;
+    a.fz_G = G;
+    a.fused = 1;
+    return true;
+}
+
 size_t decode_lds_bytes(int fmt, const DecodeArgs& a) {
     const int CH = chunk_elems(fmt);
     const int KS = a.K + (a.shared ? 1 : 0);

@@ -44,7 +44,29 @@ struct DecodeArgs {
     int xf_words;
     int dn_wave;              // wave-centric down (one wave per slot)
     int gu_ru;                // wave-centric gate_up: row pairs per wave
+    // one-launch decode (gemv_fused.hpp): one token, no shared expert
+    int fused;                // launch the fused kernel instead of the roles
+    uint32_t* sync;           // kSyncBytes of epoch-tagged words, zero before first use
+    float* hrep;              // kSyncCopies copies of h, fused_h_stride(K, I) floats apart
+    int fz_G, fz_ru, fz_rh;   // grid, row pairs per wave, rows per half-wave
 };
+
+// Sync words at the head of every forward workspace (32-bit word offsets):
+// [0] the epoch word, [1] the error word; from kSyncFlagOff, kSyncCopies
+// copies of the per-work-group flags (kSyncFlagStride words apart); from
+// kSyncRtagOff, kSyncCopies copies of the 64-bit router rows
+// (kSyncRtagStride 64-bit words apart).  Work-group b reads copy
+// b % kSyncCopies, so no memory channel serves every work-group's polls.
+constexpr int kSyncCopies = 32;
+constexpr int kSyncMaxGrid = 256;
+constexpr int kSyncMaxE = 512;
+constexpr int kSyncFlagStride = kSyncMaxGrid + 64;
+constexpr int kSyncRtagStride = kSyncMaxE + 32;
+constexpr size_t kSyncFlagOff = 64;
+constexpr size_t kSyncRtagOff = kSyncFlagOff + size_t(kSyncCopies) * kSyncFlagStride;
+constexpr size_t kSyncBytes = (kSyncRtagOff + size_t(kSyncCopies) * kSyncRtagStride * 2) * 4;
+// h copies of the fused decode: kSyncCopies rows of K * I fp32 padded to this
+__host__ __device__ constexpr int fused_h_stride(int K, int I) { return ((K * I + 63) & ~63) + 64; }
 
 // Words per token of the formatted h (n = KS * I elements):
 // the staged planes, one fp32 sum per group of eight, padded to 16 bytes.
@@ -59,6 +81,9 @@ constexpr int kRoleRouter = 1, kRoleGateUp = 2, kRoleDown = 4;
 
 
 void decode_plan(int fmt, DecodeArgs& a, int roles);
+// Plans the fused kernel (sets fused and the fz_* fields) when the shape
+// fits it; returns whether it does.
+bool decode_plan_fused(int fmt, DecodeArgs& a);
 size_t decode_lds_bytes(int fmt, const DecodeArgs& a);
 hipError_t decode_launch(hipStream_t st, int fmt, const DecodeArgs& a);
 int chunk_elems(int fmt);

@@ -928,8 +928,29 @@ inline hipError_t pick_lpg(hipStream_t st, const DecodeArgs& a) {
     return hipErrorInvalidValue;
 }
 
+}  // namespace grim
+#include "gemv_fused.hpp"
+namespace grim {
+
+template <int F>
+inline hipError_t fused_launch(hipStream_t st, const DecodeArgs& a) {
+    if constexpr (kWaveGateUp<F>) {
+        const dim3 g(a.fz_G), blk(kFzThreads);
+        if (a.fz_ru == 3 && a.fz_rh == 4) hipLaunchKernelGGL((moe_decode_fused_kernel<F, 3, 4>), g, blk, 0, st, a);
+        else if (a.fz_ru == 2 && a.fz_rh == 4) hipLaunchKernelGGL((moe_decode_fused_kernel<F, 2, 4>), g, blk, 0, st, a);
+        else if (a.fz_ru == 4 && a.fz_rh == 4) hipLaunchKernelGGL((moe_decode_fused_kernel<F, 4, 4>), g, blk, 0, st, a);
+        else if (a.fz_ru == 2 && a.fz_rh == 2) hipLaunchKernelGGL((moe_decode_fused_kernel<F, 2, 2>), g, blk, 0, st, a);
+        else if (a.fz_ru == 3 && a.fz_rh == 2) hipLaunchKernelGGL((moe_decode_fused_kernel<F, 3, 2>), g, blk, 0, st, a);
+        else if (a.fz_ru == 4 && a.fz_rh == 2) hipLaunchKernelGGL((moe_decode_fused_kernel<F, 4, 2>), g, blk, 0, st, a);
+        else return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
+}
+
 #define GRIM_DECODE_INSTANTIATE(F)                                               \
     hipError_t decode_launch_fmt_##F(hipStream_t st, const DecodeArgs& a) {   \
+        if (a.fused) return fused_launch<F>(st, a);                             \
         return a.shared ? pick_lpg<F, true>(st, a) : pick_lpg<F, false>(st, a); \
     }
 

@@ -281,7 +281,8 @@ class MoeForward:
         self.route = route
         self.regime = regime
         nbytes = int(lib().grimoire_moe_forward_workspace_bytes(self.struct, max_tokens))
-        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=L.router.device)
+        # zeroed once: its head holds the one-launch decode's sync words
+        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=L.router.device)
         self.max_tokens = max_tokens
 
     def __call__(self, x, y, out_expert=None, out_weight=None, stream=None):

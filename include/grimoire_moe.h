@@ -652,8 +652,13 @@ typedef struct grim_route_params {
                                   selection bias; or NULL */
 } grim_route_params;
 
-/* Workspace bytes for grimoire_moe_forward at `tokens` (no initial contents
- * required); calls that share one workspace must not overlap. */
+/* Workspace bytes for grimoire_moe_forward at `tokens`.  Its first
+ * GRIM_SYNC_BYTES hold the one-launch decode's epoch-tagged sync words and
+ * must be zero before the workspace's first use (hipMemset once after
+ * allocating it); every call leaves them consistent, so they are never
+ * cleared again.  The rest needs no initial contents.  Calls that share
+ * one workspace must not overlap. */
+#define GRIM_SYNC_BYTES 180480
 size_t grimoire_moe_forward_workspace_bytes(const grim_moe_layer* L, int tokens);
 
 /* y fp32 [T][H] = MoE(x fp32 [T][H]).  shared_gate_w bf16 [H] (may be NULL:
@@ -663,7 +668,11 @@ size_t grimoire_moe_forward_workspace_bytes(const grim_moe_layer* L, int tokens)
  * 16 <= T*K <= 2E whose shapes it takes; else slot GEMV for T*K <= 64;
  * else the expert-grouped GEMV for T*K <= 2E on INT4 / MXFP4 experts;
  * else the grouped MFMA GEMM), 1 = GEMV,
- * 2 = grouped GEMM, 3 = GEMV with one launch per stage, 4 = expert-grouped
+ * 2 = grouped GEMM, 3 = GEMV with one launch per stage, 7 = GEMV in one
+ * launch for one token with no shared expert (INT4 / MXFP4 experts,
+ * K <= 8, H <= 2048, I <= 1024, K * I <= 8192: router, top-k, gate_up and
+ * down in one kernel whose work-groups exchange epoch-tagged words; other
+ * shapes take regime 1), 4 = expert-grouped
  * GEMV (MXFP4 with hidden and inter multiples of 64 above 256: on the
  * scaled fp4 matrix core, K padded to 256; otherwise on the vector ALU), 5 = expert-grouped GEMV on
  * the vector ALU.  No reference counterpart for 3-5 (regimes of this
