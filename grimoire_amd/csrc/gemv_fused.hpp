@@ -165,6 +165,7 @@ __global__ __launch_bounds__(kFzThreads) void moe_decode_fused_kernel(DecodeArgs
     __shared__ float sel_w[16];
     __shared__ float tk_scratch[512 + 64];
     __shared__ RankLds rl;
+    __shared__ __align__(16) float hs[kFzWaves * 4];   // this work-group's h values
     __shared__ float part[8][2 * RH];
     __shared__ uint32_t fl[kFzChunks * 36];   // formatted x, later h (format_to_lds)
 
@@ -335,12 +336,30 @@ __global__ __launch_bounds__(kFzThreads) void moe_decode_fused_kernel(DecodeArgs
         for (int r = 0; r < RU; ++r) {
             const float g = wave_sum(ga[r]);
             const float up = wave_sum(ua[r]);
-            if (lane < kSyncCopies)
-                sync_stf(a.hrep + lane * hst + gslot * I + i0 + r, gactive ? fast_silu(g) * up : 0.0f);
+            if (lane == r) hs[wave * RU + r] = gactive ? fast_silu(g) * up : 0.0f;
         }
     }
-    // every wave's h stores complete (and, with them, this wave's weight
-    // loads) before the work-group's flag
+    __syncthreads();
+    // the work-group's units are consecutive, so its h values are one
+    // span [8 RU b, + nv) of the flat h: nv / 4 16-byte write-through
+    // stores per copy (one 4-byte store per value and copy measured
+    // ~3 us slower: ~200 K partial-line writes per layer)
+    {
+        const int v0 = kFzWaves * RU * b;
+        const int nv = min(kFzWaves * RU, K * I - v0);
+        const int n4 = nv > 0 ? nv / 4 : 0;
+        const int t = threadIdx.x;
+        if (t < kSyncCopies * n4) {
+            const int c = t / n4, q = t % n4;
+            const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
+                a.hrep, 0, kSyncCopies * hst * 4, 0x00020000);
+            const float4 v = *reinterpret_cast<const float4*>(hs + 4 * q);
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{f_bits(v.x), f_bits(v.y), f_bits(v.z), f_bits(v.w)},
+                                                   hr, uint32_t(4 * (c * hst + v0 + 4 * q)), 0, 16);
+        }
+    }
+    // every h store complete (and, with them, this wave's weight loads)
+    // before the work-group's flag
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (wave == 0 && lane < kSyncCopies) sync_st(flags + lane * kSyncFlagStride + b, epoch);
@@ -373,6 +392,9 @@ __global__ __launch_bounds__(kFzThreads) void moe_decode_fused_kernel(DecodeArgs
             return make_float4(bits_f(v.x), bits_f(v.y), bits_f(v.z), bits_f(v.w));
         });
     }
+#ifdef GRIM_TIMING
+    if (a.ts && threadIdx.x == 0) a.ts[(2048 + b) * 8 + 3] = __builtin_amdgcn_s_memrealtime();
+#endif
     XChunk<F, true> hx;
     chunk_from_lds<F, true>(fl, (s < K ? s : 0) * CI + ccl, hx);
     float acc[RH];
@@ -396,6 +418,9 @@ __global__ __launch_bounds__(kFzThreads) void moe_decode_fused_kernel(DecodeArgs
         }
     }
     __syncthreads();
+#ifdef GRIM_TIMING
+    if (a.ts && threadIdx.x == 0) a.ts[(2048 + b) * 8 + 4] = __builtin_amdgcn_s_memrealtime();
+#endif
     // (6) slot-order combine
     if (int(threadIdx.x) < RB) {
         const int r = threadIdx.x;
