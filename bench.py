@@ -148,6 +148,30 @@ def decode_bench(steps, warmup, dev, stream, regime=1):
                 one_us=one_us, layers=layers, x=x, oes=oes, ows=ows)
 
 
+def decode_one_launch(d, dev, stream, steps):
+    """The same 48 layers through the one-launch decode (regime 7): µs per
+    layer in one graph, for comparison with the default three launches."""
+    cfg = d["cfg"]
+    fwds = [ops.MoeForward(L, 1, configs.route_params(cfg, None), regime=7) for L in d["layers"]]
+    ys = [torch.empty(1, cfg.H, device=dev) for _ in fwds]
+
+    def step():
+        for f, y in zip(fwds, ys):
+            f(d["x"], y, stream=stream)
+
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.synchronize()
+    g = _graph(step, stream)
+    _replay(g, stream, 3)
+    torch.cuda.synchronize()
+    with Timer(stream) as tm:
+        _replay(g, stream, steps)
+    us = tm.ms() * 1e3 / (steps * LAYERS)
+    return {"kernel": "grim::moe_decode_fused_kernel (router, top-k, gate_up, down in one launch)",
+            "us_per_layer": round(us, 2), "GB/s": round(d["step_bytes"] / LAYERS / (us * 1e-6) / 1e9, 1)}
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
     summary (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel
@@ -591,6 +615,9 @@ def main():
             "bytes_per_launch": int(d["gu_bytes"]),
         },
     }
+    if a.decode_regime == 1:
+        log("one-launch decode (regime 7) on the same layers...")
+        out["c2_one_launch"] = decode_one_launch(d, dev, stream, a.steps)
     if not a.no_prefill:
         log("prefill bench (C4)...")
         out["prefill"] = prefill_bench(dev, stream)

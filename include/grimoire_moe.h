@@ -653,11 +653,12 @@ typedef struct grim_route_params {
 } grim_route_params;
 
 /* Workspace bytes for grimoire_moe_forward at `tokens`.  Its first
- * GRIM_SYNC_BYTES hold the one-launch decode's epoch-tagged sync words and
- * must be zero before the workspace's first use (hipMemset once after
- * allocating it); every call leaves them consistent, so they are never
- * cleared again.  The rest needs no initial contents.  Calls that share
- * one workspace must not overlap. */
+ * GRIM_SYNC_BYTES hold the one-launch decode's (regime 7) epoch-tagged sync
+ * words: they must be zero before the workspace's first regime-7 call
+ * (hipMemset once after allocating it); every call leaves them
+ * consistent and no other regime writes them, so they are never cleared
+ * again.  Otherwise no initial contents are needed.  Calls that share one
+ * workspace must not overlap. */
 #define GRIM_SYNC_BYTES 180480
 size_t grimoire_moe_forward_workspace_bytes(const grim_moe_layer* L, int tokens);
 
