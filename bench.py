@@ -248,6 +248,17 @@ def prefill_bench(dev, stream, reps=5):
     gu_flops, dn_flops = 4.0 * R * cfg.H * cfg.I, 2.0 * R * cfg.H * cfg.I
     ebytes = L.expert_bytes()
     layer_bytes = touched * ebytes + L.shared_bytes() + cfg.E * cfg.H * 4 + 2 * cfg.T * cfg.H * 4
+    # algorithmic bytes of each GEMM: the touched experts' int8 rows with
+    # their bf16 row scales, the two int8 activation limbs per row, the
+    # fp32 output rows; its roofline time is the larger of the FLOP time at
+    # the bf16 peak and the byte time at the HBM peak
+    gu_bytes = touched * 2 * cfg.I * (cfg.H + 2) + R * 2 * cfg.H + R * cfg.I * 4
+    dn_bytes = touched * cfg.H * (cfg.I + 2) + R * 2 * cfg.I + R * cfg.H * 4
+
+    def roof(flops, nbytes, ms):
+        floor_s = max(flops / (BF16_MFMA_PEAK_TFLOPS * 1e12), nbytes / (HBM_PEAK_GBS * 1e9))
+        return round(floor_s / (ms * 1e-3), 4)
+
     return {
         "workload": "c4: T=4096 H=2048 E=512 top-10 softmax (Zipf 1.2) I=512 int8 + shared I=512",
         "layer_us": round(layer_ms * 1e3, 1),
@@ -261,6 +272,17 @@ def prefill_bench(dev, stream, reps=5):
         "gemm_arithmetic": "int8 MFMA on two int8 activation limbs per row (2 passes, the cost of one bf16 pass); FLOP/s algorithmic, against the bf16 dense peak",
         "mfma_peak_tflops": BF16_MFMA_PEAK_TFLOPS,
         "gate_up_mfma_frac": round(gu_flops / (gu_ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4),
+        "down_mfma_frac": round(dn_flops / (dn_ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4),
+        "gate_up_gemm_bytes": int(gu_bytes),
+        "gate_up_gemm_hbm_frac": round(gu_bytes / (gu_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "down_gemm_bytes": int(dn_bytes),
+        "down_gemm_hbm_frac": round(dn_bytes / (dn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "gate_up_roofline_frac": roof(gu_flops, gu_bytes, gu_ms),
+        "down_roofline_frac": roof(dn_flops, dn_bytes, dn_ms),
+        "roofline_note": "every one of the 512 experts is touched under Zipf(1.2) routing, so the GEMMs "
+                         "stream 1.07 GB (gate_up) and 0.54 GB (down) of int8 weights: the roofline "
+                         "time is max(FLOP time at 2.5 PF, byte time at 8 TB/s), and the byte time "
+                         "is the larger one",
     }
 
 
