@@ -332,12 +332,14 @@ __global__ __launch_bounds__(kFzThreads) void moe_decode_fused_kernel(DecodeArgs
 #ifdef GRIM_TIMING
         if (a.ts && threadIdx.x == 0) a.ts[(2048 + b) * 8] = __builtin_amdgcn_s_memrealtime();
 #endif
+        float gu[2 * RU];
 #pragma unroll
-        for (int r = 0; r < RU; ++r) {
-            const float g = wave_sum(ga[r]);
-            const float up = wave_sum(ua[r]);
-            if (lane == r) hs[wave * RU + r] = gactive ? fast_silu(g) * up : 0.0f;
-        }
+        for (int r = 0; r < RU; ++r) { gu[r] = ga[r]; gu[RU + r] = ua[r]; }
+        wave_sum_n(gu);
+        float hv = 0.0f;
+#pragma unroll
+        for (int r = 0; r < RU; ++r) hv = lane == r ? (gactive ? fast_silu(gu[r]) * gu[RU + r] : 0.0f) : hv;
+        if (lane < RU) hs[wave * RU + lane] = hv;
     }
     __syncthreads();
     // the work-group's units are consecutive, so its h values are one
@@ -403,19 +405,16 @@ __global__ __launch_bounds__(kFzThreads) void moe_decode_fused_kernel(DecodeArgs
         const float d = dot_chunk<F, true>(pw[r], hx);
         acc[r] = cl < CI ? d : 0.0f;
     }
+    {
+        float h0[RH], h1[RH];
+        half_sums_n(acc, h0, h1);
+        float pv = 0.0f;
 #pragma unroll
-    for (int r = 0; r < RH; ++r) {
-        float v = acc[r];
-        v += dpp_f<kDppXor1>(v);
-        v += dpp_f<kDppXor2>(v);
-        v += dpp_f<kDppHalfMirror>(v);
-        v += dpp_f<kDppMirror>(v);
-        const float h0 = lane_f(v, 0) + lane_f(v, 16);
-        const float h1 = lane_f(v, 32) + lane_f(v, 48);
-        if (lane == 0) {
-            part[s][r] = dvalid ? h0 : 0.0f;
-            part[s][RH + r] = dvalid ? h1 : 0.0f;
+        for (int r = 0; r < RH; ++r) {
+            pv = lane == r ? h0[r] : pv;
+            pv = lane == RH + r ? h1[r] : pv;
         }
+        if (lane < 2 * RH) part[s][lane] = dvalid ? pv : 0.0f;
     }
     __syncthreads();
 #ifdef GRIM_TIMING

@@ -71,6 +71,43 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 
+// wave_sum of N independent values with the same operations and order per
+// value, step by step across the values: a lone DPP chain waits on each
+// step (the compiler pads it with s_nop), N chains fill each other's gaps.
+template <int N>
+__device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
+#pragma unroll
+    for (int r = 0; r < N; ++r) v[r] += dpp_f<kDppXor1>(v[r]);
+#pragma unroll
+    for (int r = 0; r < N; ++r) v[r] += dpp_f<kDppXor2>(v[r]);
+#pragma unroll
+    for (int r = 0; r < N; ++r) v[r] += dpp_f<kDppHalfMirror>(v[r]);
+#pragma unroll
+    for (int r = 0; r < N; ++r) v[r] += dpp_f<kDppMirror>(v[r]);
+#pragma unroll
+    for (int r = 0; r < N; ++r) v[r] = (lane_f(v[r], 0) + lane_f(v[r], 16)) + (lane_f(v[r], 32) + lane_f(v[r], 48));
+}
+
+// The two half-wave sums of N values (lanes 0-31 and 32-63), interleaved
+// as wave_sum_n: after the four DPP steps h0 = lane 0 + lane 16, h1 =
+// lane 32 + lane 48.
+template <int N>
+__device__ __forceinline__ void half_sums_n(float (&v)[N], float (&h0)[N], float (&h1)[N]) {
+#pragma unroll
+    for (int r = 0; r < N; ++r) v[r] += dpp_f<kDppXor1>(v[r]);
+#pragma unroll
+    for (int r = 0; r < N; ++r) v[r] += dpp_f<kDppXor2>(v[r]);
+#pragma unroll
+    for (int r = 0; r < N; ++r) v[r] += dpp_f<kDppHalfMirror>(v[r]);
+#pragma unroll
+    for (int r = 0; r < N; ++r) v[r] += dpp_f<kDppMirror>(v[r]);
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+        h0[r] = lane_f(v[r], 0) + lane_f(v[r], 16);
+        h1[r] = lane_f(v[r], 32) + lane_f(v[r], 48);
+    }
+}
+
 // One weight chunk requested through buffer descriptors: the payload, and
 // the raw scale / zero the chunk needs (decoded where it is used).
 struct WRsrc {
@@ -282,14 +319,19 @@ __global__ __launch_bounds__(kGemvThreads) void moe_gate_up_wave_kernel(DecodeAr
     // rows as formatted groups of eight (the down kernel's staging layout),
     // one row per lane of wave 0
     __shared__ float hrow[RB];
+    {
+        float gu[2 * RU];
 #pragma unroll
-    for (int r = 0; r < RU; ++r) {
-        const float g = wave_sum(ga[r]);
-        const float u = wave_sum(ua[r]);
-        if (lane == 0) {
-            const int i = i0 + r;
-            hrow[wave * RU + r] = (active && i < I) ? fast_silu(g) * u : 0.0f;
+        for (int r = 0; r < RU; ++r) { gu[r] = ga[r]; gu[RU + r] = ua[r]; }
+        wave_sum_n(gu);
+        // lane r < RU stores row r: a select chain, no branch per row
+        float hv = 0.0f;
+#pragma unroll
+        for (int r = 0; r < RU; ++r) {
+            const float v = (active && i0 + r < I) ? fast_silu(gu[r]) * gu[RU + r] : 0.0f;
+            hv = lane == r ? v : hv;
         }
+        if (lane < RU) hrow[wave * RU + lane] = hv;
     }
     __syncthreads();
     if (wave == 0 && lane < RB) put_rows_fmt<F>(a.hf + int64_t(t) * fmt_words(KS * I), KS * I,
@@ -403,19 +445,17 @@ __global__ __launch_bounds__(512) void moe_down_wave_kernel(DecodeArgs a) {
     }
     __shared__ float part[16][RB];
     __shared__ float slot_w[16];
+    {
+        float h0[RH], h1[RH];
+        half_sums_n(acc, h0, h1);
+        // lane r < 2 RH stores part row r: a select chain
+        float pv = 0.0f;
 #pragma unroll
-    for (int r = 0; r < RH; ++r) {
-        float v = acc[r];
-        v += dpp_f<kDppXor1>(v);
-        v += dpp_f<kDppXor2>(v);
-        v += dpp_f<kDppHalfMirror>(v);
-        v += dpp_f<kDppMirror>(v);
-        const float h0 = lane_f(v, 0) + lane_f(v, 16);
-        const float h1 = lane_f(v, 32) + lane_f(v, 48);
-        if (lane == 0 && s < KS) {
-            part[s][r] = valid ? h0 : 0.0f;
-            part[s][RH + r] = valid ? h1 : 0.0f;
+        for (int r = 0; r < RH; ++r) {
+            pv = lane == r ? h0[r] : pv;
+            pv = lane == RH + r ? h1[r] : pv;
         }
+        if (lane < 2 * RH && s < KS) part[s][lane] = valid ? pv : 0.0f;
     }
     if (lane == 0 && s < K) slot_w[s] = valid ? rw : 0.0f;
     GRIM_TS(a, 2, 3);
