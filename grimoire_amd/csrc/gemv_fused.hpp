@@ -425,13 +425,16 @@ __global__ __launch_bounds__(kFzThreads) void moe_decode_fused_kernel(DecodeArgs
         const int r = threadIdx.x;
         const int o = b * RB + r;
         if (o < H) {
-            float total = 0.0f;
-            for (int q = 0; q < K; ++q) {
-                const float wq = sel_w[q];
-                const int eq = sel_e[q];
-                if (wq == 0.0f || eq < 0 || eq >= E) continue;
-                total = __builtin_fmaf(wq, part[q][r], total);
+            float wv[8], pv[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int eq = q < K ? sel_e[q] : -1;
+                wv[q] = (eq >= 0 && eq < E) ? sel_w[q] : 0.0f;
+                pv[q] = q < K ? part[q][r] : 0.0f;
             }
+            float total = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) total = wv[q] != 0.0f ? __builtin_fmaf(wv[q], pv[q], total) : total;
             a.y[o] = total;
         }
     }

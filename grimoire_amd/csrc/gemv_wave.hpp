@@ -466,12 +466,18 @@ __global__ __launch_bounds__(512) void moe_down_wave_kernel(DecodeArgs a) {
         const int o = ob * RB + r;
         if (o < H) {
             // part rows: half-wave 0 holds rows [0, RH), half 1 [RH, 2RH)
-            float total = 0.0f;
-            for (int q = 0; q < K; ++q) {
-                const float wq = slot_w[q];
-                if (wq == 0.0f) continue;
-                total = __builtin_fmaf(wq, part[q][r], total);
+            // every slot's weight and part read before the fma chain (one
+            // LDS round trip instead of K); slots past K or of weight 0
+            // leave the total as the skipping loop does
+            float wv[8], pv[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                wv[q] = q < K ? slot_w[q] : 0.0f;
+                pv[q] = q < K ? part[q][r] : 0.0f;
             }
+            float total = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) total = wv[q] != 0.0f ? __builtin_fmaf(wv[q], pv[q], total) : total;
             if (SH) {
                 const float g = a.gate_in ? a.gate_in[t] : 1.0f;
                 total = __builtin_fmaf(g, part[K][r], total);
