@@ -1,8 +1,9 @@
 """grimoire_moe_forward_noalloc (the forward without a workspace argument,
 its scratch a fixed device array inside the library) against
 grimoire_moe_forward on the same inputs: outputs and routes bit for bit,
-on two calls in a row, the second with a smaller input, and the host-side
-rejection of a call whose workspace exceeds the array."""
+on two calls in a row, the second with a smaller input, the one-launch
+decode on the array's sync words, and the host-side rejection of a call
+whose workspace exceeds the array."""
 import ctypes as C
 
 import pytest
@@ -50,6 +51,18 @@ def test_noalloc_matches_forward_twice(gpu):
     _both(configs.make_workload(cfg, "cpu", seed=6), gpu, regime=2)
     print("noalloc: c4 scaled, decode T=2", flush=True)
     _both(configs.make_workload(cfg, "cpu", seed=7), gpu, regime=1, T=2)
+
+
+def test_noalloc_one_launch_decode(gpu):
+    """The one-launch decode (regime 7) on the library's array: its sync
+    words start zero (zero-initialised storage) and stay consistent, so
+    repeated calls, a layer of another grid in between, and the same layer
+    again all match grimoire_moe_forward bit for bit."""
+    c2 = configs.make_workload(configs.CONFIGS["c2"], "cpu", seed=8)
+    small = configs.make_workload(configs.Config("s1", 1, 512, 16, 4, 256, "int4"), "cpu", seed=9)
+    for wl in (c2, c2, small, c2):
+        print(f"noalloc: one-launch decode {wl.cfg.name}", flush=True)
+        _both(wl, gpu, regime=7)
 
 
 def test_noalloc_rejects_beyond_its_scratch(gpu):
