@@ -673,7 +673,10 @@ size_t grimoire_moe_forward_workspace_bytes(const grim_moe_layer* L, int tokens)
  * launch for one token with no shared expert (INT4 / MXFP4 experts,
  * K <= 8, H <= 2048, I <= 1024, K * I <= 8192: router, top-k, gate_up and
  * down in one kernel whose work-groups exchange epoch-tagged words; other
- * shapes take regime 1), 4 = expert-grouped
+ * shapes take regime 1.  Its work-groups (at most one per CU) must all be
+ * resident at once: kernels of other streams that hold CUs can make its
+ * bounded polls (20 ms) time out, which sets 32-bit word 1 of the
+ * workspace and leaves the outputs undefined), 4 = expert-grouped
  * GEMV (MXFP4 with hidden and inter multiples of 64 above 256: on the
  * scaled fp4 matrix core, K padded to 256; otherwise on the vector ALU), 5 = expert-grouped GEMV on
  * the vector ALU.  No reference counterpart for 3-5 (regimes of this
