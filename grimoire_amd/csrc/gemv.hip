@@ -91,9 +91,18 @@ bool decode_plan_fused(int fmt, DecodeArgs& a) {
     if (!wave_fmt || a.M != 1 || a.shared || !a.sync || a.K > 8 || a.K < 1 || a.E > 512 ||
         a.H % 32 || a.H > 2048 || a.I % 32 || a.I > 1024 || a.H < 32 || a.I < 32 || a.K * a.I > 8192)
         return false;
-    // at most one 512-thread work-group per CU, so every work-group is
-    // resident while others poll for its results
-    constexpr int kMaxGrid = kSyncMaxGrid;
+    // at most one 512-thread work-group per CU of this device (a partitioned
+    // device has fewer than 256), so every work-group is resident while
+    // others poll for its results
+    static int cu_count[64];   // per device, looked up once
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    int cus = __atomic_load_n(&cu_count[dev], __ATOMIC_RELAXED);
+    if (cus == 0) {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return false;
+        __atomic_store_n(&cu_count[dev], cus, __ATOMIC_RELAXED);
+    }
+    const int kMaxGrid = std::min(cus, kSyncMaxGrid);
     auto gu_groups = [&](int ru) { return (a.K * (a.I / ru) + 7) / 8; };
     int ru = 0;
     for (int r : {2, 3, 4})
