@@ -347,8 +347,9 @@ __device__ __forceinline__ void gvm_issue(uint8_t* st, uint8_t* sup, __amdgpu_bu
 }
 
 // One persistent kernel for both products (GU: gate_up + SwiGLU, rows are
-// (gate, up) pairs, out h; else down, out y).  Items: (group, chunk of
-// kGvmWaves x 32 pairs / 64 rows); work-group b walks b, b + gridDim.x, ...
+// (gate, up) pairs, out h; else down, out y).  Items are per wave: (group,
+// chunk of 32 pairs / 64 rows); wave w of work-group b walks 4 b + w,
+// + 4 gridDim.x, ...
 // A wave's ring stage s (K [256 s, +256)) holds its 64 rows' codes (one
 // 128-byte line per row), their scales, and the group's limb rows at those
 // K with their block scales: everything a stage's MFMAs read comes with the
@@ -370,9 +371,14 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
     const bool nt = lrow % 128 == 0;
     constexpr int PW = GU ? kGvmRows / 2 : kGvmRows;         // rows (pairs) per wave
     constexpr int NRB = kGvmRows / 16;                       // 16-row blocks per wave
-    const int per_item = kGvmWaves * PW;
     const int rows_per_expert = GU ? 2 * N : N;
-    const int n_chunks = (N + per_item - 1) / per_item;
+    // items are per wave: (group, chunk of PW rows / pairs); wave w of
+    // work-group b takes items 4 b + w, + 4 gridDim.x, ... (the waves of a
+    // work-group share nothing, so a wave needs no partner: an expert whose
+    // rows end mid-work-group leaves no wave idle on padding, and the last
+    // round spreads over the waves of every work-group)
+    const int n_chunks = (N + PW - 1) / PW;
+    const int wstride = int(gridDim.x) * kGvmWaves;
     const int n_live = __builtin_amdgcn_readfirstlane(*a.n_live);
     const int groups = n_live + (a.T_sh + kGvMT - 1) / kGvMT;
     const int n_items = groups * n_chunks;
@@ -400,7 +406,7 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
     auto make = [&](int item0, int& item) {
         Desc d;
         d.mc = 0;
-        for (item = item0; item < n_items; item += gridDim.x) {
+        for (item = item0; item < n_items; item += wstride) {
             const int g = item / n_chunks, chunk = item % n_chunks;
             int64_t wrow0 = 0;
             if (g < n_live) {
@@ -421,7 +427,7 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
             d.pb = w.payload + wrow0 * lrow;
             d.sbp = static_cast<const uint8_t*>(w.scales) + wrow0 * srb;
             d.ab = d.sh ? a.af_sh : a.af;
-            d.i0 = chunk * per_item + wave * PW;             // this wave's first row (pair)
+            d.i0 = chunk * PW;                               // this wave's first row (pair)
             // weight row of the wave's row r (GU: r < 32 gate, else up); rows
             // past N repeat the last (loaded, never stored)
             auto wrow = [&](int r) {
@@ -506,9 +512,9 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
     // descriptor formed inside a lambda keeps the host pass from emitting
     // the kernel)
     int item_c = 0, item_n = 0;
-    cur = make(blockIdx.x, item_c);
+    cur = make(int(blockIdx.x) * kGvmWaves + wave, item_c);
     if (cur.mc <= 0) return;
-    nxt = make(item_c + gridDim.x, item_n);
+    nxt = make(item_c + wstride, item_n);
     cp = gvm_rsrc(cur.pb, rows_per_expert * lrow);
     cs = gvm_rsrc(cur.sbp, rows_per_expert * srb);
     ca = gvm_rsrc(cur.ab, 0x7FFFFFFF);
@@ -677,7 +683,7 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
         cp = np;
         cs = ns;
         ca = na;
-        nxt = make(item_n + gridDim.x, item_n);
+        nxt = make(item_n + wstride, item_n);
         np = gvm_rsrc(nxt.pb, rows_per_expert * lrow);
         ns = gvm_rsrc(nxt.sbp, rows_per_expert * srb);
         na = gvm_rsrc(nxt.ab, 0x7FFFFFFF);
