@@ -210,3 +210,23 @@ def test_pool_cpus_partition():
         assert all(len(p) in (len(allowed) // ranks, len(allowed) // ranks + 1) for p in parts)
     cx = tiered.CpuExperts(3, cpus=[-1] + tiered.cpu_pool_cpus(1, 0)[:2])
     assert cx.threads == 3
+
+
+def test_pool_wakes_after_idle():
+    """Idle pool threads go to sleep on the bell; calls spaced out past the
+    spin phase must still complete with the same bits as back-to-back ones."""
+    import time
+    H, I = 256, 128
+    L = tiered.layout(H, I)
+    blocks = _blocks(O.tmoe_layout(H, I), 4, 21)
+    rng = np.random.default_rng(3)
+    x = torch.from_numpy((rng.standard_normal(H) * 0.05).astype(np.float32))
+    w = torch.tensor([0.4, 0.3, 0.2, 0.1])
+    cx = tiered.CpuExperts(5)
+    want = torch.empty(H)
+    cx.ffn(L, blocks, w, x, want)
+    for _ in range(6):
+        time.sleep(0.05)
+        y = torch.full((H,), float("nan"))
+        cx.ffn(L, blocks, w, x, y)
+        assert torch.equal(y, want)
