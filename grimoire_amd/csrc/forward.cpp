@@ -14,6 +14,7 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <atomic>
 #include <mutex>
 
 #include "../../include/grimoire_moe.h"
@@ -45,6 +46,14 @@ struct Carve {
         return p;
     }
 };
+
+// Poll bound of the one-launch decode, in real-time counter ticks; the
+// default unless a test lowers it (grimoire_moe_debug_spin_ticks).
+std::atomic<uint64_t> g_spin_ticks{kSpinTicksDefault};
+
+__global__ void zero_words_kernel(uint32_t* p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
 
 // The decode path with device-side routing covers up to this many tokens.
 constexpr int kDecodeMaxTokens = 8;
@@ -402,6 +411,41 @@ extern "C" int grimoire_moe_forward(void* stream, const grim_moe_layer* L,
                         workspace, workspace_bytes, kRoleRouter | kRoleGateUp | kRoleDown);
 }
 
+// ---- the one-launch decode's sync words: status and reset
+//
+// workspace == NULL addresses the current device's array of
+// grimoire_moe_forward_noalloc.
+
+static int sync_words(void* workspace, size_t bytes, uint32_t** out);
+
+extern "C" int grimoire_moe_decode_sync_status(void* stream, const void* workspace, size_t workspace_bytes,
+                                               int* status) {
+    if (!status) return ferr(GRIM_ERR_ARG, "decode_sync_status: null status");
+    uint32_t* w = nullptr;
+    if (int r = sync_words(const_cast<void*>(workspace), workspace_bytes, &w)) return r;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint32_t v = 0;
+    hipError_t e = hipMemcpyAsync(&v, w + 1, sizeof v, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    *status = v ? 1 : 0;
+    return GRIM_OK;
+}
+
+extern "C" int grimoire_moe_decode_sync_reset(void* stream, void* workspace, size_t workspace_bytes) {
+    uint32_t* w = nullptr;
+    if (int r = sync_words(workspace, workspace_bytes, &w)) return r;
+    const int n = int(kSyncBytes / 4);
+    zero_words_kernel<<<(n + 1023) / 1024, 256, 0, static_cast<hipStream_t>(stream)>>>(w, n);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    return GRIM_OK;
+}
+
+extern "C" uint64_t grimoire_moe_debug_spin_ticks(int64_t ticks) {
+    return g_spin_ticks.exchange(ticks < 0 ? kSpinTicksDefault : uint64_t(ticks));
+}
+
 // ---- the allocation-free variant
 //
 // Its workspace is one file-scope device array per GPU (the module's copy
@@ -439,6 +483,18 @@ int scratch_ptr(void** out) {
     return GRIM_OK;
 }
 }  // namespace
+
+static int sync_words(void* workspace, size_t bytes, uint32_t** out) {
+    if (workspace) {
+        if (bytes < kSyncBytes) return ferr(GRIM_ERR_WORKSPACE, "workspace smaller than its sync words");
+        *out = static_cast<uint32_t*>(workspace);
+        return GRIM_OK;
+    }
+    void* ws = nullptr;
+    if (int r = scratch_ptr(&ws)) return ferr(r, "no device address for the scratch array");
+    *out = static_cast<uint32_t*>(ws);
+    return GRIM_OK;
+}
 
 extern "C" size_t grimoire_moe_forward_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
 
@@ -573,6 +629,7 @@ static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_
         // one token through all three roles: the one-launch kernel
         a.sync = p.sync;
         a.hrep = p.hrep;
+        a.spin_ticks = g_spin_ticks.load(std::memory_order_relaxed);
         if (roles == (kRoleRouter | kRoleGateUp | kRoleDown) && regime == 7 &&
             decode_plan_fused(L->gate_up.fmt, a)) {
             hipError_t e = decode_launch(st, L->gate_up.fmt, a);

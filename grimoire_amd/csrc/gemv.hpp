@@ -49,7 +49,11 @@ struct DecodeArgs {
     uint32_t* sync;           // kSyncBytes of epoch-tagged words, zero before first use
     float* hrep;              // kSyncCopies copies of h, fused_h_stride(K, I) floats apart
     int fz_G, fz_ru, fz_rh;   // grid, row pairs per wave, rows per half-wave
+    uint64_t spin_ticks;      // bound of each poll, real-time counter ticks (100 MHz)
 };
+
+// Default poll bound of the one-launch decode: 20 ms.
+constexpr uint64_t kSpinTicksDefault = 2000000;
 
 // Sync words at the head of every forward workspace (32-bit word offsets):
 // [0] the epoch word, [1] the error word; from kSyncFlagOff, kSyncCopies

@@ -20,15 +20,23 @@
 // copy b % kSyncCopies: reads that miss L2 are served by the memory
 // channel that holds the line, and 256 work-groups reading one copy of
 // 24 KB of h measured ~6 us (a few channels serving every request).
-// The epoch is the epoch word plus one.  Every work-group reads the word
-// before it publishes its flag (the flag holds the epoch), and work-group 0
-// advances the word only after it has seen every work-group's flag, so all
-// work-groups of a call agree on the epoch.  The sync words must be zero before
-// a workspace's first use (a stale tag is then always below the epoch).
-// Polls are bounded by the real-time counter (kSpinTicks); a work-group that
-// runs out of time records it in the error word and carries on, so every
-// wave exits.
-//
+// The epoch is the epoch word plus one (skipping 0, the value of cleared
+// words).  Every work-group reads the word before it publishes its flag
+// (the flag holds the epoch), and work-group 0 advances the word only after
+// it has seen every work-group's flag, so all work-groups of a call agree on
+// the epoch.  Tags are compared for equality: every word a call reads is
+// also written by that call, so a stale value is the one an earlier call
+// left, and it is taken for current only if exactly a multiple of 2^32
+// calls separate the two (the 32-bit epoch wraps).  The sync words must be
+// zero before a workspace's first use.
+// Polls are bounded by the real-time counter (DecodeArgs::spin_ticks).  A
+// work-group that runs out of time sets the error word, writes NaN to the
+// outputs it owns (and, work-group 0, expert -1 / weight NaN routes) and
+// carries on, so every wave exits.  A set error word poisons the
+// workspace: work-group 0 does not advance the epoch after a time-out, and
+// every later call reads the error word first and only writes NaN outputs,
+// until the caller clears the sync words (grimoire_moe_decode_sync_reset).
+// Late work-groups of a timed-out call therefore never feed the next one.
 // All work-groups must be resident at once (a poll waits on work-groups
 // that have not started otherwise): the host keeps the grid at or below one
 // work-group of 512 threads per CU.
@@ -47,7 +55,6 @@ namespace grim {
 
 constexpr int kFzThreads = 512;
 constexpr int kFzWaves = kFzThreads / kWave;
-constexpr uint64_t kSpinTicks = 2000000;   // 20 ms at the 100 MHz real-time counter
 
 __device__ __forceinline__ uint32_t sync_ld(const uint32_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -132,11 +139,11 @@ __device__ __forceinline__ WRsrc expert_rsrc(const WView& w, int64_t rows0, uint
 // Polls until pred() holds for the whole wave or the time bound passes;
 // returns false on a time-out.
 template <typename P>
-__device__ __forceinline__ bool wave_poll(P pred) {
+__device__ __forceinline__ bool wave_poll(uint64_t ticks, P pred) {
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     while (true) {
         if (__ballot(!pred()) == 0) return true;
-        if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) return false;
+        if (__builtin_amdgcn_s_memrealtime() - t0 > ticks) return false;
         __builtin_amdgcn_s_sleep(1);
     }
 }
@@ -159,7 +166,7 @@ __global__ __launch_bounds__(kFzThreads) void moe_decode_fused_kernel(DecodeArgs
     const uint32_t* my_flags = flags + mine * kSyncFlagStride;
     const uint64_t* my_rtags = rtags + mine * kSyncRtagStride;
 
-    __shared__ uint32_t s_epoch;
+    __shared__ uint32_t s_epoch, s_err, s_bad;
     __shared__ float red[4];
     __shared__ int sel_e[16];
     __shared__ float sel_w[16];
@@ -174,7 +181,12 @@ __global__ __launch_bounds__(kFzThreads) void moe_decode_fused_kernel(DecodeArgs
     if (a.ts && threadIdx.x == 0) a.ts[(2048 + b) * 8 + 1] = __builtin_amdgcn_s_memtime();
 #endif
     // (1) the epoch, the router row's loads, this lane's x chunk
-    if (threadIdx.x == 0) s_epoch = sync_ld(epoch_word) + 1u;
+    if (threadIdx.x == 0) {
+        const uint32_t e = sync_ld(epoch_word) + 1u;
+        s_epoch = e == 0u ? 1u : e;
+        s_err = sync_ld(err);
+        s_bad = 0u;
+    }
     // router rows e = b, b + G, ...: threads 0..255 hold router_row1's
     // elements (k = 4t + 1024m) and follow its FMA order and reduction, so
     // the logits equal grimoire_moe_router_logits' bit for bit
@@ -185,6 +197,17 @@ __global__ __launch_bounds__(kFzThreads) void moe_decode_fused_kernel(DecodeArgs
     const float4* x4 = reinterpret_cast<const float4*>(a.x);
     const bool x_lo = format_to_lds<F>(fl, H, [&](int i) { return x4[i]; });
     const uint32_t epoch = s_epoch;
+    constexpr int RB = 2 * RH;
+    if (s_err != 0u) {
+        // poisoned workspace (an earlier call timed out): NaN outputs only
+        const float qnan = __builtin_nanf("");
+        for (int o = b * RB + int(threadIdx.x); o < min(H, (b + 1) * RB); o += kFzThreads) a.y[o] = qnan;
+        if (b == 0 && int(threadIdx.x) < K) {
+            a.rex[threadIdx.x] = -1;
+            a.rwt[threadIdx.x] = qnan;
+        }
+        return;
+    }
     for (int e = b; e < E; e += G) {
         if (e != b && rt) router_row1_load(a.router + int64_t(e) * H, a.x, H, rr);
         float acc = 0.0f;
@@ -218,7 +241,7 @@ __global__ __launch_bounds__(kFzThreads) void moe_decode_fused_kernel(DecodeArgs
             rb[j] = (a.rbias && j < V && e < E) ? a.rbias[e] : 0.0f;
         }
         // every tag requested before any is compared
-        const bool ok = wave_poll([&]() {
+        const bool ok = wave_poll(a.spin_ticks, [&]() {
             uint64_t v[kMaxV];
 #pragma unroll
             for (int j = 0; j < kMaxV; ++j) {
@@ -233,7 +256,10 @@ __global__ __launch_bounds__(kFzThreads) void moe_decode_fused_kernel(DecodeArgs
             }
             return all;
         });
-        if (!ok && lane == 0) sync_st(err, 1u);
+        if (!ok && lane == 0) {
+            sync_st(err, 1u);
+            s_bad = 1u;
+        }
         GRIM_TS(a, 0, 2);
         if (b == 0) {
 #pragma unroll
@@ -261,8 +287,8 @@ __global__ __launch_bounds__(kFzThreads) void moe_decode_fused_kernel(DecodeArgs
     }
     GRIM_TS(a, 0, 7);
     if (b == 0 && int(threadIdx.x) < K) {
-        a.rex[threadIdx.x] = sel_e[threadIdx.x];
-        a.rwt[threadIdx.x] = sel_w[threadIdx.x];
+        a.rex[threadIdx.x] = s_bad ? -1 : sel_e[threadIdx.x];
+        a.rwt[threadIdx.x] = s_bad ? __builtin_nanf("") : sel_w[threadIdx.x];
     }
 
     // (3) gate_up weights of this wave's unit, then down weights of this
@@ -283,7 +309,6 @@ __global__ __launch_bounds__(kFzThreads) void moe_decode_fused_kernel(DecodeArgs
         wprefetch<F>(grs, a.gu, ghz, uint32_t(i0 + r), uint32_t(cx), pg[r]);
         wprefetch<F>(grs, a.gu, ghz, uint32_t(I + i0 + r), uint32_t(cx), pu[r]);
     }
-    constexpr int RB = 2 * RH;
     const int nb = (H + RB - 1) / RB;
     const bool has_dn = b < nb;
     const int s = wave;                      // down: wave s = slot s
@@ -371,14 +396,18 @@ __global__ __launch_bounds__(kFzThreads) void moe_decode_fused_kernel(DecodeArgs
     // (5) wait for every work-group's flag (its h, and its read of the
     // epoch word), then the down dots
     if (wave == 0) {
-        const bool ok = wave_poll([&]() {
+        const bool ok = wave_poll(a.spin_ticks, [&]() {
             bool all = true;
             for (int q = lane; q < G; q += kWave) all = all && sync_ld(my_flags + q) == epoch;
             return all;
         });
-        if (!ok && lane == 0) sync_st(err, 1u);
+        if (!ok && lane == 0) {
+            sync_st(err, 1u);
+            s_bad = 1u;
+        }
         // every work-group has read the epoch word: the next call's epoch
-        if (b == 0 && lane == 0) sync_st(epoch_word, epoch);
+        // (not after a time-out: the workspace is poisoned then)
+        if (b == 0 && lane == 0 && ok) sync_st(epoch_word, epoch);
     }
     __syncthreads();
     GRIM_TS(a, 0, 5);
@@ -435,7 +464,7 @@ __global__ __launch_bounds__(kFzThreads) void moe_decode_fused_kernel(DecodeArgs
             float total = 0.0f;
 #pragma unroll
             for (int q = 0; q < 8; ++q) total = wv[q] != 0.0f ? __builtin_fmaf(wv[q], pv[q], total) : total;
-            a.y[o] = total;
+            a.y[o] = s_bad ? __builtin_nanf("") : total;
         }
     }
     GRIM_TS(a, 0, 6);

@@ -8,6 +8,7 @@ rejects the arguments; nothing here computes on the CPU.
 """
 from __future__ import annotations
 
+import ctypes as C
 from typing import Optional
 
 import torch
@@ -296,6 +297,20 @@ class MoeForward:
                                          _p(self.workspace), self.workspace.numel()),
               "moe_forward")
 
+
+    def sync_status(self, stream=None) -> int:
+        """1 when a one-launch decode call on this workspace timed out (the
+        workspace is poisoned until sync_reset), else 0; waits for the stream."""
+        out = C.c_int(-1)
+        check(lib().grimoire_moe_decode_sync_status(_stream(stream), _p(self.workspace),
+                                                    self.workspace.numel(), C.byref(out)),
+              "decode_sync_status")
+        return int(out.value)
+
+    def sync_reset(self, stream=None):
+        """Clears the one-launch decode's sync words (stream order)."""
+        check(lib().grimoire_moe_decode_sync_reset(_stream(stream), _p(self.workspace),
+                                                   self.workspace.numel()), "decode_sync_reset")
 
     STAGE_ROUTER, STAGE_GATE_UP, STAGE_DOWN = 1, 2, 4
 

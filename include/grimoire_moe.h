@@ -655,9 +655,11 @@ typedef struct grim_route_params {
 /* Workspace bytes for grimoire_moe_forward at `tokens`.  Its first
  * GRIM_SYNC_BYTES hold the one-launch decode's (regime 7) epoch-tagged sync
  * words: they must be zero before the workspace's first regime-7 call
- * (hipMemset once after allocating it); every call leaves them
- * consistent and no other regime writes them, so they are never cleared
- * again.  Otherwise no initial contents are needed.  Calls that share one
+ * (hipMemset once after allocating it, or grimoire_moe_decode_sync_reset);
+ * no other regime writes them, and a call that completes leaves them ready
+ * for the next.  A regime-7 call whose polls time out sets the error word
+ * and poisons the workspace (see grimoire_moe_decode_sync_status).
+ * Otherwise no initial contents are needed.  Calls that share one
  * workspace must not overlap. */
 #define GRIM_SYNC_BYTES 180480
 size_t grimoire_moe_forward_workspace_bytes(const grim_moe_layer* L, int tokens);
@@ -675,8 +677,10 @@ size_t grimoire_moe_forward_workspace_bytes(const grim_moe_layer* L, int tokens)
  * down in one kernel whose work-groups exchange epoch-tagged words; other
  * shapes take regime 1.  Its work-groups (at most one per CU) must all be
  * resident at once: kernels of other streams that hold CUs can make its
- * bounded polls (20 ms) time out, which sets 32-bit word 1 of the
- * workspace and leaves the outputs undefined), 4 = expert-grouped
+ * bounded polls (20 ms) time out; that call and every later regime-7 call
+ * on the workspace then write NaN outputs (routes: expert -1, weight NaN)
+ * until grimoire_moe_decode_sync_reset, and
+ * grimoire_moe_decode_sync_status reports it), 4 = expert-grouped
  * GEMV (MXFP4 with hidden and inter multiples of 64 above 256: on the
  * scaled fp4 matrix core, K padded to 256; otherwise on the vector ALU), 5 = expert-grouped GEMV on
  * the vector ALU.  No reference counterpart for 3-5 (regimes of this
@@ -698,6 +702,26 @@ int grimoire_moe_forward(void* stream, const grim_moe_layer* L, const grim_route
  * (other streams, other threads) race and must be serialised by the
  * caller. */
 size_t grimoire_moe_forward_noalloc_max_bytes(void);
+
+/* Status of the one-launch decode (regime 7) on a workspace: *status = 1
+ * when a call's bounded polls timed out (the workspace is poisoned: every
+ * regime-7 call on it writes NaN outputs), else 0.  Reads the error word
+ * in stream order and waits for the stream (a host synchronisation; not
+ * for capture).  workspace NULL = the current device's array of
+ * grimoire_moe_forward_noalloc.  No reference counterpart (the reference
+ * has no one-launch decode). */
+int grimoire_moe_decode_sync_status(void* stream, const void* workspace, size_t workspace_bytes,
+                                    int* status);
+/* Clears the sync words (epoch, error word, flags, router tags) of a
+ * workspace in stream order with a fill kernel, so a poisoned workspace is
+ * usable again; also the first-use initialisation.  workspace NULL = the
+ * noalloc array of the current device.  No reference counterpart. */
+int grimoire_moe_decode_sync_reset(void* stream, void* workspace, size_t workspace_bytes);
+/* Test hook: sets the poll bound of the one-launch decode in real-time
+ * counter ticks (100 MHz; a negative value restores the 20 ms default) and
+ * returns the previous one.  A tiny bound makes the polls give up at once
+ * while every kernel still exits normally.  No reference counterpart. */
+uint64_t grimoire_moe_debug_spin_ticks(int64_t ticks);
 int grimoire_moe_forward_noalloc(void* stream, const grim_moe_layer* L, const grim_route_params* rp,
                                  const uint16_t* shared_gate_w, const float* x, float* y,
                                  int tokens, int32_t* out_expert, float* out_weight, int regime);

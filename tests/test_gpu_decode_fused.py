@@ -130,3 +130,37 @@ def test_fused_decode_graph_replays(gpu):
             assert torch.equal(y.cpu(), eager[i][0]) and torch.equal(oe.cpu(), eager[i][1]), \
                 f"replay {rep} input {i}"
     assert int(_flags(fwd)[ERR]) == 0
+
+
+def test_fused_decode_timeout_is_reported(gpu):
+    """A poll that runs out of time (forced from the host: a bound of zero
+    ticks makes every poll give up after its first look, and every wave
+    still exits) sets the error word; that call and every later one on the
+    workspace write NaN outputs and routes -1 until the sync words are
+    cleared, and the status entry point reports it.  After a reset, with
+    the default bound back, the forward is bit-identical to a fresh one."""
+    cfg = CASES["c2"]
+    print("fused decode: forced poll time-out", flush=True)
+    wl, Lg, fwd = _fwd(cfg, gpu, 13)
+    xg = wl.x.to(gpu)
+    ref = _call(fwd, xg, cfg, gpu)
+    assert fwd.sync_status() == 0
+    lib = _abi.lib()
+    prev = lib.grimoire_moe_debug_spin_ticks(0)
+    try:
+        y, oe, ow = _call(fwd, xg, cfg, gpu)
+    finally:
+        lib.grimoire_moe_debug_spin_ticks(-1)
+    assert prev == 2000000
+    assert fwd.sync_status() == 1
+    # poisoned: the next calls, with the normal bound, write NaN only
+    for _ in range(2):
+        y, oe, ow = _call(fwd, xg, cfg, gpu)
+        assert torch.isnan(y).all() and (oe == -1).all() and torch.isnan(ow).all()
+        assert fwd.sync_status() == 1
+    fwd.sync_reset()
+    assert fwd.sync_status() == 0
+    outs = [_call(fwd, xg, cfg, gpu) for _ in range(2)]
+    for o in outs:
+        assert all(torch.equal(p, q) for p, q in zip(o, ref))
+    assert fwd.sync_status() == 0 and int(_flags(fwd)[EPOCH]) == 2

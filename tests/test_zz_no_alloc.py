@@ -63,6 +63,15 @@ def test_noalloc_one_launch_decode(gpu):
     for wl in (c2, c2, small, c2):
         print(f"noalloc: one-launch decode {wl.cfg.name}", flush=True)
         _both(wl, gpu, regime=7)
+    # the array's error word, read and cleared through the status / reset
+    # entry points with no workspace
+    lib = _abi.lib()
+    st = C.c_int(-1)
+    assert lib.grimoire_moe_decode_sync_status(None, None, 0, C.byref(st)) == 0 and st.value == 0
+    assert lib.grimoire_moe_decode_sync_reset(None, None, 0) == 0
+    torch.cuda.synchronize()
+    _both(c2, gpu, regime=7)
+    assert lib.grimoire_moe_decode_sync_status(None, None, 0, C.byref(st)) == 0 and st.value == 0
 
 
 def test_noalloc_rejects_beyond_its_scratch(gpu):
