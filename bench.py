@@ -569,6 +569,43 @@ def c5_bench(dev, stream, reps=5):
             "bound": "hbm (intensity ~6.6 FLOP/B, far below the ~315 FLOP/B bf16 ridge)"}
 
 
+def c5_shard_bench(dev, stream, reps=10, begin=96, count=32):
+    """One GPU's share of C5 under 8-way expert parallelism
+    (grimoire_moe_forward_shard): the global router and group-limited top-k
+    over all 256 experts, experts [96, 128) local, routes to others masked;
+    no shared expert on this shard.  Bytes = the local experts the routing
+    touches + the global router + x + y."""
+    from grimoire_amd.weights import MoeLayer
+    cfg = configs.CONFIGS["c5"]
+    loc = configs.make_layer(configs.scaled(cfg, E=count), dev, seed=510)
+    g = torch.Generator(device=dev).manual_seed(510)
+    router = (torch.randn((cfg.E, cfg.H), generator=g, device=dev) * 0.02).contiguous()
+    L = MoeLayer(cfg.H, cfg.I, cfg.E, cfg.K, loc.gate_up, loc.down, router)
+    bias = configs.make_route_bias(cfg, dev, seed=5)
+    x = configs.make_x(cfg, dev, seed=5)
+    fwd = ops.MoeForward(L, cfg.T, configs.route_params(cfg, bias), regime=0)
+    y = torch.empty(cfg.T, cfg.H, device=dev)
+    oe = torch.empty(cfg.T, cfg.K, dtype=torch.int32, device=dev)
+    ow = torch.empty(cfg.T, cfg.K, dtype=torch.float32, device=dev)
+    with torch.cuda.stream(stream):
+        fwd.shard(x, y, begin, count, oe, ow, stream=stream)
+        torch.cuda.synchronize()
+        with Timer(stream) as t:
+            for _ in range(reps):
+                fwd.shard(x, y, begin, count, oe, ow, stream=stream)
+    us = t.ms() * 1e3 / reps
+    e = oe.cpu().flatten()
+    local = sorted(set(int(v) for v in e.tolist() if begin <= v < begin + count))
+    nbytes = len(local) * loc.expert_bytes() + cfg.E * cfg.H * 4 + 2 * cfg.T * cfg.H * 4
+    routes = int(((e >= begin) & (e < begin + count)).sum())
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"workload": f"c5 shard: experts [{begin}, {begin + count}) of 256 local (8-way expert "
+                        "parallelism, one GPU's share), T=32 H=7168 I=2048 MXFP4, global group-limited "
+                        "routing, no shared expert",
+            "us_per_layer": round(us, 1), "local_routes": routes, "local_experts_touched": len(local),
+            "bytes_per_layer": int(nbytes), "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -578,7 +615,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 64 MiB device copy 5 times (HBM counter calibration)")
-    ap.add_argument("--only", choices=("c3", "c4", "c5", "edges"),
+    ap.add_argument("--only", choices=("c3", "c4", "c5", "c5_shard", "edges"),
                     help="run only this workload's section and print it alone (for profiling runs)")
     ap.add_argument("--decode-regime", type=int, default=1, choices=(1, 3, 7),
                     help="1: router logits, gate_up (with the top-k), down; "
@@ -600,7 +637,8 @@ def main():
         torch.cuda.synchronize()
     if a.only:
         run = {"c3": lambda: c3_bench(dev, stream), "c4": lambda: prefill_bench(dev, stream),
-               "c5": lambda: c5_bench(dev, stream), "edges": lambda: edges_bench(dev, stream)}[a.only]
+               "c5": lambda: c5_bench(dev, stream), "c5_shard": lambda: c5_shard_bench(dev, stream),
+               "edges": lambda: edges_bench(dev, stream)}[a.only]
         print(json.dumps({"only": a.only, a.only: run()}), flush=True)
         return
     log("decode bench (C2, 48 layers)...")
@@ -648,6 +686,7 @@ def main():
         out["c3"] = c3_bench(dev, stream)
         out["c3_decode_kernels"] = c3_bench(dev, stream, regime=1)
         out["c5"] = c5_bench(dev, stream)
+        out["c5_shard"] = c5_shard_bench(dev, stream)
         log("edges (fused norms, ingestion)...")
         out["edges"] = edges_bench(dev, stream)
     if not a.no_cpu:

@@ -196,6 +196,8 @@ SIGNATURES = {
     "grimoire_moe_forward": (I32, [P, LP, RPP, P, P, P, I32, P, P, I32, P, SZ]),
     "grimoire_moe_forward_noalloc_max_bytes": (SZ, []),
     "grimoire_moe_forward_noalloc": (I32, [P, LP, RPP, P, P, P, I32, P, P, I32]),
+    "grimoire_moe_forward_shard": (I32, [P, LP, RPP, P, P, P, I32, P, P, I32, I32, I32, P, SZ]),
+    "grimoire_moe_route_local": (I32, [P, P, P, P, P, I32, I32, I32]),
     "grimoire_moe_decode_sync_status": (I32, [P, P, SZ, C.POINTER(C.c_int)]),
     "grimoire_moe_decode_sync_reset": (I32, [P, P, SZ]),
     "grimoire_moe_debug_spin_ticks": (C.c_uint64, [C.c_int64]),

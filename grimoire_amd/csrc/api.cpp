@@ -90,7 +90,8 @@ int check_layer(const grim_moe_layer* L) {
     const auto& c = L->cfg;
     if (c.hidden <= 0 || c.inter <= 0 || c.num_experts <= 0 || c.top_k <= 0)
         return fail(GRIM_ERR_SHAPE, "bad config");
-    if (c.top_k > 16 || c.top_k > c.num_experts) return fail(GRIM_ERR_SHAPE, "top_k=%d", c.top_k);
+    // top_k may exceed num_experts on an expert shard (most slots then -1)
+    if (c.top_k > 16) return fail(GRIM_ERR_SHAPE, "top_k=%d", c.top_k);
     if (c.num_experts > 512) return fail(GRIM_ERR_SHAPE, "num_experts=%d > 512", c.num_experts);
     int r = check_weight(&L->gate_up, "gate_up", int64_t(c.num_experts) * 2 * c.inter, c.hidden);
     if (r) return r;
@@ -360,6 +361,15 @@ int grimoire_moe_remap_bf16(void* stream, const uint16_t* hidden, const int32_t*
     a.perm_token = nullptr; a.tile_e = nullptr; a.tile_mb = nullptr; a.tmax = 0; a.mc = 0;
     a.workspace = workspace;
     return dispatch_common(stream, a, workspace_bytes);
+}
+
+int grimoire_moe_route_local(void* stream, const int32_t* topk_ids, const float* topk_w, int32_t* local_ids,
+                             float* local_w, int routes, int expert_begin, int expert_count) {
+    if (routes <= 0) return GRIM_OK;
+    if (!topk_ids || !topk_w || !local_ids || !local_w) return fail(GRIM_ERR_ARG, "null pointer");
+    if (expert_begin < 0 || expert_count <= 0) return fail(GRIM_ERR_ARG, "expert range");
+    return status(route_local_launch(S(stream), topk_ids, topk_w, local_ids, local_w, routes, expert_begin,
+                                     expert_count));
 }
 
 static int combine_common(void* stream, const CombineArgs& a) {

@@ -327,6 +327,28 @@ static void combine_k(hipStream_t st, const CombineArgs& a) {
 #undef GRIM_COMBINE
 }
 
+// Routes of one expert shard: an expert in [begin, begin + count) becomes
+// its local index, any other route expert -1 with weight 0
+// (src/grimoire.cpp:15392-15399, :23231-23240).
+__global__ __launch_bounds__(256) void route_local_kernel(const int32_t* __restrict__ ids,
+                                                          const float* __restrict__ w,
+                                                          int32_t* __restrict__ lids, float* __restrict__ lw,
+                                                          int R, int begin, int count) {
+    const int r = blockIdx.x * 256 + threadIdx.x;
+    if (r >= R) return;
+    const int e = ids[r];
+    const bool own = e >= begin && e - begin < count;
+    lids[r] = own ? e - begin : -1;
+    lw[r] = own ? w[r] : 0.0f;
+}
+
+hipError_t route_local_launch(hipStream_t st, const int32_t* ids, const float* w, int32_t* lids, float* lw,
+                              int R, int begin, int count) {
+    if (R <= 0) return hipSuccess;
+    route_local_kernel<<<(R + 255) / 256, 256, 0, st>>>(ids, w, lids, lw, R, begin, count);
+    return hipGetLastError();
+}
+
 hipError_t combine_launch(hipStream_t st, const CombineArgs& a) {
     if (a.T <= 0) return hipSuccess;
     if (a.K <= 0 || a.K > 16) return hipErrorInvalidValue;

@@ -58,6 +58,9 @@ size_t dispatch_workspace_bytes(int T, int K, int E);
 int32_t* dispatch_live_tiles(void* workspace, int T, int K, int E);
 hipError_t dispatch_launch(hipStream_t st, const DispatchArgs& a);
 hipError_t combine_launch(hipStream_t st, const CombineArgs& a);
+// Global routes -> one shard's local routes (expert - begin, or -1 / 0).
+hipError_t route_local_launch(hipStream_t st, const int32_t* ids, const float* w, int32_t* lids, float* lw,
+                              int R, int begin, int count);
 hipError_t combine_norm_launch(hipStream_t st, const NormArgs& a);
 
 }  // namespace grim

@@ -82,6 +82,8 @@ struct Plan {
     float* logits;
     int32_t* rex;
     float* rwt;
+    int32_t* lrex;  // one shard's local routes (grimoire_moe_forward_shard)
+    float* lrwt;
     float* gate;
     // GEMV
     float* h;
@@ -131,6 +133,8 @@ size_t carve(const grim_moe_layer* L, int T, bool gemv, char* base, Plan& p) {
     p.logits = cv.take<float>(size_t(T) * E);
     p.rex = cv.take<int32_t>(R);
     p.rwt = cv.take<float>(R);
+    p.lrex = cv.take<int32_t>(R);
+    p.lrwt = cv.take<float>(R);
     p.gate = cv.take<float>(T);
     if (gemv) {
         p.h = cv.take<float>(size_t(T) * (K + (sh ? 1 : 0)) * I);
@@ -400,7 +404,7 @@ static int forward_gv(hipStream_t st, const grim_moe_layer* L, const Plan& p, co
 static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_params* rp,
                         const uint16_t* shared_gate_w, const float* x, float* y, int tokens,
                         int32_t* out_expert, float* out_weight, int regime, void* workspace,
-                        size_t workspace_bytes, int roles);
+                        size_t workspace_bytes, int roles, int shard_begin = 0, int shard_count = 0);
 
 extern "C" int grimoire_moe_forward(void* stream, const grim_moe_layer* L,
                                     const grim_route_params* rp, const uint16_t* shared_gate_w,
@@ -522,6 +526,17 @@ extern "C" int grimoire_moe_forward_noalloc(void* stream, const grim_moe_layer* 
                         ws, kNoAllocScratchBytes, kRoleRouter | kRoleGateUp | kRoleDown);
 }
 
+extern "C" int grimoire_moe_forward_shard(void* stream, const grim_moe_layer* L, const grim_route_params* rp,
+                                          const uint16_t* shared_gate_w, const float* x, float* y, int tokens,
+                                          int32_t* out_expert, float* out_weight, int regime, int expert_begin,
+                                          int expert_count, void* workspace, size_t workspace_bytes) {
+    if (expert_count <= 0) return ferr(GRIM_ERR_ARG, "expert_count must be > 0");
+    if (regime == 1 || regime == 7) regime = 3;   // the in-kernel top-k decode has no shard form
+    return forward_impl(stream, L, rp, shared_gate_w, x, y, tokens, out_expert, out_weight, regime,
+                        workspace, workspace_bytes, kRoleRouter | kRoleGateUp | kRoleDown, expert_begin,
+                        expert_count);
+}
+
 extern "C" int grimoire_moe_decode_stage(void* stream, const grim_moe_layer* L,
                                          const grim_route_params* rp,
                                          const uint16_t* shared_gate_w, const float* x, float* y,
@@ -538,7 +553,7 @@ extern "C" int grimoire_moe_decode_stage(void* stream, const grim_moe_layer* L,
 static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_params* rp,
                         const uint16_t* shared_gate_w, const float* x, float* y, int tokens,
                         int32_t* out_expert, float* out_weight, int regime, void* workspace,
-                        size_t workspace_bytes, int roles) {
+                        size_t workspace_bytes, int roles, int shard_begin, int shard_count) {
     if (!L || !x || !y) return ferr(GRIM_ERR_ARG, "null layer/x/y");
     if (tokens <= 0) return GRIM_OK;
     if (!L->router) return ferr(GRIM_ERR_ARG, "layer has no router");
@@ -554,7 +569,11 @@ static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_
     if (out_weight) p.rwt = out_weight;
     hipStream_t st = static_cast<hipStream_t>(stream);
 
-    const int E = c.num_experts, K = c.top_k, H = c.hidden, I = c.inter;
+    int E = c.num_experts;
+    const int K = c.top_k, H = c.hidden, I = c.inter;
+    const bool shard = shard_count > 0;
+    if (shard && (shard_begin < 0 || int64_t(shard_begin) + shard_count > E))
+        return ferr(GRIM_ERR_ARG, "expert shard outside [0, num_experts)");
     const int mode = rp ? rp->mode : GRIM_ROUTE_SOFTMAX;
     if (H % 4) return ferr(GRIM_ERR_SHAPE, "hidden must be a multiple of 4");
     if (mode < GRIM_ROUTE_SOFTMAX || mode > GRIM_ROUTE_GROUP) return ferr(GRIM_ERR_ARG, "unknown route mode");
@@ -562,7 +581,7 @@ static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_
         (!rp || rp->n_group <= 0 || rp->n_group > 64 || E % rp->n_group || rp->topk_group <= 0 ||
          rp->topk_group > rp->n_group || K > rp->topk_group * (E / rp->n_group)))
         return ferr(GRIM_ERR_SHAPE, "group-limited routing parameters");
-    if (E > 512 || K > 16) return ferr(GRIM_ERR_SHAPE, "E <= 512 and top_k <= 16");
+    if (E > 512 || K > 16 || K > E) return ferr(GRIM_ERR_SHAPE, "E <= 512 and top_k <= min(16, E)");
     const float* rbias = (mode == GRIM_ROUTE_SOFTMAX && rp) ? static_cast<const float*>(rp->bias) : nullptr;
     const int topk_mode = mode == GRIM_ROUTE_SOFTMAX ? 0 : (mode == GRIM_ROUTE_SIGMOID ? 2 : 3);
     const uint16_t* b16 = mode == GRIM_ROUTE_SIGMOID ? static_cast<const uint16_t*>(rp->bias) : nullptr;
@@ -570,7 +589,7 @@ static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_
     const float scaling = (rp && mode != GRIM_ROUTE_SOFTMAX) ? rp->scaling : 1.0f;
     const bool sh = L->has_shared;
 
-    if (gemv && regime != 3 && tokens <= kDecodeMaxTokens) {
+    if (gemv && regime != 3 && tokens <= kDecodeMaxTokens && !shard) {
         // three launches: router GEMV, gate_up (each item runs its token's
         // top-k; h written in the staged layout), down
         if (sh && (L->shared_gate_up.fmt != L->gate_up.fmt || L->shared_down.fmt != L->down.fmt))
@@ -655,11 +674,25 @@ static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_
     const bool gv = !gemv && p.gv_te &&
                     (regime == 4 || regime == 5 || (regime == 0 && int64_t(tokens) * K <= 2 * int64_t(E)));
     const bool gv_mx = gv && regime != 5 && L->gate_up.fmt == GRIM_FMT_MXFP4 && gvm_shape_ok(H, I);
-    if (gv_mx && int64_t(tokens) * K <= kGvmRouteMax)
+    if (gv_mx && int64_t(tokens) * K <= kGvmRouteMax && !shard)
         return forward_gv(st, L, p, x, y, tokens, shared_gate_w, true, &tka);
     {
         hipError_t e = topk_launch(st, tka);
         if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+    }
+    // one expert shard: the routes it owns become local indices, the rest
+    // expert -1 / weight 0, and everything after the top-k sees a layer of
+    // shard_count experts (the routing itself stays global)
+    grim_moe_layer local;
+    if (shard) {
+        hipError_t e = route_local_launch(st, p.rex, p.rwt, p.lrex, p.lrwt, tokens * K, shard_begin, shard_count);
+        if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+        p.rex = p.lrex;
+        p.rwt = p.lrwt;
+        local = *L;
+        local.cfg.num_experts = shard_count;
+        L = &local;
+        E = shard_count;
     }
 
     if (gemv) {

@@ -298,6 +298,19 @@ class MoeForward:
               "moe_forward")
 
 
+    def shard(self, x, y, begin, count, out_expert=None, out_weight=None, stream=None):
+        """grimoire_moe_forward_shard: this layer holds experts [begin,
+        begin + count) of a layer whose router is global."""
+        _dev(x)
+        T = x.shape[0]
+        if T > self.max_tokens:
+            raise _abi.GrimoireError("more tokens than the workspace was sized for")
+        check(lib().grimoire_moe_forward_shard(_stream(stream), self.struct, self.route,
+                                               _p(self.L.shared_gate_w), _p(x), _p(y), T,
+                                               _p(out_expert), _p(out_weight), self.regime, begin, count,
+                                               _p(self.workspace), self.workspace.numel()),
+              "moe_forward_shard")
+
     def sync_status(self, stream=None) -> int:
         """1 when a one-launch decode call on this workspace timed out (the
         workspace is poisoned until sync_reset), else 0; waits for the stream."""

@@ -47,6 +47,12 @@ class Weight:
         return Weight(self.fmt, self.N, self.K, mv(self.payload), mv(self.scales), mv(self.zeros),
                       self.row_scales)
 
+    def rows(self, r0: int, n: int) -> "Weight":
+        """Rows [r0, r0 + n) as a view of the same memory."""
+        sl = lambda t: None if t is None else t[r0:r0 + n]
+        return Weight(self.fmt, n, self.K, self.payload[r0:r0 + n], sl(self.scales), sl(self.zeros),
+                      self.row_scales)
+
     def nbytes(self) -> int:
         n = self.payload.numel()
         for t in (self.scales, self.zeros):
@@ -161,6 +167,16 @@ class MoeLayer:
                         mv(self.shared_down),
                         None if self.shared_gate_w is None else self.shared_gate_w.to(device),
                         self.norm_topk)
+
+    def shard(self, begin: int, count: int, shared: bool = True) -> "MoeLayer":
+        """Experts [begin, begin + count) of this layer as views (the router
+        stays global: grimoire_moe_forward_shard's layer); the shared expert
+        kept when `shared`."""
+        return MoeLayer(self.hidden, self.inter, self.num_experts, self.top_k,
+                        self.gate_up.rows(begin * 2 * self.inter, count * 2 * self.inter),
+                        self.down.rows(begin * self.hidden, count * self.hidden), self.router,
+                        self.shared_gate_up if shared else None, self.shared_down if shared else None,
+                        self.shared_gate_w if shared else None, self.norm_topk)
 
     def expert_bytes(self) -> float:
         """Bytes of one routed expert (gate, up and down rows with scales)."""

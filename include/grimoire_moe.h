@@ -690,6 +690,28 @@ int grimoire_moe_forward(void* stream, const grim_moe_layer* L, const grim_route
                          int32_t* out_expert, float* out_weight, int regime, void* workspace,
                          size_t workspace_bytes);
 
+/* One expert shard of the layer (expert parallelism on one GPU's share;
+ * src/grimoire.cpp:15392-15399 decode, :23231-23240 batched): the router
+ * (L->router, [num_experts][H]) and the top-k are global, while
+ * L->gate_up / L->down hold only experts [expert_begin, expert_begin +
+ * expert_count) (local index e - expert_begin).  Routes to other experts
+ * become expert -1 / weight 0 and are skipped, so y is this shard's
+ * partial sum; a shared expert in L is added as usual (give it to one
+ * shard).  out_expert / out_weight receive the global routing.  regime as
+ * grimoire_moe_forward, except that 1 and 7 run as 3 (their top-k lives
+ * inside the expert kernels).  The workspace is
+ * grimoire_moe_forward_workspace_bytes(L, tokens).  The sum over shards is
+ * the caller's collective. */
+int grimoire_moe_forward_shard(void* stream, const grim_moe_layer* L, const grim_route_params* rp,
+                               const uint16_t* shared_gate_w, const float* x, float* y, int tokens,
+                               int32_t* out_expert, float* out_weight, int regime, int expert_begin,
+                               int expert_count, void* workspace, size_t workspace_bytes);
+/* The shard remap alone: local_ids[r] = topk_ids[r] - expert_begin and
+ * local_w[r] = topk_w[r] when the expert is in [expert_begin, expert_begin
+ * + expert_count), else -1 and 0 (src/grimoire.cpp:23231-23240). */
+int grimoire_moe_route_local(void* stream, const int32_t* topk_ids, const float* topk_w, int32_t* local_ids,
+                             float* local_w, int routes, int expert_begin, int expert_count);
+
 /* grimoire_moe_forward without a workspace argument and without any
  * allocation: for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid
