@@ -209,8 +209,8 @@ __global__ __launch_bounds__(kGvmRouteThreads) void gvm_route_kernel(TopkArgs tk
         return;
     }
     __shared__ __attribute__((aligned(16))) int32_t ids[kGvmRouteMax];
-    __shared__ int32_t cnt[kGvmRouteThreads], sc[kGvmRouteThreads], sg[kGvmRouteThreads];
-    const int tid = threadIdx.x;
+    __shared__ int32_t cnt[kGvmRouteThreads], wsum[kGvmRouteThreads / kWave][2];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
     const int T = tk.T, E = tk.E, K = tk.K, R = T * K;
     if (fused_topk) {
         // T <= 16: wave t selects token t's experts (topk_kernel's code,
@@ -218,7 +218,6 @@ __global__ __launch_bounds__(kGvmRouteThreads) void gvm_route_kernel(TopkArgs tk
         // barrier (one work-group: its waves share the CU's cache)
         __shared__ float gsel[kGvmRouteThreads / kWave][512];
         __shared__ float gscore[kGvmRouteThreads / kWave][64];
-        const int wv = tid / kWave;
         if (wv < T)
             topk_wave(tk.logits + int64_t(wv) * E, E, K, tk.mode, tk.normalize, tk.scaling, tk.bias16, tk.bias32,
                       tk.n_group, tk.topk_group, tk.out_e + int64_t(wv) * K, tk.out_w + int64_t(wv) * K, gsel[wv],
@@ -231,20 +230,27 @@ __global__ __launch_bounds__(kGvmRouteThreads) void gvm_route_kernel(TopkArgs tk
     const int my_id = tid < R ? ids[tid] : -1;
     if (my_id >= 0 && my_id < E) atomicAdd(&cnt[my_id], 1);
     __syncthreads();
-    // inclusive scans of the counts and of the groups per expert
+    // inclusive scans of the counts and of the groups per expert: within
+    // each wave by lane shifts, then the waves' totals (two barriers in
+    // place of a block-wide scan's twenty)
     const int c = tid < E ? cnt[tid] : 0;
     const int ng = (c + kGvMT - 1) / kGvMT;
-    sc[tid] = c;
-    sg[tid] = ng;
-    __syncthreads();
-    for (int off = 1; off < kGvmRouteThreads; off <<= 1) {
-        const int a = tid >= off ? sc[tid - off] : 0, b = tid >= off ? sg[tid - off] : 0;
-        __syncthreads();
-        sc[tid] += a;
-        sg[tid] += b;
-        __syncthreads();
+    int ic = c, ig = ng;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int a = __shfl_up(ic, off, kWave), b = __shfl_up(ig, off, kWave);
+        if (lane >= off) { ic += a; ig += b; }
     }
-    const int off_e = sc[tid] - c, g0 = sg[tid] - ng, groups = sg[kGvmRouteThreads - 1];
+    if (lane == kWave - 1) { wsum[wv][0] = ic; wsum[wv][1] = ig; }
+    __syncthreads();
+    int bc = 0, bg = 0, groups = 0;
+    for (int w = 0; w < kGvmRouteThreads / kWave; ++w) {
+        const int tc = wsum[w][0], tg = wsum[w][1];
+        bc += w < wv ? tc : 0;
+        bg += w < wv ? tg : 0;
+        groups += tg;
+    }
+    const int off_e = bc + ic - c, g0 = bg + ig - ng;
     if (tid < E) {
         ra.counts[tid] = c;
         ra.offsets[tid] = off_e;
