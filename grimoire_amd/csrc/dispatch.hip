@@ -77,29 +77,35 @@ __global__ __launch_bounds__(1024) void disp_scan(int E, int32_t* __restrict__ c
                                                   int32_t* __restrict__ tile_e,
                                                   int32_t* __restrict__ tile_mb, int tmax, int mc,
                                                   int32_t* __restrict__ n_tiles_out) {
-    __shared__ int32_t part[1024];
-    __shared__ int32_t tpart[1024];
+    // per 1024-expert chunk: inclusive scans of counts and tiles within each
+    // wave by lane shifts, then over the 16 waves' totals (two barriers)
+    __shared__ int32_t wsum[16][2];
     __shared__ int32_t carry[2];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     if (threadIdx.x == 0) { carry[0] = 0; carry[1] = 0; }
     __syncthreads();
     for (int e0 = 0; e0 < E; e0 += 1024) {
         const int e = e0 + threadIdx.x;
         const int c = e < E ? counts[e] : 0;
         const int nt = (mc > 0 && e < E) ? (c + mc - 1) / mc : 0;
-        part[threadIdx.x] = c;
-        tpart[threadIdx.x] = nt;
-        __syncthreads();
-        // inclusive Hillis-Steele scans of counts and tiles
-        for (int off = 1; off < 1024; off <<= 1) {
-            const int a = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
-            const int b = threadIdx.x >= off ? tpart[threadIdx.x - off] : 0;
-            __syncthreads();
-            part[threadIdx.x] += a;
-            tpart[threadIdx.x] += b;
-            __syncthreads();
+        int ic = c, it = nt;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int a = __shfl_up(ic, off, 64), b = __shfl_up(it, off, 64);
+            if (lane >= off) { ic += a; it += b; }
         }
-        const int rbase = carry[0] + part[threadIdx.x] - c;
-        const int tbase = carry[1] + tpart[threadIdx.x] - nt;
+        if (lane == 63) { wsum[wv][0] = ic; wsum[wv][1] = it; }
+        __syncthreads();
+        int bc = carry[0], bt = carry[1], totc = 0, tott = 0;
+        for (int w = 0; w < 16; ++w) {
+            const int tc = wsum[w][0], tt = wsum[w][1];
+            bc += w < wv ? tc : 0;
+            bt += w < wv ? tt : 0;
+            totc += tc;
+            tott += tt;
+        }
+        const int rbase = bc + ic - c;
+        const int tbase = bt + it - nt;
         if (e < E) {
             offsets[e] = rbase;
             if (tile_e)
@@ -107,7 +113,7 @@ __global__ __launch_bounds__(1024) void disp_scan(int E, int32_t* __restrict__ c
                     if (tbase + i < tmax) { tile_e[tbase + i] = e; tile_mb[tbase + i] = i; }
         }
         __syncthreads();
-        if (threadIdx.x == 1023) { carry[0] += part[1023]; carry[1] += tpart[1023]; }
+        if (threadIdx.x == 0) { carry[0] += totc; carry[1] += tott; }
         __syncthreads();
     }
     if (tile_e)
