@@ -6,6 +6,8 @@
 #include "router.hpp"
 #include "topk.hpp"
 
+#include <algorithm>
+
 namespace grim {
 
 constexpr int kTopkWaves = 4;
@@ -438,12 +440,193 @@ __global__ __launch_bounds__(256) void router_bf16x3(const float* __restrict__ W
     }
 }
 
+// The same three-limb products on 128 x 128 tiles with K split in two
+// halves (grid z).  What bounds router_bf16x3 at T = 4096, E = 512 is the
+// operand feed: every 64 x 64 tile reads its 64 x rows and 64 W rows over
+// the whole K (1 MB), 2 MB per CU.  Here a work-group reads 128 x rows and
+// 128 W rows over half of K, 1 MB per CU.  The two halves are added into
+// zeroed logits by two float atomics, so the sum is exactly a + b
+// whichever lands first; a bias is added after (logits = (a + b) + bias).
+// x is split only where it is not a bf16 value: the barrier after each K
+// tile's LDS stores tells every wave (per-wave flags in LDS) whether some
+// x of the tile has a mid / lo limb; if none has, the three products of
+// x's only limb run (xh.wl, xh.wm, xh.wh), else the six of router_bf16x3,
+// in its order.
+constexpr int kRsBM = 128, kRsBN = 128, kRsPre = 3, kRsThreads = 512;
+
+// One K tile (32) of 128 rows of src into registers: two 16-byte pieces
+// per thread (row c / 8, K offset 4 (c % 8), c = thread + 512 i); rows past
+// n repeat the last one.
+__device__ __forceinline__ void rs_load(const float* __restrict__ src, int n, int H, int r0, int k0,
+                                        f32x4n (&reg)[2]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = int(threadIdx.x) + i * kRsThreads, r = c >> 3, kc = (c & 7) * 4;
+        const int rr = min(r0 + r, n - 1);
+        reg[i] = *reinterpret_cast<const f32x4n*>(src + int64_t(rr) * H + k0 + kc);
+    }
+}
+
+// The pieces as three bf16 limb planes in LDS; returns whether some value
+// of the thread's pieces is not a bf16 value (when `check`).
+__device__ __forceinline__ int rs_split_store(uint16_t* __restrict__ dst, int plane, const f32x4n (&reg)[2],
+                                              bool check) {
+    uint32_t any = 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = int(threadIdx.x) + i * kRsThreads, r = c >> 3, kc = (c & 7) * 4;
+        if (check)
+            any |= (__float_as_uint(reg[i].x) | __float_as_uint(reg[i].y) | __float_as_uint(reg[i].z) |
+                    __float_as_uint(reg[i].w)) & 0xFFFFu;
+        uint32_t w[3][2];
+        split3(reg[i], w);
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+            *reinterpret_cast<uint2*>(&dst[p * plane + r * kR3LD + kc]) = make_uint2(w[p][0], w[p][1]);
+    }
+    return any != 0u ? 1 : 0;
+}
+
+// 8 waves: wave w computes tokens 32 (w / 2) .. + 32 and experts
+// 64 (w % 2) .. + 64 of the tile (two 32 x 32 MFMA blocks), so two waves
+// share each SIMD and one's LDS traffic and splitting overlap the other's
+// matrix products.
+__global__ __launch_bounds__(kRsThreads) void router_bf16x3_sk(const float* __restrict__ W,
+                                                               const float* __restrict__ x,
+                                                               float* __restrict__ logits, int T, int E, int H) {
+    constexpr int PS = kRsBM * kR3LD;                 // one plane of one operand (BM == BN)
+    constexpr int NW = kRsThreads / 64;
+    __shared__ __attribute__((aligned(16))) uint16_t Xs[2][3 * PS];
+    __shared__ __attribute__((aligned(16))) uint16_t Ws[2][3 * PS];
+    __shared__ __attribute__((aligned(16))) int wflag[2][NW];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, h = lane >> 5;
+    // blockIdx.x = token block (the expert blocks of one token block share
+    // an XCD and its copy of x), blockIdx.z = K half
+    const int t0 = blockIdx.x * kRsBM, e0 = blockIdx.y * kRsBN;
+    const int nk = H / kR3BK / 2, kb = blockIdx.z * nk;
+    f32x4n rx[kRsPre][2], rw[kRsPre][2];
+    f32x16r acc[2];
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[ni][v] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRsPre; ++j) {
+        rs_load(x, T, H, t0, (kb + j) * kR3BK, rx[j]);
+        rs_load(W, E, H, e0, (kb + j) * kR3BK, rw[j]);
+    }
+    {
+        const int any = rs_split_store(Xs[0], PS, rx[0], true);
+        rs_split_store(Ws[0], PS, rw[0], false);
+        const bool b = __ballot(any) != 0;
+        if (lane == 0) wflag[0][wave] = b ? 1 : 0;
+    }
+    __syncthreads();
+    for (int k0 = 0; k0 < nk; k0 += kRsPre) {
+#pragma unroll
+        for (int u = 0; u < kRsPre; ++u) {
+            const int kt = k0 + u, buf = kt & 1;
+            if (kt >= nk) break;
+            const int kn = (kb + min(kt + kRsPre, nk - 1)) * kR3BK;
+            rs_load(x, T, H, t0, kn, rx[u]);
+            rs_load(W, E, H, e0, kn, rw[u]);
+            int fl = 0;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) fl |= wflag[buf][w];
+            const bool full = fl != 0;   // uniform
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const int kk = 16 * h + 8 * ks;
+                const uint16_t* xa = &Xs[buf][(wm * 32 + (lane & 31)) * kR3LD + kk];
+                const bf16x8r a0 = *reinterpret_cast<const bf16x8r*>(xa);
+                bf16x8r b[2][3];
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                    for (int p = 0; p < 3; ++p)
+                        b[ni][p] = *reinterpret_cast<const bf16x8r*>(
+                            &Ws[buf][p * PS + (wn * 64 + ni * 32 + (lane & 31)) * kR3LD + kk]);
+                // router_bf16x3's order: mm, lh, hl, mh, hm, hh (the x-limb
+                // products are zero when the tile's x are bf16 values)
+                if (full) {
+                    const bf16x8r a1 = *reinterpret_cast<const bf16x8r*>(xa + PS);
+                    const bf16x8r a2 = *reinterpret_cast<const bf16x8r*>(xa + 2 * PS);
+#pragma unroll
+                    for (int ni = 0; ni < 2; ++ni) {
+                        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b[ni][1], acc[ni], 0, 0, 0);
+                        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b[ni][0], acc[ni], 0, 0, 0);
+                        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b[ni][2], acc[ni], 0, 0, 0);
+                        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b[ni][0], acc[ni], 0, 0, 0);
+                    }
+                } else {
+#pragma unroll
+                    for (int ni = 0; ni < 2; ++ni)
+                        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b[ni][2], acc[ni], 0, 0, 0);
+                }
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+                    acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b[ni][1], acc[ni], 0, 0, 0);
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+                    acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b[ni][0], acc[ni], 0, 0, 0);
+            }
+            if (kt + 1 < nk) {
+                const int un = (u + 1) % kRsPre;
+                const int any = rs_split_store(Xs[buf ^ 1], PS, rx[un], true);
+                rs_split_store(Ws[buf ^ 1], PS, rw[un], false);
+                const bool b = __ballot(any) != 0;
+                if (lane == 0) wflag[buf ^ 1][wave] = b ? 1 : 0;
+            }
+            __syncthreads();
+        }
+    }
+    // acc[ni][v]: token row (v&3) + 4*(lane>>5) + 8*(v>>2), expert lane&31
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+        const int e = e0 + wn * 64 + ni * 32 + (lane & 31);
+        if (e >= E) continue;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int t = t0 + wm * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
+            if (t < T) unsafeAtomicAdd(&logits[int64_t(t) * E + e], acc[ni][v]);
+        }
+    }
+}
+
+// logits = 0 (bias null) or logits += bias, four values per thread when E
+// is a multiple of 4
+__global__ __launch_bounds__(256) void router_fill_kernel(float* __restrict__ logits, const float* __restrict__ bias,
+                                                          int64_t n, int E) {
+    const int64_t i = (int64_t(blockIdx.x) * 256 + threadIdx.x) * 4;
+    if (i >= n) return;
+    if (E % 4 == 0) {
+        f32x4n v = f32x4n{0.0f, 0.0f, 0.0f, 0.0f};
+        if (bias) {
+            v = *reinterpret_cast<const f32x4n*>(logits + i);
+            const f32x4n b = *reinterpret_cast<const f32x4n*>(bias + i % E);
+            v = f32x4n{v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w};
+        }
+        *reinterpret_cast<f32x4n*>(logits + i) = v;
+    } else {
+        for (int64_t k = i; k < min(n, i + 4); ++k) logits[k] = bias ? logits[k] + bias[k % E] : 0.0f;
+    }
+}
+
 hipError_t router_logits_launch(hipStream_t st, const float* W, const float* x,
                                 const float* bias, float* logits, int T, int E, int H) {
     if (T <= 32 && H % 4 == 0 && router_nk_launch(st, W, x, bias, logits, T, E, H)) {
     } else if (T <= 32 && H % 4 == 0) {
         dim3 grid(E, (T + kRouterTok - 1) / kRouterTok);
         hipLaunchKernelGGL(router_gemv, grid, dim3(256), 0, st, W, x, bias, logits, T, E, H);
+    } else if (H % (2 * kR3BK) == 0 && H >= 2 * kR3BK * kRsPre && T >= 256) {
+        // split K: zero the logits, both halves add into them, then the bias
+        const int64_t n = int64_t(T) * E;
+        const unsigned fb = unsigned((n + 1023) / 1024);
+        hipLaunchKernelGGL(router_fill_kernel, dim3(fb), dim3(256), 0, st, logits, nullptr, n, E);
+        dim3 grid((T + kRsBM - 1) / kRsBM, (E + kRsBN - 1) / kRsBN, 2);
+        hipLaunchKernelGGL(router_bf16x3_sk, grid, dim3(kRsThreads), 0, st, W, x, logits, T, E, H);
+        if (bias) hipLaunchKernelGGL(router_fill_kernel, dim3(fb), dim3(256), 0, st, logits, bias, n, E);
     } else if (H % (kR3BK * kR3Pre) == 0) {
         dim3 grid((T + 63) / 64, (E + 63) / 64);
         hipLaunchKernelGGL(router_bf16x3, grid, dim3(256), 0, st, W, x, bias, logits, T, E, H);
