@@ -99,6 +99,7 @@ struct Plan {
     // INT8 weights: activation limbs for the int8 MFMA
     int8_t *xq, *xrowq, *hq, *hshq;
     float *sx, *sxrow, *sh, *shsh, *h32, *h32sh;
+    int32_t* qperm;   // token of every routed row (the gate_up GEMM's gather map)
     // expert-grouped GEMV (gemv_grouped.hip): its own tile table (MT-row
     // blocks), the route -> token map and fp32 h rows
     int32_t *gv_te, *gv_tm, *gv_perm;
@@ -176,9 +177,10 @@ size_t carve(const grim_moe_layer* L, int T, bool gemv, char* base, Plan& p) {
             p.h32 = cv.take<float>(R * I);
             p.hq = cv.take<int8_t>(R * 2 * I);
             p.sh = cv.take<float>(R);
+            p.xrowq = cv.take<int8_t>(size_t(T) * 2 * H);
+            p.sxrow = cv.take<float>(T);
+            p.qperm = cv.take<int32_t>(R);
             if (sh) {
-                p.xrowq = cv.take<int8_t>(size_t(T) * 2 * H);
-                p.sxrow = cv.take<float>(T);
                 p.h32sh = cv.take<float>(size_t(T) * I);
                 p.hshq = cv.take<int8_t>(size_t(T) * 2 * I);
                 p.shsh = cv.take<float>(T);
@@ -228,8 +230,10 @@ extern "C" __attribute__((visibility("default"))) void grim_timing_set(void* p) 
 #endif
 
 // GEMM regime for INT8 weights: the activations go to the int8 MFMA as
-// two limbs per row (gemm_i8.hip): routes -> limbs of x at the permuted rows
-// -> gate_up + SwiGLU (h fp32) -> limbs of h -> down -> combine.
+// two limbs per row (gemm_i8.hip): routes -> limbs of x (once per token,
+// gathered by the GEMM through the route -> token map; at every permuted
+// row when K is too short for the gather) -> gate_up + SwiGLU (h fp32) ->
+// limbs of h -> down -> combine.
 static int forward_gemm_i8(hipStream_t st, const grim_moe_layer* L, const Plan& p, const float* x,
                            float* y, int tokens, const uint16_t* shared_gate_w) {
     const auto& c = L->cfg;
@@ -241,8 +245,13 @@ static int forward_gemm_i8(hipStream_t st, const grim_moe_layer* L, const Plan& 
                                        kGemmBM, K, nullptr, p.disp_ws,
                                        dispatch_workspace_bytes(tokens, K, E));
     if (r) return r;
-    hipError_t e = quant_permute_launch(st, x, tokens, H, K, p.inverse, p.xq, p.sx,
-                                        sh ? p.xrowq : nullptr, sh ? p.sxrow : nullptr);
+    // gather mode: x limbs once per token, the gate_up GEMM reads each
+    // routed row's token row through qperm; otherwise limbs at every
+    // routed row
+    const bool gather = gemm_i8_gather_ok(H, tokens) && E <= kI8MaxListExperts;
+    hipError_t e = quant_permute_launch(st, x, tokens, H, K, p.inverse, gather ? nullptr : p.xq, p.sx,
+                                        (sh || gather) ? p.xrowq : nullptr,
+                                        (sh || gather) ? p.sxrow : nullptr, gather ? p.qperm : nullptr);
     if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
     if (sh && shared_gate_w) {
         e = rowdot_sigmoid_launch(st, x, shared_gate_w, p.gate, tokens, H);
@@ -261,8 +270,10 @@ static int forward_gemm_i8(hipStream_t st, const grim_moe_layer* L, const Plan& 
     g.K = H;
     g.I = I;
     g.swiglu = 1;
-    g.A = p.xq;
+    g.A = gather ? p.xrowq : p.xq;
     g.sa = p.sx;
+    g.gather = gather ? p.qperm : nullptr;
+    g.gather_rows = tokens;
     g.A_sh = p.xrowq;
     g.sa_sh = p.sxrow;
     g.out = p.h32;
@@ -300,6 +311,7 @@ static int forward_gemm_i8(hipStream_t st, const grim_moe_layer* L, const Plan& 
     d.swiglu = 0;
     d.A = p.hq;
     d.sa = p.sh;
+    d.gather = nullptr;
     d.A_sh = p.hshq;
     d.sa_sh = p.shsh;
     d.out = p.yperm;

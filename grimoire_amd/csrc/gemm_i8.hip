@@ -50,6 +50,9 @@ constexpr int kQStages = 4;
 constexpr int kQStageBytes = 32768;          // A 16 KiB (2 limbs x 4 x 2 fragments), B 16 KiB
 constexpr int kQXcds = 8;
 constexpr float kLoScale = 1.0f / 254.0f;
+// gather mode: the A offset of a row past an item's count (beyond every
+// gather buffer, which the host keeps below it: the load returns zeros)
+constexpr int kI8FarOffset = 0x70000000;
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -250,7 +253,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t i8_rsrc(const void* p, int byt
 template <bool SWIGLU>
 __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, int parts,
                                            int n_routed, int tp_addr, int slot, int per_xcd,
-                                           uint8_t (*smem)[kQStageBytes], float (*meta)[512]) {
+                                           uint8_t (*smem)[kQStageBytes], float (*meta)[512],
+                                           int32_t (*rmap)[256]) {
     // 8 waves, two per SIMD: wave w owns tile columns [64 (w % 4), +64) for
     // rows [64 (w / 4), +64)
     constexpr int MIW = 2;                   // 32-row MFMA tiles per wave
@@ -294,14 +298,12 @@ __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, 
     // here and again at every item's start, so that they are not kept live
     // (and spilled) across the epilogue, whose reloads would make the
     // compiler wait for every outstanding load before each fragment read.
-    int a_off[NJ], b_off[NJ], fa_off[2][2][MIW], fb_off[2][2];
+    int a_off[NJ], a_offn[NJ], b_off[NJ], fa_off[2][2][MIW], fb_off[2][2];
 #define GRIM_I8_OFFSETS()                                                                         \
     do {                                                                                          \
         const int ln = lane_id();                                                                 \
         _Pragma("unroll") for (int j = 0; j < NJ; ++j) {                                          \
             const int ja = NJ * wave + j;                                                         \
-            const int r = 8 * ja + (ln >> 3), pc = ln & 7;                                        \
-            a_off[j] = r * a_row_bytes + ((pc ^ ((r >> 1) & 7)) << 4);                            \
             const int col = 16 * ja + (ln >> 2), pcb = ln & 3;                                    \
             const int nsub = col >> 5, x = col & 31;                                              \
             /* SwiGLU: h columns [32 w', +32) of wave w' = nsub / 2: gate rows */                 \
@@ -324,6 +326,27 @@ __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, 
         }                                                                                         \
     } while (0)
     GRIM_I8_OFFSETS();
+    // A rows: lane (j, ln) moves tile row 8 (NJ wave + j) + ln / 8, chunk
+    // ln % 8.  Contiguous items read row r of their base; gather-mode
+    // routed items read the row the map names (from the map's LDS copy at
+    // rm_addr), and rows past the item's count an address past the buffer
+    // (zeros).
+    const bool gat = g.gather != nullptr;
+    const int rmap_base = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int32_t*)(&rmap[0][0])));
+    auto a_offsets = [&](const I8Item& it, int rm_addr, int (&o)[NJ]) {
+        const int ln = lane_id();
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int r = 8 * (NJ * wave + j) + (ln >> 3), pc = ln & 7;
+            const int sw = (pc ^ ((r >> 1) & 7)) << 4;
+            if (gat && !it.sh) {
+                const int src = lds_i32(rm_addr + 4 * r);
+                o[j] = r < it.rows ? src * a_row_bytes + sw : kI8FarOffset;
+            } else {
+                o[j] = r * a_row_bytes + sw;
+            }
+        }
+    };
 
     auto tile_of = [&](int ii) { return lo + ii / n_col_tiles; };
     auto col_of = [&](int ii) { return ii % n_col_tiles; };
@@ -333,6 +356,7 @@ __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, 
     // I rows later (gate rows past I read up rows: their columns are never
     // stored).  rows == 0 (past the last item) gives empty buffers.
     auto rsrc_a = [&](const I8Item& it) {
+        if (gat && !it.sh) return i8_rsrc(src_r.A, it.rows > 0 ? g.gather_rows * a_row_bytes : 0);
         const int8_t* A = it.sh ? src_s.A : src_r.A;
         return i8_rsrc(A + it.arow0 * a_row_bytes, it.rows * a_row_bytes);
     };
@@ -341,13 +365,17 @@ __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, 
         return i8_rsrc(w + it.wrow * wrb, it.rows > 0 ? int((n_slab - it.col0) * wrb) : 0);
     };
     // scale requests: wave 0 the 128 row scales (lanes 32..63 past the end
-    // read zero into padding), wave 1 the 256 column scales
+    // read zero into padding), wave 1 the 256 column scales; in gather mode
+    // wave 2 the item's row map
     auto request_meta = [&](const I8Item& it, int par) {
         const int ln = lane_id();
         if (wave == 0) {
             dma16<0>(i8_rsrc((it.sh ? src_s.sa : src_r.sa) + it.arow0, it.rows * 4),
                      reinterpret_cast<uint8_t*>(&meta[par][0]),
                      ln * 16, 0);
+        } else if (wave == 2 && gat) {
+            dma16<0>(i8_rsrc(g.gather + it.arow0, it.sh ? 0 : it.rows * 4),
+                     reinterpret_cast<uint8_t*>(&rmap[par][0]), ln * 16, 0);
         } else if (wave == 1) {
             const int m_off = (SWIGLU && ln >= 32) ? g.I * 4 + (ln - 32) * 16 : ln * 16;
             dma16<0>(i8_rsrc((it.sh ? src_s.ws : src_r.ws) + it.wrow, it.rows > 0 ? (n_slab - it.col0) * 4 : 0),
@@ -364,11 +392,17 @@ __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, 
             dma16<0>(rb, st + 16384 + (NJ * wave + j) * 1024, b_off[j], t * QBK);
     };
 
-    const int nk = K / QBK;   // >= 3
+    const int nk = K / QBK;   // >= 3 (gather mode: >= 6)
     I8Item cur = i8_item<SWIGLU, QBM, QBN>(g, n_routed, tile_of(i), col_of(i), tp_addr);
     I8Item none;
     none.arow0 = 0; none.wrow = 0; none.rows = 0; none.col0 = 0; none.sh = 0;
     request_meta(cur, 0);
+    if (gat) {
+        // the first item's map, before its first tiles
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+    a_offsets(cur, rmap_base, a_off);
 #pragma unroll
     for (int p = 0; p < kQStages - 1; ++p) request(cur, p, p);
 
@@ -381,6 +415,9 @@ __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, 
     i32x4 fb[2][2], fa[2][2][MIW];
     for (; i < items; i += per_xcd) {
         GRIM_I8_OFFSETS();
+        a_offsets(cur, rmap_base + par * 1024, a_off);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) a_offn[j] = a_off[j];
         const bool more = i + per_xcd < items;
         const I8Item nxt = more ? i8_item<SWIGLU, QBM, QBN>(g, n_routed, tile_of(i + per_xcd), col_of(i + per_xcd), tp_addr)
                                 : none;
@@ -430,13 +467,15 @@ __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, 
                                                                         acc[l][mi_][ni], 0, 0, 0)
 #define GRIM_I8_DMA(q)                                                                            \
         do {                                                                                      \
-            if ((q) < NJ) dma16<0>(qa, nx + (NJ * wave + (q)) * 1024, a_off[(q) % NJ], tu * 128); \
+            if ((q) < NJ) dma16<0>(qa, nx + (NJ * wave + (q)) * 1024, own ? a_off[(q) % NJ] : a_offn[(q) % NJ], tu * 128); \
             else dma16<0>(qb, nx + 16384 + (NJ * wave + (q) - NJ) * 1024, b_off[(q) % NJ], tu * QBK); \
         } while (0)
 #define GRIM_I8_ITER(t_, META)                                                                    \
         do {                                                                                      \
             const int t = (t_);                                                                   \
             GRIM_I8_WAIT((t < 3 && !first) ? 1 : 0);                                              \
+            /* the next item's row map (requested at t = 0, landed by t = 3) */                   \
+            if (gat && t == nk - (kQStages - 1)) a_offsets(nxt, rmap_base + (par ^ 1) * 1024, a_offn); \
             const int sb = ((gs + t) & 3) * kQStageBytes + smem_base;                             \
             _Pragma("unroll") for (int ks = 0; ks < 2; ++ks) {                                    \
                 GRIM_I8_DSR(fb[ks][0], sb + fb_off[ks][0]);                                       \
@@ -554,13 +593,14 @@ __global__ __launch_bounds__(kQThreads) void grouped_gemm_i8_kernel(GemmI8Args g
                                                                    int parts) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kQStages][kQStageBytes];
     __shared__ __attribute__((aligned(16))) float meta[2][512];
+    __shared__ __attribute__((aligned(16))) int32_t rmap[2][256];
     int n_routed = 0;
     if (parts & 1) {
         n_routed = g.n_tiles_dev ? __builtin_amdgcn_readfirstlane(*g.n_tiles_dev) : g.tmax;
         n_routed = n_routed < g.tmax ? n_routed : g.tmax;
     }
     i8_big_run<SWIGLU>(g, n_col_tiles, parts, n_routed, -1, blockIdx.x / kQXcds, gridDim.x / kQXcds,
-                       smem, meta);
+                       smem, meta, rmap);
 }
 
 // ------------------------------------------------------- narrow tiles
@@ -592,7 +632,8 @@ bool gemm_i8_narrow_ok(int K) { return K % NBK == 0 && K >= (kNStages - 1) * NBK
 template <bool SWIGLU>
 __device__ __forceinline__ void i8_narrow_run(const GemmI8Args& g, int n_col_tiles, int total,
                                               int tp_addr, int slot, int per_xcd,
-                                              uint8_t (*smem)[kNStageBytes], float (*meta)[512]) {
+                                              uint8_t (*smem)[kNStageBytes], float (*meta)[512],
+                                              int32_t (*rmap)[256]) {
     constexpr int NJA = 2, NJB = 8;          // A / B instructions per wave per stage
     constexpr int OPS = NJA + NJB;
     // meta, per item parity: row scales [32] at 0 (the DMA pads to 256),
@@ -616,14 +657,10 @@ __device__ __forceinline__ void i8_narrow_run(const GemmI8Args& g, int n_col_til
     //     n * 128, chunk c at slot c ^ ((n >> 1) & 7).
     // A fragment read (32 rows, one chunk) and a B fragment read (32
     // columns, one chunk) each hit 16 distinct 16-byte slots per 16 lanes.
-    int a_off[NJA], b_off[NJB], fa_off[2][2][2], fb_off[2][2][2];
+    int a_off[NJA], a_offn[NJA], b_off[NJB], fa_off[2][2][2], fb_off[2][2][2];
 #define GRIM_N8_OFFSETS()                                                                         \
     do {                                                                                          \
         const int ln = lane_id();                                                                 \
-        _Pragma("unroll") for (int j = 0; j < NJA; ++j) {                                         \
-            const int r = 4 * (NJA * wave + j) + (ln >> 4), sl = ln & 15;                         \
-            a_off[j] = r * a_row_bytes + ((sl ^ (r & 15)) << 4);                                  \
-        }                                                                                         \
         _Pragma("unroll") for (int j = 0; j < NJB; ++j) {                                         \
             const int col = 8 * (NJB * wave + j) + (ln >> 3), sl = ln & 7;                        \
             const int nsub = col >> 5, x = col & 31;                                              \
@@ -643,12 +680,31 @@ __device__ __forceinline__ void i8_narrow_run(const GemmI8Args& g, int n_col_til
             }                                                                                     \
     } while (0)
     GRIM_N8_OFFSETS();
+    // A rows: lane (j, ln) moves tile row 4 (NJA wave + j) + ln / 16,
+    // chunk ln % 16; gather mode as in the 128-row kernel
+    const bool gat = g.gather != nullptr;
+    const int rmap_base = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int32_t*)(&rmap[0][0])));
+    auto a_offsets = [&](const I8Item& it, int rm_addr, int (&o)[NJA]) {
+        const int ln = lane_id();
+#pragma unroll
+        for (int j = 0; j < NJA; ++j) {
+            const int r = 4 * (NJA * wave + j) + (ln >> 4), sl = ln & 15;
+            const int sw = (sl ^ (r & 15)) << 4;
+            if (gat) {
+                const int src = lds_i32(rm_addr + 4 * r);
+                o[j] = r < it.rows ? src * a_row_bytes + sw : kI8FarOffset;
+            } else {
+                o[j] = r * a_row_bytes + sw;
+            }
+        }
+    };
 
     auto tile_of = [&](int ii) { return lo + ii / n_col_tiles; };
     auto col_of = [&](int ii) { return ii % n_col_tiles; };
     const int n_slab = SWIGLU ? 2 * g.I : g.N;
     const int ldo = SWIGLU ? g.I : g.N;
     auto rsrc_a = [&](const I8Item& it) {
+        if (gat) return i8_rsrc(g.A, it.rows > 0 ? g.gather_rows * a_row_bytes : 0);
         return i8_rsrc(g.A + it.arow0 * a_row_bytes, it.rows * a_row_bytes);
     };
     auto rsrc_b = [&](const I8Item& it) {
@@ -660,6 +716,9 @@ __device__ __forceinline__ void i8_narrow_run(const GemmI8Args& g, int n_col_til
         const int ln = lane_id();
         if (wave == 0) {
             dma16<0>(i8_rsrc(g.sa + it.arow0, it.rows * 4), reinterpret_cast<uint8_t*>(&meta[par][0]),
+                     ln * 16, 0);
+        } else if (wave == 2 && gat) {
+            dma16<0>(i8_rsrc(g.gather + it.arow0, it.rows * 4), reinterpret_cast<uint8_t*>(&rmap[par][0]),
                      ln * 16, 0);
         } else if (wave == 1) {
             const int m_off = (SWIGLU && ln >= 32) ? g.I * 4 + (ln - 32) * 16 : ln * 16;
@@ -676,11 +735,16 @@ __device__ __forceinline__ void i8_narrow_run(const GemmI8Args& g, int n_col_til
         for (int j = 0; j < NJB; ++j) dma16<0>(rb, st + kNA + (NJB * wave + j) * 1024, b_off[j], t * NBK);
     };
 
-    const int nk = K / NBK;   // >= kNStages - 1
+    const int nk = K / NBK;   // >= kNStages - 1 (gather mode: >= 4)
     I8Item cur = i8_item<SWIGLU, NBM, NBN>(g, total, tile_of(i), col_of(i), tp_addr);
     I8Item none;
     none.arow0 = 0; none.wrow = 0; none.rows = 0; none.col0 = 0; none.sh = 0;
     request_meta(cur, 0);
+    if (gat) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+    a_offsets(cur, rmap_base, a_off);
 #pragma unroll
     for (int p = 0; p < kNStages - 1; ++p) request(cur, p, p);
 
@@ -692,6 +756,9 @@ __device__ __forceinline__ void i8_narrow_run(const GemmI8Args& g, int n_col_til
     i32x4 fb[2][2], fa[2][2];
     for (; i < items; i += per_xcd) {
         GRIM_N8_OFFSETS();
+        a_offsets(cur, rmap_base + par * 1024, a_off);
+#pragma unroll
+        for (int j = 0; j < NJA; ++j) a_offn[j] = a_off[j];
         const bool more = i + per_xcd < items;
         const I8Item nxt = more ? i8_item<SWIGLU, NBM, NBN>(g, total, tile_of(i + per_xcd), col_of(i + per_xcd), tp_addr)
                                 : none;
@@ -735,13 +802,15 @@ __device__ __forceinline__ void i8_narrow_run(const GemmI8Args& g, int n_col_til
         }
 #define GRIM_N8_DMA(q)                                                                            \
         do {                                                                                      \
-            if ((q) < NJA) dma16<0>(qa, nx + (NJA * wave + (q)) * 1024, a_off[(q) % NJA], tu * 256); \
+            if ((q) < NJA) dma16<0>(qa, nx + (NJA * wave + (q)) * 1024, own ? a_off[(q) % NJA] : a_offn[(q) % NJA], tu * 256); \
             else dma16<0>(qb, nx + kNA + (NJB * wave + (q) - NJA) * 1024, b_off[((q) + NJB - NJA) % NJB], tu * NBK); \
         } while (0)
 #define GRIM_N8_ITER(t_, META)                                                                    \
         do {                                                                                      \
             const int t = (t_);                                                                   \
             GRIM_N8_WAIT((t < kNStages - 1 && !first) ? 1 : 0);                                   \
+            /* the next item's row map (requested at t = 0, landed by t = 2) */                   \
+            if (gat && t == nk - (kNStages - 1)) a_offsets(nxt, rmap_base + (par ^ 1) * 1024, a_offn); \
             const int slot = (gs + t) % kNStages;                                                 \
             const int sb = slot * kNStageBytes + smem_base;                                       \
             GRIM_N8_READS(0);                                                                     \
@@ -843,6 +912,7 @@ __global__ __launch_bounds__(kQThreads) void grouped_gemm_i8_rows_kernel(GemmI8A
     __shared__ __attribute__((aligned(1024))) uint8_t ring[kQStages * kQStageBytes];
     __shared__ __attribute__((aligned(16))) float meta[2][512];
     __shared__ int32_t tpb[kI8MaxListExperts], tpn[kI8MaxListExperts];
+    __shared__ __attribute__((aligned(16))) int32_t rmap[2][256];
     static_assert(kNStages * kNStageBytes <= kQStages * kQStageBytes, "narrow ring fits");
     int32_t* tmp = reinterpret_cast<int32_t*>(ring);
     const int E = g.num_experts;
@@ -851,13 +921,13 @@ __global__ __launch_bounds__(kQThreads) void grouped_gemm_i8_rows_kernel(GemmI8A
     const int S = gridDim.x / kQXcds;            // work-group slots per XCD
     const int tpa_b = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int32_t*)(&tpb[0])));
     const int next = i8_big_run<SWIGLU>(g, nct_big, parts, nb, tpa_b, blockIdx.x / kQXcds, S,
-                                        reinterpret_cast<uint8_t (*)[kQStageBytes]>(ring), meta);
+                                        reinterpret_cast<uint8_t (*)[kQStageBytes]>(ring), meta, rmap);
     if (nn == 0) return;
     __syncthreads();                             // every wave is past the 128-row ring
     if (threadIdx.x >= kNThreads) return;
     const int tpa_n = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int32_t*)(&tpn[0])));
     i8_narrow_run<SWIGLU>(g, nct_nar, nn, tpa_n, next, S,
-                          reinterpret_cast<uint8_t (*)[kNStageBytes]>(ring), meta);
+                          reinterpret_cast<uint8_t (*)[kNStageBytes]>(ring), meta, rmap);
 }
 
 // ------------------------------------------------------------ quantisers
@@ -972,13 +1042,16 @@ __global__ __launch_bounds__(256) void quant_rows_short_kernel(const float* __re
 }
 
 // The activations of every token as limbs, written to each of its K
-// permuted rows (inverse) and to its own row (xrow, the shared expert's
-// input) when given.  One work-group of 256 threads per token, n <= 8192.
+// permuted rows (inverse) when xq is given and to its own row (xrowq: the
+// shared expert's input, and the gather source of gather mode) when given;
+// the scale to every permuted row, and the token to perm[permuted row].
+// One work-group of 256 threads per token, n <= 8192.
 __global__ __launch_bounds__(256) void quant_permute_kernel(const float* __restrict__ x, int n, int K,
                                                             const int32_t* __restrict__ inverse,
                                                             int8_t* __restrict__ xq, float* __restrict__ sq,
                                                             int8_t* __restrict__ xrowq,
-                                                            float* __restrict__ srow) {
+                                                            float* __restrict__ srow,
+                                                            int32_t* __restrict__ perm) {
     __shared__ float red[4];
     const int t = blockIdx.x;
     const float* s = x + int64_t(t) * n;
@@ -1009,7 +1082,7 @@ __global__ __launch_bounds__(256) void quant_permute_kernel(const float* __restr
             const float v[8] = {va[q].x, va[q].y, va[q].z, va[q].w, vb[q].x, vb[q].y, vb[q].z, vb[q].w};
             uint32_t h0, h1, l0, l1;
             limbs8(v, inv, h0, h1, l0, l1);
-            for (int k = 0; k < K; ++k) {
+            for (int k = 0; k < K && xq; ++k) {
                 if (dst[k] < 0) continue;
                 int8_t* d = xq + int64_t(dst[k]) * 2 * n + limb_block(c);
                 *reinterpret_cast<uint2*>(d) = make_uint2(h0, h1);
@@ -1024,7 +1097,10 @@ __global__ __launch_bounds__(256) void quant_permute_kernel(const float* __restr
     }
     if (int(threadIdx.x) < K) {
         const int dk = inverse[int64_t(t) * K + threadIdx.x];
-        if (dk >= 0) sq[dk] = sc;
+        if (dk >= 0) {
+            sq[dk] = sc;
+            if (perm) perm[dk] = t;
+        }
     }
     if (srow && threadIdx.x == 0) srow[t] = sc;
 }
@@ -1083,8 +1159,17 @@ bool gemm_i8_shape_ok(int N, int K, int I, int swiglu) {
     return N > 0;
 }
 
+bool gemm_i8_gather_ok(int K, int rows) {
+    // the next item's row map is read at its first streamed tile: 128-row
+    // kernel nk - 3 >= 3, narrow kernel (when it runs) nk - 2 >= 2
+    const bool big = K % QBK == 0 && K / QBK >= 6;
+    const bool nar = !gemm_i8_narrow_ok(K) || K / NBK >= 4;
+    return big && nar && rows > 0 && int64_t(rows) * 2 * K < kI8FarOffset;
+}
+
 hipError_t gemm_i8_launch(hipStream_t st, const GemmI8Args& g) {
     if (!gemm_i8_shape_ok(g.N, g.K, g.I, g.swiglu)) return hipErrorInvalidValue;
+    if (g.gather && !gemm_i8_gather_ok(g.K, g.gather_rows)) return hipErrorInvalidValue;
     if (g.split > 0 && (g.num_experts <= 0 || g.num_experts > kI8MaxListExperts))
         return hipErrorInvalidValue;
     if (g.split > 0) {
@@ -1118,11 +1203,11 @@ hipError_t quant_rows_launch(hipStream_t st, const float* src, int rows, int n, 
 
 hipError_t quant_permute_launch(hipStream_t st, const float* x, int T, int n, int K,
                                 const int32_t* inverse, int8_t* xq, float* sq, int8_t* xrowq,
-                                float* srow) {
+                                float* srow, int32_t* perm) {
     if (T <= 0) return hipSuccess;
     if (n % 64 || n > 8192 || K > 16) return hipErrorInvalidValue;
     hipLaunchKernelGGL(quant_permute_kernel, dim3(T), dim3(256), 0, st, x, n, K, inverse, xq, sq,
-                       xrowq, srow);
+                       xrowq, srow, perm);
     return hipGetLastError();
 }
 

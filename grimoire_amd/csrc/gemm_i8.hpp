@@ -36,6 +36,11 @@ struct GemmI8Args {
     int split;
     int num_experts;
     int list_lo;                // set by the launcher: the 128-row list takes counts > list_lo
+    // gather mode (gather != null): the routed rows are not stored permuted;
+    // routed row r reads row gather[r] of A (gather_rows rows), the row
+    // scales stay per routed row (sa[r])
+    const int32_t* gather;
+    int gather_rows;
 };
 
 constexpr int kI8MaxListExperts = 1024;
@@ -43,15 +48,20 @@ constexpr int kI8MaxListExperts = 1024;
 constexpr int kI8DefaultSplit = 64;
 
 bool gemm_i8_shape_ok(int N, int K, int I, int swiglu);
+// gather mode needs K tiles enough for a row map requested with an item's
+// first tile to land before the item streams its successor's first tiles
+bool gemm_i8_gather_ok(int K, int rows);
 hipError_t gemm_i8_launch(hipStream_t st, const GemmI8Args& g);
 // src fp32 [rows][n] -> limb rows [rows][n/64][2][64] + scale [rows]
 // (n % 64 == 0, n <= 4096)
 hipError_t quant_rows_launch(hipStream_t st, const float* src, int rows, int n, int8_t* dst,
                              float* scale);
 // token rows of x fp32 [T][n] -> limbs at their K permuted rows (inverse
-// [T][K]) and, when xrowq is given, at their own row
+// [T][K]) when xq is given, at their own row when xrowq is given; the row
+// scale at every permuted row (sq) and own row (srow); perm, when given,
+// gets the token of every permuted row (the gather map of gather mode)
 hipError_t quant_permute_launch(hipStream_t st, const float* x, int T, int n, int K,
                                 const int32_t* inverse, int8_t* xq, float* sq, int8_t* xrowq,
-                                float* srow);
+                                float* srow, int32_t* perm);
 
 }  // namespace grim

@@ -85,6 +85,21 @@ def test_forward_c4_scaled_both_regimes(gpu, regime):
     assert_close(y, yo, what=f"c4 scaled regime {regime}")
 
 
+@pytest.mark.parametrize("H", [384, 512, 2048])
+def test_forward_int8_gather_edges(gpu, H):
+    """The INT8 prefill reads x limbs per token through the route -> token
+    map when K = H holds enough K tiles (H >= 512 here), and writes them at
+    every permuted row otherwise (H = 384); both against the oracle, with
+    the shared expert, on a Zipf-skewed routing that fills both tile kinds."""
+    print(f"forward int8 gather edge H={H}", flush=True)
+    cfg = configs.scaled(configs.CONFIGS["c4"], T=200, H=H, E=32, I=128)
+    wl = configs.make_workload(cfg, "cpu", seed=9)
+    Lg, y, oe, ow, logits = _run(wl, gpu, regime=2)
+    _check_routing(wl, logits, oe, ow)
+    yo = _oracle_y(wl.layer, wl.x, oe, ow, wl.layer.shared_gate_w)
+    assert_close(y, yo, what=f"int8 prefill H={H}")
+
+
 def test_forward_c5_scaled(gpu):
     print("forward c5 scaled (group-limited sigmoid, mxfp4, shared)", flush=True)
     cfg = configs.scaled(configs.CONFIGS["c5"], T=32, H=1024, E=64, I=256)
