@@ -91,6 +91,7 @@ struct Plan {
     uint32_t* xf;   // decode: x formatted for the wave-centric gate_up
     float* hrep;    // fused decode: copies of h
     // GEMM
+    float* logits2;   // the split-K router's second partial
     void* disp_ws;
     int32_t *counts, *offsets, *inverse, *tile_e, *tile_mb;
     int tmax;
@@ -145,6 +146,7 @@ size_t carve(const grim_moe_layer* L, int T, bool gemv, char* base, Plan& p) {
     } else {
         const size_t dws = dispatch_workspace_bytes(T, K, E);
         p.disp_ws = cv.take<char>(dws);
+        p.logits2 = cv.take<float>(size_t(T) * E);
         p.counts = cv.take<int32_t>(E);
         p.offsets = cv.take<int32_t>(E);
         p.inverse = cv.take<int32_t>(R);
@@ -674,20 +676,32 @@ static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_
         return GRIM_OK;
     }
 
+    int deferred = 0;
     {
-        hipError_t e = router_logits_launch(st, L->router, x, rbias, p.logits, tokens, E, H);
+        hipError_t e = router_logits_launch(st, L->router, x, rbias, p.logits, tokens, E, H,
+                                            gemv ? nullptr : p.logits2, &deferred);
         if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
     }
     int r = GRIM_OK;
-    const TopkArgs tka{p.logits, tokens, E, K, topk_mode, c.norm_topk, scaling, b16, b32,
-                       rp ? rp->n_group : 0, rp ? rp->topk_group : 0, p.rex, p.rwt};
+    TopkArgs tka{p.logits, tokens, E, K, topk_mode, c.norm_topk, scaling, b16, b32,
+                 rp ? rp->n_group : 0, rp ? rp->topk_group : 0, p.rex, p.rwt};
     // few rows per expert (on average at most 2): stream each expert once
     // per group of rows instead of once per 128-row MFMA tile
     const bool gv = !gemv && p.gv_te &&
                     (regime == 4 || regime == 5 || (regime == 0 && int64_t(tokens) * K <= 2 * int64_t(E)));
     const bool gv_mx = gv && regime != 5 && L->gate_up.fmt == GRIM_FMT_MXFP4 && gvm_shape_ok(H, I);
-    if (gv_mx && int64_t(tokens) * K <= kGvmRouteMax && !shard)
+    if (gv_mx && int64_t(tokens) * K <= kGvmRouteMax && !shard) {
+        if (deferred) {
+            hipError_t e = router_finish_launch(st, p.logits, p.logits2, rbias, tokens, E);
+            if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
+        }
         return forward_gv(st, L, p, x, y, tokens, shared_gate_w, true, &tka);
+    }
+    if (deferred) {
+        // the top-k finishes the split router's sum as it loads
+        tka.part1 = p.logits2;
+        tka.lbias = rbias;
+    }
     {
         hipError_t e = topk_launch(st, tka);
         if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));

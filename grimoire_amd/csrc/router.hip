@@ -25,6 +25,41 @@ __global__ __launch_bounds__(kTopkWaves * kWave) void topk_kernel(
               topk_group, out_e + int64_t(t) * K, out_w + int64_t(t) * K, gsel[wv], gscore[wv]);
 }
 
+// The same on split-K router partials: logits = (a + b) + bias formed as
+// they are loaded (the arithmetic of the router's own finishing pass, so
+// the same bits) and written back in place, then the top-k.
+__global__ __launch_bounds__(kTopkWaves * kWave) void topk_split_kernel(
+    float* __restrict__ logits, const float* __restrict__ part1, const float* __restrict__ lbias,
+    int T, int E, int K, int mode, int normalize,
+    float scaling, const uint16_t* __restrict__ bias16, const float* __restrict__ bias32,
+    int n_group, int topk_group, int32_t* __restrict__ out_e, float* __restrict__ out_w) {
+    __shared__ float gsel[kTopkWaves][512];
+    __shared__ float gscore[kTopkWaves][64];
+    const int wv = threadIdx.x / kWave;
+    const int t = blockIdx.x * kTopkWaves + wv;
+    if (t >= T) return;   // whole wave exits together
+    const int lane = threadIdx.x & (kWave - 1);
+    const int V = (E + kWave - 1) / kWave;
+    float* row = logits + int64_t(t) * E;
+    const float* row1 = part1 + int64_t(t) * E;
+    float lv[kMaxV];
+#pragma unroll
+    for (int j = 0; j < kMaxV; ++j) {
+        const int e = lane * V + j;
+        const int ec = (j < V && e < E) ? e : 0;
+        float v = row[ec] + row1[ec];
+        if (lbias) v += lbias[ec];
+        lv[j] = v;
+    }
+#pragma unroll
+    for (int j = 0; j < kMaxV; ++j) {
+        const int e = lane * V + j;
+        if (j < V && e < E) row[e] = lv[j];
+    }
+    topk_wave_regs(lv, E, K, mode, normalize, scaling, bias16, bias32, n_group, topk_group,
+                   out_e + int64_t(t) * K, out_w + int64_t(t) * K, gsel[wv], gscore[wv]);
+}
+
 // launch_router_topk_bf16_batched (src/ops.cpp:1425-1480): the batched
 // softmax top-k (mode 1) on bf16 logits
 __global__ __launch_bounds__(kTopkWaves * kWave) void topk_bf16_kernel(
@@ -51,6 +86,13 @@ hipError_t topk_bf16_launch(hipStream_t st, const uint16_t* logits, int T, int E
 
 hipError_t topk_launch(hipStream_t st, const TopkArgs& a) {
     dim3 grid((a.T + kTopkWaves - 1) / kTopkWaves);
+    if (a.part1) {
+        hipLaunchKernelGGL(topk_split_kernel, grid, dim3(kTopkWaves * kWave), 0, st,
+                           const_cast<float*>(a.logits), a.part1, a.lbias, a.T, a.E, a.K, a.mode,
+                           a.normalize, a.scaling, a.bias16, a.bias32, a.n_group, a.topk_group, a.out_e,
+                           a.out_w);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(topk_kernel, grid, dim3(kTopkWaves * kWave), 0, st, a.logits, a.T, a.E,
                        a.K, a.mode, a.normalize, a.scaling, a.bias16, a.bias32, a.n_group,
                        a.topk_group, a.out_e, a.out_w);
@@ -493,7 +535,8 @@ __device__ __forceinline__ int rs_split_store(uint16_t* __restrict__ dst, int pl
 // matrix products.
 __global__ __launch_bounds__(kRsThreads) void router_bf16x3_sk(const float* __restrict__ W,
                                                                const float* __restrict__ x,
-                                                               float* __restrict__ logits, int T, int E, int H) {
+                                                               float* __restrict__ logits,
+                                                               float* __restrict__ part1, int T, int E, int H) {
     constexpr int PS = kRsBM * kR3LD;                 // one plane of one operand (BM == BN)
     constexpr int NW = kRsThreads / 64;
     __shared__ __attribute__((aligned(16))) uint16_t Xs[2][3 * PS];
@@ -589,7 +632,9 @@ __global__ __launch_bounds__(kRsThreads) void router_bf16x3_sk(const float* __re
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const int t = t0 + wm * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
-            if (t < T) unsafeAtomicAdd(&logits[int64_t(t) * E + e], acc[ni][v]);
+            if (t >= T) continue;
+            if (part1) (blockIdx.z == 0 ? logits : part1)[int64_t(t) * E + e] = acc[ni][v];
+            else unsafeAtomicAdd(&logits[int64_t(t) * E + e], acc[ni][v]);
         }
     }
 }
@@ -597,36 +642,59 @@ __global__ __launch_bounds__(kRsThreads) void router_bf16x3_sk(const float* __re
 // logits = 0 (bias null) or logits += bias, four values per thread when E
 // is a multiple of 4
 __global__ __launch_bounds__(256) void router_fill_kernel(float* __restrict__ logits, const float* __restrict__ bias,
-                                                          int64_t n, int E) {
+                                                          int64_t n, int E, const float* __restrict__ part1) {
     const int64_t i = (int64_t(blockIdx.x) * 256 + threadIdx.x) * 4;
     if (i >= n) return;
     if (E % 4 == 0) {
         f32x4n v = f32x4n{0.0f, 0.0f, 0.0f, 0.0f};
+        if (bias || part1) v = *reinterpret_cast<const f32x4n*>(logits + i);
+        if (part1) {
+            const f32x4n q = *reinterpret_cast<const f32x4n*>(part1 + i);
+            v = f32x4n{v.x + q.x, v.y + q.y, v.z + q.z, v.w + q.w};
+        }
         if (bias) {
-            v = *reinterpret_cast<const f32x4n*>(logits + i);
             const f32x4n b = *reinterpret_cast<const f32x4n*>(bias + i % E);
             v = f32x4n{v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w};
         }
         *reinterpret_cast<f32x4n*>(logits + i) = v;
     } else {
-        for (int64_t k = i; k < min(n, i + 4); ++k) logits[k] = bias ? logits[k] + bias[k % E] : 0.0f;
+        for (int64_t k = i; k < min(n, i + 4); ++k) {
+            float v = (bias || part1) ? logits[k] : 0.0f;
+            if (part1) v += part1[k];
+            if (bias) v += bias[k % E];
+            logits[k] = v;
+        }
     }
 }
 
 hipError_t router_logits_launch(hipStream_t st, const float* W, const float* x,
-                                const float* bias, float* logits, int T, int E, int H) {
+                                const float* bias, float* logits, int T, int E, int H, float* part1,
+                                int* deferred) {
+    if (deferred) *deferred = 0;
     if (T <= 32 && H % 4 == 0 && router_nk_launch(st, W, x, bias, logits, T, E, H)) {
     } else if (T <= 32 && H % 4 == 0) {
         dim3 grid(E, (T + kRouterTok - 1) / kRouterTok);
         hipLaunchKernelGGL(router_gemv, grid, dim3(256), 0, st, W, x, bias, logits, T, E, H);
     } else if (H % (2 * kR3BK) == 0 && H >= 2 * kR3BK * kRsPre && T >= 256) {
-        // split K: zero the logits, both halves add into them, then the bias
+        // split K.  With part1 and deferred: the halves store a (logits) and
+        // b (part1), and the caller finishes (a + b) + bias (the top-k's
+        // loads do it).  Otherwise: zero the logits, both halves add into
+        // them (0 + a + b = a + b in either order), then the bias.
         const int64_t n = int64_t(T) * E;
         const unsigned fb = unsigned((n + 1023) / 1024);
-        hipLaunchKernelGGL(router_fill_kernel, dim3(fb), dim3(256), 0, st, logits, nullptr, n, E);
         dim3 grid((T + kRsBM - 1) / kRsBM, (E + kRsBN - 1) / kRsBN, 2);
-        hipLaunchKernelGGL(router_bf16x3_sk, grid, dim3(kRsThreads), 0, st, W, x, logits, T, E, H);
-        if (bias) hipLaunchKernelGGL(router_fill_kernel, dim3(fb), dim3(256), 0, st, logits, bias, n, E);
+        if (part1 && deferred) {
+            hipLaunchKernelGGL(router_bf16x3_sk, grid, dim3(kRsThreads), 0, st, W, x, logits, part1, T, E, H);
+            *deferred = 1;
+            return hipGetLastError();
+        }
+        hipLaunchKernelGGL(router_fill_kernel, dim3(fb), dim3(256), 0, st, logits, nullptr, n, E,
+                           static_cast<const float*>(nullptr));
+        hipLaunchKernelGGL(router_bf16x3_sk, grid, dim3(kRsThreads), 0, st, W, x, logits,
+                           static_cast<float*>(nullptr), T, E, H);
+        if (bias)
+            hipLaunchKernelGGL(router_fill_kernel, dim3(fb), dim3(256), 0, st, logits, bias, n, E,
+                               static_cast<const float*>(nullptr));
     } else if (H % (kR3BK * kR3Pre) == 0) {
         dim3 grid((T + 63) / 64, (E + 63) / 64);
         hipLaunchKernelGGL(router_bf16x3, grid, dim3(256), 0, st, W, x, bias, logits, T, E, H);
@@ -637,6 +705,15 @@ hipError_t router_logits_launch(hipStream_t st, const float* W, const float* x,
         dim3 grid((E + 63) / 64, (T + 63) / 64);
         hipLaunchKernelGGL(router_gemm, grid, dim3(256), 0, st, W, x, bias, logits, T, E, H);
     }
+    return hipGetLastError();
+}
+
+hipError_t router_finish_launch(hipStream_t st, float* logits, const float* part1, const float* bias, int T,
+                                int E) {
+    const int64_t n = int64_t(T) * E;
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(router_fill_kernel, dim3(unsigned((n + 1023) / 1024)), dim3(256), 0, st, logits, bias, n, E,
+                       part1);
     return hipGetLastError();
 }
 
