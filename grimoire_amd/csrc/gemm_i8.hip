@@ -221,6 +221,11 @@ __device__ __forceinline__ I8Item i8_item(const GemmI8Args& g, int n_routed, int
     return it;
 }
 
+// The share of an XCD's list of n items that a run walks: part 0 all of
+// it, part 1 the first half, part 2 the second half.
+__device__ __forceinline__ int i8_part_begin(int n, int part) { return part == 2 ? n / 2 : 0; }
+__device__ __forceinline__ int i8_part_end(int n, int part) { return part == 1 ? n / 2 : n; }
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t i8_rsrc(const void* p, int bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
 }
@@ -252,7 +257,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t i8_rsrc(const void* p, int byt
 // a list that follows).
 template <bool SWIGLU>
 __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, int parts,
-                                           int n_routed, int tp_addr, int slot, int per_xcd,
+                                           int n_routed, int tp_addr, int part, int slot, int per_xcd,
                                            uint8_t (*smem)[kQStageBytes], float (*meta)[512],
                                            int32_t (*rmap)[256]) {
     // 8 waves, two per SIMD: wave w owns tile columns [64 (w % 4), +64) for
@@ -273,8 +278,8 @@ __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, 
     // A row block stay under one L2
     const int xcd = blockIdx.x % kQXcds;
     const int lo = int(int64_t(total) * xcd / kQXcds), hi = int(int64_t(total) * (xcd + 1) / kQXcds);
-    const int items = (hi - lo) * n_col_tiles;
-    int i = slot;
+    const int items = i8_part_end((hi - lo) * n_col_tiles, part);
+    int i = i8_part_begin((hi - lo) * n_col_tiles, part) + slot;
     if (i >= items) return i - items;
 
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
@@ -599,7 +604,7 @@ __global__ __launch_bounds__(kQThreads) void grouped_gemm_i8_kernel(GemmI8Args g
         n_routed = g.n_tiles_dev ? __builtin_amdgcn_readfirstlane(*g.n_tiles_dev) : g.tmax;
         n_routed = n_routed < g.tmax ? n_routed : g.tmax;
     }
-    i8_big_run<SWIGLU>(g, n_col_tiles, parts, n_routed, -1, blockIdx.x / kQXcds, gridDim.x / kQXcds,
+    i8_big_run<SWIGLU>(g, n_col_tiles, parts, n_routed, -1, 0, blockIdx.x / kQXcds, gridDim.x / kQXcds,
                        smem, meta, rmap);
 }
 
@@ -631,7 +636,7 @@ bool gemm_i8_narrow_ok(int K) { return K % NBK == 0 && K >= (kNStages - 1) * NBK
 // tp_addr.  smem / meta: the kernel's LDS.
 template <bool SWIGLU>
 __device__ __forceinline__ void i8_narrow_run(const GemmI8Args& g, int n_col_tiles, int total,
-                                              int tp_addr, int slot, int per_xcd,
+                                              int tp_addr, int part, int slot, int per_xcd,
                                               uint8_t (*smem)[kNStageBytes], float (*meta)[512],
                                               int32_t (*rmap)[256]) {
     constexpr int NJA = 2, NJB = 8;          // A / B instructions per wave per stage
@@ -640,8 +645,8 @@ __device__ __forceinline__ void i8_narrow_run(const GemmI8Args& g, int n_col_til
     // column scales at 256 (plain: [256]; SwiGLU: gate [128] then up [128])
     const int xcd = blockIdx.x % kQXcds;
     const int lo = int(int64_t(total) * xcd / kQXcds), hi = int(int64_t(total) * (xcd + 1) / kQXcds);
-    const int items = (hi - lo) * n_col_tiles;
-    int i = slot;
+    const int items = i8_part_end((hi - lo) * n_col_tiles, part);
+    int i = i8_part_begin((hi - lo) * n_col_tiles, part) + slot;
     if (i >= items) return;
 
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
@@ -898,14 +903,41 @@ __device__ __forceinline__ void i8_narrow_run(const GemmI8Args& g, int n_col_til
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// The number of s_barrier instructions i8_narrow_run executes for the
+// same arguments (its gather prologue, then one per K stage of each of its
+// items): what the waves that sit the narrow run out execute instead, so
+// that every barrier of the work-group still pairs up.
+__device__ __forceinline__ int i8_narrow_barriers(const GemmI8Args& g, int n_col_tiles, int total, int part,
+                                                  int slot, int per_xcd) {
+    const int xcd = blockIdx.x % kQXcds;
+    const int lo = int(int64_t(total) * xcd / kQXcds), hi = int(int64_t(total) * (xcd + 1) / kQXcds);
+    const int items = i8_part_end((hi - lo) * n_col_tiles, part);
+    const int i = i8_part_begin((hi - lo) * n_col_tiles, part) + slot;
+    if (i >= items) return 0;
+    const int mine = (items - i + per_xcd - 1) / per_xcd;
+    return (g.gather ? 1 : 0) + mine * (g.K / NBK);
+}
+
 // Rows mode, one launch: every work-group forms both tile lists (experts
 // above list_lo rows in 128-row tiles, then the shared expert's for parts &
-// 2; experts of 1..split rows in 32-row tiles when list_lo > 0) and walks
-// its share of the 128-row items, then -- continuing the same round robin
-// over its XCD's work-groups -- its share of the narrow ones, on its first
-// four waves (the others end there; a barrier waits for the surviving
-// waves only).  One launch instead of two: no second ramp-up, and the
-// first list's tail overlaps the second list's start.
+// 2; experts of 1..split rows in 32-row tiles when list_lo > 0).
+//
+// With both lists non-empty the work-groups of an XCD form two halves that
+// take the lists in opposite orders: even slots walk the first half of the
+// 128-row items and then the second half of the narrow ones, odd slots the
+// first half of the narrow items and then the second half of the 128-row
+// ones.  The 128-row items are bound by the matrix core and the LDS (their
+// operands come mostly from the L2), the narrow ones by the memory stream
+// (each expert's weights read once for a few rows): run side by side on
+// different CUs they overlap, where run one after the other on every CU
+// the narrow phase had all 256 CUs contending for memory (a narrow item
+// took 1.5x as long as with half of them).  The narrow run uses the first
+// four waves; the other four end after it, or (odd slots, which run the
+// 128-row items afterwards) execute as many barriers as it does and wait.
+//
+// With one list only: every work-group walks its share of the 128-row
+// items, then -- continuing the same round robin over its XCD's work-groups
+// -- its share of the narrow ones.
 template <bool SWIGLU>
 __global__ __launch_bounds__(kQThreads) void grouped_gemm_i8_rows_kernel(GemmI8Args g, int nct_big,
                                                                         int nct_nar, int parts) {
@@ -919,15 +951,36 @@ __global__ __launch_bounds__(kQThreads) void grouped_gemm_i8_rows_kernel(GemmI8A
     const int nb = (parts & 1) ? i8_list_scan<QBM, kQThreads>(g.counts, E, g.list_lo, 0x7FFFFFFF, tpb, tmp) : 0;
     const int nn = ((parts & 1) && g.list_lo > 0) ? i8_list_scan<NBM, kQThreads>(g.counts, E, 0, g.split, tpn, tmp) : 0;
     const int S = gridDim.x / kQXcds;            // work-group slots per XCD
+    const int q = blockIdx.x / kQXcds;           // this work-group's slot
     const int tpa_b = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int32_t*)(&tpb[0])));
-    const int next = i8_big_run<SWIGLU>(g, nct_big, parts, nb, tpa_b, blockIdx.x / kQXcds, S,
-                                        reinterpret_cast<uint8_t (*)[kQStageBytes]>(ring), meta, rmap);
+    const int tpa_n = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int32_t*)(&tpn[0])));
+    const int nb_total = nb + ((parts & 2) ? (g.T_sh + QBM - 1) / QBM : 0);
+    auto big = reinterpret_cast<uint8_t (*)[kQStageBytes]>(ring);
+    auto nar = reinterpret_cast<uint8_t (*)[kNStageBytes]>(ring);
+    if (nn > 0 && nb_total > 0 && S >= 2 && S % 2 == 0) {
+        const int h = S / 2, p = q >> 1;
+        if ((q & 1) == 0) {
+            i8_big_run<SWIGLU>(g, nct_big, parts, nb, tpa_b, 1, p, h, big, meta, rmap);
+            __syncthreads();                     // every wave is past the 128-row ring
+            if (threadIdx.x >= kNThreads) return;
+            i8_narrow_run<SWIGLU>(g, nct_nar, nn, tpa_n, 2, p, h, nar, meta, rmap);
+        } else {
+            if (threadIdx.x < kNThreads) {
+                i8_narrow_run<SWIGLU>(g, nct_nar, nn, tpa_n, 1, p, h, nar, meta, rmap);
+            } else {
+                const int nbar = i8_narrow_barriers(g, nct_nar, nn, 1, p, h);
+                for (int b = 0; b < nbar; ++b) __builtin_amdgcn_s_barrier();
+            }
+            __syncthreads();                     // every wave is past the narrow ring
+            i8_big_run<SWIGLU>(g, nct_big, parts, nb, tpa_b, 2, p, h, big, meta, rmap);
+        }
+        return;
+    }
+    const int next = i8_big_run<SWIGLU>(g, nct_big, parts, nb, tpa_b, 0, q, S, big, meta, rmap);
     if (nn == 0) return;
     __syncthreads();                             // every wave is past the 128-row ring
     if (threadIdx.x >= kNThreads) return;
-    const int tpa_n = int(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int32_t*)(&tpn[0])));
-    i8_narrow_run<SWIGLU>(g, nct_nar, nn, tpa_n, next, S,
-                          reinterpret_cast<uint8_t (*)[kNStageBytes]>(ring), meta, rmap);
+    i8_narrow_run<SWIGLU>(g, nct_nar, nn, tpa_n, 0, next, S, nar, meta, rmap);
 }
 
 // ------------------------------------------------------------ quantisers
