@@ -292,6 +292,9 @@ static int forward_gemm_i8(hipStream_t st, const grim_moe_layer* L, const Plan& 
         g.split = kI8DefaultSplit;
         g.num_experts = E;
     }
+#ifdef GRIM_TIMING
+    g.ts = g_timing;
+#endif
     e = gemm_i8_launch(st, g);
     if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
     // h limbs (rows beyond the routed count are never read)
@@ -314,6 +317,9 @@ static int forward_gemm_i8(hipStream_t st, const grim_moe_layer* L, const Plan& 
     d.A = p.hq;
     d.sa = p.sh;
     d.gather = nullptr;
+#ifdef GRIM_TIMING
+    d.ts = g_timing ? g_timing + 256 * 128 * 2 : nullptr;
+#endif
     d.A_sh = p.hshq;
     d.sa_sh = p.shsh;
     d.out = p.yperm;

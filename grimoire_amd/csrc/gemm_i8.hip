@@ -41,6 +41,21 @@
 
 namespace grim {
 
+// Item timestamps for kernel studies, compiled in only with GRIM_TIMING:
+// per work-group b < 256, 128 (time, info) pairs; the 128-row items at
+// pairs 0..61 (start, end alternating), the narrow ones at 64..125.
+#ifdef GRIM_TIMING
+#define GRIM_ITEM_TS(base, ev, info)                                                              \
+    do {                                                                                          \
+        if (g.ts && threadIdx.x == 0 && blockIdx.x < 256 && (ev) < 62) {                          \
+            g.ts[(blockIdx.x * 128 + (base) + (ev)) * 2] = __builtin_amdgcn_s_memrealtime();      \
+            g.ts[(blockIdx.x * 128 + (base) + (ev)) * 2 + 1] = (info);                            \
+        }                                                                                         \
+    } while (0)
+#else
+#define GRIM_ITEM_TS(base, ev, info) do {} while (0)
+#endif
+
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
@@ -418,7 +433,10 @@ __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, 
     bool first = true;
     i32x16 acc[2][MIW][2];
     i32x4 fb[2][2], fa[2][2][MIW];
+    int nev = 0;
+    (void)nev;
     for (; i < items; i += per_xcd) {
+        GRIM_ITEM_TS(0, 2 * nev, (unsigned long long)(cur.rows) | ((unsigned long long)cur.sh << 16));
         GRIM_I8_OFFSETS();
         a_offsets(cur, rmap_base + par * 1024, a_off);
 #pragma unroll
@@ -470,6 +488,15 @@ __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, 
             _Pragma("unroll") for (int l = 0; l < 2; ++l)                                         \
                 acc[l][mi_][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks_][l][mi_], fb[ks_][ni], \
                                                                         acc[l][mi_][ni], 0, 0, 0)
+#define GRIM_I8_READS(ks_)                                                                        \
+        do {                                                                                      \
+            GRIM_I8_DSR(fb[ks_][0], sb + fb_off[ks_][0]);                                         \
+            GRIM_I8_DSR(fb[ks_][1], sb + fb_off[ks_][1]);                                         \
+            _Pragma("unroll") for (int mi = 0; mi < MIW; ++mi) {                                  \
+                GRIM_I8_DSR(fa[ks_][0][mi], sb + fa_off[ks_][0][mi]);                             \
+                GRIM_I8_DSR(fa[ks_][1][mi], sb + fa_off[ks_][1][mi]);                             \
+            }                                                                                     \
+        } while (0)
 #define GRIM_I8_DMA(q)                                                                            \
         do {                                                                                      \
             if ((q) < NJ) dma16<0>(qa, nx + (NJ * wave + (q)) * 1024, own ? a_off[(q) % NJ] : a_offn[(q) % NJ], tu * 128); \
@@ -482,14 +509,7 @@ __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, 
             /* the next item's row map (requested at t = 0, landed by t = 3) */                   \
             if (gat && t == nk - (kQStages - 1)) a_offsets(nxt, rmap_base + (par ^ 1) * 1024, a_offn); \
             const int sb = ((gs + t) & 3) * kQStageBytes + smem_base;                             \
-            _Pragma("unroll") for (int ks = 0; ks < 2; ++ks) {                                    \
-                GRIM_I8_DSR(fb[ks][0], sb + fb_off[ks][0]);                                       \
-                GRIM_I8_DSR(fb[ks][1], sb + fb_off[ks][1]);                                       \
-                _Pragma("unroll") for (int mi = 0; mi < MIW; ++mi) {                              \
-                    GRIM_I8_DSR(fa[ks][0][mi], sb + fa_off[ks][0][mi]);                           \
-                    GRIM_I8_DSR(fa[ks][1][mi], sb + fa_off[ks][1][mi]);                           \
-                }                                                                                 \
-            }                                                                                     \
+            GRIM_I8_READS(0);                                                                     \
             if (META) request_meta(nxt, par ^ 1);                                                 \
             /* stream tile t + 3: this item's, or the next item's 0, 1, 2 */                      \
             const int u = t + kQStages - 1;                                                       \
@@ -498,8 +518,13 @@ __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, 
             const __amdgpu_buffer_rsrc_t qb = rsrc_b(own ? cur : nxt);                            \
             const int tu = own ? u : u - nk;                                                      \
             uint8_t* nx = smem[(gs + u) & 3];                                                     \
-            /* 12 reads in flight: (ks, mi) needs the first 4 / 6 / 10 / 12 */                    \
-            GRIM_I8_LGKM(8, 0, 0); GRIM_I8_MMA_MI(0, 0); GRIM_I8_DMA(0);                          \
+            /* K half 0's 6 reads in flight: (0, 0) needs the first 4; K half 1's 6 */          \
+            /* are issued behind (0, 0)'s products, so the LDS serves them while the */          \
+            /* matrix core works: (0, 1) needs 6 of the 8 then in flight, (1, 0) 4 of */          \
+            /* the last 6 */                                                                      \
+            GRIM_I8_LGKM(2, 0, 0); GRIM_I8_MMA_MI(0, 0); GRIM_I8_DMA(0);                          \
+            __builtin_amdgcn_sched_barrier(0);                                                    \
+            GRIM_I8_READS(1);                                                                     \
             GRIM_I8_LGKM(6, 0, 1); GRIM_I8_MMA_MI(0, 1); GRIM_I8_DMA(1);                          \
             GRIM_I8_LGKM(2, 1, 0); GRIM_I8_MMA_MI(1, 0); GRIM_I8_DMA(2);                          \
             GRIM_I8_LGKM(0, 1, 1); GRIM_I8_MMA_MI(1, 1); GRIM_I8_DMA(3);                          \
@@ -515,6 +540,7 @@ __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, 
 #undef GRIM_I8_LGKM
 #undef GRIM_I8_MMA_MI
 #undef GRIM_I8_DMA
+#undef GRIM_I8_READS
 
         // ---- epilogue.  acc[l][mi][ni][v] is row 32 mi + 8 (v/4) + 4 (l/32)
         // + v%4, column 32 (2 w + ni) + l%32 of the tile.  Scales from LDS
@@ -580,6 +606,8 @@ __device__ __forceinline__ int i8_big_run(const GemmI8Args& g, int n_col_tiles, 
                 }
             }
         }
+        GRIM_ITEM_TS(0, 2 * nev + 1, 0ull);
+        ++nev;
         gs += nk;
         par ^= 1;
         cur = nxt;
@@ -759,7 +787,10 @@ __device__ __forceinline__ void i8_narrow_run(const GemmI8Args& g, int n_col_til
     bool first = true;
     i32x16 acc[2][2];
     i32x4 fb[2][2], fa[2][2];
+    int nev = 0;
+    (void)nev;
     for (; i < items; i += per_xcd) {
+        GRIM_ITEM_TS(64, 2 * nev, (unsigned long long)(cur.rows) | (2ull << 16));
         GRIM_N8_OFFSETS();
         a_offsets(cur, rmap_base + par * 1024, a_off);
 #pragma unroll
@@ -894,6 +925,8 @@ __device__ __forceinline__ void i8_narrow_run(const GemmI8Args& g, int n_col_til
                         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ro, off, 0, 0);
                     }
         }
+        GRIM_ITEM_TS(64, 2 * nev + 1, 0ull);
+        ++nev;
         gs = (gs + nk) % kNStages;
         par ^= 1;
         cur = nxt;

@@ -41,6 +41,7 @@ struct GemmI8Args {
     // scales stay per routed row (sa[r])
     const int32_t* gather;
     int gather_rows;
+    unsigned long long* ts;     // item timestamps (GRIM_TIMING builds only), else null
 };
 
 constexpr int kI8MaxListExperts = 1024;
