@@ -11,6 +11,7 @@
 namespace grim {
 
 constexpr int kTopkWaves = 4;
+typedef float f32x4n __attribute__((ext_vector_type(4)));   // native vector (HIP's float4 is a struct)
 
 __global__ __launch_bounds__(kTopkWaves * kWave) void topk_kernel(
     const float* __restrict__ logits, int T, int E, int K, int mode, int normalize,
@@ -43,18 +44,35 @@ __global__ __launch_bounds__(kTopkWaves * kWave) void topk_split_kernel(
     float* row = logits + int64_t(t) * E;
     const float* row1 = part1 + int64_t(t) * E;
     float lv[kMaxV];
+    if (E == kWave * kMaxV) {
+        // every lane's kMaxV logits are contiguous: 16-byte loads and stores
 #pragma unroll
-    for (int j = 0; j < kMaxV; ++j) {
-        const int e = lane * V + j;
-        const int ec = (j < V && e < E) ? e : 0;
-        float v = row[ec] + row1[ec];
-        if (lbias) v += lbias[ec];
-        lv[j] = v;
-    }
+        for (int j = 0; j < kMaxV; j += 4) {
+            const int e = lane * kMaxV + j;
+            f32x4n v = *reinterpret_cast<const f32x4n*>(row + e);
+            const f32x4n q = *reinterpret_cast<const f32x4n*>(row1 + e);
+            v = f32x4n{v.x + q.x, v.y + q.y, v.z + q.z, v.w + q.w};
+            if (lbias) {
+                const f32x4n b = *reinterpret_cast<const f32x4n*>(lbias + e);
+                v = f32x4n{v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w};
+            }
+            *reinterpret_cast<f32x4n*>(row + e) = v;
+            lv[j] = v.x; lv[j + 1] = v.y; lv[j + 2] = v.z; lv[j + 3] = v.w;
+        }
+    } else {
 #pragma unroll
-    for (int j = 0; j < kMaxV; ++j) {
-        const int e = lane * V + j;
-        if (j < V && e < E) row[e] = lv[j];
+        for (int j = 0; j < kMaxV; ++j) {
+            const int e = lane * V + j;
+            const int ec = (j < V && e < E) ? e : 0;
+            float v = row[ec] + row1[ec];
+            if (lbias) v += lbias[ec];
+            lv[j] = v;
+        }
+#pragma unroll
+        for (int j = 0; j < kMaxV; ++j) {
+            const int e = lane * V + j;
+            if (j < V && e < E) row[e] = lv[j];
+        }
     }
     topk_wave_regs(lv, E, K, mode, normalize, scaling, bias16, bias32, n_group, topk_group,
                    out_e + int64_t(t) * K, out_w + int64_t(t) * K, gsel[wv], gscore[wv]);
@@ -255,7 +273,6 @@ __global__ __launch_bounds__(256) void router_gemm(const float* __restrict__ W,
 // blocks, two per CU, where 128 x 128 tiles would leave half the CUs idle.
 constexpr int kRtBK = 32, kRtLD = kRtBK + 4;
 typedef float f32x16r __attribute__((__vector_size__(16 * sizeof(float))));
-typedef float f32x4n __attribute__((ext_vector_type(4)));   // native vector (HIP's float4 is a struct)
 
 // staging of one K tile: ROWS/32 f32x4n per thread from `src` (row c/8,
 // K offset 4 (c % 8)); rows past `n` repeat the last one

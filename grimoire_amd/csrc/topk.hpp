@@ -16,6 +16,7 @@
 namespace grim {
 
 constexpr int kMaxV = 8;          // E <= 512
+static_assert(kMaxV % 4 == 0, "the E == 64 kMaxV loads move four logits at a time");
 constexpr int kRouterTok = 8;     // tokens per router_row call
 
 // Router logits of one expert row for nt <= kRouterTok tokens by one
@@ -140,6 +141,16 @@ __device__ __forceinline__ float lane_f(float v, int lane) {
 __device__ __forceinline__ void topk_load(const float* __restrict__ row, int E, float (&lv)[kMaxV]) {
     const int lane = threadIdx.x & (kWave - 1);
     const int V = (E + kWave - 1) / kWave;
+    if (E == kWave * kMaxV) {
+        // every lane's logits contiguous: 16-byte loads
+        typedef float f4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int j = 0; j < kMaxV; j += 4) {
+            const f4 v = *reinterpret_cast<const f4*>(row + lane * kMaxV + j);
+            lv[j] = v.x; lv[j + 1] = v.y; lv[j + 2] = v.z; lv[j + 3] = v.w;
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < kMaxV; ++j) {
         const int e = lane * V + j;
