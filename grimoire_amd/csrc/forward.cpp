@@ -251,11 +251,15 @@ static int forward_gemm_i8(hipStream_t st, const grim_moe_layer* L, const Plan& 
     // routed row's token row through qperm; otherwise limbs at every
     // routed row
     const bool gather = gemm_i8_gather_ok(H, tokens) && E <= kI8MaxListExperts;
+    // the shared expert's gate from the same loads of x when its weights
+    // are 16-byte aligned
+    const bool gate_fused = sh && shared_gate_w && (reinterpret_cast<uintptr_t>(shared_gate_w) & 15) == 0;
     hipError_t e = quant_permute_launch(st, x, tokens, H, K, p.inverse, gather ? nullptr : p.xq, p.sx,
                                         (sh || gather) ? p.xrowq : nullptr,
-                                        (sh || gather) ? p.sxrow : nullptr, gather ? p.qperm : nullptr);
+                                        (sh || gather) ? p.sxrow : nullptr, gather ? p.qperm : nullptr,
+                                        gate_fused ? shared_gate_w : nullptr, gate_fused ? p.gate : nullptr);
     if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
-    if (sh && shared_gate_w) {
+    if (sh && shared_gate_w && !gate_fused) {
         e = rowdot_sigmoid_launch(st, x, shared_gate_w, p.gate, tokens, H);
         if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
     }

@@ -1130,19 +1130,23 @@ __global__ __launch_bounds__(256) void quant_rows_short_kernel(const float* __re
 // The activations of every token as limbs, written to each of its K
 // permuted rows (inverse) when xq is given and to its own row (xrowq: the
 // shared expert's input, and the gather source of gather mode) when given;
-// the scale to every permuted row, and the token to perm[permuted row].
+// the scale to every permuted row, and the token to perm[permuted row];
+// with gate_w (bf16 [n], 16-byte aligned) also gate[t] = sigmoid(x_t . w),
+// the shared expert's gate, from the same loads.
 // One work-group of 256 threads per token, n <= 8192.
 __global__ __launch_bounds__(256) void quant_permute_kernel(const float* __restrict__ x, int n, int K,
                                                             const int32_t* __restrict__ inverse,
                                                             int8_t* __restrict__ xq, float* __restrict__ sq,
                                                             int8_t* __restrict__ xrowq,
                                                             float* __restrict__ srow,
-                                                            int32_t* __restrict__ perm) {
-    __shared__ float red[4];
+                                                            int32_t* __restrict__ perm,
+                                                            const uint16_t* __restrict__ gate_w,
+                                                            float* __restrict__ gate) {
+    __shared__ float red[4], gred[4];
     const int t = blockIdx.x;
     const float* s = x + int64_t(t) * n;
     float4 va[4], vb[4];
-    float m = 0.0f;
+    float m = 0.0f, d = 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int c = threadIdx.x * 8 + q * 2048;
@@ -1151,12 +1155,31 @@ __global__ __launch_bounds__(256) void quant_permute_kernel(const float* __restr
             vb[q] = *reinterpret_cast<const float4*>(s + c + 4);
             m = fmaxf(m, fmaxf(fmaxf(fabsf(va[q].x), fabsf(va[q].y)), fmaxf(fabsf(va[q].z), fabsf(va[q].w))));
             m = fmaxf(m, fmaxf(fmaxf(fabsf(vb[q].x), fabsf(vb[q].y)), fmaxf(fabsf(vb[q].z), fabsf(vb[q].w))));
+            if (gate_w) {
+                // the shared expert's gate: x . w in one fixed order (the
+                // thread's 8 elements per 2048, then the waves' DPP sums,
+                // then the four waves in order)
+                const uint4 u = *reinterpret_cast<const uint4*>(gate_w + c);
+                d = __builtin_fmaf(bits_f(u.x << 16), va[q].x, d);
+                d = __builtin_fmaf(bits_f(u.x & 0xFFFF0000u), va[q].y, d);
+                d = __builtin_fmaf(bits_f(u.y << 16), va[q].z, d);
+                d = __builtin_fmaf(bits_f(u.y & 0xFFFF0000u), va[q].w, d);
+                d = __builtin_fmaf(bits_f(u.z << 16), vb[q].x, d);
+                d = __builtin_fmaf(bits_f(u.z & 0xFFFF0000u), vb[q].y, d);
+                d = __builtin_fmaf(bits_f(u.w << 16), vb[q].z, d);
+                d = __builtin_fmaf(bits_f(u.w & 0xFFFF0000u), vb[q].w, d);
+            }
         }
     }
     m = wave_max_f(m);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x / 64] = m;
+    if (gate_w) d = group_sum<kWave>(d);
+    if ((threadIdx.x & 63) == 0) {
+        red[threadIdx.x / 64] = m;
+        gred[threadIdx.x / 64] = d;
+    }
     __syncthreads();
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    if (gate_w && threadIdx.x == 0) gate[t] = det_sigmoid((gred[0] + gred[1]) + (gred[2] + gred[3]));
     const float sc = m > 0.0f ? m / 127.0f : 1.0f;
     const float inv = m > 0.0f ? 127.0f / m : 0.0f;
     int dst[16];
@@ -1289,11 +1312,12 @@ hipError_t quant_rows_launch(hipStream_t st, const float* src, int rows, int n, 
 
 hipError_t quant_permute_launch(hipStream_t st, const float* x, int T, int n, int K,
                                 const int32_t* inverse, int8_t* xq, float* sq, int8_t* xrowq,
-                                float* srow, int32_t* perm) {
+                                float* srow, int32_t* perm, const uint16_t* gate_w, float* gate) {
     if (T <= 0) return hipSuccess;
     if (n % 64 || n > 8192 || K > 16) return hipErrorInvalidValue;
+    if (gate_w && (reinterpret_cast<uintptr_t>(gate_w) & 15)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(quant_permute_kernel, dim3(T), dim3(256), 0, st, x, n, K, inverse, xq, sq,
-                       xrowq, srow, perm);
+                       xrowq, srow, perm, gate_w, gate);
     return hipGetLastError();
 }
 

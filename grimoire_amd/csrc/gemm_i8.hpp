@@ -60,9 +60,11 @@ hipError_t quant_rows_launch(hipStream_t st, const float* src, int rows, int n, 
 // token rows of x fp32 [T][n] -> limbs at their K permuted rows (inverse
 // [T][K]) when xq is given, at their own row when xrowq is given; the row
 // scale at every permuted row (sq) and own row (srow); perm, when given,
-// gets the token of every permuted row (the gather map of gather mode)
+// gets the token of every permuted row (the gather map of gather mode);
+// gate_w (bf16 [n], 16-byte aligned, or null): gate[t] = sigmoid(x_t . w)
 hipError_t quant_permute_launch(hipStream_t st, const float* x, int T, int n, int K,
                                 const int32_t* inverse, int8_t* xq, float* sq, int8_t* xrowq,
-                                float* srow, int32_t* perm);
+                                float* srow, int32_t* perm, const uint16_t* gate_w = nullptr,
+                                float* gate = nullptr);
 
 }  // namespace grim
