@@ -186,6 +186,7 @@ SIGNATURES = {
     "grimoire_moe_quant_limbs": (I32, [P, P, I32, I32, P, P]),
     "grimoire_moe_grouped_gemm_i8": (I32, [P, QWP, I32, I32, P, P, P, P, P, P, P, I32, I32]),
     "grimoire_moe_grouped_gemm_i8_rows": (I32, [P, QWP, I32, I32, P, P, P, P, P, I32, I32]),
+    "grimoire_moe_grouped_gemm_i8_rows_gather": (I32, [P, QWP, I32, I32, P, I32, P, P, P, P, P, I32, I32]),
     "grimoire_xe2_grouped_mxfp4_bf16": (None, [P, P, P, P, P, I32, I32, P, P, I32, P]),
     "grimoire_xe2_grouped_mxfp4_bf16_full": (None, [P, P, P, P, P, I32, I32, P, P, I32, P]),
     "grimoire_xe2_grouped_mxfp4_bf16_m8": (None, [P, P, P, P, P, I32, I32, P, P, I32, P]),

@@ -797,6 +797,43 @@ int grimoire_moe_grouped_gemm_i8_rows(void* stream, const grim_quant_weight* w, 
     return status(gemm_i8_launch(S(stream), g));
 }
 
+int grimoire_moe_grouped_gemm_i8_rows_gather(void* stream, const grim_quant_weight* w, int N, int swiglu,
+                                             const int8_t* A, int a_rows, const int32_t* row_map,
+                                             const float* a_scale, float* out, const int32_t* offsets,
+                                             const int32_t* counts, int num_experts, int split) {
+    if (!w || !A || !row_map || !a_scale || !out || !offsets || !counts)
+        return fail(GRIM_ERR_ARG, "null pointer");
+    if (w->fmt != GRIM_FMT_INT8) return fail(GRIM_ERR_FORMAT, "INT8 weights only");
+    if (num_experts <= 0 || num_experts > kI8MaxListExperts)
+        return fail(GRIM_ERR_SHAPE, "num_experts=%d: 1..%d", num_experts, kI8MaxListExperts);
+    int r = check_weight(w, "grouped weight", int64_t(num_experts) * N, w->K);
+    if (r) return r;
+    if (swiglu && N % 2) return fail(GRIM_ERR_SHAPE, "swiglu needs even N");
+    if (!gemm_i8_shape_ok(N, w->K, swiglu ? N / 2 : 0, swiglu))
+        return fail(GRIM_ERR_SHAPE, "K=%d: a multiple of 64 in [192, 8192]", w->K);
+    if (!gemm_i8_gather_ok(w->K, a_rows))
+        return fail(GRIM_ERR_SHAPE, "gather: K=%d needs >= 6 K tiles of 64 (>= 4 of 128 when K %% 128 == 0), "
+                    "a_rows=%d rows of 2K bytes below 1.75 GiB", w->K, a_rows);
+    GemmI8Args g{};
+    g.w = w->payload;
+    g.ws = static_cast<const float*>(w->scales);
+    g.row_bytes = w->row_bytes;
+    g.N = N;
+    g.K = w->K;
+    g.I = swiglu ? N / 2 : 0;
+    g.swiglu = swiglu;
+    g.A = A;
+    g.sa = a_scale;
+    g.out = out;
+    g.offsets = offsets;
+    g.counts = counts;
+    g.split = split > 0 ? split : kI8DefaultSplit;
+    g.num_experts = num_experts;
+    g.gather = row_map;
+    g.gather_rows = a_rows;
+    return status(gemm_i8_launch(S(stream), g));
+}
+
 int grimoire_moe_grouped_gemm(void* stream, const grim_quant_weight* w, int N, int swiglu,
                               const uint16_t* A, int a_pair, void* out, int out_bf16,
                               const int32_t* offsets, const int32_t* counts, int num_experts,

@@ -257,6 +257,17 @@ def grouped_gemm_i8_rows(w: Weight, N, swiglu, A, a_scale, out, offsets, counts,
                                                   num_experts, int(split)), "grouped_gemm_i8_rows")
 
 
+def grouped_gemm_i8_rows_gather(w: Weight, N, swiglu, A, row_map, a_scale, out, offsets, counts,
+                                num_experts, split=0, stream=None):
+    """grouped_gemm_i8_rows with routed row r read from A[row_map[r]]
+    (A: limb rows of e.g. the tokens; a_scale per routed row)."""
+    _dev(A)
+    check(lib().grimoire_moe_grouped_gemm_i8_rows_gather(_stream(stream), w.struct(), N, int(swiglu), _p(A),
+                                                         A.shape[0], _p(row_map), _p(a_scale), _p(out),
+                                                         _p(offsets), _p(counts), num_experts, int(split)),
+          "grouped_gemm_i8_rows_gather")
+
+
 def grouped_gemm_i8(w: Weight, N, swiglu, A, a_scale, out, offsets, counts, num_experts,
                     tile_e=None, tile_mb=None, stream=None):
     """INT8 experts on the int8 MFMA (limb rows from quant_limbs), fp32 out,

@@ -574,6 +574,21 @@ int grimoire_moe_grouped_gemm_i8_rows(void* stream, const grim_quant_weight* w, 
                                       const int32_t* offsets, const int32_t* counts, int num_experts,
                                       int split);
 
+/* grimoire_moe_grouped_gemm_i8_rows on rows that are not stored in expert
+ * order: routed row r (the order offsets / counts describe) reads row
+ * row_map[r] of A [a_rows][2K] limb rows (e.g. the token rows, each read
+ * once per route instead of copied K times); a_scale stays per routed row
+ * [R].  Needs K / 64 >= 6 and, when K % 128 == 0, K / 128 >= 4, and
+ * a_rows * 2K below 0x70000000 bytes (GRIM_ERR_SHAPE otherwise).  Same
+ * products, bit for bit, as the call on the rows copied into routed order.
+ * No reference counterpart (the reference materialises permuted rows,
+ * src/prefill.cpp:2784-2806); the forward's INT8 gate_up uses it.
+ * Allocates nothing. */
+int grimoire_moe_grouped_gemm_i8_rows_gather(void* stream, const grim_quant_weight* w, int N, int swiglu,
+                                             const int8_t* A, int a_rows, const int32_t* row_map,
+                                             const float* a_scale, float* out, const int32_t* offsets,
+                                             const int32_t* counts, int num_experts, int split);
+
 /* ------------------------------------------------------------------------
  * Bridges (the vLLM-XPU grouped GEMMs the reference dlopens).  Same
  * argument lists apart from the queue.  rows_per_expert [ne] gives the

@@ -177,3 +177,51 @@ def test_gemm_i8_rows_mode_matches_tiles(gpu, E, split, K, swiglu):
         g_, u_ = want[:, :I], want[:, I:]
         want = g_ / (1 + torch.exp(-g_)) * u_
     assert rel_l2(out.cpu(), want) < 2e-4
+
+
+@pytest.mark.parametrize("E,split,K,T", [(37, 64, 512, 300), (14, 1, 640, 97), (1000, 64, 2048, 700),
+                                         (37, 100000, 384 + 64, 50)])
+@pytest.mark.parametrize("swiglu", [False, True])
+def test_gemm_i8_gather_matches_copied_rows(gpu, E, split, K, T, swiglu):
+    """Gather mode (routed row r reads token row map[r]) gives the products
+    of the call on the rows copied into routed order, bit for bit: the same
+    limbs reach the same MFMAs.  K = 512 is the smallest K that runs both
+    tile kinds in gather mode (its narrow tiles' row map is read at their
+    third K stage), K = 448 one with 128-row tiles only."""
+    print(f"gemm i8 gather E={E} split={split} K={K} T={T} swiglu={swiglu}", flush=True)
+    I = 320
+    N = 2 * I if swiglu else 576
+    w = make_int8(E * N, K, seed=E + K)
+    counts = _rows_case(E, E + 11)
+    offsets = (torch.cumsum(counts, 0) - counts).int()
+    R = int(counts.sum())
+    g = torch.Generator().manual_seed(K + T)
+    X = torch.randn(T, K, generator=g).bfloat16().float()
+    qt, st = _limbs(gpu, X)
+    row_map = torch.randint(0, T, (R,), generator=g, dtype=torch.int32)
+    idx = row_map.long().to(gpu)
+    q, s = qt[idx].contiguous(), st[idx].contiguous()
+    cols = I if swiglu else N
+    ref = torch.full((R, cols), float("nan"), device=gpu)
+    out = torch.full((R, cols), float("nan"), device=gpu)
+    wg = w.to(gpu)
+    ops.grouped_gemm_i8_rows(wg, N, swiglu, q, s, ref, offsets.to(gpu), counts.to(gpu), E, split=split)
+    ops.grouped_gemm_i8_rows_gather(wg, N, swiglu, qt, row_map.to(gpu), s, out, offsets.to(gpu),
+                                    counts.to(gpu), E, split=split)
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any()
+    assert torch.equal(out.cpu(), ref.cpu())
+
+
+def test_gemm_i8_gather_rejects_short_k(gpu):
+    """K with too few K tiles for the row map's timing is refused on the host."""
+    E, N, K = 4, 256, 256
+    w = make_int8(E * N, K, seed=3).to(gpu)
+    counts = torch.tensor([10, 0, 5, 1], dtype=torch.int32)
+    offsets = (torch.cumsum(counts, 0) - counts).int()
+    q = torch.zeros(8, 2 * K, dtype=torch.int8, device=gpu)
+    s = torch.ones(16, device=gpu)
+    out = torch.empty(16, N, device=gpu)
+    with pytest.raises(Exception, match="gather"):
+        ops.grouped_gemm_i8_rows_gather(w, N, False, q, torch.zeros(16, dtype=torch.int32, device=gpu), s, out,
+                                        offsets.to(gpu), counts.to(gpu), E)
