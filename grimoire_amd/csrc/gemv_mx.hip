@@ -305,15 +305,15 @@ hipError_t gvm_route_launch(hipStream_t st, const TopkArgs& tk, const GvmRouteAr
     return hipGetLastError();
 }
 
-// Stage s of an item into the ring stage at st: exactly 15 instructions,
-// every lane active (the stage loop's vmcnt wait counts 15 per stage: a
+// Stage s of an item into the ring stage at st: exactly 13 instructions,
+// every lane active (the stage loop's vmcnt wait counts 13 per stage: a
 // lane-masked load whose lanes are all off would be branched around and
 // not counted).  Lanes with nothing to load read past the buffer
 // (kGvmNoLoad): zeros, into LDS that no MFMA of theirs reads.  Codes: instruction j covers the wave's rows
 // 8 j + lane / 8, slot lane % 8 holding 16-byte piece (lane % 8) ^
-// ((row >> 1) & 7).  Scales: the 12 bytes of each row from the 4-byte-
-// aligned start of its 8 (row r's at 12 r; lane 64 jj + i is dword i % 3
-// of row (64 jj + i) / 3).  Activations: piece p = 64 ja + lane of [row m][limb L]
+// ((row >> 1) & 7).  Scales: row lane's 16 bytes at sup + 16 lane (S16:
+// two stages' 8 bytes every other stage; else the stage's 8 bytes inside
+// the 16 from their 4-byte-aligned start).  Activations: piece p = 64 ja + lane of [row m][limb L]
 // [16 x 16 B] (192 pieces; rows past mc are not loaded: their columns are
 // never stored), then the 4 rows' 8 block scales (lane = 2 m + half).
 template <bool S16>
@@ -321,7 +321,7 @@ __device__ __forceinline__ void gvm_issue(uint8_t* st, uint8_t* sup, __amdgpu_bu
                                           __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t ra, const int (&pofs)[8],
                                           const int (&sofs)[3], const int (&aofs)[3], int asofs, int mc, int lane,
                                           int s, bool nt) {
-    constexpr int NS = 3;
+    static_assert(kGvmStages <= 3, "a stage's scale window buffer: one of the wave's three 1 KiB areas");
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         // non-temporal when a row's 128 bytes of a stage are whole memory
@@ -338,10 +338,12 @@ __device__ __forceinline__ void gvm_issue(uint8_t* st, uint8_t* sup, __amdgpu_bu
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (gvm_lds_ptr_t)sup, 16, (s & 1) ? kGvmNoLoad : sofs[0],
                                                  (s >> 1) * 16, 0, 0);
     } else {
-#pragma unroll
-        for (int jj = 0; jj < NS; ++jj)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (gvm_lds_ptr_t)(st + kGvmOS + jj * 256), 4, sofs[jj], s * 8,
-                                                     0, 0);
+        // the stage's 8 scale bytes of each of the wave's 64 rows inside a
+        // 16-byte window from their 4-byte-aligned start (row = lane; the
+        // 8 bytes start 0 or 2 bytes in), into the stage's own 1 KiB of sup:
+        // one instruction, where three 4-byte-lane ones (each reaching 21
+        // rows' lines) cost ~10% of a C3 layer
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (gvm_lds_ptr_t)sup, 16, sofs[0], s * 8, 0, 0);
     }
 #pragma unroll
     for (int ja = 0; ja < 3; ++ja) {
@@ -366,7 +368,7 @@ __device__ __forceinline__ void gvm_issue(uint8_t* st, uint8_t* sup, __amdgpu_bu
 // rows' lines), into a double-buffered per-wave super-stage area.
 template <bool GU, bool S16>
 __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
-    constexpr int NT = S16 ? 13 : 15;                        // DMA instructions per stage
+    constexpr int NT = 13;                                   // DMA instructions per stage
     constexpr int ST = kGvmStages;
     constexpr int WAIT = NT * (ST - 1);
     static_assert(WAIT <= 63, "vmcnt holds 63");
@@ -472,16 +474,10 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
                 const int r = 8 * j + (lane >> 3);
                 d.pofs[j] = wrow(r) * lrow + (((lane & 7) ^ ((r >> 1) & 7)) << 4);
             }
-            if constexpr (S16) {
-                d.sofs[0] = wrow(lane) * srb;                    // row lane's scales
-                d.sofs[1] = d.sofs[2] = 0;
-            } else {
-#pragma unroll
-                for (int jj = 0; jj < 3; ++jj) {
-                    const int gi = 64 * jj + lane;               // row gi / 3, dword gi % 3
-                    d.sofs[jj] = ((wrow(gi / 3) * srb) & ~3) + (gi % 3) * 4;
-                }
-            }
+            // row lane's scales (S16: 16-byte aligned; else from the 4-byte-
+            // aligned start of its first byte)
+            d.sofs[0] = S16 ? wrow(lane) * srb : (wrow(lane) * srb) & ~3;
+            d.sofs[1] = d.sofs[2] = 0;
 #pragma unroll
             for (int ja = 0; ja < 3; ++ja) {
                 const int pc = 64 * ja + lane;
@@ -499,9 +495,10 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
     // Stage s of the current item (the next one when nx) into ring slot
     // q % ST (gvm_issue)
     // (S16: global stage q's super-stage buffer is (q / 2) % 2; items hold
-    // an even number of stages, so q and s have the same parity)
+    // an even number of stages, so q and s have the same parity; else the
+    // stage's scale window buffer q % 3, reused with its ring slot)
     auto issue = [&](bool nx, int s, int q) {
-        uint8_t* sup = supw + ((q & 1) ? 2048 : ((q >> 1) & 1) * 1024);
+        uint8_t* sup = S16 ? supw + ((q & 1) ? 2048 : ((q >> 1) & 1) * 1024) : supw + (q % ST) * 1024;
         if (nx)
             gvm_issue<S16>(ring + (q % ST) * kGvmStage, sup, np, ns, na, nxt.pofs, nxt.sofs, nxt.aofs, nxt.asofs,
                            nxt.mc, lane, s, nt);
@@ -575,7 +572,7 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
                     asm volatile("ds_read_b128 %0, %1"
                                  : "=v"(aq[rb]) : "v"(stb + r * 128 + ((pc ^ ((r >> 1) & 7)) << 4)));
                     const uint32_t sadr = S16 ? sup_base + uint32_t(((q >> 1) & 1) * 1024 + r * 16 + (s & 1) * 8 + pc)
-                                              : stb + uint32_t(kGvmOS + r * 12 + (soff[rb] & 3) + pc);
+                                              : sup_base + uint32_t((q % ST) * 1024 + r * 16 + (soff[rb] & 3) + pc);
                     asm volatile("ds_read_u8 %0, %1" : "=v"(sa[rb]) : "v"(sadr));
                 }
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
