@@ -302,8 +302,8 @@ static int forward_gemm_i8(hipStream_t st, const grim_moe_layer* L, const Plan& 
     e = gemm_i8_launch(st, g);
     if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
     // h limbs (rows beyond the routed count are never read)
-    e = quant_rows_launch(st, p.h32, int(R), I, p.hq, p.sh);
-    if (e == hipSuccess && sh) e = quant_rows_launch(st, p.h32sh, tokens, I, p.hshq, p.shsh);
+    e = quant_rows_launch(st, p.h32, int(R), I, p.hq, p.sh, sh ? p.h32sh : nullptr, sh ? tokens : 0,
+                          p.hshq, p.shsh);
     if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
     GemmI8Args d = g;
     d.w = L->down.payload;

@@ -1087,11 +1087,24 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float* __restrict
 // quant_rows_kernel (limbs8), so the same limbs and scales.
 constexpr int kQuantRowsPerWave = 4;
 
+// Two row sets in one launch: the waves of the first cover rows / 4 of
+// them, the rest the second set's (src2, may be empty).
 __global__ __launch_bounds__(256) void quant_rows_short_kernel(const float* __restrict__ src, int rows,
                                                                int n, int8_t* __restrict__ dst,
-                                                               float* __restrict__ scale) {
+                                                               float* __restrict__ scale,
+                                                               const float* __restrict__ src2, int rows2,
+                                                               int8_t* __restrict__ dst2,
+                                                               float* __restrict__ scale2) {
     const int lane = threadIdx.x & 63;
-    const int r0 = (blockIdx.x * 4 + int(threadIdx.x) / 64) * kQuantRowsPerWave;
+    const int wv = blockIdx.x * 4 + int(threadIdx.x) / 64;
+    const int nw1 = (rows + kQuantRowsPerWave - 1) / kQuantRowsPerWave;
+    if (wv >= nw1) {
+        src = src2;
+        rows = rows2;
+        dst = dst2;
+        scale = scale2;
+    }
+    const int r0 = (wv >= nw1 ? wv - nw1 : wv) * kQuantRowsPerWave;
     if (r0 >= rows) return;
     const int c = lane * 8;
     const bool in = c < n;
@@ -1296,15 +1309,22 @@ hipError_t gemm_i8_launch(hipStream_t st, const GemmI8Args& g) {
 }
 
 hipError_t quant_rows_launch(hipStream_t st, const float* src, int rows, int n, int8_t* dst,
-                             float* scale) {
-    if (rows <= 0) return hipSuccess;
+                             float* scale, const float* src2, int rows2, int8_t* dst2, float* scale2) {
     if (n % 64 || n > 4096) return hipErrorInvalidValue;
+    if (!src2) rows2 = 0;
+    if (rows <= 0 && rows2 <= 0) return hipSuccess;
     if (n <= 512) {
-        const int per_block = 4 * kQuantRowsPerWave;
-        hipLaunchKernelGGL(quant_rows_short_kernel, dim3((rows + per_block - 1) / per_block), dim3(256), 0, st,
-                           src, rows, n, dst, scale);
+        const int waves = (rows + kQuantRowsPerWave - 1) / kQuantRowsPerWave +
+                          (rows2 + kQuantRowsPerWave - 1) / kQuantRowsPerWave;
+        hipLaunchKernelGGL(quant_rows_short_kernel, dim3((waves + 3) / 4), dim3(256), 0, st,
+                           src, rows, n, dst, scale, src2, rows2, dst2, scale2);
         return hipGetLastError();
     }
+    if (rows2 > 0) {
+        hipError_t e = quant_rows_launch(st, src2, rows2, n, dst2, scale2);
+        if (e != hipSuccess) return e;
+    }
+    if (rows <= 0) return hipSuccess;
     hipLaunchKernelGGL(quant_rows_kernel, dim3((rows + kQuantRowsPerBlock - 1) / kQuantRowsPerBlock),
                        dim3(256), 0, st, src, rows, n, dst, scale);
     return hipGetLastError();

@@ -55,8 +55,10 @@ bool gemm_i8_gather_ok(int K, int rows);
 hipError_t gemm_i8_launch(hipStream_t st, const GemmI8Args& g);
 // src fp32 [rows][n] -> limb rows [rows][n/64][2][64] + scale [rows]
 // (n % 64 == 0, n <= 4096)
+// (src2, rows2, dst2, scale2: a second row set in the same launch)
 hipError_t quant_rows_launch(hipStream_t st, const float* src, int rows, int n, int8_t* dst,
-                             float* scale);
+                             float* scale, const float* src2 = nullptr, int rows2 = 0,
+                             int8_t* dst2 = nullptr, float* scale2 = nullptr);
 // token rows of x fp32 [T][n] -> limbs at their K permuted rows (inverse
 // [T][K]) when xq is given, at their own row when xrowq is given; the row
 // scale at every permuted row (sq) and own row (srow); perm, when given,
