@@ -24,10 +24,8 @@ constexpr int kDispThreads = 256;
 constexpr int kRoutesPerBlock = 256;
 
 __global__ __launch_bounds__(kDispThreads) void disp_count(const int32_t* __restrict__ ids, int R,
-                                                           int E, int32_t* __restrict__ bcount,
-                                                           int32_t* __restrict__ ticket) {
+                                                           int E, int32_t* __restrict__ bcount) {
     extern __shared__ int32_t hist[];
-    if (blockIdx.x == 0 && threadIdx.x == 0) *ticket = 0;   // the column scan's arrival count
     for (int e = threadIdx.x; e < E; e += blockDim.x) hist[e] = 0;
     __syncthreads();
     const int r0 = blockIdx.x * kRoutesPerBlock;
@@ -42,28 +40,14 @@ __global__ __launch_bounds__(kDispThreads) void disp_count(const int32_t* __rest
     for (int e = threadIdx.x; e < E; e += blockDim.x) bcount[int64_t(blockIdx.x) * E + e] = hist[e];
 }
 
-// The expert offsets, the m-tile table and the live tile count from the
-// expert totals, by one block of 1024 threads.
-__device__ void disp_scan_body(int E, const int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-                               int32_t* __restrict__ tile_e, int32_t* __restrict__ tile_mb, int tmax, int mc,
-                               int32_t* __restrict__ n_tiles_out);
-
 // Per-block bases inside each expert: one block per 64 experts, 16 threads
 // per expert each summing a contiguous slice of the count blocks (all its
 // loads in flight together), slices combined in LDS; writes the exclusive
-// bases back into bcount and the expert's total into counts.  The last
-// block to finish (an arrival count the count launch zeroed) then forms the
-// offsets and the tile table from all the totals (disp_scan_body).
+// bases back into bcount and the expert's total into counts.
 constexpr int kColExperts = 64, kColSlices = 16;
 __global__ __launch_bounds__(kColExperts * kColSlices) void disp_colscan(int32_t* __restrict__ bcount,
                                                                        int nb, int E,
-                                                                       int32_t* __restrict__ counts,
-                                                                       int32_t* __restrict__ ticket,
-                                                                       int32_t* __restrict__ offsets,
-                                                                       int32_t* __restrict__ tile_e,
-                                                                       int32_t* __restrict__ tile_mb, int tmax,
-                                                                       int mc, int32_t* __restrict__ n_tiles_out) {
-    __shared__ int last;
+                                                                       int32_t* __restrict__ counts) {
     __shared__ int32_t ssum[kColSlices][kColExperts];
     const int el = threadIdx.x % kColExperts, sl = threadIdx.x / kColExperts;
     const int e = blockIdx.x * kColExperts + el;
@@ -84,21 +68,15 @@ __global__ __launch_bounds__(kColExperts * kColSlices) void disp_colscan(int32_t
         }
         if (sl == kColSlices - 1) counts[e] = base;
     }
-    // release this block's totals, then count the arrival
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(ticket, 1) == int(gridDim.x) - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();   // acquire the other blocks' totals
-    disp_scan_body(E, counts, offsets, tile_e, tile_mb, tmax, mc, n_tiles_out);
 }
 
-// Per 1024-expert chunk of the totals: exclusive offsets, the m-tile table,
-// and at the end the live tile count.
-__device__ void disp_scan_body(int E, const int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-                               int32_t* __restrict__ tile_e, int32_t* __restrict__ tile_mb, int tmax, int mc,
-                               int32_t* __restrict__ n_tiles_out) {
+// One block of 1024 threads over the expert totals: exclusive offsets, the
+// m-tile table and the live tile count.
+__global__ __launch_bounds__(1024) void disp_scan(int E, int32_t* __restrict__ counts,
+                                                  int32_t* __restrict__ offsets,
+                                                  int32_t* __restrict__ tile_e,
+                                                  int32_t* __restrict__ tile_mb, int tmax, int mc,
+                                                  int32_t* __restrict__ n_tiles_out) {
     // per 1024-expert chunk: inclusive scans of counts and tiles within each
     // wave by lane shifts, then over the 16 waves' totals (two barriers)
     __shared__ int32_t wsum[16][2];
@@ -223,11 +201,12 @@ hipError_t dispatch_launch(hipStream_t st, const DispatchArgs& a) {
     int32_t* ntiles = bcount + int64_t(nb > 0 ? nb : 1) * a.E;
     if (nb > 0)
         hipLaunchKernelGGL(disp_count, dim3(nb), dim3(kDispThreads), size_t(a.E) * 4, st, a.ids, R,
-                           a.E, bcount, ntiles + 1);
+                           a.E, bcount);
     // T > 0 here (the callers return before), so nb >= 1
     hipLaunchKernelGGL(disp_colscan, dim3((a.E + kColExperts - 1) / kColExperts),
-                       dim3(kColExperts * kColSlices), 0, st, bcount, nb, a.E, a.counts, ntiles + 1, a.offsets,
-                       a.tile_e, a.tile_mb, a.tmax, a.mc, ntiles);
+                       dim3(kColExperts * kColSlices), 0, st, bcount, nb, a.E, a.counts);
+    hipLaunchKernelGGL(disp_scan, dim3(1), dim3(1024), 0, st, a.E, a.counts, a.offsets, a.tile_e,
+                       a.tile_mb, a.tmax, a.mc, ntiles);
     if (nb > 0)
         hipLaunchKernelGGL(disp_rank, dim3(nb), dim3(kDispThreads), 0, st, a.ids, R, a.E, a.K,
                            bcount, a.offsets, a.inverse, a.perm_token);
