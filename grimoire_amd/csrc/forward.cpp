@@ -92,6 +92,7 @@ struct Plan {
     float* hrep;    // fused decode: copies of h
     // GEMM
     float* logits2;   // the split-K router's second partial
+    void* wimg;       // the split-K router's W limb image
     void* disp_ws;
     int32_t *counts, *offsets, *inverse, *tile_e, *tile_mb;
     int tmax;
@@ -147,6 +148,8 @@ size_t carve(const grim_moe_layer* L, int T, bool gemv, char* base, Plan& p) {
         const size_t dws = dispatch_workspace_bytes(T, K, E);
         p.disp_ws = cv.take<char>(dws);
         p.logits2 = cv.take<float>(size_t(T) * E);
+        const size_t wib = router_wimg_bytes(T, E, H);
+        p.wimg = wib ? static_cast<void*>(cv.take<char>(wib)) : nullptr;
         p.counts = cv.take<int32_t>(E);
         p.offsets = cv.take<int32_t>(E);
         p.inverse = cv.take<int32_t>(R);
@@ -689,7 +692,8 @@ static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_
     int deferred = 0;
     {
         hipError_t e = router_logits_launch(st, L->router, x, rbias, p.logits, tokens, E, H,
-                                            gemv ? nullptr : p.logits2, &deferred);
+                                            gemv ? nullptr : p.logits2, &deferred,
+                                            gemv ? nullptr : p.wimg);
         if (e != hipSuccess) return ferr(int(e), hipGetErrorString(e));
     }
     int r = GRIM_OK;

@@ -7,11 +7,13 @@
 #include "topk.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace grim {
 
 constexpr int kTopkWaves = 4;
 typedef float f32x4n __attribute__((ext_vector_type(4)));   // native vector (HIP's float4 is a struct)
+typedef uint32_t u32x4n __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(kTopkWaves * kWave) void topk_kernel(
     const float* __restrict__ logits, int T, int E, int K, int mode, int normalize,
@@ -500,160 +502,285 @@ __global__ __launch_bounds__(256) void router_bf16x3(const float* __restrict__ W
 }
 
 // The same three-limb products on 128 x 128 tiles with K split in two
-// halves (grid z).  What bounds router_bf16x3 at T = 4096, E = 512 is the
-// operand feed: every 64 x 64 tile reads its 64 x rows and 64 W rows over
-// the whole K (1 MB), 2 MB per CU.  Here a work-group reads 128 x rows and
-// 128 W rows over half of K, 1 MB per CU.  The two halves are added into
-// zeroed logits by two float atomics, so the sum is exactly a + b
-// whichever lands first; a bias is added after (logits = (a + b) + bias).
-// x is split only where it is not a bf16 value: the barrier after each K
-// tile's LDS stores tells every wave (per-wave flags in LDS) whether some
-// x of the tile has a mid / lo limb; if none has, the three products of
-// x's only limb run (xh.wl, xh.wm, xh.wh), else the six of router_bf16x3,
-// in its order.
-constexpr int kRsBM = 128, kRsBN = 128, kRsPre = 3, kRsThreads = 512;
+// halves (grid z).  At T = 4096, E = 512 a 64 x 64 tile per work-group reads
+// its 64 x rows and 64 W rows over the whole K (2 MB per CU); a 128 x 128
+// tile over half of K reads 1 MB.  The halves store their partial sums a
+// (logits) and b (part1) for the caller to finish as (a + b) + bias, or,
+// without part1, add them into zeroed logits by two float atomics
+// (0 + a + b = a + b whichever lands first).
+//
+// The work is divided by wave, not by phase: loading a K tile, splitting
+// it into limbs and storing the limb planes in LDS is vector-ALU and load
+// work that one wave per SIMD cannot issue fast enough, and run in the same
+// waves as the matrix products their times add.  Waves 4..11 (producers)
+// load K tile kt + 3 into registers and store tile kt + 1 into the other LDS
+// buffer while waves 0..3 (consumers, one per SIMD) run tile kt's products,
+// one barrier per tile.  Consumer c owns tokens 64 (c / 2) .. + 64 and
+// experts 64 (c % 2) .. + 64 of the tile (2 x 2 blocks of 32 x 32).
+// IMG: W's limb planes come from router_wimg_kernel's image (split once per
+// call, in K-tile order), so the producers only copy them; else the
+// producers split W as they split x.  x is split only where it is not a
+// bf16 value: a producer wave whose x pieces are all bf16 values stores the
+// hi plane only and flags the tile clean; if some wave flags it, the
+// consumers run the six products of router_bf16x3 in its order (mm, lh, hl,
+// mh, hm, hh), else the three of x's one limb (hl, hm, hh) -- the skipped
+// products are exact zeros.  x's mid / lo planes start at zero in both
+// buffers; a wave clears its mid / lo pieces again only after a tile that
+// had them.
+constexpr int kRsBM = 128, kRsBN = 128, kRsPre = 3;
+// producer waves: 4 copy the W image and handle x; 8 split W and x
+template <bool IMG> constexpr int rs_prod() { return 8; }
+template <bool IMG> constexpr int rs_threads() { return 64 * (4 + rs_prod<IMG>()); }
+constexpr int kRsPlane = kRsBM * kR3LD;                       // bf16 per limb plane of one operand
+constexpr size_t kRsLds = size_t(2) * 6 * kRsPlane * sizeof(uint16_t) + 2 * 8 * sizeof(int);
+// W image: per (128-row expert block, K tile of 32), the three limb planes
+// [plane][row][32] bf16 (24 KiB); rows past E repeat the last
+constexpr int kRsImgPieces = 3 * kRsBN * kR3BK / 8;          // 16-byte pieces per block (1536)
 
-// One K tile (32) of 128 rows of src into registers: two 16-byte pieces
-// per thread (row c / 8, K offset 4 (c % 8), c = thread + 512 i); rows past
-// n repeat the last one.
-__device__ __forceinline__ void rs_load(const float* __restrict__ src, int n, int H, int r0, int k0,
-                                        f32x4n (&reg)[2]) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = int(threadIdx.x) + i * kRsThreads, r = c >> 3, kc = (c & 7) * 4;
-        const int rr = min(r0 + r, n - 1);
-        reg[i] = *reinterpret_cast<const f32x4n*>(src + int64_t(rr) * H + k0 + kc);
-    }
+size_t router_wimg_bytes(int T, int E, int H) {
+    if (!(H % (2 * kR3BK) == 0 && H >= 2 * kR3BK * kRsPre && T >= 256)) return 0;
+    return size_t((E + kRsBN - 1) / kRsBN) * (H / kR3BK) * kRsImgPieces * 16;
 }
 
-// The pieces as three bf16 limb planes in LDS; returns whether some value
-// of the thread's pieces is not a bf16 value (when `check`).
-__device__ __forceinline__ int rs_split_store(uint16_t* __restrict__ dst, int plane, const f32x4n (&reg)[2],
-                                              bool check) {
-    uint32_t any = 0;
+// One thread per 8 consecutive weights of a row: their three limbs, 16
+// bytes per plane (split3, the split the GEMM would do).
+__global__ __launch_bounds__(256) void router_wimg_kernel(const float* __restrict__ W, int E, int H,
+                                                          uint4* __restrict__ img) {
+    const int nkt = H / kR3BK, neb = (E + kRsBN - 1) / kRsBN;
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= int64_t(neb) * nkt * (kRsBN * kR3BK / 8)) return;
+    const int q = int(i % (kRsBN * kR3BK / 8));                  // row * 4 + 8-column group
+    const int64_t blk = i / (kRsBN * kR3BK / 8);                 // eb * nkt + kt
+    const int eb = int(blk / nkt), kt = int(blk % nkt);
+    const int e = min(eb * kRsBN + (q >> 2), E - 1);
+    const float* src = W + int64_t(e) * H + kt * kR3BK + (q & 3) * 8;
+    uint32_t w0[3][2], w1[3][2];
+    split3(*reinterpret_cast<const f32x4n*>(src), w0);
+    split3(*reinterpret_cast<const f32x4n*>(src + 4), w1);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = int(threadIdx.x) + i * kRsThreads, r = c >> 3, kc = (c & 7) * 4;
-        if (check)
-            any |= (__float_as_uint(reg[i].x) | __float_as_uint(reg[i].y) | __float_as_uint(reg[i].z) |
-                    __float_as_uint(reg[i].w)) & 0xFFFFu;
-        uint32_t w[3][2];
-        split3(reg[i], w);
-#pragma unroll
-        for (int p = 0; p < 3; ++p)
-            *reinterpret_cast<uint2*>(&dst[p * plane + r * kR3LD + kc]) = make_uint2(w[p][0], w[p][1]);
-    }
-    return any != 0u ? 1 : 0;
+    for (int p = 0; p < 3; ++p)
+        img[blk * kRsImgPieces + p * (kRsImgPieces / 3) + q] = make_uint4(w0[p][0], w0[p][1], w1[p][0], w1[p][1]);
 }
 
-// 8 waves: wave w computes tokens 32 (w / 2) .. + 32 and experts
-// 64 (w % 2) .. + 64 of the tile (two 32 x 32 MFMA blocks), so two waves
-// share each SIMD and one's LDS traffic and splitting overlap the other's
-// matrix products.
-__global__ __launch_bounds__(kRsThreads) void router_bf16x3_sk(const float* __restrict__ W,
+// Barrier for LDS hand-offs: waits for the wave's own LDS accesses, not for
+// its global loads in flight (a __syncthreads() fence would wait for those too).
+__device__ __forceinline__ void rs_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <bool IMG>
+__global__ __launch_bounds__(rs_threads<IMG>()) void router_bf16x3_ws(const float* __restrict__ W,
+                                                               const uint4* __restrict__ wimg,
                                                                const float* __restrict__ x,
                                                                float* __restrict__ logits,
                                                                float* __restrict__ part1, int T, int E, int H) {
-    constexpr int PS = kRsBM * kR3LD;                 // one plane of one operand (BM == BN)
-    constexpr int NW = kRsThreads / 64;
-    __shared__ __attribute__((aligned(16))) uint16_t Xs[2][3 * PS];
-    __shared__ __attribute__((aligned(16))) uint16_t Ws[2][3 * PS];
-    __shared__ __attribute__((aligned(16))) int wflag[2][NW];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1, h = lane >> 5;
-    // blockIdx.x = token block (the expert blocks of one token block share
-    // an XCD and its copy of x), blockIdx.z = K half
+    constexpr int kRsProd = rs_prod<IMG>();
+    constexpr int PS = kRsPlane, NP = 64 * kRsProd;
+    extern __shared__ __attribute__((aligned(16))) uint16_t rs_lds[];
+    uint16_t* Xs0 = rs_lds;                                   // [buf][plane][128][kR3LD]
+    uint16_t* Ws0 = rs_lds + 2 * 3 * PS;
+    int* wflag = reinterpret_cast<int*>(rs_lds + 4 * 3 * PS); // [buf][producer wave]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // blockIdx.x = token block (the expert blocks and K halves of one token
+    // block share an XCD and its copy of x)
     const int t0 = blockIdx.x * kRsBM, e0 = blockIdx.y * kRsBN;
     const int nk = H / kR3BK / 2, kb = blockIdx.z * nk;
-    f32x4n rx[kRsPre][2], rw[kRsPre][2];
-    f32x16r acc[2];
+    if (wave >= 4) {
+        // ---------------- producers: thread p's x pieces (and W pieces
+        // without the image) are c = p + NP i: row c / 8, K 4 (c % 8) .. + 4
+        const int p = tid - 256, pw = wave - 4;
+        for (int i = p; i < 2 * 2 * PS / 4; i += NP) {
+            const int b = i / (2 * PS / 4), o = i % (2 * PS / 4);
+            reinterpret_cast<uint2*>(Xs0 + b * 3 * PS + PS)[o] = make_uint2(0u, 0u);
+        }
+        constexpr int NX = kRsBM * kR3BK / 4 / NP;                 // x pieces per thread (2)
+        constexpr int NW = IMG ? kRsImgPieces / NP : NX;           // W pieces (3 image / 2 fp32)
+        static_assert(NX * NP * 4 == kRsBM * kR3BK && (!IMG || NW * NP == kRsImgPieces), "pieces");
+        typedef typename std::conditional<IMG, u32x4n, f32x4n>::type WPiece;
+        f32x4n rx[kRsPre][NX];
+        WPiece rv[kRsPre][NW];
+        const u32x4n* wblk = IMG ? reinterpret_cast<const u32x4n*>(wimg) + int64_t(blockIdx.y) * (H / kR3BK) * kRsImgPieces
+                                  : nullptr;
+        auto load = [&](int kt, f32x4n (&ax)[NX], WPiece (&aw)[NW]) {
+            const int k0 = (kb + kt) * kR3BK;
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni)
+            for (int i = 0; i < NX; ++i) {
+                const int c = p + NP * i, r = c >> 3, kc = (c & 7) * 4;
+                ax[i] = *reinterpret_cast<const f32x4n*>(x + int64_t(min(t0 + r, T - 1)) * H + k0 + kc);
+            }
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[ni][v] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kRsPre; ++j) {
-        rs_load(x, T, H, t0, (kb + j) * kR3BK, rx[j]);
-        rs_load(W, E, H, e0, (kb + j) * kR3BK, rw[j]);
-    }
-    {
-        const int any = rs_split_store(Xs[0], PS, rx[0], true);
-        rs_split_store(Ws[0], PS, rw[0], false);
-        const bool b = __ballot(any) != 0;
-        if (lane == 0) wflag[0][wave] = b ? 1 : 0;
-    }
-    __syncthreads();
-    for (int k0 = 0; k0 < nk; k0 += kRsPre) {
-#pragma unroll
-        for (int u = 0; u < kRsPre; ++u) {
-            const int kt = k0 + u, buf = kt & 1;
-            if (kt >= nk) break;
-            const int kn = (kb + min(kt + kRsPre, nk - 1)) * kR3BK;
-            rs_load(x, T, H, t0, kn, rx[u]);
-            rs_load(W, E, H, e0, kn, rw[u]);
-            int fl = 0;
-#pragma unroll
-            for (int w = 0; w < NW; ++w) fl |= wflag[buf][w];
-            const bool full = fl != 0;   // uniform
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const int kk = 16 * h + 8 * ks;
-                const uint16_t* xa = &Xs[buf][(wm * 32 + (lane & 31)) * kR3LD + kk];
-                const bf16x8r a0 = *reinterpret_cast<const bf16x8r*>(xa);
-                bf16x8r b[2][3];
-#pragma unroll
-                for (int ni = 0; ni < 2; ++ni)
-#pragma unroll
-                    for (int p = 0; p < 3; ++p)
-                        b[ni][p] = *reinterpret_cast<const bf16x8r*>(
-                            &Ws[buf][p * PS + (wn * 64 + ni * 32 + (lane & 31)) * kR3LD + kk]);
-                // router_bf16x3's order: mm, lh, hl, mh, hm, hh (the x-limb
-                // products are zero when the tile's x are bf16 values)
-                if (full) {
-                    const bf16x8r a1 = *reinterpret_cast<const bf16x8r*>(xa + PS);
-                    const bf16x8r a2 = *reinterpret_cast<const bf16x8r*>(xa + 2 * PS);
-#pragma unroll
-                    for (int ni = 0; ni < 2; ++ni) {
-                        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b[ni][1], acc[ni], 0, 0, 0);
-                        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b[ni][0], acc[ni], 0, 0, 0);
-                        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b[ni][2], acc[ni], 0, 0, 0);
-                        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b[ni][0], acc[ni], 0, 0, 0);
-                    }
+            for (int i = 0; i < NW; ++i) {
+                if constexpr (IMG) {
+                    aw[i] = wblk[int64_t(kb + kt) * kRsImgPieces + p + NP * i];
                 } else {
+                    const int c = p + NP * i, r = c >> 3, kc = (c & 7) * 4;
+                    aw[i] = *reinterpret_cast<const f32x4n*>(W + int64_t(min(e0 + r, E - 1)) * H + k0 + kc);
+                }
+            }
+        };
+        int dirty = 0;   // bit b: this wave left x mid / lo pieces in buffer b
+        auto store = [&](int buf, const f32x4n (&ax)[NX], const WPiece (&aw)[NW]) {
+            uint16_t* xs = Xs0 + buf * 3 * PS;
+            uint16_t* ws = Ws0 + buf * 3 * PS;
+            uint32_t any = 0;
 #pragma unroll
-                    for (int ni = 0; ni < 2; ++ni)
-                        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b[ni][2], acc[ni], 0, 0, 0);
+            for (int i = 0; i < NX; ++i)
+                any |= (__float_as_uint(ax[i].x) | __float_as_uint(ax[i].y) | __float_as_uint(ax[i].z) |
+                        __float_as_uint(ax[i].w)) & 0xFFFFu;
+            const bool full = __ballot(any != 0u) != 0;   // uniform
+#pragma unroll
+            for (int i = 0; i < NX; ++i) {
+                const int c = p + NP * i, o = (c >> 3) * kR3LD + (c & 7) * 4;
+                if (full) {
+                    uint32_t w[3][2];
+                    split3(ax[i], w);
+#pragma unroll
+                    for (int q = 0; q < 3; ++q)
+                        *reinterpret_cast<uint2*>(&xs[q * PS + o]) = make_uint2(w[q][0], w[q][1]);
+                } else {
+                    // bf16 values: the hi limb is the upper half of each word
+                    const uint32_t h0 = __builtin_amdgcn_perm(__float_as_uint(ax[i].y), __float_as_uint(ax[i].x),
+                                                              0x07060302u);
+                    const uint32_t h1 = __builtin_amdgcn_perm(__float_as_uint(ax[i].w), __float_as_uint(ax[i].z),
+                                                              0x07060302u);
+                    *reinterpret_cast<uint2*>(&xs[o]) = make_uint2(h0, h1);
+                    if (dirty & (1 << buf)) {
+                        *reinterpret_cast<uint2*>(&xs[PS + o]) = make_uint2(0u, 0u);
+                        *reinterpret_cast<uint2*>(&xs[2 * PS + o]) = make_uint2(0u, 0u);
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < NW; ++i) {
+                if constexpr (IMG) {
+                    // image piece q: plane q / 512, row (q % 512) / 4, columns 8 (q % 4) .. + 8
+                    const int q = p + NP * i;
+                    *reinterpret_cast<u32x4n*>(&ws[(q >> 9) * PS + ((q & 511) >> 2) * kR3LD + (q & 3) * 8]) = aw[i];
+                } else {
+                    const int c = p + NP * i, o = (c >> 3) * kR3LD + (c & 7) * 4;
+                    uint32_t w[3][2];
+                    split3(aw[i], w);
+#pragma unroll
+                    for (int q = 0; q < 3; ++q)
+                        *reinterpret_cast<uint2*>(&ws[q * PS + o]) = make_uint2(w[q][0], w[q][1]);
+                }
+            }
+            dirty = full ? (dirty | (1 << buf)) : (dirty & ~(1 << buf));
+            if (lane == 0) wflag[buf * kRsProd + pw] = full ? 1 : 0;
+        };
+#pragma unroll
+        for (int j = 0; j < kRsPre; ++j) load(min(j, nk - 1), rx[j], rv[j]);
+        store(0, rx[0], rv[0]);
+        rs_barrier();
+        for (int k0 = 0; k0 < nk; k0 += kRsPre) {
+#pragma unroll
+            for (int u = 0; u < kRsPre; ++u) {
+                const int kt = k0 + u;
+                if (kt >= nk) break;
+                // set u held tile kt (stored already): request tile kt + kRsPre
+                // (past the end the last again, never stored: loads under a
+                // branch would make the compiler wait for every load in flight)
+                load(min(kt + kRsPre, nk - 1), rx[u], rv[u]);
+                if (kt + 1 < nk) store((kt + 1) & 1, rx[(u + 1) % kRsPre], rv[(u + 1) % kRsPre]);
+                rs_barrier();
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        return;
+    }
+    // ---------------- consumers
+    const int wm = wave >> 1, wn = wave & 1, h = lane >> 5;
+    f32x16r acc[2][2];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.0f;
+    rs_barrier();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        const uint16_t* xs = Xs0 + buf * 3 * PS;
+        const uint16_t* ws = Ws0 + buf * 3 * PS;
+        // both K steps' fragments of the planes every tile uses, and the
+        // flags, issued together (lane half h supplies K = 16 h + 8 ks .. + 7,
+        // the same for x and W); x's mid / lo planes after, when flagged
+        bf16x8r a[2][2], b[2][2][3];   // [ks][mi] hi plane, [ks][ni][plane]
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int kk = 16 * h + 8 * ks;
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+                a[ks][mi] = *reinterpret_cast<const bf16x8r*>(&xs[(wm * 64 + mi * 32 + (lane & 31)) * kR3LD + kk]);
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+                for (int q = 0; q < 3; ++q)
+                    b[ks][ni][q] = *reinterpret_cast<const bf16x8r*>(
+                        &ws[q * PS + (wn * 64 + ni * 32 + (lane & 31)) * kR3LD + kk]);
+        }
+        int fl = 0;
+#pragma unroll
+        for (int w = 0; w < kRsProd; ++w) fl |= wflag[buf * kRsProd + w];
+        const bool full = fl != 0;   // uniform
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            // per accumulator: mm, lh, hl, mh, hm, hh (router_bf16x3's order)
+            bf16x8r am[2], al[2];   // x's mid / lo planes (full tiles only)
+            if (full) {
+#pragma unroll
+                for (int mi = 0; mi < 2; ++mi) {
+                    const uint16_t* xa = &xs[(wm * 64 + mi * 32 + (lane & 31)) * kR3LD + 16 * h + 8 * ks];
+                    am[mi] = *reinterpret_cast<const bf16x8r*>(xa + PS);
+                    al[mi] = *reinterpret_cast<const bf16x8r*>(xa + 2 * PS);
                 }
 #pragma unroll
-                for (int ni = 0; ni < 2; ++ni)
-                    acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b[ni][1], acc[ni], 0, 0, 0);
+                for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-                for (int ni = 0; ni < 2; ++ni)
-                    acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b[ni][0], acc[ni], 0, 0, 0);
+                    for (int ni = 0; ni < 2; ++ni) {
+                        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[mi], b[ks][ni][1], acc[mi][ni], 0, 0, 0);
+                        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[mi], b[ks][ni][0], acc[mi][ni], 0, 0, 0);
+                    }
             }
-            if (kt + 1 < nk) {
-                const int un = (u + 1) % kRsPre;
-                const int any = rs_split_store(Xs[buf ^ 1], PS, rx[un], true);
-                rs_split_store(Ws[buf ^ 1], PS, rw[un], false);
-                const bool b = __ballot(any) != 0;
-                if (lane == 0) wflag[buf ^ 1][wave] = b ? 1 : 0;
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks][mi], b[ks][ni][2], acc[mi][ni], 0, 0, 0);
+            if (full) {
+#pragma unroll
+                for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                    for (int ni = 0; ni < 2; ++ni)
+                        acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[mi], b[ks][ni][0], acc[mi][ni], 0, 0, 0);
             }
-            __syncthreads();
-        }
-    }
-    // acc[ni][v]: token row (v&3) + 4*(lane>>5) + 8*(v>>2), expert lane&31
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
-        const int e = e0 + wn * 64 + ni * 32 + (lane & 31);
-        if (e >= E) continue;
+            for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int t = t0 + wm * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
-            if (t >= T) continue;
-            if (part1) (blockIdx.z == 0 ? logits : part1)[int64_t(t) * E + e] = acc[ni][v];
-            else unsafeAtomicAdd(&logits[int64_t(t) * E + e], acc[ni][v]);
+                for (int ni = 0; ni < 2; ++ni)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks][mi], b[ks][ni][1], acc[mi][ni], 0, 0, 0);
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks][mi], b[ks][ni][0], acc[mi][ni], 0, 0, 0);
         }
+        rs_barrier();
     }
+    // acc[mi][ni][v]: token row (v&3) + 4*(lane>>5) + 8*(v>>2), expert lane&31
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+            const int e = e0 + wn * 64 + ni * 32 + (lane & 31);
+            if (e >= E) continue;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int t = t0 + wm * 64 + mi * 32 + (v & 3) + 4 * (lane >> 5) + 8 * (v >> 2);
+                if (t >= T) continue;
+                if (part1) (blockIdx.z == 0 ? logits : part1)[int64_t(t) * E + e] = acc[mi][ni][v];
+                else unsafeAtomicAdd(&logits[int64_t(t) * E + e], acc[mi][ni][v]);
+            }
+        }
 }
 
 // logits = 0 (bias null) or logits += bias, four values per thread when E
@@ -686,7 +813,7 @@ __global__ __launch_bounds__(256) void router_fill_kernel(float* __restrict__ lo
 
 hipError_t router_logits_launch(hipStream_t st, const float* W, const float* x,
                                 const float* bias, float* logits, int T, int E, int H, float* part1,
-                                int* deferred) {
+                                int* deferred, void* wimg) {
     if (deferred) *deferred = 0;
     if (T <= 32 && H % 4 == 0 && router_nk_launch(st, W, x, bias, logits, T, E, H)) {
     } else if (T <= 32 && H % 4 == 0) {
@@ -699,16 +826,32 @@ hipError_t router_logits_launch(hipStream_t st, const float* W, const float* x,
         // them (0 + a + b = a + b in either order), then the bias.
         const int64_t n = int64_t(T) * E;
         const unsigned fb = unsigned((n + 1023) / 1024);
+        // (wimg: W's limb planes split once here by router_wimg_kernel,
+        // router_wimg_bytes(T, E, H) bytes, 16-byte aligned)
         dim3 grid((T + kRsBM - 1) / kRsBM, (E + kRsBN - 1) / kRsBN, 2);
+        const uint4* img = static_cast<const uint4*>(wimg);
+        if (img && (reinterpret_cast<uintptr_t>(img) & 15)) return hipErrorInvalidValue;
+        if (img) {
+            const int64_t nt = int64_t((E + kRsBN - 1) / kRsBN) * (H / kR3BK) * (kRsBN * kR3BK / 8);
+            hipLaunchKernelGGL(router_wimg_kernel, dim3(unsigned((nt + 255) / 256)), dim3(256), 0, st, W, E, H,
+                               static_cast<uint4*>(wimg));
+        }
+        auto gemm = [&](float* p1) {
+            if (img)
+                hipLaunchKernelGGL(router_bf16x3_ws<true>, grid, dim3(rs_threads<true>()), kRsLds, st, W, img, x, logits,
+                                   p1, T, E, H);
+            else
+                hipLaunchKernelGGL(router_bf16x3_ws<false>, grid, dim3(rs_threads<false>()), kRsLds, st, W, img, x, logits,
+                                   p1, T, E, H);
+        };
         if (part1 && deferred) {
-            hipLaunchKernelGGL(router_bf16x3_sk, grid, dim3(kRsThreads), 0, st, W, x, logits, part1, T, E, H);
+            gemm(part1);
             *deferred = 1;
             return hipGetLastError();
         }
         hipLaunchKernelGGL(router_fill_kernel, dim3(fb), dim3(256), 0, st, logits, nullptr, n, E,
                            static_cast<const float*>(nullptr));
-        hipLaunchKernelGGL(router_bf16x3_sk, grid, dim3(kRsThreads), 0, st, W, x, logits,
-                           static_cast<float*>(nullptr), T, E, H);
+        gemm(nullptr);
         if (bias)
             hipLaunchKernelGGL(router_fill_kernel, dim3(fb), dim3(256), 0, st, logits, bias, n, E,
                                static_cast<const float*>(nullptr));

@@ -28,10 +28,15 @@ hipError_t topk_bf16_launch(hipStream_t st, const uint16_t* logits, int T, int E
 // logits = x W^T + bias.  With part1 ([T][E] scratch) and deferred, a
 // split-K launch may leave the two partials in logits and part1 and set
 // *deferred: the caller then finishes (topk_launch with part1 / lbias, or
-// router_finish_launch).
+// router_finish_launch).  wimg (optional, router_wimg_bytes(T, E, H) bytes,
+// 16-byte aligned): scratch for W's limb planes, split once per call
+// instead of once per token block.
 hipError_t router_logits_launch(hipStream_t st, const float* W, const float* x,
                                 const float* bias, float* logits, int T, int E, int H,
-                                float* part1 = nullptr, int* deferred = nullptr);
+                                float* part1 = nullptr, int* deferred = nullptr, void* wimg = nullptr);
+// Bytes of the split router's W limb image for this shape (0: that path is
+// not taken).
+size_t router_wimg_bytes(int T, int E, int H);
 // logits = (logits + part1) + bias (bias may be null)
 hipError_t router_finish_launch(hipStream_t st, float* logits, const float* part1, const float* bias, int T,
                                 int E);

@@ -100,6 +100,26 @@ def test_forward_int8_gather_edges(gpu, H):
     assert_close(y, yo, what=f"int8 prefill H={H}")
 
 
+def test_forward_split_router_fp32_x(gpu):
+    """T >= 256 takes the split-K router with W's limb planes split once per
+    call into the workspace; x not bf16 valued on every other block of 64
+    rows (all six limb products there): routing bit-exact against the top-k
+    of the standalone router's logits, outputs against the oracle (I = 256:
+    the INT8 experts, whose two activation limbs keep fp32 x to ~2^-16 of
+    its row's largest value)."""
+    print("forward split router, fp32 x", flush=True)
+    cfg = configs.scaled(configs.CONFIGS["c4"], T=300, H=512, E=96, I=256)
+    wl = configs.make_workload(cfg, "cpu", seed=12)
+    x = torch.randn(cfg.T, cfg.H, generator=torch.Generator().manual_seed(12))
+    rows = (torch.arange(cfg.T) // 64) % 2 == 0
+    x[rows] = x[rows].bfloat16().float()
+    wl = configs.Workload(cfg, wl.layer, x.contiguous(), wl.route_bias)
+    Lg, y, oe, ow, logits = _run(wl, gpu, regime=2)
+    _check_routing(wl, logits, oe, ow)
+    yo = _oracle_y(wl.layer, wl.x, oe, ow, wl.layer.shared_gate_w)
+    assert_close(y, yo, what="split router, fp32 x")
+
+
 def test_forward_c5_scaled(gpu):
     print("forward c5 scaled (group-limited sigmoid, mxfp4, shared)", flush=True)
     cfg = configs.scaled(configs.CONFIGS["c5"], T=32, H=1024, E=64, I=256)

@@ -42,6 +42,28 @@ def test_router_logits(gpu, T, E, H):
     assert rel_l2(out.cpu(), want) < 1e-5
 
 
+# T >= 256, H % 64 == 0: the split-K three-limb kernel.  x that is not bf16
+# valued takes the six limb products on the tiles that hold it: all rows
+# fp32, or every other block of 64 rows, so that clean and full tiles and
+# producer waves meet in one launch; ragged token and expert blocks.
+@pytest.mark.parametrize("T,E,H,kind", [(1000, 200, 1024, "fp32"), (520, 512, 2048, "mixed"),
+                                        (256, 130, 384, "fp32")])
+def test_router_logits_split_fp32_x(gpu, T, E, H, kind):
+    print(f"router_logits split T={T} E={E} H={H} x={kind}", flush=True)
+    g = torch.Generator().manual_seed(T + E + H)
+    W = torch.randn(E, H, generator=g) * 0.02
+    x = torch.randn(T, H, generator=g)
+    if kind == "mixed":
+        rows = (torch.arange(T) // 64) % 2 == 0
+        x[rows] = x[rows].bfloat16().float()
+    out = torch.empty(T, E, device=gpu)
+    ops.router_logits(W.to(gpu), x.to(gpu), out)
+    torch.cuda.synchronize()
+    want = O.router_logits(W, x)
+    assert (out.cpu() - want).abs().max() < 1e-4
+    assert rel_l2(out.cpu(), want) < 1e-5
+
+
 @pytest.mark.parametrize("T,E,K", [(1, 128, 8), (1, 256, 8), (5, 64, 4), (40, 512, 10), (3, 20, 16),
                                    (9, 300, 7)])
 @pytest.mark.parametrize("normalize", [True, False])
