@@ -512,14 +512,19 @@ def _touched_bytes(L, oe):
     return len(set(oe.flatten().tolist())) * L.expert_bytes() + L.shared_bytes()
 
 
-def c3_bench(dev, stream, n_layers=4, reps=10, regime=0):
+def c3_bench(dev, stream, n_layers=4, reps=10, regime=0, padded=True):
     """C3 (T=8 users, H=2880, E=128, top-4 softmax with Zipf(1.1)
     popularity, I=2880, MXFP4): the forward of n_layers distinct layers in
     one graph (their touched experts exceed the 256 MB MALL).  regime 0 is
     what the forward picks (the matrix-core expert-grouped GEMV); regime 1,
-    the per-route decode kernels, is reported beside it."""
+    the per-route decode kernels, is reported beside it.  padded: the
+    experts' MXFP4 rows padded once at load to 3072 elements
+    (MoeLayer.pad_mxfp4 / grimoire_moe_pad_mxfp4_rows: whole memory lines
+    per streamed piece, the same outputs bit for bit); bytes and GB/s are
+    the unpadded rows' either way."""
     cfg = configs.CONFIGS["c3"]
-    layers = [configs.make_layer(cfg, dev, seed=300 + i) for i in range(n_layers)]
+    base = [configs.make_layer(cfg, dev, seed=300 + i) for i in range(n_layers)]
+    layers = [L.pad_mxfp4() for L in base] if padded else base
     bias = configs.make_route_bias(cfg, dev, seed=3)
     x = configs.make_x(cfg, dev, seed=3)
     fwds = [ops.MoeForward(L, cfg.T, configs.route_params(cfg, bias), regime=regime) for L in layers]
@@ -540,7 +545,7 @@ def c3_bench(dev, stream, n_layers=4, reps=10, regime=0):
     with Timer(stream) as t:
         _replay(g, stream, reps)
     us = t.ms() * 1e3 / (reps * n_layers)
-    nbytes = sum(_touched_bytes(L, oe.cpu()) for L, oe in zip(layers, oes)) / n_layers
+    nbytes = sum(_touched_bytes(L, oe.cpu()) for L, oe in zip(base, oes)) / n_layers
     nbytes += cfg.E * cfg.H * 4 + 2 * cfg.T * cfg.H * 4
     touched = sum(len(set(oe.cpu().flatten().tolist())) for oe in oes) / n_layers
     gbs = nbytes / (us * 1e-6) / 1e9
@@ -548,6 +553,7 @@ def c3_bench(dev, stream, n_layers=4, reps=10, regime=0):
                         f"{n_layers} distinct layers in one graph",
             "regime": ["chosen by the forward (expert-grouped GEMV, matrix core)", "per-route decode kernels"][
                 min(regime, 1)],
+            "weight_rows": "padded to 3072 elements at load" if padded else "packed (the reference's layout)",
             "us_per_layer": round(us, 2), "experts_touched": touched,
             "bytes_per_layer": int(nbytes), "gbs": round(gbs, 1),
             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
@@ -701,6 +707,7 @@ def main():
     if not a.no_prefill:
         log("C3 (T=8 MXFP4 decode) and C5 (T=32 verify, 6 GB of experts)...")
         out["c3"] = c3_bench(dev, stream)
+        out["c3_packed_rows"] = c3_bench(dev, stream, padded=False)
         out["c3_decode_kernels"] = c3_bench(dev, stream, regime=1)
         out["c5"] = c5_bench(dev, stream)
         out["c5_shard"] = c5_shard_bench(dev, stream)

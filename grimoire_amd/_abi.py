@@ -184,6 +184,8 @@ SIGNATURES = {
     "grimoire_heat_propose": (I32, [P, P, P, C.POINTER(ExpertSwap), I32]),
     "grimoire_moe_grouped_gemm": (I32, [P, QWP, I32, I32, P, I32, P, I32, P, P, I32, I32]),
     "grimoire_moe_quant_limbs": (I32, [P, P, I32, I32, P, P]),
+    "grimoire_moe_mxfp4_padded_k": (I32, [I32]),
+    "grimoire_moe_pad_mxfp4_rows": (I32, [P, QWP, QWP]),
     "grimoire_moe_grouped_gemm_i8": (I32, [P, QWP, I32, I32, P, P, P, P, P, P, P, I32, I32]),
     "grimoire_moe_grouped_gemm_i8_rows": (I32, [P, QWP, I32, I32, P, P, P, P, P, I32, I32]),
     "grimoire_moe_grouped_gemm_i8_rows_gather": (I32, [P, QWP, I32, I32, P, I32, P, P, P, P, P, I32, I32]),

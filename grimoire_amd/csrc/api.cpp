@@ -22,6 +22,7 @@
 #include "ingest.hpp"
 #include "tiered.hpp"
 #include "router.hpp"
+#include "gemv_mx.hpp"
 
 using namespace grim;
 
@@ -722,6 +723,38 @@ int grimoire_moe_scale_by_sigmoid_batched(void* stream, float* x, const float* g
     if (!x || !gate) return fail(GRIM_ERR_ARG, "null pointer");
     if (hidden <= 0) return fail(GRIM_ERR_SHAPE, "hidden=%d", hidden);
     return status(scale_by_sigmoid_launch(S(stream), x, gate, int64_t(tokens) * hidden, hidden));
+}
+
+int grimoire_moe_mxfp4_padded_k(int K) {
+    if (K <= 0 || K % 32) return 0;
+    return gvm_padded_k(K);
+}
+
+int grimoire_moe_pad_mxfp4_rows(void* stream, const grim_quant_weight* src, const grim_quant_weight* dst) {
+    if (!src || !dst || !src->payload || !src->scales || !dst->payload || !dst->scales)
+        return fail(GRIM_ERR_ARG, "null pointer");
+    if (src->fmt != GRIM_FMT_MXFP4 || dst->fmt != GRIM_FMT_MXFP4) return fail(GRIM_ERR_FORMAT, "MXFP4 only");
+    const int N = src->N, K = src->K;
+    if (dst->N != N || dst->K != K || K <= 0 || K % 32 || N <= 0) return fail(GRIM_ERR_SHAPE, "N, K");
+    const int64_t kb = K / 2, ks = K / 32;
+    if (src->row_bytes < kb || src->row_scales < ks || dst->row_bytes < kb || dst->row_scales < ks)
+        return fail(GRIM_ERR_SHAPE, "rows shorter than K");
+    hipStream_t st = S(stream);
+    const uint8_t* ss = static_cast<const uint8_t*>(src->scales);
+    uint8_t* dp = const_cast<uint8_t*>(dst->payload);
+    uint8_t* ds = static_cast<uint8_t*>(const_cast<void*>(dst->scales));
+    hipError_t e = hipMemcpy2DAsync(dp, size_t(dst->row_bytes), src->payload, size_t(src->row_bytes), size_t(kb),
+                                    size_t(N), hipMemcpyDefault, st);
+    if (e == hipSuccess && dst->row_bytes > kb)
+        e = hipMemset2DAsync(dp + kb, size_t(dst->row_bytes), 0, size_t(dst->row_bytes - kb), size_t(N), st);
+    if (e == hipSuccess)
+        e = hipMemcpy2DAsync(ds, size_t(dst->row_scales), ss, size_t(src->row_scales), size_t(ks), size_t(N),
+                             hipMemcpyDefault, st);
+    // padding blocks: zero codes under scale byte 127 (2^0), so every
+    // product there is an exact zero
+    if (e == hipSuccess && dst->row_scales > ks)
+        e = hipMemset2DAsync(ds + ks, size_t(dst->row_scales), 127, size_t(dst->row_scales - ks), size_t(N), st);
+    return status(e);
 }
 
 int grimoire_moe_quant_limbs(void* stream, const float* src, int rows, int n, int8_t* dst,

@@ -110,18 +110,37 @@ struct Plan {
     uint32_t *gv_xf, *gv_hf, *gv_hfsh;   // formatted activation rows
 };
 
+// MXFP4 rows padded for the matrix-core grouped GEMV (gvm_padded_k):
+// payload K'/2, K'/32 scale bytes per row, K' = gvm_padded_k(K) > K.
+static bool mx_padded(const grim_quant_weight& w, int K) {
+    const int kp = gvm_padded_k(K);
+    return w.fmt == GRIM_FMT_MXFP4 && kp != K && w.row_bytes == int64_t(kp / 2) && w.row_scales == kp / 32;
+}
+
+// Some weight of the layer holds padded MXFP4 rows: of the grouped GEMVs
+// only the matrix-core one reads them (as rows of K' elements).
+static bool layer_mx_padded(const grim_moe_layer* L) {
+    const int H = L->cfg.hidden, I = L->cfg.inter;
+    return mx_padded(L->gate_up, H) || mx_padded(L->down, I) ||
+           (L->has_shared && (mx_padded(L->shared_gate_up, H) || mx_padded(L->shared_down, I)));
+}
+
 // The expert-grouped GEMV covers these shapes and formats.
 bool gv_ok(const grim_moe_layer* L) {
     const int f = L->gate_up.fmt;
     const int H = L->cfg.hidden, I = L->cfg.inter;
     // payload rows packed (K / 2 bytes): a sub-block's rows are one span
-    auto packed = [](const grim_quant_weight& w, int K) {
+    // (or MXFP4 rows padded for the matrix-core kernel, all alike)
+    const bool pad = layer_mx_padded(L);
+    auto packed = [pad](const grim_quant_weight& w, int K) {
+        if (pad) return mx_padded(w, K);
         // INT4 scale groups of >= 32 elements: at most K / 16 scale bytes per row
         return w.row_bytes == int64_t(K / 2) && int64_t(w.row_scales) * 32 <= K;
     };
     return f == L->down.fmt && gv_shape_ok(f, H, I) && packed(L->gate_up, H) && packed(L->down, I) &&
            (!L->has_shared || (L->shared_gate_up.fmt == f && L->shared_down.fmt == f &&
-                               packed(L->shared_gate_up, H) && packed(L->shared_down, I)));
+                               packed(L->shared_gate_up, H) && packed(L->shared_down, I))) &&
+           (!pad || gvm_shape_ok(H, I));
 }
 
 size_t carve(const grim_moe_layer* L, int T, bool gemv, char* base, Plan& p) {
@@ -380,8 +399,11 @@ static int forward_gv(hipStream_t st, const grim_moe_layer* L, const Plan& p, co
     g.af = p.gv_xf;
     g.af_sh = p.gv_xf;
     g.w_sh = sh ? make_view(L->shared_gate_up) : g.w;
+    // padded MXFP4 rows: the weights' K' (the activation rows are formatted
+    // for K and padded with zeros to the same K')
+    const bool pad = mx && layer_mx_padded(L);
     g.N = I;
-    g.K = H;
+    g.K = pad ? gvm_padded_k(H) : H;
     g.x = x;
     g.perm_token = p.gv_perm;
     g.h = p.gv_h;
@@ -413,7 +435,7 @@ static int forward_gv(hipStream_t st, const grim_moe_layer* L, const Plan& p, co
     d.w = make_view(L->down);
     d.w_sh = sh ? make_view(L->shared_down) : d.w;
     d.N = H;
-    d.K = I;
+    d.K = pad ? gvm_padded_k(I) : I;
     d.y = p.yperm;
     d.y_sh = p.ysh;
 #ifdef GRIM_TIMING
@@ -702,7 +724,8 @@ static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_
     // few rows per expert (on average at most 2): stream each expert once
     // per group of rows instead of once per 128-row MFMA tile
     const bool gv = !gemv && p.gv_te &&
-                    (regime == 4 || regime == 5 || (regime == 0 && int64_t(tokens) * K <= 2 * int64_t(E)));
+                    (regime == 4 || regime == 5 || (regime == 0 && int64_t(tokens) * K <= 2 * int64_t(E))) &&
+                    !(regime == 5 && layer_mx_padded(L));   // the vector-ALU one reads packed rows only
     const bool gv_mx = gv && regime != 5 && L->gate_up.fmt == GRIM_FMT_MXFP4 && gvm_shape_ok(H, I);
     if (gv_mx && int64_t(tokens) * K <= kGvmRouteMax && !shard) {
         if (deferred) {
@@ -746,6 +769,8 @@ static int forward_impl(void* stream, const grim_moe_layer* L, const grim_route_
     }
 
     if (gv) return forward_gv(st, L, p, x, y, tokens, shared_gate_w, gv_mx, nullptr);
+    if (regime == 5 && layer_mx_padded(L))
+        return ferr(GRIM_ERR_FORMAT, "regime 5 reads packed MXFP4 rows (K/2 bytes); these are padded");
     if (regime == 4 || regime == 5)
         return ferr(GRIM_ERR_FORMAT, "regimes 4, 5: int4 / mxfp4 experts, hidden and inter % 32");
 

@@ -697,6 +697,8 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
 // K a multiple of 64 (2-byte aligned scale rows) with at least ST - 1
 // stages per item (the stream's look-ahead reaches at most into the next
 // item).
+int gvm_padded_k(int K) { return gvm_kpad(K); }
+
 bool gvm_shape_ok(int H, int I) {
     const int kmin = (kGvmStages - 1) * kGvmKS;
     return H % 64 == 0 && I % 64 == 0 && gvm_kpad(H) >= kmin && gvm_kpad(I) >= kmin;

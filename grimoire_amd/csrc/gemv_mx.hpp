@@ -9,6 +9,12 @@ namespace grim {
 
 // MXFP4 experts whose reduction lengths are multiples of 128 (one MFMA K step).
 bool gvm_shape_ok(int H, int I);
+// K rounded up to whole 256-element stages: the row length a weight padded
+// for this kernel holds (payload K'/2 bytes, K'/32 scale bytes per row,
+// zero codes under scale byte 127 past K).  Rows of 128-byte multiples
+// stream whole memory lines; with K' % 512 == 0 the scale rows are
+// 16-byte aligned too.
+int gvm_padded_k(int K);
 // Bytes of one activation row of K elements in the limb format.
 size_t gvm_act_bytes(int K);
 // Format rows0 rows of src0 into dst0 and rows1 rows of src1 into dst1.

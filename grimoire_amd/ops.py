@@ -218,6 +218,21 @@ def grouped_gemm(w: Weight, N, swiglu, A, out, offsets, counts, num_experts, tot
                                           _p(counts), num_experts, total_rows), "grouped_gemm")
 
 
+def pad_mxfp4(w, stream=None):
+    """grimoire_moe_pad_mxfp4_rows: a GPU copy of MXFP4 weight w with rows
+    padded to grimoire_moe_mxfp4_padded_k(K) elements (zero codes under
+    scale byte 127 past K)."""
+    _dev(w.payload)
+    kp = lib().grimoire_moe_mxfp4_padded_k(w.K)
+    if kp <= 0:
+        raise ValueError(f"K={w.K}: a multiple of 32")
+    dst = Weight(w.fmt, w.N, w.K, torch.empty((w.N, kp // 2), dtype=torch.uint8, device=w.payload.device),
+                 torch.empty((w.N, kp // 32), dtype=torch.uint8, device=w.payload.device), None, kp // 32)
+    s, d = w.struct(), dst.struct()
+    check(lib().grimoire_moe_pad_mxfp4_rows(_stream(stream), C.byref(s), C.byref(d)), "pad_mxfp4_rows")
+    return dst
+
+
 def quant_limbs(src, dst, scale, stream=None):
     """Activation rows fp32 [rows][n] -> two int8 limbs per element (row layout
     [n/64][2][64]) and one fp32 scale per row: a = s * (hi + lo / 254)."""

@@ -53,6 +53,19 @@ class Weight:
         return Weight(self.fmt, n, self.K, self.payload[r0:r0 + n], sl(self.scales), sl(self.zeros),
                       self.row_scales)
 
+    def pad_mxfp4(self) -> "Weight":
+        """This MXFP4 weight with rows padded to mxfp4_padded_k(K) elements
+        (zero codes under scale byte 127 past K), on the same device: the
+        rows the matrix-core grouped GEMV streams as whole memory lines.
+        grimoire_moe_pad_mxfp4_rows does the same on the GPU."""
+        assert self.fmt == _abi.FMT_MXFP4
+        kp = mxfp4_padded_k(self.K)
+        pay = torch.zeros((self.N, kp // 2), dtype=torch.uint8, device=self.payload.device)
+        pay[:, :self.K // 2] = self.payload[:, :self.K // 2]
+        sc = torch.full((self.N, kp // 32), 127, dtype=torch.uint8, device=self.payload.device)
+        sc[:, :self.K // 32] = self.scales[:, :self.K // 32]
+        return Weight(self.fmt, self.N, self.K, pay, sc, None, kp // 32)
+
     def nbytes(self) -> int:
         n = self.payload.numel()
         for t in (self.scales, self.zeros):
@@ -63,6 +76,12 @@ class Weight:
     def row_bytes_total(self) -> float:
         """Bytes one row streams (payload + its scales / zeros)."""
         return self.nbytes() / self.N
+
+
+def mxfp4_padded_k(K: int) -> int:
+    """K rounded up to the matrix-core grouped GEMV's 256-element stages
+    (grimoire_moe_mxfp4_padded_k)."""
+    return (K + 255) // 256 * 256
 
 
 def _gen(device, seed):
@@ -177,6 +196,14 @@ class MoeLayer:
                         self.down.rows(begin * self.hidden, count * self.hidden), self.router,
                         self.shared_gate_up if shared else None, self.shared_down if shared else None,
                         self.shared_gate_w if shared else None, self.norm_topk)
+
+    def pad_mxfp4(self) -> "MoeLayer":
+        """The layer with every MXFP4 weight's rows padded (Weight.pad_mxfp4):
+        the same products, rows of whole memory lines for the grouped GEMV."""
+        pw = lambda w: None if w is None else w.pad_mxfp4()
+        return MoeLayer(self.hidden, self.inter, self.num_experts, self.top_k,
+                        self.gate_up.pad_mxfp4(), self.down.pad_mxfp4(), self.router,
+                        pw(self.shared_gate_up), pw(self.shared_down), self.shared_gate_w, self.norm_topk)
 
     def expert_bytes(self) -> float:
         """Bytes of one routed expert (gate, up and down rows with scales)."""

@@ -368,6 +368,30 @@ int grimoire_moe_ingest_projection(void* stream, const grim_expert_src* src,
 int grimoire_moe_ingest_projections(void* stream, const grim_expert_src* srcs,
                                     const int32_t* row0, int n, const grim_quant_weight* dst);
 
+/* MXFP4 rows padded for the matrix-core expert-grouped GEMV.  No
+ * counterpart in the reference, whose MXFP4 rows are K/2 payload bytes and
+ * K/32 scale bytes (formats.hpp:105-126); a layout of this library's own,
+ * for callers that pad their MXFP4 experts once at load.  At K = 2880 a
+ * row is 1440 bytes and every 128-byte piece the kernel streams straddles
+ * two memory lines; padded to K' = grimoire_moe_mxfp4_padded_k(K) (K
+ * rounded up to 256; 3072 there) every piece is one line and, with
+ * K' % 512 == 0, the scale rows are 16-byte aligned.  The padded elements
+ * hold zero codes under scale byte 127 (2^0): every product there is an
+ * exact zero, so the layer's results are those of the unpadded rows.
+ * grimoire_moe_forward takes a layer whose MXFP4 weights are all padded
+ * (row_bytes = K'/2, row_scales = K'/32) on every regime but 5: the
+ * expert-grouped GEMV on the vector ALU reads packed rows only, and regime
+ * 5 returns GRIM_ERR_FORMAT for such a layer.
+ *
+ * grimoire_moe_mxfp4_padded_k returns K' (0 when K is not a positive
+ * multiple of 32).  grimoire_moe_pad_mxfp4_rows copies src (any row
+ * strides of at least K/2 and K/32) into dst (same fmt, N, K; dst->payload
+ * and dst->scales device memory of dst->N rows of dst->row_bytes and
+ * dst->row_scales bytes) and fills dst's elements past K as above;
+ * stream-ordered, no allocation. */
+int grimoire_moe_mxfp4_padded_k(int K);
+int grimoire_moe_pad_mxfp4_rows(void* stream, const grim_quant_weight* src, const grim_quant_weight* dst);
+
 /* Signed-s4 conversion of a layer's INT4 experts (src/grimoire.cpp:
  * 8386-8397): when every zero point in gu_zeros and dn_zeros is 8, XOR
  * every payload byte with 0x88 (offset binary -> two's complement) and set

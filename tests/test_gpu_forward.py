@@ -227,6 +227,45 @@ def test_forward_grouped_gemv_fp32_activations(gpu, regime):
     assert_close(y, yo, what="grouped gemv fp32 x")
 
 
+def test_pad_mxfp4_rows_matches_host(gpu):
+    """grimoire_moe_pad_mxfp4_rows on the GPU equals the host padding."""
+    print("pad mxfp4 rows", flush=True)
+    w = configs.MAKERS["mxfp4"](300, 2880, seed=7)
+    want = w.pad_mxfp4()
+    got = ops.pad_mxfp4(w.to(gpu))
+    torch.cuda.synchronize()
+    assert got.row_bytes == 1536 and got.row_scales == 96
+    assert torch.equal(got.payload.cpu(), want.payload) and torch.equal(got.scales.cpu(), want.scales)
+
+
+@pytest.mark.parametrize("regime", [0, 1, 2, 4, 5])
+@pytest.mark.parametrize("name,kw", [
+    ("c3", dict(H=960, I=704, E=32)),                     # K' = 1024 / 768: padded rows of whole lines
+    ("c5", dict(T=12, H=1088, E=32, I=320)),              # shared expert, group-limited sigmoid
+])
+def test_forward_mxfp4_padded_rows(gpu, name, kw, regime):
+    """A layer whose MXFP4 rows are padded to grimoire_moe_mxfp4_padded_k(K)
+    gives the unpadded layer's routing and outputs bit for bit on every
+    regime (the matrix-core grouped GEMV reads the padded rows whole; the
+    other kernels stop at K); regime 5, the vector-ALU grouped GEMV, reads
+    packed rows only and refuses them."""
+    print(f"forward mxfp4 padded rows {name} {kw} regime {regime}", flush=True)
+    cfg = configs.scaled(configs.CONFIGS[name], **kw)
+    wl = configs.make_workload(cfg, "cpu", seed=13)
+    wp = configs.Workload(cfg, wl.layer.pad_mxfp4(), wl.x, wl.route_bias)
+    if regime == 5:
+        with pytest.raises(_abi.GrimoireError, match="packed MXFP4 rows"):
+            _run(wp, gpu, regime=regime)
+        return
+    Lg, y, oe, ow, logits = _run(wl, gpu, regime=regime)
+    _, yp, oep, owp, _ = _run(wp, gpu, regime=regime)
+    assert torch.equal(oep, oe) and torch.equal(owp, ow)
+    assert torch.equal(yp, y)
+    _check_routing(wl, logits, oe, ow)
+    yo = _oracle_y(wl.layer, wl.x, oe, ow, wl.layer.shared_gate_w)
+    assert_close(y, yo, what=f"padded mxfp4 {name}")
+
+
 @pytest.mark.parametrize("name,kw,regime", [
     ("c3", {}, 0),                                        # matrix-core grouped GEMV, merged dispatch
     ("c5", dict(T=32, H=1024, E=64, I=512), 0),           # the same, aligned scale loads, shared expert

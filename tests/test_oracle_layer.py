@@ -10,6 +10,7 @@ import torch
 
 from oracle import oracle as O
 from grimoire_amd import _abi, configs
+from grimoire_amd import weights as weights_mod
 from grimoire_amd.weights import MoeLayer, Weight, make_bf16, make_gptq_int4, make_int8, make_mxfp4
 from tests.helpers import dequant, rel_l2
 
@@ -370,3 +371,27 @@ def test_grouped_gemm_oracle_vs_dense():
                              O._p(counts), E)
     g, u = want[:, : N // 2], want[:, N // 2:]
     assert rel_l2(out2, g / (1 + torch.exp(-g)) * u) < 1e-6
+
+
+@pytest.mark.parametrize("K", [32, 224, 256, 2880, 3072, 7168])
+def test_mxfp4_padded_k_matches_library(K):
+    # the Python helper and the C entry agree on K' (K rounded up to 256)
+    assert _abi.lib().grimoire_moe_mxfp4_padded_k(K) == weights_mod.mxfp4_padded_k(K)
+    assert weights_mod.mxfp4_padded_k(K) % 256 == 0 and 0 <= weights_mod.mxfp4_padded_k(K) - K < 256
+
+
+def test_mxfp4_padded_layer_same_outputs():
+    # padded rows (zero codes under scale byte 127 past K) are exact zeros:
+    # the oracle, reading rows through row_bytes / row_scales, gives the
+    # unpadded layer's outputs bit for bit; the padding bytes are as stated
+    cfg, L = _small_layer("mxfp4", E=6, H=352, I=160, K=2, shared=True, seed=4)
+    P = L.pad_mxfp4()
+    assert P.gate_up.row_bytes == 512 // 2 and P.gate_up.row_scales == 512 // 32
+    assert P.down.row_bytes == 256 // 2 and P.down.row_scales == 256 // 32
+    assert (P.gate_up.payload[:, 352 // 2:] == 0).all() and (P.gate_up.scales[:, 352 // 32:] == 127).all()
+    assert torch.equal(P.gate_up.payload[:, :352 // 2], L.gate_up.payload)
+    x = configs.make_x(cfg, "cpu", 5, T=5)
+    ids, w = _route(5, cfg.E, cfg.K, 6)
+    y = O.moe_forward(L.struct(), ids, w, None, x)
+    yp = O.moe_forward(P.struct(), ids, w, None, x)
+    assert torch.equal(y, yp)
