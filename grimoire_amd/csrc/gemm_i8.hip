@@ -1158,6 +1158,9 @@ __global__ __launch_bounds__(256) void quant_permute_kernel(const float* __restr
     __shared__ float red[4], gred[4];
     const int t = blockIdx.x;
     const float* s = x + int64_t(t) * n;
+    // this thread's route row (threads < K), requested with the row's loads
+    // instead of after the reduction's barrier
+    const int dk_own = int(threadIdx.x) < K ? inverse[int64_t(t) * K + threadIdx.x] : -1;
     float4 va[4], vb[4];
     float m = 0.0f, d = 0.0f;
 #pragma unroll
@@ -1196,7 +1199,8 @@ __global__ __launch_bounds__(256) void quant_permute_kernel(const float* __restr
     const float sc = m > 0.0f ? m / 127.0f : 1.0f;
     const float inv = m > 0.0f ? 127.0f / m : 0.0f;
     int dst[16];
-    for (int k = 0; k < K; ++k) dst[k] = inverse[int64_t(t) * K + k];
+    if (xq)
+        for (int k = 0; k < K; ++k) dst[k] = inverse[int64_t(t) * K + k];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int c = threadIdx.x * 8 + q * 2048;
@@ -1217,12 +1221,9 @@ __global__ __launch_bounds__(256) void quant_permute_kernel(const float* __restr
             }
         }
     }
-    if (int(threadIdx.x) < K) {
-        const int dk = inverse[int64_t(t) * K + threadIdx.x];
-        if (dk >= 0) {
-            sq[dk] = sc;
-            if (perm) perm[dk] = t;
-        }
+    if (dk_own >= 0) {
+        sq[dk_own] = sc;
+        if (perm) perm[dk_own] = t;
     }
     if (srow && threadIdx.x == 0) srow[t] = sc;
 }

@@ -30,9 +30,10 @@ __global__ __launch_bounds__(kTopkWaves * kWave) void topk_kernel(
 
 // The same on split-K router partials: logits = (a + b) + bias formed as
 // they are loaded (the arithmetic of the router's own finishing pass, so
-// the same bits) and written back in place, then the top-k.
+// the same bits), then the top-k.  The finished logits are not stored:
+// nothing after the top-k reads them.
 __global__ __launch_bounds__(kTopkWaves * kWave) void topk_split_kernel(
-    float* __restrict__ logits, const float* __restrict__ part1, const float* __restrict__ lbias,
+    const float* __restrict__ logits, const float* __restrict__ part1, const float* __restrict__ lbias,
     int T, int E, int K, int mode, int normalize,
     float scaling, const uint16_t* __restrict__ bias16, const float* __restrict__ bias32,
     int n_group, int topk_group, int32_t* __restrict__ out_e, float* __restrict__ out_w) {
@@ -43,7 +44,7 @@ __global__ __launch_bounds__(kTopkWaves * kWave) void topk_split_kernel(
     if (t >= T) return;   // whole wave exits together
     const int lane = threadIdx.x & (kWave - 1);
     const int V = (E + kWave - 1) / kWave;
-    float* row = logits + int64_t(t) * E;
+    const float* row = logits + int64_t(t) * E;
     const float* row1 = part1 + int64_t(t) * E;
     float lv[kMaxV];
     if (E == kWave * kMaxV) {
@@ -58,7 +59,6 @@ __global__ __launch_bounds__(kTopkWaves * kWave) void topk_split_kernel(
                 const f32x4n b = *reinterpret_cast<const f32x4n*>(lbias + e);
                 v = f32x4n{v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w};
             }
-            *reinterpret_cast<f32x4n*>(row + e) = v;
             lv[j] = v.x; lv[j + 1] = v.y; lv[j + 2] = v.z; lv[j + 3] = v.w;
         }
     } else {
@@ -69,11 +69,6 @@ __global__ __launch_bounds__(kTopkWaves * kWave) void topk_split_kernel(
             float v = row[ec] + row1[ec];
             if (lbias) v += lbias[ec];
             lv[j] = v;
-        }
-#pragma unroll
-        for (int j = 0; j < kMaxV; ++j) {
-            const int e = lane * V + j;
-            if (j < V && e < E) row[e] = lv[j];
         }
     }
     topk_wave_regs(lv, E, K, mode, normalize, scaling, bias16, bias32, n_group, topk_group,
@@ -108,7 +103,7 @@ hipError_t topk_launch(hipStream_t st, const TopkArgs& a) {
     dim3 grid((a.T + kTopkWaves - 1) / kTopkWaves);
     if (a.part1) {
         hipLaunchKernelGGL(topk_split_kernel, grid, dim3(kTopkWaves * kWave), 0, st,
-                           const_cast<float*>(a.logits), a.part1, a.lbias, a.T, a.E, a.K, a.mode,
+                           a.logits, a.part1, a.lbias, a.T, a.E, a.K, a.mode,
                            a.normalize, a.scaling, a.bias16, a.bias32, a.n_group, a.topk_group, a.out_e,
                            a.out_w);
         return hipGetLastError();
