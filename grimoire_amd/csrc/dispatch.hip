@@ -153,6 +153,80 @@ __global__ __launch_bounds__(kDispThreads) void disp_rank(const int32_t* __restr
     if (perm_token) perm_token[p] = r / K;
 }
 
+// disp_rank for calls without a tile table: every block forms the
+// exclusive expert offsets itself (a block-wide scan of the E counts, the
+// same sums as disp_scan's), so the single-block scan launch drops out;
+// block 0 publishes them (and the m-tile count when mc > 0).
+constexpr int kRankScanMaxE = 2048;
+__global__ __launch_bounds__(kDispThreads) void disp_rank_scan(const int32_t* __restrict__ ids, int R, int E,
+                                                               int K, const int32_t* __restrict__ bbase,
+                                                               const int32_t* __restrict__ counts,
+                                                               int32_t* __restrict__ offsets,
+                                                               int32_t* __restrict__ inverse,
+                                                               int32_t* __restrict__ perm_token, int mc,
+                                                               int32_t* __restrict__ n_tiles_out) {
+    static_assert(kRoutesPerBlock == kDispThreads, "one route per thread");
+    constexpr int PER = kRankScanMaxE / kDispThreads;
+    __shared__ __attribute__((aligned(16))) int32_t le[kRoutesPerBlock];
+    __shared__ int32_t off_s[kRankScanMaxE];
+    __shared__ int32_t wsum[kDispThreads / 64][2];
+    const int i = threadIdx.x, lane = i & 63, wv = i >> 6;
+    const int r0 = blockIdx.x * kRoutesPerBlock;
+    const int n = R - r0 < kRoutesPerBlock ? R - r0 : kRoutesPerBlock;
+    le[i] = i < n ? ids[r0 + i] : -1;
+    // thread i's experts [i * per, +per): counts, their sum and tile count
+    const int per = (E + kDispThreads - 1) / kDispThreads;
+    int loc[PER];
+    int sum = 0, tiles = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int e = i * per + j;
+        loc[j] = (j < per && e < E) ? counts[e] : 0;
+        sum += loc[j];
+        tiles += mc > 0 ? (loc[j] + mc - 1) / mc : 0;
+    }
+    int incl = sum, tinc = tiles;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int a = __shfl_up(incl, off, 64), b = __shfl_up(tinc, off, 64);
+        if (lane >= off) { incl += a; tinc += b; }
+    }
+    if (lane == 63) { wsum[wv][0] = incl; wsum[wv][1] = tinc; }
+    __syncthreads();
+    int base = incl - sum, ttot = 0;
+    for (int w = 0; w < kDispThreads / 64; ++w) {
+        base += w < wv ? wsum[w][0] : 0;
+        ttot += wsum[w][1];
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int e = i * per + j;
+        if (j < per && e < E) {
+            off_s[e] = base;
+            if (blockIdx.x == 0) offsets[e] = base;
+        }
+        base += loc[j];
+    }
+    if (blockIdx.x == 0 && i == 0 && n_tiles_out) *n_tiles_out = ttot;
+    __syncthreads();
+    const int my_e = le[i];
+    int rank = 0;
+#pragma unroll 4
+    for (int j = 0; j < kRoutesPerBlock; j += 4) {
+        const int4 q = *reinterpret_cast<const int4*>(&le[j]);
+        rank += (j < i && q.x == my_e) ? 1 : 0;
+        rank += (j + 1 < i && q.y == my_e) ? 1 : 0;
+        rank += (j + 2 < i && q.z == my_e) ? 1 : 0;
+        rank += (j + 3 < i && q.w == my_e) ? 1 : 0;
+    }
+    if (i >= n) return;
+    const int r = r0 + i;
+    if (my_e < 0 || my_e >= E) { inverse[r] = -1; return; }
+    const int p = off_s[my_e] + bbase[int64_t(blockIdx.x) * E + my_e] + rank;
+    inverse[r] = p;
+    if (perm_token) perm_token[p] = r / K;
+}
+
 // One block per token: bf16 row written to each of its K permuted rows.
 template <bool SRC_BF16>
 __global__ __launch_bounds__(kDispThreads) void disp_permute(const void* __restrict__ hidden,
@@ -205,11 +279,17 @@ hipError_t dispatch_launch(hipStream_t st, const DispatchArgs& a) {
     // T > 0 here (the callers return before), so nb >= 1
     hipLaunchKernelGGL(disp_colscan, dim3((a.E + kColExperts - 1) / kColExperts),
                        dim3(kColExperts * kColSlices), 0, st, bcount, nb, a.E, a.counts);
-    hipLaunchKernelGGL(disp_scan, dim3(1), dim3(1024), 0, st, a.E, a.counts, a.offsets, a.tile_e,
-                       a.tile_mb, a.tmax, a.mc, ntiles);
-    if (nb > 0)
-        hipLaunchKernelGGL(disp_rank, dim3(nb), dim3(kDispThreads), 0, st, a.ids, R, a.E, a.K,
-                           bcount, a.offsets, a.inverse, a.perm_token);
+    if (!a.tile_e && a.E <= kRankScanMaxE && nb > 0) {
+        // no tile table: the rank blocks form the offsets themselves
+        hipLaunchKernelGGL(disp_rank_scan, dim3(nb), dim3(kDispThreads), 0, st, a.ids, R, a.E, a.K, bcount,
+                           a.counts, a.offsets, a.inverse, a.perm_token, a.mc, ntiles);
+    } else {
+        hipLaunchKernelGGL(disp_scan, dim3(1), dim3(1024), 0, st, a.E, a.counts, a.offsets, a.tile_e,
+                           a.tile_mb, a.tmax, a.mc, ntiles);
+        if (nb > 0)
+            hipLaunchKernelGGL(disp_rank, dim3(nb), dim3(kDispThreads), 0, st, a.ids, R, a.E, a.K,
+                               bcount, a.offsets, a.inverse, a.perm_token);
+    }
     if (a.xperm && a.T > 0) {
         if (a.hidden_bf16)
             hipLaunchKernelGGL(disp_permute<true>, dim3(a.T), dim3(kDispThreads), 0, st, a.hidden,

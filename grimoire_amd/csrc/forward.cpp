@@ -264,8 +264,12 @@ static int forward_gemm_i8(hipStream_t st, const grim_moe_layer* L, const Plan& 
     const int E = c.num_experts, K = c.top_k, H = c.hidden, I = c.inter;
     const bool sh = L->has_shared;
     const int64_t R = int64_t(tokens) * K;
+    // rows mode (E <= kI8MaxListExperts): the GEMM lists its tiles from the
+    // counts itself, so the dispatch forms no tile table
+    const bool rows_mode = E <= kI8MaxListExperts;
     int r = grimoire_moe_route_grouped(st, x, p.rex, nullptr, nullptr, p.counts, p.offsets,
-                                       p.inverse, p.tile_e, p.tile_mb, p.tmax, tokens, H, E,
+                                       p.inverse, rows_mode ? nullptr : p.tile_e,
+                                       rows_mode ? nullptr : p.tile_mb, p.tmax, tokens, H, E,
                                        kGemmBM, K, nullptr, p.disp_ws,
                                        dispatch_workspace_bytes(tokens, K, E));
     if (r) return r;
@@ -314,7 +318,7 @@ static int forward_gemm_i8(hipStream_t st, const grim_moe_layer* L, const Plan& 
     g.n_tiles_dev = dispatch_live_tiles(p.disp_ws, tokens, K, E);
     g.T_sh = sh ? tokens : 0;
     // experts with few rows on 32-row tiles (tile lists formed in the kernels)
-    if (E <= kI8MaxListExperts) {
+    if (rows_mode) {
         g.split = kI8DefaultSplit;
         g.num_experts = E;
     }

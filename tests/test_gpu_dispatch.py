@@ -215,3 +215,30 @@ def test_swiglu_and_scale_by_sigmoid(gpu):
     assert ((xd.cpu().double() - wx).abs() <= 2e-7 * wx.abs() + 1e-30).all()
     w1 = x1.double() / (1 + torch.exp(-gate[0].double()))
     assert ((x1d.cpu().double() - w1).abs() <= 2e-7 * w1.abs() + 1e-30).all()
+
+
+@pytest.mark.parametrize("T,K,E,invalid", [
+    (4096, 10, 512, 0),                # C4: 160 rank blocks forming their own offsets
+    (700, 6, 2048, 9),                 # the largest E the rank blocks scan; skipped routes
+    (300, 4, 3000, 0),                 # beyond it: the single-block scan as with a table
+    (5, 3, 7, 0),
+])
+def test_route_without_tile_table_matches(gpu, T, K, E, invalid):
+    """Without a tile table the rank blocks form the expert offsets
+    themselves: counts, offsets, rows and token map equal the oracle's
+    counting sort (and so the call with a table)."""
+    print(f"route without tile table T={T} K={K} E={E}", flush=True)
+    ids = _ids(T, K, E, 31 + E, zipf=1.1, invalid=invalid)
+    R = T * K
+    counts = torch.empty(E, dtype=torch.int32, device=gpu)
+    offsets = torch.empty(E, dtype=torch.int32, device=gpu)
+    inverse = torch.empty(R, dtype=torch.int32, device=gpu)
+    perm = torch.full((R,), -7, dtype=torch.int32, device=gpu)
+    ops.launch_moe_route_grouped(None, ids.to(gpu), None, None, counts, offsets, inverse, None, None, 0,
+                                 T, 64, E, 0, K, perm_token=perm)
+    torch.cuda.synchronize()
+    d = O.dispatch(ids, E, 0, 0)
+    assert torch.equal(counts.cpu(), d["counts"]) and torch.equal(offsets.cpu(), d["offsets"])
+    assert torch.equal(inverse.cpu(), d["inverse"])
+    n = int(d["counts"].sum())
+    assert torch.equal(perm.cpu()[:n], d["perm_token"][:n])
