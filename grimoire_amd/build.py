@@ -1,10 +1,17 @@
 """Build libgrimoire_moe.so (gfx950) in-tree with hipcc.
 
-    python -m grimoire_amd.build          # or grimoire_amd.build.build()
+    python -m grimoire_amd.build            # or grimoire_amd.build.build()
+    python -m grimoire_amd.build --timing   # the phase-stamp build (below)
 
 Each HIP source compiles to an object in grimoire_amd/_build/, then one
 shared library grimoire_amd/libgrimoire_moe.so is linked.  The built
 library travels with the source tree; nothing is installed.
+
+--timing builds the same sources with GRIM_TIMING into
+grimoire_amd/_timing/libgrimoire_moe.so: the decode kernels then stamp the
+real-time counter at their phase boundaries into a buffer the caller hands
+over (grim_timing_set), which grimoire_amd.phase_timeline reads.  It is a
+measurement build, never the product library.
 """
 from __future__ import annotations
 
@@ -64,6 +71,20 @@ def _compile_host(src: str) -> Path:
     return obj
 
 
+def build_timing(verbose: bool = True) -> Path:
+    """The GRIM_TIMING build into grimoire_amd/_timing/ (objects in
+    grimoire_amd/_build_timing/)."""
+    global OUT, OBJ, FLAGS, HOST_FLAGS
+    saved = OUT, OBJ, FLAGS, HOST_FLAGS
+    OUT, OBJ = PKG / "_timing" / "libgrimoire_moe.so", PKG / "_build_timing"
+    FLAGS, HOST_FLAGS = FLAGS + ["-DGRIM_TIMING"], HOST_FLAGS + ["-DGRIM_TIMING"]
+    try:
+        OUT.parent.mkdir(exist_ok=True)
+        return build(verbose)
+    finally:
+        OUT, OBJ, FLAGS, HOST_FLAGS = saved
+
+
 def build(verbose: bool = True) -> Path:
     """Compile every source and link the shared library; returns its path."""
     OBJ.mkdir(exist_ok=True)
@@ -82,4 +103,4 @@ def build(verbose: bool = True) -> Path:
 
 
 if __name__ == "__main__":
-    build()
+    build_timing() if "--timing" in sys.argv[1:] else build()
