@@ -212,20 +212,27 @@ __global__ __launch_bounds__(kGvmRouteThreads) void gvm_route_kernel(TopkArgs tk
     __shared__ int32_t cnt[kGvmRouteThreads], wsum[kGvmRouteThreads / kWave][2];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
     const int T = tk.T, E = tk.E, K = tk.K, R = T * K;
+    cnt[tid] = 0;
     if (fused_topk) {
         // T <= 16: wave t selects token t's experts (topk_kernel's code,
-        // so the same bits); the picks are read back below after the
-        // barrier (one work-group: its waves share the CU's cache)
+        // so the same bits) into LDS; the picks are stored from there
         __shared__ float gsel[kGvmRouteThreads / kWave][512];
         __shared__ float gscore[kGvmRouteThreads / kWave][64];
+        __shared__ int32_t pick_e[kGvmRouteThreads / kWave][16];
+        __shared__ float pick_w[kGvmRouteThreads / kWave][16];
         if (wv < T)
             topk_wave(tk.logits + int64_t(wv) * E, E, K, tk.mode, tk.normalize, tk.scaling, tk.bias16, tk.bias32,
-                      tk.n_group, tk.topk_group, tk.out_e + int64_t(wv) * K, tk.out_w + int64_t(wv) * K, gsel[wv],
-                      gscore[wv]);
+                      tk.n_group, tk.topk_group, pick_e[wv], pick_w[wv], gsel[wv], gscore[wv]);
         __syncthreads();
+        if (tid < R) {
+            const int32_t pe = pick_e[tid / K][tid % K];
+            ids[tid] = pe;
+            tk.out_e[tid] = pe;
+            tk.out_w[tid] = pick_w[tid / K][tid % K];
+        }
+    } else {
+        if (tid < R) ids[tid] = tk.out_e[tid];
     }
-    cnt[tid] = 0;
-    if (tid < R) ids[tid] = tk.out_e[tid];
     __syncthreads();
     const int my_id = tid < R ? ids[tid] : -1;
     if (my_id >= 0 && my_id < E) atomicAdd(&cnt[my_id], 1);

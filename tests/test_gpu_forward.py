@@ -194,6 +194,11 @@ def test_forward_c5_full_size_sampled(gpu):
     ("c5", dict(T=8, H=1536, E=16, I=1472)),              # matrix core, 6 stages, scale rows 4- / 2-byte aligned
     ("c1", {}),                                           # GPTQ int4, T=16
     ("c2", dict(T=24)),                                   # GPTQ int4, more rows than experts' groups
+    # the routing launch's rank top-k: sigmoid + bias over a ragged E, every
+    # key slot used (16 tokens x 128, 4 tokens x 512)
+    ("c3", dict(T=10, H=1024, E=96, I=256, zipf=0.0, route=_abi.ROUTE_SIGMOID, bias_std=0.05, scaling=2.0)),
+    ("c3", dict(T=16, H=512, E=128, K=8, I=256)),
+    ("c1", dict(T=4, H=512, E=512, K=10, I=256)),
 ])
 def test_forward_grouped_gemv(gpu, name, kw, regime):
     """The expert-grouped GEMV regimes: each expert's weights streamed once
