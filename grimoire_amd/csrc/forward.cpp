@@ -110,11 +110,16 @@ struct Plan {
     uint32_t *gv_xf, *gv_hf, *gv_hfsh;   // formatted activation rows
 };
 
-// MXFP4 rows padded for the matrix-core grouped GEMV (gvm_padded_k):
-// payload K'/2, K'/32 scale bytes per row, K' = gvm_padded_k(K) > K.
-static bool mx_padded(const grim_quant_weight& w, int K) {
+// MXFP4 rows of the matrix-core grouped GEMV's length (gvm_padded_k):
+// payload K'/2, K'/32 scale bytes per row, K' = gvm_padded_k(K) >= K.
+static bool mx_rows_kp(const grim_quant_weight& w, int K) {
     const int kp = gvm_padded_k(K);
-    return w.fmt == GRIM_FMT_MXFP4 && kp != K && w.row_bytes == int64_t(kp / 2) && w.row_scales == kp / 32;
+    return w.fmt == GRIM_FMT_MXFP4 && w.row_bytes == int64_t(kp / 2) && w.row_scales == kp / 32;
+}
+
+// ... and longer than K: padded rows.
+static bool mx_padded(const grim_quant_weight& w, int K) {
+    return gvm_padded_k(K) != K && mx_rows_kp(w, K);
 }
 
 // Some weight of the layer holds padded MXFP4 rows: of the grouped GEMVs
@@ -133,7 +138,7 @@ bool gv_ok(const grim_moe_layer* L) {
     // (or MXFP4 rows padded for the matrix-core kernel, all alike)
     const bool pad = layer_mx_padded(L);
     auto packed = [pad](const grim_quant_weight& w, int K) {
-        if (pad) return mx_padded(w, K);
+        if (pad) return mx_rows_kp(w, K);   // (K' = K where K is whole stages already)
         // INT4 scale groups of >= 32 elements: at most K / 16 scale bytes per row
         return w.row_bytes == int64_t(K / 2) && int64_t(w.row_scales) * 32 <= K;
     };

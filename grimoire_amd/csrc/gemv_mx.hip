@@ -50,6 +50,19 @@ typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void* gvm_lds_ptr_t;
 
+// Wave timestamps for kernel studies, compiled in only with GRIM_TIMING: 16
+// per wave of the grid (wave 4 b + w), lane 0: 0 start, 1 first stage in,
+// 2 + k end of the wave's item k (k < 13), 15 exit.
+#ifdef GRIM_TIMING
+#define GVM_TS(i)                                                                                 \
+    do {                                                                                          \
+        if (a.ts && lane == 0 && (i) < 16)                                                        \
+            a.ts[(blockIdx.x * kGvmWaves + wave) * 16 + (i)] = __builtin_amdgcn_s_memrealtime();   \
+    } while (0)
+#else
+#define GVM_TS(i) do {} while (0)
+#endif
+
 constexpr int kGvmWaves = 4;
 constexpr int kGvmRows = 64;                    // weight rows per wave and item
 constexpr int kGvmKS = 256;                     // K per ring stage (two MFMA steps)
@@ -521,7 +534,8 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
     // (the descriptors are built here, not in the lambdas: a buffer
     // descriptor formed inside a lambda keeps the host pass from emitting
     // the kernel)
-    int item_c = 0, item_n = 0;
+    int item_c = 0, item_n = 0, n_done = 0;
+    GVM_TS(0);
     cur = make(int(blockIdx.x) * kGvmWaves + wave, item_c);
     if (cur.mc <= 0) return;
     nxt = make(item_c + wstride, item_n);
@@ -559,6 +573,7 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
             else if (nxt.mc > 0) issue(true, ahead - S, q + ST - 1);
             else issue(false, S - 1, q + ST - 1);
             asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WAIT) : "memory");
+            if (q == 0) GVM_TS(1);
             const uint32_t stb = ring_base + uint32_t(q % ST) * kGvmStage;
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
@@ -688,6 +703,8 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
                 }
             }
         }
+        if (n_done < 13) GVM_TS(2 + n_done);
+        ++n_done;
         if (nxt.mc <= 0) break;
         cur = nxt;
         cp = np;
@@ -699,6 +716,8 @@ __global__ __launch_bounds__(kGvmWaves * kWave) void gvm_kernel(GvArgs a) {
         na = gvm_rsrc(nxt.ab, 0x7FFFFFFF);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the repeats past the last item
+    GVM_TS(15);
+    (void)n_done;
 }
 
 // K a multiple of 64 (2-byte aligned scale rows) with at least ST - 1

@@ -247,6 +247,10 @@ def test_pad_mxfp4_rows_matches_host(gpu):
 @pytest.mark.parametrize("name,kw", [
     ("c3", dict(H=960, I=704, E=32)),                     # K' = 1024 / 768: padded rows of whole lines
     ("c5", dict(T=12, H=1088, E=32, I=320)),              # shared expert, group-limited sigmoid
+    # H a whole number of stages already: only down's rows are padded (the
+    # grouped GEMV takes the mixed layer: K' = K for gate_up), 16-byte scale rows
+    ("c3", dict(H=1536, I=1472, E=32)),
+    ("c5", dict(T=12, H=1536, E=32, I=1472)),             # with the shared expert
 ])
 def test_forward_mxfp4_padded_rows(gpu, name, kw, regime):
     """A layer whose MXFP4 rows are padded to grimoire_moe_mxfp4_padded_k(K)
@@ -273,6 +277,7 @@ def test_forward_mxfp4_padded_rows(gpu, name, kw, regime):
 
 @pytest.mark.parametrize("name,kw,regime", [
     ("c3", {}, 0),                                        # matrix-core grouped GEMV, merged dispatch
+    ("c3", dict(pad=True), 0),                            # padded rows (the bench's C3 layer)
     ("c5", dict(T=32, H=1024, E=64, I=512), 0),           # the same, aligned scale loads, shared expert
     ("c4", dict(T=256, H=1024, E=64, I=256), 2),          # INT8 rows mode (128- and 32-row tiles)
 ])
@@ -281,9 +286,11 @@ def test_forward_graph_replays(gpu, name, kw, regime):
     three rounds with eager work and synchronisations between replays:
     every replay equals the eager forward on the same input, bit for bit."""
     print(f"forward graph replays {name} {kw} regime {regime}", flush=True)
+    kw = dict(kw)
+    pad = kw.pop("pad", False)
     cfg = configs.scaled(configs.CONFIGS[name], **kw) if kw else configs.CONFIGS[name]
     wl = configs.make_workload(cfg, "cpu", seed=21)
-    Lg = wl.layer.to(gpu)
+    Lg = (wl.layer.pad_mxfp4() if pad else wl.layer).to(gpu)
     bias = None if wl.route_bias is None else wl.route_bias.to(gpu)
     fwd = ops.MoeForward(Lg, cfg.T, configs.route_params(cfg, bias), regime)
     xs = [(wl.x * (1.0 + 0.25 * s)).to(gpu) for s in range(3)]
@@ -310,3 +317,4 @@ def test_forward_graph_replays(gpu, name, kw, regime):
             torch.cuda.synchronize()
             assert torch.equal(oe.cpu(), eager[i][1]), f"routes, replay {rep} input {i}"
             assert torch.equal(y.cpu(), eager[i][0]), f"output, replay {rep} input {i}"
+
